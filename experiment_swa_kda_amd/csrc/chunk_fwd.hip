@@ -1,0 +1,664 @@
+// Chunked (C = 64) WY forward of Kimi Delta Attention on gfx950.
+//
+// Reference algebra: nanochat/mixers/cuda_kda/chunk_wy_forward.cu (A/M build and solve
+// :125-405, U/W :761-863, inter-chunk state scan :940-1276, output :1498-1588).  For a
+// chunk with inclusive in-chunk cumulative log decay G (per key channel):
+//   A[i,j]  = sum_c qh[i,c] kh[j,c] exp(G[i,c]-G[j,c])            j <= i
+//   M'[i,j] = sum_c kh[i,c] kh[j,c] exp(G[i,c]-G[j,c])            j <  i
+//   T = (I + diag(beta) M')^-1,  U = T (beta v),  W = T (beta kh exp(G))
+//   delta = U - W S ;  O = (qh exp(G)) S + A delta ;  S <- diag(exp(G_last)) S + Kd^T delta
+// with qh = scale * q/||q||, kh = k/||k||, Kd = kh exp(G_last - G).
+//
+// MI355X design:
+//  * kda_chunk_prep: builds the chunk / sequence tables (B x T or packed cu_seqlens).
+//  * intra kernel: one 256-thread workgroup per (chunk, head) tile, everything staged in
+//    LDS (f32 qh/kh/G).  The 64x64 A and M' are built as 16x16 MFMA tiles
+//    (v_mfma_f32_16x16x32_bf16).  Pairwise decays exp(G_i - G_j) are factorised around
+//    the first row r of the row block: exp(G_i - G_r) <= 1 and, for j < r,
+//    exp(G_r - G_j) <= 1, so no factor can overflow; only the diagonal block can, and a
+//    diagonal block whose decay span exceeds 80 nats falls back to an exact per-pair
+//    f32 loop.  T is formed in f32 by blocked forward substitution (16x16 blocks), then
+//    U and W by MFMA.  Factors are written once to the workspace in both row- and
+//    column-major form so every later MFMA operand is a contiguous 16-byte load.
+//  * scan kernel: one workgroup per (sequence, head, 16-wide V strip) walks the chunks
+//    in order holding its 128x16 f32 state slice in VGPRs as MFMA accumulators; the V
+//    columns of the state evolve independently, so strips never communicate.  Each step
+//    computes delta = U - W S, the output tile, and S <- lam S + Kd^T delta, and records
+//    the bf16 state and delta for the backward pass.
+// Every reduction has a fixed order, so the forward is bitwise deterministic.
+#include "chunk_host.hpp"
+#include "kda_device.hpp"
+#include "kda_host.hpp"
+
+namespace kda {
+
+struct FwdArgs {
+  int H;
+  int gate_mode;
+  float lb;
+  float scale;
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const void* gate;
+  const bf16* beta;
+  const float* A_log;
+  const float* dt_bias;
+  const float* s0;
+  bf16* out;
+  float* sfin;
+  Regions ws;
+};
+
+// ---------------------------------------------------------------------------
+// chunk / sequence tables
+// ---------------------------------------------------------------------------
+__global__ void chunk_prep_kernel(int B, int T, int num_seqs, const int* __restrict__ cu,
+                                  int max_chunks, int4* __restrict__ chunks,
+                                  int2* __restrict__ seqs) {
+  __shared__ int s_total;
+  const int tid = threadIdx.x;
+  if (cu == nullptr) {
+    const int nc = (T + kChunk - 1) / kChunk;
+    for (int c = tid; c < max_chunks; c += blockDim.x) {
+      const int s = c / nc, j = c % nc;
+      chunks[c] = make_int4(s * T + j * kChunk, min(kChunk, T - j * kChunk), s, j);
+    }
+    for (int s = tid; s < num_seqs; s += blockDim.x) seqs[s] = make_int2(s * nc, nc);
+    return;
+  }
+  if (tid == 0) {
+    int acc = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+      // clamp to [0, T] so a malformed cu_seqlens can never address outside the inputs
+      int a = min(max(cu[s], 0), T), b = min(max(cu[s + 1], 0), T);
+      int n = b > a ? (b - a + kChunk - 1) / kChunk : 0;
+      if (acc + n > max_chunks) n = 0;
+      seqs[s] = make_int2(acc, n);
+      acc += n;
+    }
+    s_total = acc;
+  }
+  __syncthreads();
+  for (int c = s_total + tid; c < max_chunks; c += blockDim.x) chunks[c] = make_int4(0, 0, -1, 0);
+  for (int s = tid; s < num_seqs; s += blockDim.x) {
+    const int2 sq = seqs[s];
+    const int a = min(max(cu[s], 0), T), b = min(max(cu[s + 1], 0), T);
+    for (int j = 0; j < sq.y; ++j)
+      chunks[sq.x + j] = make_int4(a + j * kChunk, min(kChunk, b - a - j * kChunk), s, j);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// intra-chunk kernel
+// ---------------------------------------------------------------------------
+template <int K, int V>
+struct IntraSmem {
+  static constexpr int KP = K + 4;  // f32 row stride (breaks power-of-two bank strides)
+  static constexpr int VP = V + 8;  // bf16 row stride
+  static constexpr int MP = 65;
+  static constexpr size_t off_q = 0;
+  static constexpr size_t off_k = off_q + 64 * KP * 4;
+  static constexpr size_t off_g = off_k + 64 * KP * 4;
+  static constexpr size_t off_m = off_g + 64 * KP * 4;
+  static constexpr size_t off_t = off_m + 64 * MP * 4;
+  static constexpr size_t off_x = off_t + 64 * MP * 4;
+  static constexpr size_t off_v = off_x + 3 * 16 * 17 * 4;
+  static constexpr size_t off_b = off_v + 64 * VP * 2;
+  static constexpr size_t off_f = off_b + 64 * 4;
+  static constexpr size_t bytes = off_f + 16;
+};
+
+__device__ __constant__ int kPairA[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
+__device__ __constant__ int kPairB[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
+  using L = IntraSmem<K, V>;
+  constexpr int KP = L::KP, VP = L::VP, MP = L::MP;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* sQ = (float*)(smem + L::off_q);
+  float* sK = (float*)(smem + L::off_k);
+  float* sG = (float*)(smem + L::off_g);
+  float* sM = (float*)(smem + L::off_m);
+  float* sT = (float*)(smem + L::off_t);
+  float* sX = (float*)(smem + L::off_x);
+  bf16* sV = (bf16*)(smem + L::off_v);
+  float* sB = (float*)(smem + L::off_b);
+  int* sF = (int*)(smem + L::off_f);
+
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int len = ch.y;
+  if (len <= 0) return;
+  const int H = a.H, h = blockIdx.y;
+  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int row0 = ch.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+
+  if (tid < 4) sF[tid] = 0;
+  for (int i = tid; i < 64 * MP; i += 256) sT[i] = 0.f;
+
+  // ---- phase 1: load, normalise, activate ----
+  {
+    constexpr int LPR = K / 8;
+    constexpr int RPP = 256 / LPR;
+    const int c0 = (tid % LPR) * 8;
+    const float* A_log = a.A_log;
+    for (int t = tid / LPR; t < 64; t += RPP) {
+      float qv[8], kv[8], gv[8];
+      if (t < len) {
+        const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
+        load8(a.q + base, qv);
+        load8(a.k + base, kv);
+        if (a.gate_mode == KDA_GATE_K3) {
+          float raw[8];
+          load8((const bf16*)a.gate + base, raw);
+          const float ea = expf(A_log[h]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            gv[e] = a.lb * sigmoid_acc(ea * (raw[e] + a.dt_bias[h * K + c0 + e]));
+        } else {
+          const float4* gp = (const float4*)((const float*)a.gate + base);
+          float4 g0 = gp[0], g1 = gp[1];
+          gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
+          gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = kv[e] = gv[e] = 0.f;
+      }
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sq += qv[e] * qv[e];
+        sk += kv[e] * kv[e];
+      }
+      sq = group_sum<LPR>(sq);
+      sk = group_sum<LPR>(sk);
+      const float rq = a.scale / fmaxf(sqrtf(sq), 1e-12f);
+      const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sQ[t * KP + c0 + e] = qv[e] * rq;
+        sK[t * KP + c0 + e] = kv[e] * rk;
+        sG[t * KP + c0 + e] = gv[e];
+      }
+      if (tid % LPR == 0) {
+        const float bt = t < len ? sigmoid_acc(to_f32(a.beta[(size_t)(row0 + t) * H + h])) : 0.f;
+        sB[t] = bt;
+        ((float*)a.ws.p[R_RQ])[tile * 64 + t] = rq;
+        ((float*)a.ws.p[R_RK])[tile * 64 + t] = rk;
+        ((float*)a.ws.p[R_BETA])[tile * 64 + t] = bt;
+      }
+    }
+  }
+  __syncthreads();
+  // beta * v (bf16) and the in-chunk cumulative decay
+  for (int idx = tid; idx < 64 * (V / 8); idx += 256) {
+    const int t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
+    float vv[8];
+    if (t < len) {
+      load8(a.v + ((size_t)(row0 + t) * H + h) * V + c0, vv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vv[e] = 0.f;
+    }
+    const float bt = sB[t];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sV[t * VP + c0 + e] = to_bf16(bt * vv[e]);
+  }
+  if (tid < K) {
+    const int c = tid;
+    float* Gout = (float*)a.ws.p[R_G] + tile * 64 * K;
+    float acc = 0.f;
+    for (int t = 0; t < 64; ++t) {
+      acc += sG[t * KP + c];
+      sG[t * KP + c] = acc;
+      Gout[t * K + c] = acc;
+    }
+    ((float*)a.ws.p[R_LAM])[tile * K + c] = expf(acc);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (sG[(16 * b) * KP + c] - sG[(16 * b + 15) * KP + c] > 80.f) atomicOr(&sF[b], 1);
+  }
+  __syncthreads();
+
+  // ---- phase 2: A and M' (16x16 tiles of the lower triangle) ----
+  bf16* Aout = (bf16*)a.ws.p[R_A] + tile * 64 * 64;
+  bf16* ATout = (bf16*)a.ws.p[R_AT] + tile * 64 * 64;
+  float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
+  for (int p = wave; p < 10; p += 4) {
+    const int ba = kPairA[p], bb = kPairB[p];
+    const int r = 16 * ba;
+    f32x4 accA = zero4(), accM = zero4();
+    if (!(ba == bb && sF[ba])) {
+      const int i = 16 * ba + lr, j = 16 * bb + lr;
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) {
+        const int c = 32 * s + 8 * kg;
+        bf16x8 fq, fk, fb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float gr = sG[r * KP + c + e];
+          const float ei = __expf(sG[i * KP + c + e] - gr);
+          const float ej = __expf(gr - sG[j * KP + c + e]);
+          fq[e] = to_bf16(sQ[i * KP + c + e] * ei);
+          fk[e] = to_bf16(sK[i * KP + c + e] * ei);
+          fb[e] = to_bf16(sK[j * KP + c + e] * ej);
+        }
+        accA = mfma16(fq, fb, accA);
+        accM = mfma16(fk, fb, accM);
+      }
+    } else {
+      // exact pairwise path for a diagonal block with a large decay span
+      const int jj = 16 * bb + lr;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = 16 * ba + 4 * kg + rr;
+        float sa = 0.f, sm = 0.f;
+        if (jj <= ii) {
+          for (int c = 0; c < K; ++c) {
+            const float e = expf(sG[ii * KP + c] - sG[jj * KP + c]);
+            const float kj = sK[jj * KP + c] * e;
+            sa = fmaf(sQ[ii * KP + c], kj, sa);
+            sm = fmaf(sK[ii * KP + c], kj, sm);
+          }
+        }
+        accA[rr] = sa;
+        accM[rr] = sm;
+      }
+    }
+    const int jj = 16 * bb + lr;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * ba + 4 * kg + rr;
+      const float av = jj <= ii ? accA[rr] : 0.f;
+      const float mv = jj < ii ? accM[rr] : 0.f;
+      Aout[ii * 64 + jj] = to_bf16(av);
+      ATout[jj * 64 + ii] = to_bf16(av);
+      sM[ii * MP + jj] = mv;
+      MPout[ii * 64 + jj] = mv;
+    }
+  }
+  // strictly-upper 16x16 blocks are zero
+  for (int idx = tid; idx < 64 * 64; idx += 256) {
+    const int ii = idx / 64, jj = idx % 64;
+    if (jj / 16 > ii / 16) {
+      Aout[ii * 64 + jj] = to_bf16(0.f);
+      ATout[jj * 64 + ii] = to_bf16(0.f);
+      sM[ii * MP + jj] = 0.f;
+      MPout[ii * 64 + jj] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: T = (I + diag(beta) M')^-1, blocked forward substitution ----
+  if (tid < 64) {
+    const int blk = tid / 16, j = tid % 16;
+    const int o = 16 * blk;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == j) ? 1.f : 0.f;
+      const float bi = sB[o + i];
+#pragma unroll
+      for (int m = 0; m < i; ++m)
+        if (m >= j) s -= bi * sM[(o + i) * MP + o + m] * x[m];
+      x[i] = (i < j) ? 0.f : s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sT[(o + i) * MP + o + j] = x[i];
+  }
+  __syncthreads();
+  for (int ba = 1; ba < 4; ++ba) {
+    for (int idx = tid; idx < ba * 256; idx += 256) {
+      const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
+      const float bi = sB[16 * ba + i];
+      float s = 0.f;
+      for (int m = 16 * bb; m < 16 * ba; ++m)
+        s = fmaf(sM[(16 * ba + i) * MP + m], sT[m * MP + 16 * bb + j], s);
+      sX[(bb * 16 + i) * 17 + j] = bi * s;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < ba * 256; idx += 256) {
+      const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
+      float s = 0.f;
+#pragma unroll
+      for (int m = 0; m < 16; ++m)
+        s = fmaf(sT[(16 * ba + i) * MP + 16 * ba + m], sX[(bb * 16 + m) * 17 + j], s);
+      sT[(16 * ba + i) * MP + 16 * bb + j] = -s;
+    }
+    __syncthreads();
+  }
+  {
+    float* Tout = (float*)a.ws.p[R_T] + tile * 64 * 64;
+    for (int idx = tid; idx < 64 * 64; idx += 256) Tout[idx] = sT[(idx / 64) * MP + idx % 64];
+  }
+
+  // ---- phase 4: U = T (beta v), W = T (beta kh exp(G)) ----
+  {
+    bf16* Uout = (bf16*)a.ws.p[R_U] + tile * 64 * V;
+    bf16* Wout = (bf16*)a.ws.p[R_W] + tile * 64 * K;
+    bf16* WTout = (bf16*)a.ws.p[R_WT] + tile * K * 64;
+    constexpr int NU = 4 * (V / 16), NW = 4 * (K / 16);
+    for (int p = wave; p < NU + NW; p += 4) {
+      const bool isU = p < NU;
+      const int q = isU ? p : p - NU;
+      const int rt = q % 4, ct = q / 4;
+      const int i = 16 * rt + lr, col = 16 * ct + lr;
+      f32x4 acc = zero4();
+      const int nsteps = (16 * rt + 15) / 32 + 1;
+      for (int s = 0; s < nsteps; ++s) {
+        const int j0 = 32 * s + 8 * kg;
+        bf16x8 fa, fb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          fa[e] = to_bf16(sT[i * MP + j0 + e]);
+          const int j = j0 + e;
+          fb[e] = isU ? sV[j * VP + col]
+                      : to_bf16(sB[j] * sK[j * KP + col] * __expf(sG[j * KP + col]));
+        }
+        acc = mfma16(fa, fb, acc);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = 16 * rt + 4 * kg + rr;
+        if (isU) {
+          Uout[ii * V + col] = to_bf16(acc[rr]);
+        } else {
+          Wout[ii * K + col] = to_bf16(acc[rr]);
+          WTout[col * 64 + ii] = to_bf16(acc[rr]);
+        }
+      }
+    }
+  }
+
+  // ---- phase 5: Qg = qh exp(G), Kd = kh exp(G_last - G) and their transposes ----
+  {
+    bf16* QG = (bf16*)a.ws.p[R_QG] + tile * 64 * K;
+    bf16* KD = (bf16*)a.ws.p[R_KD] + tile * 64 * K;
+    bf16* QGT = (bf16*)a.ws.p[R_QGT] + tile * K * 64;
+    bf16* KDT = (bf16*)a.ws.p[R_KDT] + tile * K * 64;
+    for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+      const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
+      float qg[8], kd[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = sG[t * KP + c0 + e];
+        qg[e] = sQ[t * KP + c0 + e] * expf(g);
+        kd[e] = sK[t * KP + c0 + e] * expf(sG[63 * KP + c0 + e] - g);
+      }
+      store8(QG + t * K + c0, qg);
+      store8(KD + t * K + c0, kd);
+    }
+    for (int idx = tid; idx < K * 8; idx += 256) {
+      const int c = idx / 8, t0 = (idx % 8) * 8;
+      float qg[8], kd[8];
+      const float gl = sG[63 * KP + c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = sG[(t0 + e) * KP + c];
+        qg[e] = sQ[(t0 + e) * KP + c] * expf(g);
+        kd[e] = sK[(t0 + e) * KP + c] * expf(gl - g);
+      }
+      store8(QGT + c * 64 + t0, qg);
+      store8(KDT + c * 64 + t0, kd);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// inter-chunk state scan fused with the output
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
+  constexpr int KT = K / 16 / 4;  // 16-row key tiles of the state per wave
+  constexpr int SP = K + 8;
+  constexpr int DP = 64 + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sS[2][16 * SP];
+  __shared__ __attribute__((aligned(16))) bf16 sD[16 * DP];
+  const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
+  const int H = a.H;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+
+  f32x4 S[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+    if (a.s0) {
+      const float4 s = *(const float4*)(a.s0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
+      S[kt][0] = s.x; S[kt][1] = s.y; S[kt][2] = s.z; S[kt][3] = s.w;
+    } else {
+      S[kt] = zero4();
+    }
+  }
+
+  int p = 0;
+  for (int ci = 0; ci < sq.y; ++ci) {
+    const int chunk = sq.x + ci;
+    const int4 ch = chunks[chunk];
+    const size_t tile = (size_t)chunk * H + h;
+    const int len = ch.y, row0 = ch.x;
+    bf16* sSp = sS[p];
+    // (1) publish the bf16 state slice as the MFMA B operand [v][k]
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = to_bf16(S[kt][r]);
+      *(bf16x4*)(sSp + lr * SP + k0) = x;
+    }
+    __syncthreads();
+    // (2) state history [K][V] for the backward pass
+    {
+      bf16* SH = (bf16*)a.ws.p[R_SH] + tile * K * V;
+      for (int idx = tid; idx < K * 2; idx += 256) {
+        const int kk = idx / 2, vh = (idx % 2) * 8;
+        bf16x8 x;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = sSp[(vh + e) * SP + kk];
+        *(bf16x8*)(SH + (size_t)kk * V + v0 + vh) = x;
+      }
+    }
+    // (3) delta rows 16*wave.. : U - W S
+    const int i = 16 * wave + lr;
+    {
+      const bf16* Wt = (const bf16*)a.ws.p[R_W] + tile * 64 * K;
+      const bf16* Ut = (const bf16*)a.ws.p[R_U] + tile * 64 * V;
+      bf16* DL = (bf16*)a.ws.p[R_DL] + tile * 64 * V;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) {
+        const bf16x8 fa = *(const bf16x8*)(Wt + i * K + 32 * s + 8 * kg);
+        const bf16x8 fb = *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg);
+        acc = mfma16(fa, fb, acc);
+      }
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * kg + r;
+        const float d = to_f32(Ut[t * V + v0 + lr]) - acc[r];
+        x[r] = to_bf16(d);
+        DL[t * V + v0 + lr] = x[r];
+      }
+      *(bf16x4*)(sD + lr * DP + 16 * wave + 4 * kg) = x;
+    }
+    __syncthreads();
+    // (4a) S <- lam S + Kd^T delta
+    {
+      const bf16* KDT = (const bf16*)a.ws.p[R_KDT] + tile * K * 64;
+      const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int kb = 16 * (wave * KT + kt);
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const bf16x8 fa = *(const bf16x8*)(KDT + (kb + lr) * 64 + 32 * s + 8 * kg);
+          const bf16x8 fb = *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg);
+          acc = mfma16(fa, fb, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[kt][r] = fmaf(lam[kb + 4 * kg + r], S[kt][r], acc[r]);
+      }
+    }
+    // (4b) O = Qg S + A delta for rows 16*wave..
+    {
+      const bf16* QG = (const bf16*)a.ws.p[R_QG] + tile * 64 * K;
+      const bf16* AM = (const bf16*)a.ws.p[R_A] + tile * 64 * 64;
+      f32x4 o = zero4();
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) {
+        const bf16x8 fa = *(const bf16x8*)(QG + i * K + 32 * s + 8 * kg);
+        const bf16x8 fb = *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg);
+        o = mfma16(fa, fb, o);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 fa = *(const bf16x8*)(AM + i * 64 + 32 * s + 8 * kg);
+        const bf16x8 fb = *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg);
+        o = mfma16(fa, fb, o);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * kg + r;
+        if (t < len) a.out[((size_t)(row0 + t) * H + h) * V + v0 + lr] = to_bf16(o[r]);
+      }
+    }
+    p ^= 1;
+  }
+  if (a.sfin) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      *(float4*)(a.sfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
+          make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+int validate_problem(const kda_chunk_problem* p, const char* who) {
+  KDA_REQUIRE(p, "%s: null problem", who);
+  KDA_REQUIRE(p->batch >= 0 && p->seq_len >= 0 && p->heads > 0, "%s: invalid B/T/H", who);
+  KDA_REQUIRE(p->key_dim == 64 || p->key_dim == 128, "%s: key_dim must be 64 or 128", who);
+  KDA_REQUIRE(p->value_dim == 64 || p->value_dim == 128, "%s: value_dim must be 64 or 128", who);
+  KDA_REQUIRE(p->gate_mode == KDA_GATE_K3 || p->gate_mode == KDA_GATE_LOGDECAY,
+              "%s: invalid gate_mode", who);
+  if (p->cu_seqlens) {
+    KDA_REQUIRE(p->batch == 1, "%s: cu_seqlens requires batch == 1", who);
+    KDA_REQUIRE(p->num_seqs >= 1, "%s: cu_seqlens requires num_seqs >= 1", who);
+  } else {
+    KDA_REQUIRE(p->num_seqs == p->batch, "%s: num_seqs must equal batch without cu_seqlens", who);
+  }
+  KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || p->lower_bound < 0.f,
+              "%s: lower_bound must be negative", who);
+  return KDA_OK;
+}
+
+ChunkGeom make_geom(const kda_chunk_problem* p) {
+  ChunkGeom g;
+  const int nc = (p->seq_len + kChunk - 1) / kChunk;
+  g.max_chunks = p->cu_seqlens ? nc + p->num_seqs : p->batch * nc;
+  g.heads = p->heads;
+  g.K = p->key_dim;
+  g.V = p->value_dim;
+  g.num_seqs = p->num_seqs;
+  return g;
+}
+
+template <int K, int V>
+static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArgs& a,
+                          hipStream_t stream) {
+  if (g.max_chunks > 0) {
+    constexpr size_t smem = IntraSmem<K, V>::bytes;
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e = hipFuncSetAttribute((const void*)chunk_fwd_intra_kernel<K, V>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_forward: LDS attribute: %s", hipGetErrorString(e));
+      attr = true;
+    }
+    auto intra = chunk_fwd_intra_kernel<K, V>;
+    hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(256),
+                       smem, stream, a);
+    KDA_LAUNCH_CHECK("chunk_forward intra");
+  }
+  if (p->num_seqs > 0) {
+    auto scan = chunk_fwd_scan_kernel<K, V>;
+    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16),
+                       dim3(256), 0, stream, a);
+    KDA_LAUNCH_CHECK("chunk_forward scan");
+  }
+  return KDA_OK;
+}
+
+int launch_chunk_prep(const kda_chunk_problem* p, const ChunkGeom& g, const Regions& ws,
+                      hipStream_t stream) {
+  if (g.max_chunks == 0 && p->num_seqs == 0) return KDA_OK;
+  hipLaunchKernelGGL(chunk_prep_kernel, dim3(1), dim3(256), 0, stream, p->batch, p->seq_len,
+                     p->num_seqs, p->cu_seqlens, g.max_chunks, (int4*)ws.p[R_CHUNKS],
+                     (int2*)ws.p[R_SEQS]);
+  KDA_LAUNCH_CHECK("chunk_prep");
+  return KDA_OK;
+}
+
+}  // namespace kda
+
+extern "C" size_t kda_chunk_workspace_bytes(const kda_chunk_problem* p) {
+  if (kda::validate_problem(p, "chunk_workspace_bytes") != KDA_OK) return 0;
+  return kda::ws_total_bytes(kda::make_geom(p));
+}
+
+extern "C" size_t kda_chunk_backward_scratch_bytes(const kda_chunk_problem* p) {
+  if (kda::validate_problem(p, "chunk_backward_scratch_bytes") != KDA_OK) return 0;
+  return kda::sc_total_bytes(kda::make_geom(p));
+}
+
+extern "C" int kda_chunk_forward(const kda_chunk_problem* p, const void* q, const void* k,
+                                 const void* v, const void* gate, const void* beta_logits,
+                                 const float* A_log, const float* dt_bias,
+                                 const float* initial_state, void* output, float* final_state,
+                                 void* workspace, hipStream_t stream) {
+  using namespace kda;
+  int rc = validate_problem(p, "chunk_forward");
+  if (rc != KDA_OK) return rc;
+  const bool empty = (size_t)p->batch * p->seq_len == 0;
+  KDA_REQUIRE(empty || (q && k && v && gate && beta_logits && output),
+              "chunk_forward: null input/output pointer");
+  KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || (A_log && dt_bias),
+              "chunk_forward: K3 gate needs A_log and dt_bias");
+  KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,
+              "chunk_forward: workspace must be non-null and 256-byte aligned");
+  const ChunkGeom g = make_geom(p);
+  FwdArgs a;
+  a.H = p->heads;
+  a.gate_mode = p->gate_mode;
+  a.lb = p->lower_bound;
+  a.scale = p->scale;
+  a.q = (const bf16*)q;
+  a.k = (const bf16*)k;
+  a.v = (const bf16*)v;
+  a.gate = gate;
+  a.beta = (const bf16*)beta_logits;
+  a.A_log = A_log;
+  a.dt_bias = dt_bias;
+  a.s0 = initial_state;
+  a.out = (bf16*)output;
+  a.sfin = final_state;
+  a.ws = ws_regions(g, workspace);
+  rc = launch_chunk_prep(p, g, a.ws, stream);
+  if (rc != KDA_OK) return rc;
+  if (p->key_dim == 128 && p->value_dim == 128) return launch_forward<128, 128>(p, g, a, stream);
+  if (p->key_dim == 64 && p->value_dim == 64) return launch_forward<64, 64>(p, g, a, stream);
+  if (p->key_dim == 128 && p->value_dim == 64) return launch_forward<128, 64>(p, g, a, stream);
+  return launch_forward<64, 128>(p, g, a, stream);
+}

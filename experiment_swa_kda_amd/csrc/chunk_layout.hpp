@@ -1,0 +1,128 @@
+// Workspace layout shared by the chunked forward and backward kernels.
+//
+// Work is cut into "tiles" = (chunk of <= 64 tokens of one sequence, head).  The chunk
+// table maps a chunk index to {first flat token row, length, sequence, index in
+// sequence}; the sequence table maps a sequence to {first chunk, chunk count}.  Every
+// per-tile region below is an array [n_tiles][...] with tile = chunk * H + head.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kda {
+
+enum WsRegion {
+  R_CHUNKS = 0,  // int4 [max_chunks]   {row0, len, seq, index_in_seq}
+  R_SEQS,        // int2 [num_seqs]     {first_chunk, n_chunks}
+  R_QG,          // bf16 [tile][64][K]  q_hat * exp(G)              (q_hat includes the scale)
+  R_QGT,         // bf16 [tile][K][64]  transpose of R_QG
+  R_KD,          // bf16 [tile][64][K]  k_hat * exp(G_last - G)
+  R_KDT,         // bf16 [tile][K][64]  transpose of R_KD
+  R_W,           // bf16 [tile][64][K]  W = T (beta k_hat exp(G))
+  R_WT,          // bf16 [tile][K][64]  transpose of R_W
+  R_U,           // bf16 [tile][64][V]  U = T (beta v)
+  R_A,           // bf16 [tile][64][64] A (lower, incl. diagonal)
+  R_AT,          // bf16 [tile][64][64] transpose of R_A
+  R_T,           // f32  [tile][64][64] T = (I + diag(beta) M')^-1
+  R_MP,          // f32  [tile][64][64] M' (strictly lower, without beta)
+  R_G,           // f32  [tile][64][K]  G = inclusive cumsum of g in the chunk
+  R_LAM,         // f32  [tile][K]      exp(G_last)
+  R_RQ,          // f32  [tile][64]     scale / max(||q||, 1e-12)
+  R_RK,          // f32  [tile][64]     1 / max(||k||, 1e-12)
+  R_BETA,        // f32  [tile][64]     sigmoid(beta_logits)
+  R_SH,          // bf16 [tile][K][V]   state entering the chunk (written by the scan)
+  R_DL,          // bf16 [tile][64][V]  delta = U - W S (written by the scan)
+  R_COUNT
+};
+
+enum ScRegion {
+  S_DSH = 0,  // bf16 [tile][K][V]   dL/dS at the chunk end
+  S_DDL,      // f32  [tile][64][V]  dL/d delta
+  S_DA,       // f32  [tile][64][64] dL/dA (masked lower)
+  S_DMP,      // f32  [tile][64][64] dL/dM' (strictly lower, beta folded in)
+  S_GQ,       // f32  [tile][64][K]  accumulated dL/dq_hat
+  S_GK,       // f32  [tile][64][K]  accumulated dL/dk_hat
+  S_GG,       // f32  [tile][64][K]  accumulated dL/dG
+  S_PP,       // f32  [tile][2][K]   gate parameter partials {sum draw, sum draw*(z+b)}
+  S_COUNT
+};
+
+struct ChunkGeom {
+  int max_chunks;
+  int heads;
+  int K;
+  int V;
+  int num_seqs;
+};
+
+__host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
+  const size_t nt = (size_t)g.max_chunks * g.heads;
+  const size_t K = g.K, V = g.V;
+  switch (r) {
+    case R_CHUNKS: return (size_t)g.max_chunks * 16;
+    case R_SEQS: return (size_t)g.num_seqs * 8;
+    case R_QG: case R_QGT: case R_KD: case R_KDT: case R_W: case R_WT: return nt * 64 * K * 2;
+    case R_U: return nt * 64 * V * 2;
+    case R_A: case R_AT: return nt * 64 * 64 * 2;
+    case R_T: case R_MP: return nt * 64 * 64 * 4;
+    case R_G: return nt * 64 * K * 4;
+    case R_LAM: return nt * K * 4;
+    case R_RQ: case R_RK: case R_BETA: return nt * 64 * 4;
+    case R_SH: return nt * K * V * 2;
+    case R_DL: return nt * 64 * V * 2;
+    default: return 0;
+  }
+}
+
+__host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
+  const size_t nt = (size_t)g.max_chunks * g.heads;
+  const size_t K = g.K, V = g.V;
+  switch (r) {
+    case S_DSH: return nt * K * V * 2;
+    case S_DDL: return nt * 64 * V * 4;
+    case S_DA: case S_DMP: return nt * 64 * 64 * 4;
+    case S_GQ: case S_GK: case S_GG: return nt * 64 * K * 4;
+    case S_PP: return nt * 2 * K * 4;
+    default: return 0;
+  }
+}
+
+struct Regions {
+  char* p[(int)R_COUNT > (int)S_COUNT ? (int)R_COUNT : (int)S_COUNT];
+};
+
+__host__ __device__ inline size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline size_t ws_total_bytes(const ChunkGeom& g) {
+  size_t t = 0;
+  for (int r = 0; r < R_COUNT; ++r) t += round256(ws_region_bytes(g, r));
+  return t;
+}
+
+inline size_t sc_total_bytes(const ChunkGeom& g) {
+  size_t t = 0;
+  for (int r = 0; r < S_COUNT; ++r) t += round256(sc_region_bytes(g, r));
+  return t;
+}
+
+inline Regions ws_regions(const ChunkGeom& g, void* base) {
+  Regions out;
+  char* p = (char*)base;
+  for (int r = 0; r < R_COUNT; ++r) {
+    out.p[r] = p;
+    p += round256(ws_region_bytes(g, r));
+  }
+  return out;
+}
+
+inline Regions sc_regions(const ChunkGeom& g, void* base) {
+  Regions out;
+  char* p = (char*)base;
+  for (int r = 0; r < S_COUNT; ++r) {
+    out.p[r] = p;
+    p += round256(sc_region_bytes(g, r));
+  }
+  return out;
+}
+
+}  // namespace kda

@@ -1,0 +1,141 @@
+// Single-token recurrent KDA step on gfx950 (HBM-bound: one read and one write of the
+// f32 state).  Reference: nanochat/mixers/cuda_kda/recurrent_decode.cu:24-181.
+//
+//   S1 = diag(exp(g)) S ;  r = v - k^T S1 ;  S' = S1 + beta k r^T ;  o = q^T S'
+//
+// State layout is V-first [B,H,V,K] f32, so one V row is K contiguous floats.  A
+// workgroup owns 32 V rows of one (b,h); a row is covered by K/4 lanes holding a float4
+// each, so every state access is a coalesced 16-byte load/store and the two row
+// reductions are in-wave shuffles.  Grid: (B*H) x (V/32) workgroups of 256 threads.
+#include "kda_device.hpp"
+#include "kda_host.hpp"
+
+namespace kda {
+
+constexpr int kDecodeRowsPerBlock = 32;
+
+template <int K>
+__global__ __launch_bounds__(256) void decode_kernel(
+    int heads, int V, int gate_mode, float lb, float scale, const bf16* __restrict__ q,
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const void* __restrict__ gate,
+    const bf16* __restrict__ beta_logits, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* initial_state, bf16* __restrict__ out,
+    float* final_state) {
+  constexpr int LPR = K / 4;          // lanes per V row
+  constexpr int RPP = kWave / LPR;    // rows per wave pass
+  __shared__ float s_q[K], s_kd[K], s_k[K], s_eg[K];
+  __shared__ float s_beta;
+  const int bh = blockIdx.x;
+  const int h = bh % heads;
+  const int tid = threadIdx.x;
+  const size_t tok = (size_t)bh;  // [B,1,H,*] flattened: (b*H + h)
+
+  if (tid < kWave) {
+    // wave 0 prepares the per-key quantities (K <= 128 -> two keys per lane)
+    float qv[2], kv[2];
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int c = tid + j * kWave;
+      qv[j] = c < K ? to_f32(q[tok * K + c]) : 0.f;
+      kv[j] = c < K ? to_f32(k[tok * K + c]) : 0.f;
+      sq += qv[j] * qv[j];
+      sk += kv[j] * kv[j];
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    const float rq = scale / fmaxf(sqrtf(sq), 1e-12f);
+    const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int c = tid + j * kWave;
+      if (c < K) {
+        float g;
+        if (gate_mode == KDA_GATE_K3) {
+          float raw = to_f32(reinterpret_cast<const bf16*>(gate)[tok * K + c]);
+          g = lb * sigmoid_acc(expf(A_log[h]) * (raw + dt_bias[h * K + c]));
+        } else {
+          g = reinterpret_cast<const float*>(gate)[tok * K + c];
+        }
+        float eg = expf(g);
+        s_q[c] = qv[j] * rq;
+        s_k[c] = kv[j] * rk;
+        s_eg[c] = eg;
+        s_kd[c] = kv[j] * rk * eg;
+      }
+    }
+    if (tid == 0) s_beta = sigmoid_acc(to_f32(beta_logits[tok]));
+  }
+  __syncthreads();
+
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int sub = lane / LPR, kl = lane % LPR;
+  const int k0 = kl * 4;
+  const float beta = s_beta;
+  float qk[4], kk[4], kd[4], eg[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qk[e] = s_q[k0 + e];
+    kk[e] = s_k[k0 + e];
+    kd[e] = s_kd[k0 + e];
+    eg[e] = s_eg[k0 + e];
+  }
+  const int row_base = blockIdx.y * kDecodeRowsPerBlock;
+  for (int rr = wave * RPP + sub; rr < kDecodeRowsPerBlock; rr += 4 * RPP) {
+    const int row = row_base + rr;
+    if (row >= V) break;
+    const size_t off = ((size_t)bh * V + row) * K + k0;
+    float4 s = initial_state ? *reinterpret_cast<const float4*>(initial_state + off)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    float sv[4] = {s.x, s.y, s.z, s.w};
+    float pred = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pred += kd[e] * sv[e];
+    pred = group_sum<LPR>(pred);
+    const float r = to_f32(v[tok * V + row]) - pred;
+    float o = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sv[e] = eg[e] * sv[e] + beta * kk[e] * r;
+      o += qk[e] * sv[e];
+    }
+    o = group_sum<LPR>(o);
+    if (final_state)
+      *reinterpret_cast<float4*>(final_state + off) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    if (kl == 0) out[tok * V + row] = to_bf16(o);
+  }
+}
+
+}  // namespace kda
+
+extern "C" int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_dim,
+                                    int32_t value_dim, int32_t gate_mode, float lower_bound,
+                                    float scale, const void* q, const void* k, const void* v,
+                                    const void* gate, const void* beta_logits,
+                                    const float* A_log, const float* dt_bias,
+                                    const float* initial_state, void* output,
+                                    float* final_state, hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(batch >= 0 && heads > 0, "recurrent_decode: invalid batch/heads");
+  KDA_REQUIRE(key_dim == 64 || key_dim == 128, "recurrent_decode: key_dim must be 64 or 128");
+  KDA_REQUIRE(value_dim > 0 && value_dim <= 4096, "recurrent_decode: invalid value_dim");
+  KDA_REQUIRE(gate_mode == KDA_GATE_K3 || gate_mode == KDA_GATE_LOGDECAY,
+              "recurrent_decode: invalid gate_mode");
+  KDA_REQUIRE(q && k && v && gate && beta_logits && output, "recurrent_decode: null pointer");
+  KDA_REQUIRE(gate_mode != KDA_GATE_K3 || (A_log && dt_bias),
+              "recurrent_decode: K3 gate needs A_log and dt_bias");
+  if (batch == 0) return KDA_OK;
+  dim3 grid(batch * heads, (value_dim + kDecodeRowsPerBlock - 1) / kDecodeRowsPerBlock);
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, heads, value_dim, gate_mode,
+                       lower_bound, scale, (const bf16*)q, (const bf16*)k, (const bf16*)v, gate,
+                       (const bf16*)beta_logits, A_log, dt_bias, initial_state, (bf16*)output,
+                       final_state);
+  };
+  if (key_dim == 128)
+    args(decode_kernel<128>);
+  else
+    args(decode_kernel<64>);
+  KDA_LAUNCH_CHECK("recurrent_decode");
+  return KDA_OK;
+}

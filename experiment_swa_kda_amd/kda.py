@@ -1,0 +1,506 @@
+"""Kimi Delta Attention mixer API backed by the MI355X (gfx950) HIP kernels.
+
+Drop-in for the public surface of the reference module nanochat/mixers/kda.py
+(``KDAState`` :23-35, ``Linear`` :38-43, ``RMSNormGated`` :46-59, ``ShortConvolution``
+:123-212, ``k3_decay_gate`` :230-243, ``kda`` :561-673, ``KimiDeltaAttention`` :676-798,
+``prepare_kda_backend`` :478-488) with the same names, defaults, shapes and exceptions.
+
+Modes:
+  * ``"reference"``  — the eager PyTorch token loop of the reference (:269-327), run only
+    when explicitly requested (CPU or GPU tensors, autograd backward).
+  * ``"project_chunk"`` / ``"chunk"`` — the chunked WY HIP kernels with the exact HIP
+    backward (``chunk`` names the reference's FLA comparator slot; here it is served by
+    the same kernels).
+  * ``"project_recurrent"`` / ``"recurrent"`` — inference-only; one token runs the HIP
+    decode step, longer inputs run the chunked HIP forward without autograd.
+Accelerated modes fail closed: an unsupported call raises RuntimeError whatever
+``allow_fallback`` says; nothing is silently rerouted to the eager loop.
+
+Two keyword extensions serve the benchmark configurations: ``gate="precomputed"``
+feeds an already-activated f32 log decay g in place of ``raw_gate`` (A_log and dt_bias
+are then unused), and ``cu_seqlens`` packs variable-length sequences with a state reset
+at each boundary.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+
+MODES = {"reference", "chunk", "recurrent", "project_chunk", "project_recurrent"}
+
+
+@dataclass
+class KDAState:
+    """Fixed-size state for recurrent KDA decoding.
+
+    ``memory`` uses the V-first ``[B,H,V,K]`` layout.  The convolution states are
+    ``[B,D,W]`` and contain the most recent projected inputs, including the current token.
+    """
+
+    memory: torch.Tensor
+    q_conv: torch.Tensor
+    k_conv: torch.Tensor
+    v_conv: torch.Tensor
+
+
+class Linear(nn.Linear):
+    """Keep master weights in FP32 while matching activation dtype for matmul."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        bias = None if self.bias is None else self.bias.to(dtype=x.dtype)
+        return F.linear(x, self.weight.to(dtype=x.dtype), bias)
+
+
+class RMSNormGated(nn.Module):
+    def __init__(self, hidden_size: int, eps: float = 1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        normalized = F.rms_norm(x, (x.shape[-1],), weight=self.weight.to(dtype=x.dtype), eps=self.eps)
+        return normalized * gate.sigmoid()
+
+
+# ---------------------------------------------------------------------------
+# runtime provenance (reference kda.py:62-90, 469-488)
+# ---------------------------------------------------------------------------
+
+_RUNTIME_EVENTS: list[dict[str, str]] = []
+
+
+def reset_project_runtime_events() -> None:
+    _RUNTIME_EVENTS.clear()
+
+
+def project_runtime_events() -> list[dict[str, str]]:
+    return list(_RUNTIME_EVENTS)
+
+
+def _record(component: str) -> None:
+    _RUNTIME_EVENTS.append({"component": component, "backend": "project"})
+
+
+def _record_backward(output: torch.Tensor, component: str) -> torch.Tensor:
+    if output.requires_grad:
+        output.register_hook(lambda grad: (_record(component), grad)[1])
+    return output
+
+
+_COMPONENTS = {
+    "chunk_forward": ("kda_chunk_forward", "chunk_fwd.hip"),
+    "chunk_backward": ("kda_chunk_backward", "chunk_bwd.hip"),
+    "recurrent_decode": ("kda_recurrent_decode", "decode.hip"),
+    "causal_convolution_forward": ("kda_causal_conv_forward", "conv.hip"),
+    "causal_convolution_backward": ("kda_causal_conv_backward", "conv.hip"),
+    "rmsnorm_gate_forward": ("kda_rmsnorm_gate_forward", "norm_gate.hip"),
+    "rmsnorm_gate_backward": ("kda_rmsnorm_gate_backward", "norm_gate.hip"),
+}
+
+
+def kda_backend_provenance() -> dict:
+    """Which native symbol and source own each component of the project backend."""
+    from . import _lib
+
+    return {
+        "library": _lib.LIB_PATH,
+        "components": {
+            name: {"owner": "project", "symbol": sym, "source": f"csrc/{src}",
+                   "torch_operator": f"nanochat_kda::{name}"}
+            for name, (sym, src) in _COMPONENTS.items()
+        },
+    }
+
+
+def prepare_kda_backend(backend: str = "project_cuda") -> None:
+    """Load the native library and register ``torch.ops.nanochat_kda`` (fails closed).
+
+    ``"project_cuda"`` and ``"fla_triton"`` (the reference's comparator slot) both name
+    the HIP kernels here.
+    """
+    if backend not in {"project_cuda", "fla_triton"}:
+        raise ValueError(f"unknown optimized KDA backend: {backend}")
+    from . import _lib
+
+    _lib.load()
+    ops.register_operators()
+
+
+# ---------------------------------------------------------------------------
+# gate and validation
+# ---------------------------------------------------------------------------
+
+def _gate_shapes(raw_gate, A_log, dt_bias):
+    if raw_gate.ndim != 4:
+        raise ValueError("raw_gate must have shape [B, T, H, K]")
+    heads, key_dim = raw_gate.shape[-2:]
+    if A_log.shape != (heads,):
+        raise ValueError(f"A_log must have shape {(heads,)}")
+    if dt_bias.numel() != heads * key_dim:
+        raise ValueError(f"dt_bias must contain {heads * key_dim} values")
+    return heads, key_dim
+
+
+def k3_decay_gate(raw_gate, A_log, dt_bias, lower_bound: float = -5.0):
+    """K3 lower-bounded log decay: ``lb * sigmoid(exp(A) * (z+b))``."""
+    heads, key_dim = _gate_shapes(raw_gate, A_log, dt_bias)
+    if lower_bound >= 0:
+        raise ValueError("lower_bound must be negative")
+    return lower_bound * torch.sigmoid(A_log.exp().reshape(heads, 1) * (raw_gate + dt_bias.reshape(heads, key_dim)))
+
+
+def _validate_operator_inputs(q, k, v, raw_gate, beta_logits, initial_state, num_states=None):
+    if q.shape != k.shape or q.shape != raw_gate.shape or q.ndim != 4:
+        raise ValueError("q, k, and raw_gate must share shape [B, T, H, K]")
+    if v.ndim != 4 or v.shape[:3] != q.shape[:3]:
+        raise ValueError("v must have shape [B, T, H, V]")
+    if beta_logits.shape != q.shape[:3]:
+        raise ValueError("beta logits must have shape [B, T, H]")
+    batch, length, heads, key_dim = q.shape
+    value_dim = v.shape[-1]
+    if initial_state is not None:
+        n = batch if num_states is None else num_states
+        expected = (n, heads, value_dim, key_dim)
+        if initial_state.shape != expected:
+            raise ValueError(f"initial_state must be V-first [B, H, V, K] with shape {expected}")
+    return batch, length, heads, key_dim, value_dim
+
+
+def _reference_kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias, *, initial_state, lower_bound,
+                   scale, gate="k3"):
+    """Eager PyTorch token loop (reference kda.py:269-327); explicit ``mode="reference"`` only."""
+    batch, length, heads, key_dim, value_dim = _validate_operator_inputs(
+        q, k, v, raw_gate, beta_logits, initial_state)
+    query_scale = key_dim ** -0.5 if scale is None else scale
+    q_float = F.normalize(q.float(), p=2, dim=-1) * query_scale
+    k_float = F.normalize(k.float(), p=2, dim=-1)
+    v_float = v.float()
+    if gate == "k3":
+        _gate_shapes(raw_gate, A_log, dt_bias)
+        decay = k3_decay_gate(raw_gate.float(), A_log.float(), dt_bias.float(), lower_bound=lower_bound)
+    else:
+        decay = raw_gate.float()
+    beta = beta_logits.float().sigmoid()
+    if initial_state is None:
+        state = torch.zeros(batch, heads, key_dim, value_dim, dtype=torch.float32, device=q.device)
+    else:
+        state = initial_state.float().transpose(-1, -2)
+    outputs = []
+    for index in range(length):
+        ki = k_float[:, index]
+        state = state * decay[:, index].exp().unsqueeze(-1)
+        residual = v_float[:, index] - torch.einsum("bhk,bhkv->bhv", ki, state)
+        state = state + torch.einsum("bhk,bhv->bhkv", beta[:, index].unsqueeze(-1) * ki, residual)
+        outputs.append(torch.einsum("bhk,bhkv->bhv", q_float[:, index], state))
+    output = torch.stack(outputs, dim=1) if outputs else v_float.new_empty(batch, 0, heads, value_dim)
+    return output.to(v.dtype), state.transpose(-1, -2).contiguous()
+
+
+def _backend_reason(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, *, lower_bound,
+                    gate):
+    if not q.is_cuda:
+        return "the MI355X KDA kernels require a ROCm device"
+    activations = (q, k, v, beta_logits) + ((raw_gate,) if gate == "k3" else ())
+    params = (A_log, dt_bias) if gate == "k3" else ()
+    if any(t.device != q.device for t in (*activations, raw_gate, *params)):
+        return "all KDA tensors must be on the same device"
+    if any(t.dtype != torch.bfloat16 for t in activations):
+        return "the MI355X KDA kernels require bfloat16 activations"
+    if gate == "k3":
+        if A_log.dtype != torch.float32 or dt_bias.dtype != torch.float32:
+            return "A_log and dt_bias must be float32"
+        if not lower_bound < 0.0:
+            return "lower_bound must be negative"
+    elif raw_gate.dtype != torch.float32:
+        return "a precomputed log decay must be float32"
+    if q.shape[-1] not in (64, 128) or v.shape[-1] not in (64, 128):
+        return "head dimensions must be 64 or 128"
+    if initial_state is not None:
+        if initial_state.device != q.device:
+            return "initial_state must be on the same device as q"
+        if initial_state.dtype != torch.float32:
+            return "initial_state must be float32"
+    return None
+
+
+# ---------------------------------------------------------------------------
+# autograd boundaries (reference kda.py:383-466)
+# ---------------------------------------------------------------------------
+
+class _ProjectKDAAutograd(torch.autograd.Function):
+    """Chunked KDA: forward saves the residual workspace, backward runs the HIP VJP."""
+
+    @staticmethod
+    def forward(ctx, forward_component, backward_component, q, k, v, raw_gate, beta_logits, A_log,
+                dt_bias, initial_state, output_final_state, lower_bound, scale, cu_seqlens=None,
+                gate="k3"):
+        output, final_state, workspace = ops.chunk_forward(
+            q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, output_final_state,
+            lower_bound, scale, cu_seqlens=cu_seqlens, gate=gate)
+        ctx.backward_component = backward_component
+        ctx.has_initial = initial_state is not None
+        ctx.lower_bound = lower_bound
+        ctx.scale = scale
+        ctx.gate = gate
+        ctx.save_for_backward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
+                              workspace, cu_seqlens)
+        return output, final_state
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_final_state):
+        q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, workspace, cu_seqlens = ctx.saved_tensors
+        grads = ops.chunk_backward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
+                                   workspace, grad_output, grad_final_state, ctx.lower_bound,
+                                   ctx.scale, cu_seqlens=cu_seqlens, gate=ctx.gate)
+        if len(grads) != 8:
+            raise RuntimeError("project chunk backward must return eight gradients")
+        dq, dk, dv, draw_gate, dbeta, dA, ddt, dinitial = grads
+        if ddt is not None:
+            ddt = ddt.reshape(dt_bias.shape)
+        if not ctx.has_initial:
+            dinitial = None
+        return (None, None, dq, dk, dv, draw_gate, dbeta, dA, ddt, dinitial, None, None, None,
+                None, None)
+
+
+class _ProjectRMSNormGateAutograd(torch.autograd.Function):
+    """Fused RMSNorm * sigmoid(gate) on the HIP kernels (reference kda.py:418-436)."""
+
+    @staticmethod
+    def forward(ctx, x, gate, weight, epsilon):
+        output, inverse_rms = ops.rmsnorm_gate_forward(x, gate, weight, epsilon)
+        ctx.epsilon = epsilon
+        ctx.save_for_backward(x, gate, weight, inverse_rms)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, gate, weight, inverse_rms = ctx.saved_tensors
+        dx, dgate, dweight = ops.rmsnorm_gate_backward(x, gate, weight, inverse_rms,
+                                                       grad_output, ctx.epsilon)
+        return dx, dgate, dweight, None
+
+
+class _ProjectConvolutionAutograd(torch.autograd.Function):
+    """Causal conv + SiLU on the HIP kernels (reference kda.py:439-466)."""
+
+    @staticmethod
+    def forward(ctx, forward_component, backward_component, x, weight, initial_state,
+                output_final_state):
+        output, final_state = ops.causal_conv_forward(x, weight, initial_state, output_final_state)
+        ctx.backward_component = backward_component
+        ctx.has_initial = initial_state is not None
+        ctx.save_for_backward(x, weight, initial_state)
+        return output, final_state
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_final_state):
+        x, weight, initial_state = ctx.saved_tensors
+        dx, dweight, dinitial = ops.causal_conv_backward(x, weight, initial_state, grad_output,
+                                                         grad_final_state)
+        if not ctx.has_initial:
+            dinitial = None
+        return None, None, dx, dweight, dinitial, None
+
+
+# ---------------------------------------------------------------------------
+# operator entry point
+# ---------------------------------------------------------------------------
+
+def kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias, *, initial_state=None,
+        output_final_state=False, mode="reference", lower_bound=-5.0, scale=None,
+        allow_fallback=True, cu_seqlens=None, gate="k3"):
+    """Run KDA through the requested backend (reference kda.py:561-673).
+
+    Returns ``(output [B,T,H,V], final_state [N,H,V,K] or None)``.  Accelerated modes
+    never fall back to the eager loop; ``allow_fallback`` is accepted for API
+    compatibility only.
+    """
+    del allow_fallback
+    if mode not in MODES:
+        raise ValueError(f"unknown KDA mode: {mode}")
+    if gate not in ("k3", "precomputed"):
+        raise ValueError(f"unknown gate parameterisation: {gate}")
+    num_states = None if cu_seqlens is None else int(cu_seqlens.numel()) - 1
+    _validate_operator_inputs(q, k, v, raw_gate, beta_logits, initial_state, num_states)
+    if gate == "k3":
+        _gate_shapes(raw_gate, A_log, dt_bias)
+    if mode == "reference":
+        if cu_seqlens is not None:
+            raise ValueError("mode='reference' does not take cu_seqlens")
+        output, final_state = _reference_kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
+                                             initial_state=initial_state, lower_bound=lower_bound,
+                                             scale=scale, gate=gate)
+        return output, final_state if output_final_state else None
+
+    prefix = "project CUDA KDA backend unavailable" if mode.startswith("project_") else \
+        f"optimized {mode} KDA backend unavailable"
+    reason = _backend_reason(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
+                             lower_bound=lower_bound, gate=gate)
+    requested = mode.removeprefix("project_")
+    if requested == "recurrent" and torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q, k, v, raw_gate, beta_logits, A_log, dt_bias)):
+        reason = f"{'project ' if mode.startswith('project_') else ''}recurrent KDA is inference-only"
+    if reason is None and mode == "project_recurrent" and q.shape[1] != 1:
+        reason = "project recurrent KDA decodes exactly one token per call"
+    if reason is not None:
+        raise RuntimeError(f"{prefix}: {reason}")
+    if cu_seqlens is not None:
+        cu_seqlens = cu_seqlens.to(device=q.device, dtype=torch.int32)
+        host = cu_seqlens.cpu()
+        if q.shape[0] != 1 or int(host[0]) != 0 or int(host[-1]) != q.shape[1] or bool((host[1:] < host[:-1]).any()):
+            raise ValueError("cu_seqlens must start at 0, be non-decreasing and end at T (batch 1)")
+    resolved_scale = float(scale if scale is not None else q.shape[-1] ** -0.5)
+    if requested == "chunk":
+        output, final_state = _ProjectKDAAutograd.apply(
+            "chunk_forward", "chunk_backward", q, k, v, raw_gate, beta_logits, A_log, dt_bias,
+            initial_state, output_final_state, float(lower_bound), resolved_scale, cu_seqlens, gate)
+        _record("chunk_forward")
+        return _record_backward(output, "chunk_backward"), final_state
+    if q.shape[1] == 1 and cu_seqlens is None:
+        output, final_state = ops.recurrent_decode(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
+                                                   initial_state, output_final_state,
+                                                   float(lower_bound), resolved_scale, gate=gate)
+        _record("recurrent_decode")
+        return output, final_state
+    output, final_state, _ = ops.chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
+                                               initial_state, output_final_state, float(lower_bound),
+                                               resolved_scale, cu_seqlens=cu_seqlens, gate=gate)
+    _record("chunk_forward")
+    return output, final_state
+
+
+# ---------------------------------------------------------------------------
+# short convolution and the mixer block
+# ---------------------------------------------------------------------------
+
+class ShortConvolution(nn.Conv1d):
+    """Depthwise causal convolution + SiLU with explicit, non-mutating cache state."""
+
+    def __init__(self, hidden_size: int, kernel_size: int = 4):
+        super().__init__(hidden_size, hidden_size, kernel_size, groups=hidden_size, bias=False,
+                         padding=kernel_size - 1)
+
+    def forward(self, x, state=None, *, output_final_state=False, backend="fla_triton"):
+        if x.ndim != 3 or x.shape[-1] != self.in_channels:
+            raise ValueError(f"x must have shape [B,T,{self.in_channels}]")
+        batch, length, channels = x.shape
+        width = self.kernel_size[0]
+        if state is None:
+            current = x.new_zeros(batch, channels, width)
+        else:
+            expected = (batch, channels, width)
+            if state.shape != expected:
+                raise ValueError(f"convolution state must have shape {expected}")
+            current = state.to(device=x.device, dtype=x.dtype).clone()
+        if length == 0:
+            return x.new_empty(batch, 0, channels), current if output_final_state else None
+        if backend == "project_cuda" and not x.is_cuda:
+            raise RuntimeError("project CUDA causal convolution cannot fall back on CPU")
+        if x.is_cuda:
+            if backend not in {"fla_triton", "project_cuda"}:
+                raise ValueError(f"unknown CUDA short-convolution backend: {backend}")
+            output, final_state = _ProjectConvolutionAutograd.apply(
+                "causal_convolution_forward", "causal_convolution_backward", x,
+                self.weight.squeeze(1).to(dtype=x.dtype), None if state is None else current,
+                output_final_state)
+            _record("causal_convolution_forward")
+            return _record_backward(output, "causal_convolution_backward"), final_state
+        # CPU tensors: the reference's own eager form (kda.py:192-212)
+        sequence = x.transpose(1, 2)
+        convolution_input = torch.cat((current[..., 1:], sequence), dim=-1)
+        output = F.silu(F.conv1d(convolution_input, self.weight.to(dtype=x.dtype), groups=channels)).transpose(1, 2)
+        final_state = convolution_input[..., -width:].clone() if output_final_state else None
+        return output, final_state
+
+
+class KimiDeltaAttention(nn.Module):
+    """K3-compatible KDA mixer with short convolution and full-rank output gate."""
+
+    def __init__(self, hidden_size: int, num_heads: int, head_dim: int, conv_size: int = 4,
+                 layer_idx: int | None = None, mode: str = "reference", norm_eps: float = 1e-5,
+                 lower_bound: float = -5.0, allow_fallback: bool = True):
+        super().__init__()
+        if hidden_size != num_heads * head_dim:
+            raise ValueError("initial KDA implementation requires hidden_size = num_heads * head_dim")
+        if conv_size <= 0:
+            raise ValueError("conv_size must be positive")
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.conv_size = conv_size
+        self.layer_idx = layer_idx
+        self.mode = mode
+        self.lower_bound = lower_bound
+        self.allow_fallback = allow_fallback
+
+        self.q_proj = Linear(hidden_size, hidden_size, bias=False)
+        self.k_proj = Linear(hidden_size, hidden_size, bias=False)
+        self.v_proj = Linear(hidden_size, hidden_size, bias=False)
+        self.q_conv1d = ShortConvolution(hidden_size, conv_size)
+        self.k_conv1d = ShortConvolution(hidden_size, conv_size)
+        self.v_conv1d = ShortConvolution(hidden_size, conv_size)
+
+        self.A_log = nn.Parameter(torch.zeros(num_heads, dtype=torch.float32))
+        self.f_a_proj = Linear(hidden_size, head_dim, bias=False)
+        self.f_b_proj = Linear(head_dim, hidden_size, bias=False)
+        self.dt_bias = nn.Parameter(torch.zeros(hidden_size, dtype=torch.float32))
+        self.b_proj = Linear(hidden_size, num_heads, bias=False)
+
+        self.g_proj = Linear(hidden_size, hidden_size, bias=False)
+        self.o_norm = RMSNormGated(head_dim, eps=norm_eps)
+        self.o_proj = Linear(hidden_size, hidden_size, bias=False)
+
+    def forward(self, hidden_states, state: KDAState | None = None, output_final_state: bool = False,
+                mode: str | None = None, allow_fallback: bool | None = None):
+        if hidden_states.ndim != 3 or hidden_states.shape[-1] != self.hidden_size:
+            raise ValueError(f"hidden_states must have shape [B,T,{self.hidden_size}]")
+        batch, length, _ = hidden_states.shape
+        requested_mode = self.mode if mode is None else mode
+        requested_fallback = self.allow_fallback if allow_fallback is None else allow_fallback
+        want_state = output_final_state
+        q_state = None if state is None else state.q_conv
+        k_state = None if state is None else state.k_conv
+        v_state = None if state is None else state.v_conv
+        memory = None if state is None else state.memory
+        conv_backend = "project_cuda" if requested_mode.startswith("project_") else "fla_triton"
+        q, q_final = self.q_conv1d(self.q_proj(hidden_states), q_state, output_final_state=want_state,
+                                   backend=conv_backend)
+        k, k_final = self.k_conv1d(self.k_proj(hidden_states), k_state, output_final_state=want_state,
+                                   backend=conv_backend)
+        v, v_final = self.v_conv1d(self.v_proj(hidden_states), v_state, output_final_state=want_state,
+                                   backend=conv_backend)
+        q = q.reshape(batch, length, self.num_heads, self.head_dim)
+        k = k.reshape(batch, length, self.num_heads, self.head_dim)
+        v = v.reshape(batch, length, self.num_heads, self.head_dim)
+        raw_gate = self.f_b_proj(self.f_a_proj(hidden_states)).reshape(batch, length, self.num_heads,
+                                                                       self.head_dim)
+        beta_logits = self.b_proj(hidden_states)
+        mixed, final_memory = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias,
+                                  initial_state=memory, output_final_state=want_state,
+                                  mode=requested_mode, lower_bound=self.lower_bound,
+                                  allow_fallback=requested_fallback)
+        output_gate = self.g_proj(hidden_states).reshape(batch, length, self.num_heads, self.head_dim)
+        use_fused = (requested_mode != "reference" and mixed.is_cuda and mixed.dtype == torch.bfloat16
+                     and output_gate.dtype == torch.bfloat16 and self.head_dim in (64, 128)
+                     and self.o_norm.weight.dtype == torch.float32)
+        if use_fused:
+            mixed = _ProjectRMSNormGateAutograd.apply(mixed, output_gate, self.o_norm.weight, self.o_norm.eps)
+            _record("rmsnorm_gate_forward")
+            mixed = _record_backward(mixed, "rmsnorm_gate_backward")
+        else:
+            mixed = self.o_norm(mixed, output_gate)
+        output = self.o_proj(mixed.reshape(batch, length, self.hidden_size))
+        final_state = KDAState(final_memory, q_final, k_final, v_final) if want_state else None
+        return output, final_state
+
+
+__all__ = ["KDAState", "KimiDeltaAttention", "k3_decay_gate", "kda", "prepare_kda_backend",
+           "ShortConvolution", "RMSNormGated", "Linear", "kda_backend_provenance",
+           "project_runtime_events", "reset_project_runtime_events"]

@@ -1,0 +1,173 @@
+/*
+ * kda_mi355x.h — C ABI of the MI355X (gfx950) Kimi Delta Attention operator library
+ * (libkda_mi355x.so).
+ *
+ * Every entry point takes raw device pointers plus explicit sizes, launches on the
+ * given HIP stream, never synchronises, never allocates, and returns KDA_OK (0) or a
+ * nonzero status; kda_last_error() then describes the failure (thread-local).  All
+ * tensors are dense and contiguous in the layouts written next to each argument.
+ * "bf16" is IEEE bfloat16 stored as 16-bit words; "f32" is float.
+ *
+ * Layout conventions (the reference's own, nanochat/mixers/kda.py:23-35,246-266):
+ *   q, k, gate   [B, T, H, K]      v, output [B, T, H, V]      beta_logits [B, T, H]
+ *   state        [N, H, V, K] f32 ("V-first"; N = B, or the number of packed sequences)
+ *   A_log [H] f32, dt_bias [H*K] f32
+ * With cu_seqlens (device int32, num_seqs+1 entries, B must be 1) the T axis holds
+ * num_seqs packed sequences and the recurrent state resets at each boundary.
+ */
+#ifndef KDA_MI355X_H
+#define KDA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_OK 0
+#define KDA_ERR_INVALID 1   /* bad shape, size, pointer or flag */
+#define KDA_ERR_LAUNCH 2    /* a HIP launch or runtime call failed */
+
+/* Gate parameterisations. */
+#define KDA_GATE_K3 0        /* g = lb*sigmoid(exp(A_log[h])*(raw+dt_bias[h,k])); gate is bf16 raw logits */
+#define KDA_GATE_LOGDECAY 1  /* gate is the activated f32 log decay g (<= 0) */
+
+/* Shape / option descriptor shared by the chunked forward and backward. */
+typedef struct kda_chunk_problem {
+  int32_t batch;       /* B */
+  int32_t seq_len;     /* T (total packed length when cu_seqlens != NULL) */
+  int32_t heads;       /* H */
+  int32_t key_dim;     /* K: 64 or 128 */
+  int32_t value_dim;   /* V: 64 or 128 */
+  int32_t num_seqs;    /* B without cu_seqlens; number of packed sequences with it */
+  const int32_t* cu_seqlens; /* device pointer or NULL */
+  int32_t gate_mode;   /* KDA_GATE_K3 or KDA_GATE_LOGDECAY */
+  float lower_bound;   /* K3 lower bound lb (< 0) */
+  float scale;         /* query scale (resolved by the caller, normally K^-0.5) */
+} kda_chunk_problem;
+
+/* Last error message of the calling thread ("" when none). */
+const char* kda_last_error(void);
+
+/* Library version string. */
+const char* kda_version(void);
+
+/*
+ * Bytes of the residual workspace the chunked forward fills and the chunked backward
+ * reads back (chunk table, per-chunk WY factors, state and delta histories).
+ * Replaces the output-storage "sidecar" of nanochat/mixers/cuda_kda/chunk_wy_forward.cu:1613-1652.
+ */
+size_t kda_chunk_workspace_bytes(const kda_chunk_problem* p);
+
+/* Bytes of scratch the chunked backward needs in addition to the workspace. */
+size_t kda_chunk_backward_scratch_bytes(const kda_chunk_problem* p);
+
+/*
+ * Chunked (C = 64) WY forward.  Replaces torch.ops.nanochat_kda.chunk_forward
+ * (nanochat/mixers/cuda_kda/chunk.cu:1665-1756, schema chunk.cu:2118-2121).
+ *   gate: bf16 raw gate logits (K3) or f32 log decay (LOGDECAY), [B,T,H,K]
+ *   A_log, dt_bias: used for K3 only (may be NULL for LOGDECAY)
+ *   initial_state: f32 [N,H,V,K] or NULL (zeros); never written
+ *   output: bf16 [B,T,H,V];  final_state: f32 [N,H,V,K] or NULL
+ *   workspace: kda_chunk_workspace_bytes(p) bytes, 256-byte aligned
+ * Deterministic: identical inputs give bitwise identical outputs.
+ */
+int kda_chunk_forward(const kda_chunk_problem* p,
+                      const void* q, const void* k, const void* v, const void* gate,
+                      const void* beta_logits, const float* A_log, const float* dt_bias,
+                      const float* initial_state, void* output, float* final_state,
+                      void* workspace, hipStream_t stream);
+
+/*
+ * Exact chunked backward.  Replaces torch.ops.nanochat_kda.chunk_backward
+ * (nanochat/mixers/cuda_kda/chunk.cu:1758-2113, schema chunk.cu:2122-2129).
+ *   workspace: as filled by kda_chunk_forward on the same inputs
+ *   grad_output bf16 [B,T,H,V]; grad_final_state f32 [N,H,V,K] or NULL
+ *   dq, dk: bf16 [B,T,H,K]; dv: bf16 [B,T,H,V]
+ *   dgate: bf16 [B,T,H,K] (K3: d raw_gate) or f32 (LOGDECAY: dL/dg)
+ *   dbeta_logits: bf16 [B,T,H]
+ *   dA_log f32 [H], ddt_bias f32 [H*K]: K3 only (may be NULL for LOGDECAY)
+ *   dinitial_state f32 [N,H,V,K] or NULL
+ *   scratch: kda_chunk_backward_scratch_bytes(p) bytes, 256-byte aligned
+ * Parameter gradients are reduced in a fixed order (no atomics).
+ */
+int kda_chunk_backward(const kda_chunk_problem* p,
+                       const void* q, const void* k, const void* v, const void* gate,
+                       const void* beta_logits, const float* A_log, const float* dt_bias,
+                       const float* initial_state, const void* workspace,
+                       const void* grad_output, const float* grad_final_state,
+                       void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
+                       float* dA_log, float* ddt_bias, float* dinitial_state,
+                       void* scratch, hipStream_t stream);
+
+/*
+ * Single-token recurrent step (T == 1).  Replaces torch.ops.nanochat_kda.recurrent_decode
+ * (nanochat/mixers/cuda_kda/recurrent_decode.cu:24-181, schema :186-189).
+ *   q, k, gate [B,1,H,K] bf16 (gate K3 raw logits), v [B,1,H,V] bf16, beta_logits [B,1,H] bf16
+ *   initial_state f32 [B,H,V,K] or NULL; output bf16 [B,1,H,V]; final_state f32 [B,H,V,K]
+ *   or NULL.  final_state may alias initial_state (in-place update).
+ */
+int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_dim, int32_t value_dim,
+                         int32_t gate_mode, float lower_bound, float scale,
+                         const void* q, const void* k, const void* v, const void* gate,
+                         const void* beta_logits, const float* A_log, const float* dt_bias,
+                         const float* initial_state, void* output, float* final_state,
+                         hipStream_t stream);
+
+/*
+ * Depthwise causal convolution + SiLU.  Replaces torch.ops.nanochat_kda.causal_convolution_forward
+ * (nanochat/mixers/cuda_kda/causal_convolution_forward.cu:149-238, schema :241-244).
+ *   x [B,T,C] bf16, weight [C,W] bf16, initial_state [B,C,W] bf16 or NULL,
+ *   output [B,T,C] bf16, final_state [B,C,W] bf16 or NULL.  The state holds the W most
+ *   recent inputs including the current token.  C % 8 == 0, 1 <= W <= 8.
+ */
+int kda_causal_conv_forward(int32_t batch, int32_t seq_len, int32_t channels, int32_t width,
+                            const void* x, const void* weight, const void* initial_state,
+                            void* output, void* final_state, hipStream_t stream);
+
+/* Bytes of scratch kda_causal_conv_backward needs (weight-gradient partials). */
+size_t kda_causal_conv_backward_scratch_bytes(int32_t batch, int32_t seq_len, int32_t channels,
+                                              int32_t width);
+
+/*
+ * Backward of kda_causal_conv_forward.  Replaces torch.ops.nanochat_kda.causal_convolution_backward
+ * (nanochat/mixers/cuda_kda/causal_convolution_backward.cu:74-453, schema :455-460).
+ *   grad_output [B,T,C] bf16, grad_final_state [B,C,W] bf16 or NULL
+ *   dx [B,T,C] bf16, dweight [C,W] bf16, dinitial_state [B,C,W] bf16 or NULL
+ * The weight gradient is reduced over (B, T) in a fixed order.
+ */
+int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t channels, int32_t width,
+                             const void* x, const void* weight, const void* initial_state,
+                             const void* grad_output, const void* grad_final_state,
+                             void* dx, void* dweight, void* dinitial_state,
+                             void* scratch, hipStream_t stream);
+
+/*
+ * Fused RMSNorm(x) * weight * sigmoid(gate) over rows of D = 128 (or 64).  Replaces
+ * torch.ops.nanochat_kda.rmsnorm_gate_forward (nanochat/mixers/cuda_kda/rmsnorm_gate.cu:31-71,
+ * schema :278-280).  x, gate, output [rows, D] bf16; weight [D] f32; inv_rms [rows] f32.
+ */
+int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x, const void* gate,
+                             const float* weight, float eps, void* output, float* inv_rms,
+                             hipStream_t stream);
+
+/* Bytes of scratch kda_rmsnorm_gate_backward needs (weight-gradient partials). */
+size_t kda_rmsnorm_gate_backward_scratch_bytes(int64_t rows, int32_t dim);
+
+/*
+ * Backward of the fused RMSNorm*gate.  Replaces torch.ops.nanochat_kda.rmsnorm_gate_backward
+ * (nanochat/mixers/cuda_kda/rmsnorm_gate.cu:73-184, schema :281-284).
+ *   dx, dgate [rows, D] bf16; dweight [D] f32 (fixed-order reduction).
+ */
+int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* x, const void* gate,
+                              const float* weight, const float* inv_rms, const void* grad_output,
+                              float eps, void* dx, void* dgate, float* dweight, void* scratch,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_MI355X_H */

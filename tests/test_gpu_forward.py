@@ -1,0 +1,148 @@
+"""GPU parity of the HIP forward kernels against the float64 oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kda_oracle as O
+from tests.kda_testutil import make_kda_inputs, np64, rel_err
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from experiment_swa_kda_amd import ops
+
+
+def run_chunk(d, gate, final=True, cu=None):
+    out, fin, _ = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"],
+                                    d["s0"], final, -5.0, d["q"].shape[-1] ** -0.5, cu_seqlens=cu, gate=gate)
+    return out, fin
+
+
+def oracle_fwd(d, gate):
+    return O.kda_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
+                         np64(d["A_log"]), np64(d["dt_bias"]), initial_state=np64(d["s0"]),
+                         gate_mode="k3" if gate == "k3" else "logdecay")
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 31, 32, 33, 63, 64, 65, 127, 128, 129, 257])
+def test_chunk_forward_boundary_lengths_d64(T):
+    d = make_kda_inputs(1, T, 2, 64, 64, seed=100 + T, state=True)
+    out, fin = run_chunk(d, "k3")
+    eo, ef = oracle_fwd(d, "k3")
+    assert rel_err(out, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+    torch.testing.assert_close(out.double().cpu(), torch.tensor(eo), atol=5e-3, rtol=5e-3)
+    torch.testing.assert_close(fin.double().cpu(), torch.tensor(ef), atol=5e-3, rtol=5e-3)
+
+
+@pytest.mark.parametrize("gate", ["k3", "precomputed"])
+@pytest.mark.parametrize("KV", [(128, 128), (64, 128), (128, 64)])
+def test_chunk_forward_d128(gate, KV):
+    K, V = KV
+    d = make_kda_inputs(2, 200, 3, K, V, seed=7, gate=gate, state=True, dist="baseline")
+    out, fin = run_chunk(d, gate)
+    eo, ef = oracle_fwd(d, gate)
+    assert rel_err(out, eo) < 2e-2, rel_err(out, eo)
+    assert rel_err(fin, ef) < 2e-2, rel_err(fin, ef)
+
+
+def test_chunk_forward_deterministic():
+    d = make_kda_inputs(2, 300, 3, 128, 128, seed=3)
+    a = run_chunk(d, "k3")
+    b = run_chunk(d, "k3")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_chunk_forward_varlen():
+    d = make_kda_inputs(1, 400, 2, 64, 64, seed=9, state=False)
+    cu = torch.tensor([0, 1, 70, 128, 129, 400], dtype=torch.int32, device="cuda")
+    out, fin = run_chunk(d, "k3", cu=cu)
+    eo, ef = O.kda_varlen_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
+                                  np64(d["A_log"]), np64(d["dt_bias"]), cu.cpu().numpy())
+    assert rel_err(out, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+
+
+def test_extreme_gates_finite():
+    d = make_kda_inputs(1, 256, 2, 64, 64, seed=5)
+    g = d["g"].clone()
+    g[..., ::2] = -100.0
+    g[..., 1::2] = 100.0
+    d["g"] = g
+    out, fin = run_chunk(d, "k3")
+    assert torch.isfinite(out).all() and torch.isfinite(fin).all()
+    eo, ef = oracle_fwd(d, "k3")
+    assert rel_err(out, eo) < 2e-2
+
+
+def test_steep_precomputed_decay_uses_exact_path():
+    # per-token log decay ~ -8 exceeds the 80-nat span guard inside 16-token blocks
+    d = make_kda_inputs(1, 130, 2, 64, 64, seed=6, gate="precomputed", state=True)
+    d["g"] = d["g"] * 8.0
+    out, fin = run_chunk(d, "precomputed")
+    eo, ef = oracle_fwd(d, "precomputed")
+    assert torch.isfinite(out).all()
+    assert rel_err(out, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+
+
+@pytest.mark.parametrize("K", [64, 128])
+def test_decode_matches_oracle_and_chunk(K):
+    d = make_kda_inputs(4, 17, 3, K, K, seed=11, state=True)
+    state = d["s0"]
+    outs = []
+    for t in range(17):
+        o, state = ops.recurrent_decode(d["q"][:, t:t + 1], d["k"][:, t:t + 1], d["v"][:, t:t + 1],
+                                        d["g"][:, t:t + 1], d["beta"][:, t:t + 1], d["A_log"], d["dt_bias"],
+                                        state, True, -5.0, K ** -0.5)
+        outs.append(o)
+    out = torch.cat(outs, 1)
+    eo, ef = oracle_fwd(d, "k3")
+    assert rel_err(out, eo) < 1e-2 and rel_err(state, ef) < 1e-3
+    co, cf = run_chunk(d, "k3")
+    torch.testing.assert_close(out.float(), co.float(), atol=5e-3, rtol=5e-3)
+
+
+def test_decode_in_place_and_input_preserved():
+    d = make_kda_inputs(2, 1, 3, 128, 128, seed=12, state=True)
+    s = d["s0"].clone()
+    o1, f1 = ops.recurrent_decode(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"],
+                                  s, True, -5.0, 128 ** -0.5)
+    assert torch.equal(s, d["s0"])
+    o2, f2 = ops.recurrent_decode(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"],
+                                  s, True, -5.0, 128 ** -0.5, out_state=s)
+    assert torch.equal(o1, o2) and torch.equal(f1, s)
+
+
+@pytest.mark.parametrize("T,state,W", [(1, True, 4), (3, True, 4), (50, False, 4), (257, True, 4), (33, True, 3)])
+def test_conv_forward_backward(T, state, W):
+    g = torch.Generator().manual_seed(T)
+    B, C = 2, 384
+    x = torch.randn(B, T, C, generator=g).bfloat16()
+    w = (torch.randn(C, W, generator=g) * 0.5).bfloat16()
+    st = torch.randn(B, C, W, generator=g).bfloat16() if state else None
+    dy = torch.randn(B, T, C, generator=g).bfloat16()
+    dfin = torch.randn(B, C, W, generator=g).bfloat16()
+    y, fin = ops.causal_conv_forward(x.cuda(), w.cuda(), None if st is None else st.cuda(), True)
+    ey, ef = O.causal_conv_forward(np64(x), np64(w), np64(st))
+    assert rel_err(y, ey) < 5e-3
+    np.testing.assert_array_equal(np64(fin), ef)
+    dx, dw, dst = ops.causal_conv_backward(x.cuda(), w.cuda(), None if st is None else st.cuda(), dy.cuda(), dfin.cuda())
+    edx, edw, edst = O.causal_conv_backward(np64(x), np64(w), np64(dy), np64(st), np64(dfin))
+    assert rel_err(dx, edx) < 5e-3 and rel_err(dw, edw) < 5e-3
+    if state:
+        assert rel_err(dst, edst) < 5e-3
+
+
+def test_rmsnorm_gate_forward_backward():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
+    gt = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
+    w = torch.randn(128, generator=g).float()
+    dy = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
+    y, inv = ops.rmsnorm_gate_forward(x.cuda(), gt.cuda(), w.cuda(), 1e-5)
+    ey, einv = O.rmsnorm_gate_forward(np64(x), np64(gt), np64(w), 1e-5)
+    assert rel_err(y, ey) < 5e-3 and rel_err(inv, einv.reshape(-1)) < 1e-5
+    dx, dg, dw = ops.rmsnorm_gate_backward(x.cuda(), gt.cuda(), w.cuda(), inv, dy.cuda(), 1e-5)
+    edx, edg, edw = O.rmsnorm_gate_backward(np64(x), np64(gt), np64(w), 1e-5, np64(dy))
+    assert rel_err(dx, edx) < 5e-3 and rel_err(dg, edg) < 5e-3 and rel_err(dw, edw) < 1e-4
