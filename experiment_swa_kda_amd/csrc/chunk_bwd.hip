@@ -1,11 +1,928 @@
-// Chunked backward (placeholder until the kernels land).
+// Exact chunked backward of Kimi Delta Attention on gfx950.
+//
+// Reference: the production WY backward nanochat/mixers/cuda_kda/chunk_wy_backward.cu
+// (reverse dH scan :2026-2584, chunk VJP :2818-3331, pair VJPs :3337-3552, prefix
+// reverse :3787-3800, finalize :3802-3894, parameter reductions :3896-3990) and the
+// analytic token-serial statement chunk.cu:578-870.
+//
+// Per chunk (forward: delta = U - W S, O = Qg S + A delta, S' = lam S + Kd^T delta):
+//   scan (reverse, sequential):  dDelta = A^T dO + Kd dS' ;  dS = Qg^T dO + lam dS' - W^T dDelta
+//   dense VJP (chunk-parallel):  dA = tril(dO delta^T), dQg = dO S^T, dKd = delta dS'^T,
+//       dlam = rowsum(S * dS'), dW = -dDelta S^T, dU = dDelta,
+//       dT = dU (beta v)^T + dW (beta kh e^G)^T, d(beta v) = T^T dU, d(beta kh e^G) = T^T dW,
+//       dM = -T^T dT T^T (strictly lower)
+//   decay-structured VJP:  A[i,j] = sum_c qh kh exp(G_i - G_j) and M' likewise give
+//       row-side (dqh, dkh) and column-side (dkh) terms and dG = qh*Rq + kh*Rk - kh*C.
+//   finalize: dg = reverse in-chunk cumsum of dG, K3 gate chain, L2-norm and sigmoid
+//       chains; gate parameter gradients are reduced in a fixed order (no atomics).
+//
+// MI355X mapping:
+//  * scan kernel: one workgroup per (sequence, head, 16-wide V strip); dS columns are
+//    independent, so the 128x16 f32 slice of dS lives in VGPRs as MFMA accumulators.
+//  * dense kernel: one workgroup per (chunk, head); all products are 16x16x32 bf16
+//    MFMA tiles with f32 accumulation; T, dT and T^T dT stay in f32 LDS.
+//  * decay kernel: one workgroup per (chunk, head); exp(G_i - G_j) is split around the
+//    first row of the row block (row side) or the last row of the column block (column
+//    side) so that every off-diagonal factor is <= 1, exactly as in the forward; a block
+//    whose decay span exceeds 80 nats runs an exact per-pair f32 loop instead.
 #include "chunk_host.hpp"
+#include "kda_device.hpp"
 
-extern "C" int kda_chunk_backward(const kda_chunk_problem* p, const void*, const void*,
-                                  const void*, const void*, const void*, const float*,
-                                  const float*, const float*, const void*, const void*,
-                                  const float*, void*, void*, void*, void*, void*, float*,
-                                  float*, float*, void*, hipStream_t) {
-  (void)p;
-  return kda::set_error(KDA_ERR_INVALID, "chunk_backward: not implemented");
+namespace kda {
+
+struct BwdArgs {
+  int H;
+  int gate_mode;
+  float lb;
+  float scale;
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const void* gate;
+  const bf16* beta_logits;
+  const float* A_log;
+  const float* dt_bias;
+  const bf16* dout;
+  const float* dsfin;
+  bf16* dq;
+  bf16* dk;
+  bf16* dv;
+  void* dgate;
+  bf16* dbeta;
+  float* dA_log;
+  float* ddt_bias;
+  float* ds0;
+  Regions ws;
+  Regions sc;
+};
+
+// ---------------------------------------------------------------------------
+// reverse state-gradient scan
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
+  constexpr int KT = K / 16 / 4;
+  constexpr int SP = K + 8;
+  constexpr int DP = 64 + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sDS[16 * SP];  // dS' as [v][k]
+  __shared__ __attribute__((aligned(16))) bf16 sDO[16 * DP];  // dO strip as [v][t]
+  __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];  // dDelta strip as [v][t]
+  const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
+  const int H = a.H;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+
+  f32x4 dS[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+    if (a.dsfin) {
+      const float4 s = *(const float4*)(a.dsfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
+      dS[kt][0] = s.x; dS[kt][1] = s.y; dS[kt][2] = s.z; dS[kt][3] = s.w;
+    } else {
+      dS[kt] = zero4();
+    }
+  }
+
+  for (int ci = sq.y - 1; ci >= 0; --ci) {
+    const int chunk = sq.x + ci;
+    const int4 ch = chunks[chunk];
+    const size_t tile = (size_t)chunk * H + h;
+    const int len = ch.y, row0 = ch.x;
+    // (1) publish dS' (bf16, [v][k]) and stage the dO strip as [v][t]
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = to_bf16(dS[kt][r]);
+      *(bf16x4*)(sDS + lr * SP + k0) = x;
+    }
+    {
+      const int t = tid / 4, vq = (tid % 4) * 4;
+      bf16x4 x;
+      if (t < len) {
+        x = *(const bf16x4*)(a.dout + ((size_t)(row0 + t) * H + h) * V + v0 + vq);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = to_bf16(0.f);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sDO[(vq + r) * DP + t] = x[r];
+    }
+    __syncthreads();
+    // (2) f32 dS' history [K][V] for the dense VJP
+    {
+      float* DSH = (float*)a.sc.p[S_DSH] + tile * K * V;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) DSH[(size_t)(k0 + r) * V + v0 + lr] = dS[kt][r];
+      }
+    }
+    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS'
+    {
+      const bf16* AT = (const bf16*)a.ws.p[R_AT] + tile * 64 * 64;
+      const bf16* KD = (const bf16*)a.ws.p[R_KD] + tile * 64 * K;
+      float* DDL = (float*)a.sc.p[S_DDL] + tile * 64 * V;
+      const int j = 16 * wave + lr;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 fa = *(const bf16x8*)(AT + j * 64 + 32 * s + 8 * kg);
+        const bf16x8 fb = *(const bf16x8*)(sDO + lr * DP + 32 * s + 8 * kg);
+        acc = mfma16(fa, fb, acc);
+      }
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) {
+        const bf16x8 fa = *(const bf16x8*)(KD + j * K + 32 * s + 8 * kg);
+        const bf16x8 fb = *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg);
+        acc = mfma16(fa, fb, acc);
+      }
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * kg + r;
+        DDL[t * V + v0 + lr] = acc[r];
+        x[r] = to_bf16(acc[r]);
+      }
+      *(bf16x4*)(sDD + lr * DP + 16 * wave + 4 * kg) = x;
+    }
+    __syncthreads();
+    // (4) dS = lam dS' + Qg^T dO - W^T dDelta
+    {
+      const bf16* QGT = (const bf16*)a.ws.p[R_QGT] + tile * K * 64;
+      const bf16* WT = (const bf16*)a.ws.p[R_WT] + tile * K * 64;
+      const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int kb = 16 * (wave * KT + kt);
+        f32x4 pq = zero4(), pw = zero4();
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const bf16x8 fq = *(const bf16x8*)(QGT + (kb + lr) * 64 + 32 * s + 8 * kg);
+          const bf16x8 fo = *(const bf16x8*)(sDO + lr * DP + 32 * s + 8 * kg);
+          pq = mfma16(fq, fo, pq);
+          const bf16x8 fw = *(const bf16x8*)(WT + (kb + lr) * 64 + 32 * s + 8 * kg);
+          const bf16x8 fd = *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg);
+          pw = mfma16(fw, fd, pw);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dS[kt][r] = fmaf(lam[kb + 4 * kg + r], dS[kt][r], pq[r] - pw[r]);
+      }
+    }
+    __syncthreads();
+  }
+  if (a.ds0) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      *(float4*)(a.ds0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
+          make_float4(dS[kt][0], dS[kt][1], dS[kt][2], dS[kt][3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dense chunk VJP
+// ---------------------------------------------------------------------------
+template <int K, int V>
+struct DenseSmem {
+  static constexpr int MP = 65;
+  static constexpr int KP = K + 4;
+  static constexpr int VP = V + 8;
+  static constexpr size_t off_t = 0;                            // f32 [64][65] T
+  static constexpr size_t off_dt = off_t + 64 * MP * 4;         // f32 [64][65] dT
+  static constexpr size_t off_y = off_dt + 64 * MP * 4;         // f32 [64][65] T^T dT
+  static constexpr size_t off_dw = off_y + 64 * MP * 4;         // f32 [64][KP] dW
+  static constexpr size_t off_du = off_dw + 64 * KP * 4;        // bf16 [64][VP] dU
+  static constexpr size_t off_b = off_du + 64 * VP * 2;         // f32 [64] beta
+  static constexpr size_t off_gl = off_b + 64 * 4;              // f32 [4][K] dG_last partials
+  static constexpr size_t off_pv = off_gl + 4 * K * 4;          // f32 [V/16][64] dbeta partials
+  static constexpr size_t off_pk = off_pv + (V / 16) * 64 * 4;  // f32 [K/16][64]
+  static constexpr size_t off_pm = off_pk + (K / 16) * 64 * 4;  // f32 [4][64]
+  static constexpr size_t bytes = off_pm + 4 * 64 * 4;
+};
+
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
+  using L = DenseSmem<K, V>;
+  constexpr int MP = L::MP, KP = L::KP, VP = L::VP;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* sT = (float*)(smem + L::off_t);
+  float* sDT = (float*)(smem + L::off_dt);
+  float* sY = (float*)(smem + L::off_y);
+  float* sDW = (float*)(smem + L::off_dw);
+  bf16* sDU = (bf16*)(smem + L::off_du);
+  float* sB = (float*)(smem + L::off_b);
+  float* sGL = (float*)(smem + L::off_gl);
+  float* sPV = (float*)(smem + L::off_pv);
+  float* sPK = (float*)(smem + L::off_pk);
+  float* sPM = (float*)(smem + L::off_pm);
+
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int len = ch.y;
+  if (len <= 0) return;
+  const int H = a.H, h = blockIdx.y;
+  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int row0 = ch.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+
+  const float* Tg = (const float*)a.ws.p[R_T] + tile * 64 * 64;
+  const float* MPg = (const float*)a.ws.p[R_MP] + tile * 64 * 64;
+  const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
+  const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
+  const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
+  const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
+  const bf16* DL = (const bf16*)a.ws.p[R_DL] + tile * 64 * V;
+  const float* DSH = (const float*)a.sc.p[S_DSH] + tile * K * V;
+  const float* DDL = (const float*)a.sc.p[S_DDL] + tile * 64 * V;
+  float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
+  float* GK = (float*)a.sc.p[S_GK] + tile * 64 * K;
+  float* GG = (float*)a.sc.p[S_GG] + tile * 64 * K;
+  float* DA = (float*)a.sc.p[S_DA] + tile * 64 * 64;
+  float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
+
+  // ---- P0: stage T, dU, beta; clear partials ----
+  for (int idx = tid; idx < 64 * 64; idx += 256) {
+    const int i = idx / 64, j = idx % 64;
+    sT[i * MP + j] = Tg[idx];
+    sDT[i * MP + j] = 0.f;
+  }
+  for (int idx = tid; idx < 64 * (V / 8); idx += 256) {
+    const int t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
+    const float4* p = (const float4*)(DDL + t * V + c0);
+    const float4 x0 = p[0], x1 = p[1];
+    bf16x8 x;
+    x[0] = to_bf16(x0.x); x[1] = to_bf16(x0.y); x[2] = to_bf16(x0.z); x[3] = to_bf16(x0.w);
+    x[4] = to_bf16(x1.x); x[5] = to_bf16(x1.y); x[6] = to_bf16(x1.z); x[7] = to_bf16(x1.w);
+    *(bf16x8*)(sDU + t * VP + c0) = x;
+  }
+  if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
+  for (int idx = tid; idx < 4 * 64; idx += 256) sPM[idx] = 0.f;
+  __syncthreads();
+
+  auto load_dout8 = [&](int i, int c0) -> bf16x8 {
+    if (i < len) return *(const bf16x8*)(a.dout + ((size_t)(row0 + i) * H + h) * V + c0);
+    bf16x8 z;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = to_bf16(0.f);
+    return z;
+  };
+  auto f2b8 = [&](const float* p) -> bf16x8 {
+    bf16x8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = to_bf16(p[e]);
+    return x;
+  };
+
+  // ---- PA: dQg, dKd, dW over the 64 x K grid ----
+  constexpr int NKT = 4 * (K / 16);
+  for (int p = wave; p < NKT; p += 4) {
+    const int rt = p % 4, ct = p / 4;
+    const int i = 16 * rt + lr, c = 16 * ct + lr;
+    f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
+      const int vv = 32 * s + 8 * kg;
+      float xs[8], xd[8], xu[8];
+      load8f(SH + (size_t)c * V + vv, xs);
+      load8f(DSH + (size_t)c * V + vv, xd);
+      load8f(DDL + i * V + vv, xu);
+      bf16x8 sHi, sLo, dHi, dLo, uHi, uLo;
+      split8(xs, sHi, sLo);
+      split8(xd, dHi, dLo);
+      split8(xu, uHi, uLo);
+      const bf16x8 aO = load_dout8(i, vv);
+      const bf16x8 aL = *(const bf16x8*)(DL + i * V + vv);
+      accQ = mfma16(aO, sHi, accQ);
+      accQ = mfma16(aO, sLo, accQ);
+      accK = mfma16(aL, dHi, accK);
+      accK = mfma16(aL, dLo, accK);
+      accW = mfma16(uHi, sHi, accW);
+      accW = mfma16(uHi, sLo, accW);
+      accW = mfma16(uLo, sHi, accW);
+    }
+    float colsum = 0.f;
+    const float GL = Gg[63 * K + c];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * rt + 4 * kg + rr;
+      const float G = Gg[ii * K + c];
+      const bool valid = ii < len;
+      const float qh = valid ? to_f32(a.q[((size_t)(row0 + ii) * H + h) * K + c]) * RQ[ii] : 0.f;
+      const float kh = valid ? to_f32(a.k[((size_t)(row0 + ii) * H + h) * K + c]) * RK[ii] : 0.f;
+      const float eG = expf(G), eKd = expf(GL - G);
+      const float Kd = kh * eKd;
+      GQ[ii * K + c] = accQ[rr] * eG;
+      GK[ii * K + c] = accK[rr] * eKd;
+      GG[ii * K + c] = accQ[rr] * qh * eG - accK[rr] * Kd;
+      colsum += accK[rr] * Kd;
+      sDW[ii * KP + c] = -accW[rr];
+    }
+    colsum += __shfl_xor(colsum, 16, kWave);
+    colsum += __shfl_xor(colsum, 32, kWave);
+    if (kg == 0) sGL[rt * K + c] = colsum;
+  }
+  // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
+  for (int p = wave; p < 16; p += 4) {
+    const int ba = p / 4, bb = p % 4;
+    if (bb > ba) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) DA[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr] = 0.f;
+      continue;
+    }
+    const int i = 16 * ba + lr, j = 16 * bb + lr;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
+      const int vv = 32 * s + 8 * kg;
+      acc = mfma16(load_dout8(i, vv), *(const bf16x8*)(DL + j * V + vv), acc);
+    }
+    const int jj = 16 * bb + lr;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * ba + 4 * kg + rr;
+      DA[ii * 64 + jj] = jj <= ii ? acc[rr] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- PB: dT (lower blocks), d(beta v), d(beta kh e^G) ----
+  for (int p = wave; p < 10; p += 4) {
+    const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
+    const int bb = p - (ba * (ba + 1)) / 2;
+    const int i = 16 * ba + lr, j = 16 * bb + lr;
+    f32x4 acc = zero4();
+    const float bj = sB[j];
+    const bool jv = j < len;
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
+      const int vv = 32 * s + 8 * kg;
+      bf16x8 fb;
+      if (jv) {
+        float x[8];
+        load8(a.v + ((size_t)(row0 + j) * H + h) * V + vv, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * x[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(0.f);
+      }
+      acc = mfma16(*(const bf16x8*)(sDU + i * VP + vv), fb, acc);
+    }
+    const float rkj = RK[j];
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+      const int cc = 32 * s + 8 * kg;
+      bf16x8 fb;
+      if (jv) {
+        float x[8];
+        load8(a.k + ((size_t)(row0 + j) * H + h) * K + cc, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * x[e] * rkj * expf(Gg[j * K + cc + e]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(0.f);
+      }
+      acc = mfma16(f2b8(sDW + i * KP + cc), fb, acc);
+    }
+    const int jj = 16 * bb + lr;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sDT[(16 * ba + 4 * kg + rr) * MP + jj] = acc[rr];
+  }
+  // d(beta v) = T^T dU  -> dv and beta partials
+  for (int p = wave; p < 4 * (V / 16); p += 4) {
+    const int rt = p % 4, ct = p / 4;
+    const int j = 16 * rt + lr, col = 16 * ct + lr;
+    f32x4 acc = zero4();
+    for (int s = (16 * rt) / 32; s < 2; ++s) {
+      const int i0 = 32 * s + 8 * kg;
+      bf16x8 fa, fb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fa[e] = to_bf16(sT[(i0 + e) * MP + j]);
+        fb[e] = sDU[(i0 + e) * VP + col];
+      }
+      acc = mfma16(fa, fb, acc);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int jj = 16 * rt + 4 * kg + rr;
+      float part = 0.f;
+      if (jj < len) {
+        const size_t off = ((size_t)(row0 + jj) * H + h) * V + col;
+        a.dv[off] = to_bf16(sB[jj] * acc[rr]);
+        part = acc[rr] * to_f32(a.v[off]);
+      }
+      part = group_sum<16>(part);
+      if (lr == 0) sPV[ct * 64 + jj] = part;
+    }
+  }
+  // d(beta kh e^G) = T^T dW -> dkh, dG, beta partials (same ownership as PA)
+  for (int p = wave; p < NKT; p += 4) {
+    const int rt = p % 4, ct = p / 4;
+    const int j = 16 * rt + lr, c = 16 * ct + lr;
+    f32x4 acc = zero4();
+    for (int s = (16 * rt) / 32; s < 2; ++s) {
+      const int i0 = 32 * s + 8 * kg;
+      bf16x8 fa, fb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fa[e] = to_bf16(sT[(i0 + e) * MP + j]);
+        fb[e] = to_bf16(sDW[(i0 + e) * KP + c]);
+      }
+      acc = mfma16(fa, fb, acc);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int jj = 16 * rt + 4 * kg + rr;
+      float part = 0.f;
+      if (jj < len) {
+        const float kh = to_f32(a.k[((size_t)(row0 + jj) * H + h) * K + c]) * RK[jj];
+        const float eG = expf(Gg[jj * K + c]);
+        const float bt = sB[jj];
+        part = acc[rr] * kh * eG;
+        GK[jj * K + c] += bt * eG * acc[rr];
+        GG[jj * K + c] += acc[rr] * bt * kh * eG;
+      }
+      part = group_sum<16>(part);
+      if (lr == 0) sPK[ct * 64 + jj] = part;
+    }
+  }
+  __syncthreads();
+
+  // ---- PC: Y = T^T dT ----
+  for (int p = wave; p < 16; p += 4) {
+    const int rt = p / 4, ct = p % 4;
+    const int i = 16 * rt + lr, jcol = 16 * ct + lr;
+    f32x4 acc = zero4();
+    for (int s = (16 * rt) / 32; s < 2; ++s) {
+      const int a0 = 32 * s + 8 * kg;
+      bf16x8 fa, fb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fa[e] = to_bf16(sT[(a0 + e) * MP + i]);
+        fb[e] = to_bf16(sDT[(a0 + e) * MP + jcol]);
+      }
+      acc = mfma16(fa, fb, acc);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sY[(16 * rt + 4 * kg + rr) * MP + jcol] = acc[rr];
+  }
+  __syncthreads();
+
+  // ---- PD: dM = -(Y T^T), strictly lower; dM' = beta_i dM ----
+  for (int p = wave; p < 10; p += 4) {
+    const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
+    const int bb = p - (ba * (ba + 1)) / 2;
+    const int i = 16 * ba + lr, j = 16 * bb + lr;
+    f32x4 acc = zero4();
+    const int nsteps = (16 * bb + 15) / 32 + 1;
+    for (int s = 0; s < nsteps; ++s) {
+      const int b0 = 32 * s + 8 * kg;
+      bf16x8 fa, fb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fa[e] = to_bf16(sY[i * MP + b0 + e]);
+        fb[e] = to_bf16(sT[j * MP + b0 + e]);
+      }
+      acc = mfma16(fa, fb, acc);
+    }
+    const int jj = 16 * bb + lr;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * ba + 4 * kg + rr;
+      const float dm = jj < ii ? -acc[rr] : 0.f;
+      DMP[ii * 64 + jj] = sB[ii] * dm;
+      float part = dm * MPg[ii * 64 + jj];
+      part = group_sum<16>(part);
+      if (lr == 0) sPM[bb * 64 + ii] = part;
+    }
+  }
+  for (int idx = tid; idx < 64 * 64; idx += 256) {
+    const int ii = idx / 64, jj = idx % 64;
+    if (jj / 16 > ii / 16) DMP[idx] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- PE: dbeta_logits and dG_last ----
+  if (tid < 64) {
+    const int t = tid;
+    if (t < len) {
+      float db = 0.f;
+      for (int c = 0; c < V / 16; ++c) db += sPV[c * 64 + t];
+      for (int c = 0; c < K / 16; ++c) db += sPK[c * 64 + t];
+      for (int b = 0; b < 4; ++b) db += sPM[b * 64 + t];
+      const float bt = sB[t];
+      a.dbeta[(size_t)(row0 + t) * H + h] = to_bf16(db * bt * (1.f - bt));
+    }
+  }
+  if (tid < K) {
+    const int c = tid;
+    float dl = 0.f;
+    for (int vv = 0; vv < V; vv += 8) {
+      float s[8], d[8];
+      load8f(SH + (size_t)c * V + vv, s);
+      load8f(DSH + (size_t)c * V + vv, d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dl = fmaf(s[e], d[e], dl);
+    }
+    const float lam = ((const float*)a.ws.p[R_LAM])[tile * K + c];
+    float gl = dl * lam;
+    for (int rt = 0; rt < 4; ++rt) gl += sGL[rt * K + c];
+    ((float*)a.sc.p[S_DGL])[tile * K + c] = gl;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decay-structured VJP and finalisation
+// ---------------------------------------------------------------------------
+template <int K>
+struct DecaySmem {
+  static constexpr int KP = K + 4;
+  static constexpr int MP = 65;
+  static constexpr size_t off_q = 0;
+  static constexpr size_t off_k = off_q + 64 * KP * 4;
+  static constexpr size_t off_g = off_k + 64 * KP * 4;
+  static constexpr size_t off_da = off_g + 64 * KP * 4;
+  static constexpr size_t off_dm = off_da + 64 * MP * 4;
+  static constexpr size_t off_f = off_dm + 64 * MP * 4;
+  static constexpr size_t bytes = off_f + 16;
+};
+
+template <int K>
+__global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
+  using L = DecaySmem<K>;
+  constexpr int KP = L::KP, MP = L::MP;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* sQ = (float*)(smem + L::off_q);
+  float* sK = (float*)(smem + L::off_k);
+  float* sG = (float*)(smem + L::off_g);
+  float* sDA = (float*)(smem + L::off_da);
+  float* sDM = (float*)(smem + L::off_dm);
+  int* sF = (int*)(smem + L::off_f);
+
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int len = ch.y;
+  if (len <= 0) return;
+  const int H = a.H, h = blockIdx.y;
+  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int row0 = ch.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+
+  const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
+  const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
+  const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
+  float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
+  float* GK = (float*)a.sc.p[S_GK] + tile * 64 * K;
+  float* GG = (float*)a.sc.p[S_GG] + tile * 64 * K;
+
+  // ---- P0: stage qh, kh, G, dA, dM' ----
+  if (tid < 4) sF[tid] = 0;
+  for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+    const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
+    float qv[8], kv[8];
+    if (t < len) {
+      const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
+      load8(a.q + base, qv);
+      load8(a.k + base, kv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] = kv[e] = 0.f;
+    }
+    const float rq = RQ[t], rk = RK[t];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sQ[t * KP + c0 + e] = qv[e] * rq;
+      sK[t * KP + c0 + e] = kv[e] * rk;
+      sG[t * KP + c0 + e] = Gg[t * K + c0 + e];
+    }
+  }
+  {
+    const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
+    const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
+    for (int idx = tid; idx < 64 * 64; idx += 256) {
+      sDA[(idx / 64) * MP + idx % 64] = DA[idx];
+      sDM[(idx / 64) * MP + idx % 64] = DMP[idx];
+    }
+  }
+  __syncthreads();
+  if (tid < K) {
+    const int c = tid;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (sG[(16 * b) * KP + c] - sG[(16 * b + 15) * KP + c] > 80.f) atomicOr(&sF[b], 1);
+  }
+  __syncthreads();
+
+  constexpr int NKT = 4 * (K / 16);
+  // ---- P1: row side  Rq = sum_j dA_ij kh_j e^{G_i-G_j},  Rk = sum_j dM'_ij kh_j e^{G_i-G_j} ----
+  for (int p = wave; p < NKT; p += 4) {
+    const int ba = p % 4, ct = p / 4;
+    const int r = 16 * ba;
+    const int c = 16 * ct + lr;
+    f32x4 rq = zero4(), rk = zero4();
+    if (!sF[ba]) {
+      const int i = 16 * ba + lr;
+      const int jmax = 16 * ba + 15;
+      const int nsteps = jmax / 32 + 1;
+      for (int s = 0; s < nsteps; ++s) {
+        const int j0 = 32 * s + 8 * kg;
+        bf16x8 fa, fm, fbh, fbl;
+        float xb[8];
+        const float gr = sG[r * KP + c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = j0 + e;
+          fa[e] = to_bf16(sDA[i * MP + j]);
+          fm[e] = to_bf16(sDM[i * MP + j]);
+          xb[e] = j <= jmax ? sK[j * KP + c] * __expf(gr - sG[j * KP + c]) : 0.f;
+        }
+        // the decay-scaled key operand is split (hi + lo): its rounding is systematic
+        // across the row/column terms of dG, which nearly cancel
+        split8(xb, fbh, fbl);
+        rq = mfma16(fa, fbh, rq);
+        rq = mfma16(fa, fbl, rq);
+        rk = mfma16(fm, fbh, rk);
+        rk = mfma16(fm, fbl, rk);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = 16 * ba + 4 * kg + rr;
+        const float f = __expf(sG[ii * KP + c] - sG[r * KP + c]);
+        rq[rr] *= f;
+        rk[rr] *= f;
+      }
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = 16 * ba + 4 * kg + rr;
+        float sq = 0.f, sk = 0.f;
+        for (int j = 0; j <= ii; ++j) {
+          const float kj = sK[j * KP + c] * expf(sG[ii * KP + c] - sG[j * KP + c]);
+          sq = fmaf(sDA[ii * MP + j], kj, sq);
+          sk = fmaf(sDM[ii * MP + j], kj, sk);
+        }
+        rq[rr] = sq;
+        rk[rr] = sk;
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * ba + 4 * kg + rr;
+      GQ[ii * K + c] += rq[rr];
+      GK[ii * K + c] += rk[rr];
+      GG[ii * K + c] += sQ[ii * KP + c] * rq[rr] + sK[ii * KP + c] * rk[rr];
+    }
+  }
+  // ---- P2: column side  C = sum_i (dA_ij qh_i + dM'_ij kh_i) e^{G_i-G_j}  (same ownership) ----
+  for (int p = wave; p < NKT; p += 4) {
+    const int bb = p % 4, ct = p / 4;
+    const int rp = 16 * bb + 15;
+    const int c = 16 * ct + lr;
+    f32x4 cq = zero4(), ck = zero4();
+    if (!sF[bb]) {
+      const int j = 16 * bb + lr;
+      const float gr = sG[rp * KP + c];
+      for (int s = (16 * bb) / 32; s < 2; ++s) {
+        const int i0 = 32 * s + 8 * kg;
+        bf16x8 fa, fm, bqh, bql, bkh, bkl;
+        float xq[8], xk[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = i0 + e;
+          const bool ok = i >= 16 * bb;
+          const float f = ok ? __expf(sG[i * KP + c] - gr) : 0.f;
+          fa[e] = to_bf16(sDA[i * MP + j]);
+          fm[e] = to_bf16(sDM[i * MP + j]);
+          xq[e] = sQ[i * KP + c] * f;
+          xk[e] = sK[i * KP + c] * f;
+        }
+        split8(xq, bqh, bql);
+        split8(xk, bkh, bkl);
+        cq = mfma16(fa, bqh, cq);
+        cq = mfma16(fa, bql, cq);
+        ck = mfma16(fm, bkh, ck);
+        ck = mfma16(fm, bkl, ck);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int jj = 16 * bb + 4 * kg + rr;
+        const float f = __expf(gr - sG[jj * KP + c]);
+        cq[rr] *= f;
+        ck[rr] *= f;
+      }
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int jj = 16 * bb + 4 * kg + rr;
+        float sq = 0.f, sk = 0.f;
+        for (int i = jj; i < 64; ++i) {
+          const float e = expf(sG[i * KP + c] - sG[jj * KP + c]);
+          sq = fmaf(sDA[i * MP + jj], sQ[i * KP + c] * e, sq);
+          sk = fmaf(sDM[i * MP + jj], sK[i * KP + c] * e, sk);
+        }
+        cq[rr] = sq;
+        ck[rr] = sk;
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int jj = 16 * bb + 4 * kg + rr;
+      const float cc = cq[rr] + ck[rr];
+      GK[jj * K + c] += cc;
+      GG[jj * K + c] -= sK[jj * KP + c] * cc;
+    }
+  }
+  __syncthreads();
+
+  // ---- P3: dg = reverse cumsum of dG (+ dG_last), gate chain, parameter partials ----
+  if (tid < K) {
+    const int c = tid;
+    float acc = ((const float*)a.sc.p[S_DGL])[tile * K + c];
+    float p0 = 0.f, p1 = 0.f;
+    const float ea = a.gate_mode == KDA_GATE_K3 ? expf(a.A_log[h]) : 0.f;
+    const float bias = a.gate_mode == KDA_GATE_K3 ? a.dt_bias[h * K + c] : 0.f;
+    for (int t = len - 1; t >= 0; --t) {
+      acc += GG[t * K + c];
+      const size_t off = ((size_t)(row0 + t) * H + h) * K + c;
+      if (a.gate_mode == KDA_GATE_K3) {
+        const float pre = to_f32(((const bf16*)a.gate)[off]) + bias;
+        const float s = sigmoid_acc(ea * pre);
+        const float dz = acc * a.lb * s * (1.f - s) * ea;
+        ((bf16*)a.dgate)[off] = to_bf16(dz);
+        p0 += dz;
+        p1 = fmaf(dz, pre, p1);
+      } else {
+        ((float*)a.dgate)[off] = acc;
+      }
+    }
+    if (a.gate_mode == KDA_GATE_K3) {
+      float* PP = (float*)a.sc.p[S_PP] + tile * 2 * K;
+      PP[c] = p0;
+      PP[K + c] = p1;
+    }
+  }
+  // ---- P4: L2-norm chains -> dq, dk ----
+  {
+    constexpr int LPR = K / 8;
+    constexpr int RPP = 256 / LPR;
+    const int c0 = (tid % LPR) * 8;
+    for (int t = tid / LPR; t < 64; t += RPP) {
+      if (t >= len) continue;  // uniform per LPR lane group
+      const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
+      float qv[8], kv[8], gq[8], gk[8];
+      load8(a.q + base, qv);
+      load8(a.k + base, kv);
+      float sq = 0.f, sk = 0.f, dq_dot = 0.f, dk_dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gq[e] = GQ[t * K + c0 + e];
+        gk[e] = GK[t * K + c0 + e];
+        sq += qv[e] * qv[e];
+        sk += kv[e] * kv[e];
+        dq_dot += qv[e] * gq[e];
+        dk_dot += kv[e] * gk[e];
+      }
+      sq = group_sum<LPR>(sq);
+      sk = group_sum<LPR>(sk);
+      dq_dot = group_sum<LPR>(dq_dot);
+      dk_dot = group_sum<LPR>(dk_dot);
+      const float nq = sqrtf(sq), nk = sqrtf(sk);
+      const float rq = RQ[t], rk = RK[t];
+      float oq[8], ok[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // dx = r * (g - xhat (xhat . g)), xhat = x / ||x||; clamped norms pass g * r through
+        oq[e] = nq > 1e-12f ? rq * (gq[e] - qv[e] * dq_dot / sq) : rq * gq[e];
+        ok[e] = nk > 1e-12f ? rk * (gk[e] - kv[e] * dk_dot / sk) : rk * gk[e];
+      }
+      store8(a.dq + base, oq);
+      store8(a.dk + base, ok);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gate parameter reduction (fixed order)
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(K) void chunk_bwd_params_kernel(BwdArgs a, int max_chunks) {
+  __shared__ float s_red[K];
+  const int h = blockIdx.x, c = threadIdx.x;
+  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+  const float* PP = (const float*)a.sc.p[S_PP];
+  float p0 = 0.f, p1 = 0.f;
+  for (int chn = 0; chn < max_chunks; ++chn) {
+    if (chunks[chn].y <= 0) continue;
+    const size_t tile = (size_t)chn * a.H + h;
+    p0 += PP[tile * 2 * K + c];
+    p1 += PP[tile * 2 * K + K + c];
+  }
+  a.ddt_bias[h * K + c] = p0;
+  s_red[c] = p1;
+  __syncthreads();
+  for (int w = K / 2; w >= 1; w >>= 1) {
+    if (c < w) s_red[c] += s_red[c + w];
+    __syncthreads();
+  }
+  if (c == 0) a.dA_log[h] = s_red[0];
+}
+
+template <int K, int V>
+static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdArgs& a,
+                           hipStream_t stream) {
+  if (p->num_seqs > 0) {
+    auto scan = chunk_bwd_scan_kernel<K, V>;
+    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16), dim3(256), 0, stream, a);
+    KDA_LAUNCH_CHECK("chunk_backward scan");
+  }
+  if (g.max_chunks > 0) {
+    constexpr size_t smem_d = DenseSmem<K, V>::bytes;
+    constexpr size_t smem_e = DecaySmem<K>::bytes;
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e1 = hipFuncSetAttribute((const void*)chunk_bwd_dense_kernel<K, V>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_d);
+      hipError_t e2 = hipFuncSetAttribute((const void*)chunk_bwd_decay_kernel<K>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_e);
+      if (e1 != hipSuccess || e2 != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_backward: LDS attribute failed");
+      attr = true;
+    }
+    auto dense = chunk_bwd_dense_kernel<K, V>;
+    hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(256), smem_d, stream, a);
+    KDA_LAUNCH_CHECK("chunk_backward dense");
+    auto decay = chunk_bwd_decay_kernel<K>;
+    hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(256), smem_e, stream, a);
+    KDA_LAUNCH_CHECK("chunk_backward decay");
+  }
+  if (p->gate_mode == KDA_GATE_K3) {
+    auto params = chunk_bwd_params_kernel<K>;
+    hipLaunchKernelGGL(params, dim3(p->heads), dim3(K), 0, stream, a, g.max_chunks);
+    KDA_LAUNCH_CHECK("chunk_backward params");
+  }
+  return KDA_OK;
+}
+
+}  // namespace kda
+
+extern "C" int kda_chunk_backward(const kda_chunk_problem* p, const void* q, const void* k,
+                                  const void* v, const void* gate, const void* beta_logits,
+                                  const float* A_log, const float* dt_bias,
+                                  const float* initial_state, const void* workspace,
+                                  const void* grad_output, const float* grad_final_state,
+                                  void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
+                                  float* dA_log, float* ddt_bias, float* dinitial_state,
+                                  void* scratch, hipStream_t stream) {
+  using namespace kda;
+  int rc = validate_problem(p, "chunk_backward");
+  if (rc != KDA_OK) return rc;
+  (void)initial_state;
+  const bool empty = (size_t)p->batch * p->seq_len == 0;
+  KDA_REQUIRE(empty || (q && k && v && gate && beta_logits && grad_output && dq && dk && dv &&
+                        dgate && dbeta_logits),
+              "chunk_backward: null input/output pointer");
+  KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || (A_log && dt_bias && dA_log && ddt_bias),
+              "chunk_backward: K3 gate needs A_log, dt_bias, dA_log and ddt_bias");
+  KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,
+              "chunk_backward: workspace must be non-null and 256-byte aligned");
+  KDA_REQUIRE(scratch && ((uintptr_t)scratch % 256) == 0,
+              "chunk_backward: scratch must be non-null and 256-byte aligned");
+  const ChunkGeom g = make_geom(p);
+  BwdArgs a;
+  a.H = p->heads;
+  a.gate_mode = p->gate_mode;
+  a.lb = p->lower_bound;
+  a.scale = p->scale;
+  a.q = (const bf16*)q;
+  a.k = (const bf16*)k;
+  a.v = (const bf16*)v;
+  a.gate = gate;
+  a.beta_logits = (const bf16*)beta_logits;
+  a.A_log = A_log;
+  a.dt_bias = dt_bias;
+  a.dout = (const bf16*)grad_output;
+  a.dsfin = grad_final_state;
+  a.dq = (bf16*)dq;
+  a.dk = (bf16*)dk;
+  a.dv = (bf16*)dv;
+  a.dgate = dgate;
+  a.dbeta = (bf16*)dbeta_logits;
+  a.dA_log = dA_log;
+  a.ddt_bias = ddt_bias;
+  a.ds0 = dinitial_state;
+  a.ws = ws_regions(g, const_cast<void*>(workspace));
+  a.sc = sc_regions(g, scratch);
+  if (p->key_dim == 128 && p->value_dim == 128) return launch_backward<128, 128>(p, g, a, stream);
+  if (p->key_dim == 64 && p->value_dim == 64) return launch_backward<64, 64>(p, g, a, stream);
+  if (p->key_dim == 128 && p->value_dim == 64) return launch_backward<128, 64>(p, g, a, stream);
+  return launch_backward<64, 128>(p, g, a, stream);
 }

@@ -454,15 +454,14 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
       *(bf16x4*)(sSp + lr * SP + k0) = x;
     }
     __syncthreads();
-    // (2) state history [K][V] for the backward pass
+    // (2) f32 state history [K][V] for the backward pass
     {
-      bf16* SH = (bf16*)a.ws.p[R_SH] + tile * K * V;
-      for (int idx = tid; idx < K * 2; idx += 256) {
-        const int kk = idx / 2, vh = (idx % 2) * 8;
-        bf16x8 x;
+      float* SH = (float*)a.ws.p[R_SH] + tile * K * V;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sSp[(vh + e) * SP + kk];
-        *(bf16x8*)(SH + (size_t)kk * V + v0 + vh) = x;
+      for (int kt = 0; kt < KT; ++kt) {
+        const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) SH[(size_t)(k0 + r) * V + v0 + lr] = S[kt][r];
       }
     }
     // (3) delta rows 16*wave.. : U - W S

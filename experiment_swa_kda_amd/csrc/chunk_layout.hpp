@@ -30,13 +30,13 @@ enum WsRegion {
   R_RQ,          // f32  [tile][64]     scale / max(||q||, 1e-12)
   R_RK,          // f32  [tile][64]     1 / max(||k||, 1e-12)
   R_BETA,        // f32  [tile][64]     sigmoid(beta_logits)
-  R_SH,          // bf16 [tile][K][V]   state entering the chunk (written by the scan)
+  R_SH,          // f32  [tile][K][V]   state entering the chunk (written by the scan)
   R_DL,          // bf16 [tile][64][V]  delta = U - W S (written by the scan)
   R_COUNT
 };
 
 enum ScRegion {
-  S_DSH = 0,  // bf16 [tile][K][V]   dL/dS at the chunk end
+  S_DSH = 0,  // f32  [tile][K][V]   dL/dS at the chunk end
   S_DDL,      // f32  [tile][64][V]  dL/d delta
   S_DA,       // f32  [tile][64][64] dL/dA (masked lower)
   S_DMP,      // f32  [tile][64][64] dL/dM' (strictly lower, beta folded in)
@@ -44,6 +44,7 @@ enum ScRegion {
   S_GK,       // f32  [tile][64][K]  accumulated dL/dk_hat
   S_GG,       // f32  [tile][64][K]  accumulated dL/dG
   S_PP,       // f32  [tile][2][K]   gate parameter partials {sum draw, sum draw*(z+b)}
+  S_DGL,      // f32  [tile][K]      dL/dG_last (state-decay and Kd column terms)
   S_COUNT
 };
 
@@ -68,7 +69,7 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
     case R_G: return nt * 64 * K * 4;
     case R_LAM: return nt * K * 4;
     case R_RQ: case R_RK: case R_BETA: return nt * 64 * 4;
-    case R_SH: return nt * K * V * 2;
+    case R_SH: return nt * K * V * 4;
     case R_DL: return nt * 64 * V * 2;
     default: return 0;
   }
@@ -78,11 +79,12 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   const size_t nt = (size_t)g.max_chunks * g.heads;
   const size_t K = g.K, V = g.V;
   switch (r) {
-    case S_DSH: return nt * K * V * 2;
+    case S_DSH: return nt * K * V * 4;
     case S_DDL: return nt * 64 * V * 4;
     case S_DA: case S_DMP: return nt * 64 * 64 * 4;
     case S_GQ: case S_GK: case S_GG: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
+    case S_DGL: return nt * K * 4;
     default: return 0;
   }
 }
