@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X KDA operator path (one GPU).
+
+Default workload: one KDA layer forward+backward in bf16 with f32
+state and gates, B=2, T=4096, H=3, K=V=128, chunk 64, seed 42; q,k L2-normalised from
+N(0,1), v ~ N(0,1), beta logits ~ N(0,1), g = -exp(A_log) softplus(N(0,1) + dt_bias) with
+A_log ~ U(-1,1), dt_bias = 0, upstream gradient ~ N(0,1) bf16.  All inputs are resident
+in HBM before the timed region.  A "step" is one forward+backward of the operator.
+
+Prints ONE JSON line: value = algorithmic TFLOP/s of the KDA core (13.388 GFLOP per layer
+forward+backward), ms_per_step = ms per layer forward+backward, plus the forward-only
+time, the K3-gate variant, per-kernel times, the roofline of the dominant kernel and the
+CPU baseline (the reference's eager f32 path restated, timed on the host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+# Algorithmic FLOPs per (64-token chunk, head) at K = V = 128 (C = 64):
+#   forward = 11,621,717;  backward := 2 x forward.
+FWD_FLOP_PER_TILE = 11_621_717
+# per-kernel algorithmic FLOPs per tile (sum of the products each kernel owns)
+KERNEL_FLOP_PER_TILE = {
+    "fwd_intra": 3 * 1_048_576 + 1_048_576 + 87_381,   # A, M', W (2C^2K), U (2C^2V), solve C^3/3
+    "fwd_scan": 3 * 2_097_152 + 1_048_576,             # W S, Qg S, Kd^T delta (2CKV), A delta (2C^2V)
+    "bwd_scan": 3 * 2_097_152 + 1_048_576,             # Kd dS', Qg^T dO, W^T dDelta, A^T dO
+    "bwd_dense": 3 * 2_097_152 + 5 * 1_048_576 + 4 * 262_144,  # dQg dKd dW; dA dT(2) dVb dKb; Y dM
+    "bwd_decay": 4 * 1_048_576,                        # row/column terms of A and M'
+}
+STAGES = {"fwd_intra": 1, "fwd_scan": 2, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12}
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-len", type=int, default=1024,
+                    help="T of the CPU baseline sample (extrapolated linearly to T=4096)")
+    return ap.parse_args()
+
+
+def make_inputs(torch, B=2, T=4096, H=3, K=128, V=128, seed=42, gate="precomputed"):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=g), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=g), dim=-1)
+    v = torch.randn(B, T, H, V, generator=g)
+    z = torch.randn(B, T, H, K, generator=g)
+    beta = torch.randn(B, T, H, generator=g)
+    A_log = torch.rand(H, generator=g) * 2 - 1
+    dt_bias = torch.zeros(H * K)
+    do = torch.randn(B, T, H, V, generator=g)
+    if gate == "precomputed":
+        gv = (-A_log.exp().view(1, 1, H, 1) * torch.nn.functional.softplus(z + dt_bias.view(1, 1, H, K))).float()
+    else:  # reference Level-1 inputs: K3 gate, raw ~ N(0,1), A_log = dt_bias = 0
+        gv = z.bfloat16()
+        A_log = torch.zeros(H)
+    dev = "cuda"
+    t = dict(q=q.bfloat16(), k=k.bfloat16(), v=v.bfloat16(), g=gv, beta=beta.bfloat16(),
+             A_log=A_log.float(), dt_bias=dt_bias.float())
+    t = {n: x.to(dev).requires_grad_(True) for n, x in t.items()}
+    return t, do.bfloat16().to(dev)
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_times(torch, t, do, gate, reps=20):
+    """Average duration (ms) of each chunk kernel, launched alone on the current stream
+    between HIP events, after a full forward+backward has prepared its buffers."""
+    from experiment_swa_kda_amd import _lib, ops
+    from experiment_swa_kda_amd._lib import ptr
+
+    d = {n: x.detach() for n, x in t.items()}
+    K = d["q"].shape[-1]
+    out, fin, ws = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"],
+                                     None, False, -5.0, K ** -0.5, gate=gate)
+    p = ops._problem(d["q"], d["v"], None, ops.GATE_MODES[gate], -5.0, K ** -0.5)
+    lib = _lib.load()
+    scratch = torch.empty(lib.kda_chunk_backward_scratch_bytes(ctypes.byref(p)), dtype=torch.uint8, device="cuda")
+    grads = [torch.empty_like(d[n]) for n in ("q", "k", "v", "g", "beta")]
+    dA = torch.empty_like(d["A_log"])
+    ddt = torch.empty_like(d["dt_bias"])
+    stream = torch.cuda.current_stream().cuda_stream
+    fargs = (ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(d["g"]), ptr(d["beta"]), ptr(d["A_log"]),
+             ptr(d["dt_bias"]), None, ptr(out), None, ptr(ws), stream)
+    bargs = (ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(d["g"]), ptr(d["beta"]), ptr(d["A_log"]),
+             ptr(d["dt_bias"]), None, ptr(ws), ptr(do), None, *[ptr(x) for x in grads], ptr(dA), ptr(ddt),
+             None, ptr(scratch), stream)
+    _lib.check(lib.kda_chunk_backward(ctypes.byref(p), *bargs), "chunk_backward")
+    res = {}
+    for name, stage in STAGES.items():
+        if stage < 10:
+            call = lambda: lib.kda_chunk_forward_stage(stage, ctypes.byref(p), *fargs)  # noqa: E731
+        else:
+            call = lambda: lib.kda_chunk_backward_stage(stage, ctypes.byref(p), *bargs)  # noqa: E731
+        _lib.check(call(), name)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            call()
+        e.record()
+        torch.cuda.synchronize()
+        res[name] = s.elapsed_time(e) / reps
+    return res
+
+
+def cpu_baseline(sample_len):
+    """The reference's eager f32 CPU path (restated in oracle/reference_path.py), fwd+bwd."""
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.reference_path import time_fwd_bwd
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    sec = time_fwd_bwd(2, sample_len, 3, 128, 128, repeats=3)
+    ms_full = sec * 1e3 * (4096 / sample_len)
+    flop = 384 * 3 * FWD_FLOP_PER_TILE
+    return {"value": round(flop / (ms_full * 1e-3) / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port", "ms_per_layer_fwd_bwd": round(ms_full, 1),
+            "sample": f"eager f32 token loop + autograd, B2 H3 D128, T={sample_len} fwd+bwd, median of 3, "
+                      f"extrapolated linearly to T=4096"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the KDA operator path is benchmarked on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from experiment_swa_kda_amd import kda
+
+    B, T, H, K, V = 2, 4096, 3, 128, 128
+    tiles = B * (T // 64) * H
+    flop = 3 * tiles * FWD_FLOP_PER_TILE  # fwd + bwd (bwd := 2 x fwd)
+
+    results = {}
+    for gate in ("precomputed", "k3"):
+        t, do = make_inputs(torch, gate=gate)
+
+        def step():
+            for x in t.values():
+                x.grad = None
+            out, _ = kda(t["q"], t["k"], t["v"], t["g"], t["beta"], t["A_log"], t["dt_bias"],
+                         mode="project_chunk", gate=gate, allow_fallback=False)
+            out.backward(do)
+
+        def fwd():
+            with torch.no_grad():
+                kda(t["q"], t["k"], t["v"], t["g"], t["beta"], t["A_log"], t["dt_bias"],
+                    mode="project_chunk", gate=gate, allow_fallback=False)
+
+        torch.cuda.synchronize()
+        ms = time_steps(torch, step, args.steps, args.warmup)
+        ms_fwd = time_steps(torch, fwd, args.steps, args.warmup)
+        results[gate] = (ms, ms_fwd, t, do)
+
+    ms, ms_fwd, t, do = results["precomputed"]
+    kt = kernel_times(torch, t, do, "precomputed")
+    dom = max(kt, key=kt.get)
+    achieved = tiles * KERNEL_FLOP_PER_TILE[dom] / (kt[dom] * 1e-3) / 1e12
+    line = {
+        "metric": "KDA fwd+bwd TFLOP/s (B2 T4096 H3 D128 bf16)",
+        "value": round(flop / (ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config2: single KDA layer fwd+bwd, precomputed gate g=-exp(A_log)softplus(.)",
+                   "batch": B, "seq_len": T, "heads": H, "key_dim": K, "value_dim": V, "chunk": 64,
+                   "parallelism": "single GPU"},
+        "ms_fwd": round(ms_fwd, 4),
+        "tflops_fwd": round(flop / 3 / (ms_fwd * 1e-3) / 1e12, 3),
+        "tokens_per_s_fwd_bwd": round(B * T / (ms * 1e-3), 1),
+        "k3_gate": {"ms_per_step": round(results["k3"][0], 4), "ms_fwd": round(results["k3"][1], 4)},
+        "kernel_ms": {n: round(v, 4) for n, v in kt.items()},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": None},
+        "reference_gb10_ms_fwd_bwd": 3.916,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_sample_len)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

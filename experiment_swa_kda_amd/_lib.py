@@ -49,6 +49,8 @@ SIGNATURES = {
     "kda_chunk_backward_scratch_bytes": (ctypes.c_size_t, [_PP]),
     "kda_chunk_forward": (ctypes.c_int, [_PP] + [_P] * 11 + [_P]),
     "kda_chunk_backward": (ctypes.c_int, [_PP] + [_P] * 20 + [_P]),
+    "kda_chunk_forward_stage": (ctypes.c_int, [_I, _PP] + [_P] * 11 + [_P]),
+    "kda_chunk_backward_stage": (ctypes.c_int, [_I, _PP] + [_P] * 20 + [_P]),
     "kda_recurrent_decode": (ctypes.c_int, [_I, _I, _I, _I, _I, _F, _F] + [_P] * 10 + [_P]),
     "kda_causal_conv_forward": (ctypes.c_int, [_I, _I, _I, _I] + [_P] * 5 + [_P]),
     "kda_causal_conv_backward_scratch_bytes": (ctypes.c_size_t, [_I, _I, _I, _I]),

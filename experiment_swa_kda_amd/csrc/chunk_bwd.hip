@@ -838,8 +838,8 @@ __global__ __launch_bounds__(K) void chunk_bwd_params_kernel(BwdArgs a, int max_
 
 template <int K, int V>
 static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdArgs& a,
-                           hipStream_t stream) {
-  if (p->num_seqs > 0) {
+                           hipStream_t stream, int stages) {
+  if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     auto scan = chunk_bwd_scan_kernel<K, V>;
     hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16), dim3(256), 0, stream, a);
     KDA_LAUNCH_CHECK("chunk_backward scan");
@@ -857,14 +857,18 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
         return set_error(KDA_ERR_LAUNCH, "chunk_backward: LDS attribute failed");
       attr = true;
     }
-    auto dense = chunk_bwd_dense_kernel<K, V>;
-    hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(256), smem_d, stream, a);
-    KDA_LAUNCH_CHECK("chunk_backward dense");
-    auto decay = chunk_bwd_decay_kernel<K>;
-    hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(256), smem_e, stream, a);
-    KDA_LAUNCH_CHECK("chunk_backward decay");
+    if (stages & (1 << (KDA_STAGE_BWD_DENSE - 10))) {
+      auto dense = chunk_bwd_dense_kernel<K, V>;
+      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(256), smem_d, stream, a);
+      KDA_LAUNCH_CHECK("chunk_backward dense");
+    }
+    if (stages & (1 << (KDA_STAGE_BWD_DECAY - 10))) {
+      auto decay = chunk_bwd_decay_kernel<K>;
+      hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(256), smem_e, stream, a);
+      KDA_LAUNCH_CHECK("chunk_backward decay");
+    }
   }
-  if (p->gate_mode == KDA_GATE_K3) {
+  if (p->gate_mode == KDA_GATE_K3 && (stages & (1 << (KDA_STAGE_BWD_PARAMS - 10)))) {
     auto params = chunk_bwd_params_kernel<K>;
     hipLaunchKernelGGL(params, dim3(p->heads), dim3(K), 0, stream, a, g.max_chunks);
     KDA_LAUNCH_CHECK("chunk_backward params");
@@ -874,7 +878,7 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
 
 }  // namespace kda
 
-extern "C" int kda_chunk_backward(const kda_chunk_problem* p, const void* q, const void* k,
+static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const void* q, const void* k,
                                   const void* v, const void* gate, const void* beta_logits,
                                   const float* A_log, const float* dt_bias,
                                   const float* initial_state, const void* workspace,
@@ -921,8 +925,38 @@ extern "C" int kda_chunk_backward(const kda_chunk_problem* p, const void* q, con
   a.ds0 = dinitial_state;
   a.ws = ws_regions(g, const_cast<void*>(workspace));
   a.sc = sc_regions(g, scratch);
-  if (p->key_dim == 128 && p->value_dim == 128) return launch_backward<128, 128>(p, g, a, stream);
-  if (p->key_dim == 64 && p->value_dim == 64) return launch_backward<64, 64>(p, g, a, stream);
-  if (p->key_dim == 128 && p->value_dim == 64) return launch_backward<128, 64>(p, g, a, stream);
-  return launch_backward<64, 128>(p, g, a, stream);
+  if (p->key_dim == 128 && p->value_dim == 128) return launch_backward<128, 128>(p, g, a, stream, stages);
+  if (p->key_dim == 64 && p->value_dim == 64) return launch_backward<64, 64>(p, g, a, stream, stages);
+  if (p->key_dim == 128 && p->value_dim == 64) return launch_backward<128, 64>(p, g, a, stream, stages);
+  return launch_backward<64, 128>(p, g, a, stream, stages);
+}
+
+extern "C" int kda_chunk_backward(const kda_chunk_problem* p, const void* q, const void* k,
+                                  const void* v, const void* gate, const void* beta_logits,
+                                  const float* A_log, const float* dt_bias,
+                                  const float* initial_state, const void* workspace,
+                                  const void* grad_output, const float* grad_final_state,
+                                  void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
+                                  float* dA_log, float* ddt_bias, float* dinitial_state,
+                                  void* scratch, hipStream_t stream) {
+  return chunk_backward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
+                             workspace, grad_output, grad_final_state, dq, dk, dv, dgate,
+                             dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch, stream);
+}
+
+extern "C" int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,
+                                        const void* k, const void* v, const void* gate,
+                                        const void* beta_logits, const float* A_log,
+                                        const float* dt_bias, const float* initial_state,
+                                        const void* workspace, const void* grad_output,
+                                        const float* grad_final_state, void* dq, void* dk,
+                                        void* dv, void* dgate, void* dbeta_logits,
+                                        float* dA_log, float* ddt_bias, float* dinitial_state,
+                                        void* scratch, hipStream_t stream) {
+  if (stage < KDA_STAGE_BWD_SCAN || stage > KDA_STAGE_BWD_PARAMS)
+    return kda::set_error(KDA_ERR_INVALID, "chunk_backward_stage: unknown stage %d", stage);
+  return chunk_backward_impl(1 << (stage - 10), p, q, k, v, gate, beta_logits, A_log, dt_bias,
+                             initial_state, workspace, grad_output, grad_final_state, dq, dk, dv,
+                             dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch,
+                             stream);
 }

@@ -575,8 +575,8 @@ ChunkGeom make_geom(const kda_chunk_problem* p) {
 
 template <int K, int V>
 static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArgs& a,
-                          hipStream_t stream) {
-  if (g.max_chunks > 0) {
+                          hipStream_t stream, int stages) {
+  if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_INTRA))) {
     constexpr size_t smem = IntraSmem<K, V>::bytes;
     static bool attr = false;
     if (!attr) {
@@ -591,7 +591,7 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
                        smem, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward intra");
   }
-  if (p->num_seqs > 0) {
+  if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
     auto scan = chunk_fwd_scan_kernel<K, V>;
     hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16),
                        dim3(256), 0, stream, a);
@@ -622,7 +622,7 @@ extern "C" size_t kda_chunk_backward_scratch_bytes(const kda_chunk_problem* p) {
   return kda::sc_total_bytes(kda::make_geom(p));
 }
 
-extern "C" int kda_chunk_forward(const kda_chunk_problem* p, const void* q, const void* k,
+static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void* q, const void* k,
                                  const void* v, const void* gate, const void* beta_logits,
                                  const float* A_log, const float* dt_bias,
                                  const float* initial_state, void* output, float* final_state,
@@ -654,10 +654,33 @@ extern "C" int kda_chunk_forward(const kda_chunk_problem* p, const void* q, cons
   a.out = (bf16*)output;
   a.sfin = final_state;
   a.ws = ws_regions(g, workspace);
-  rc = launch_chunk_prep(p, g, a.ws, stream);
-  if (rc != KDA_OK) return rc;
-  if (p->key_dim == 128 && p->value_dim == 128) return launch_forward<128, 128>(p, g, a, stream);
-  if (p->key_dim == 64 && p->value_dim == 64) return launch_forward<64, 64>(p, g, a, stream);
-  if (p->key_dim == 128 && p->value_dim == 64) return launch_forward<128, 64>(p, g, a, stream);
-  return launch_forward<64, 128>(p, g, a, stream);
+  if (stages & (1 << KDA_STAGE_PREP)) {
+    rc = launch_chunk_prep(p, g, a.ws, stream);
+    if (rc != KDA_OK) return rc;
+  }
+  if (p->key_dim == 128 && p->value_dim == 128) return launch_forward<128, 128>(p, g, a, stream, stages);
+  if (p->key_dim == 64 && p->value_dim == 64) return launch_forward<64, 64>(p, g, a, stream, stages);
+  if (p->key_dim == 128 && p->value_dim == 64) return launch_forward<128, 64>(p, g, a, stream, stages);
+  return launch_forward<64, 128>(p, g, a, stream, stages);
+}
+
+extern "C" int kda_chunk_forward(const kda_chunk_problem* p, const void* q, const void* k,
+                                 const void* v, const void* gate, const void* beta_logits,
+                                 const float* A_log, const float* dt_bias,
+                                 const float* initial_state, void* output, float* final_state,
+                                 void* workspace, hipStream_t stream) {
+  return chunk_forward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
+                            output, final_state, workspace, stream);
+}
+
+extern "C" int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,
+                                       const void* k, const void* v, const void* gate,
+                                       const void* beta_logits, const float* A_log,
+                                       const float* dt_bias, const float* initial_state,
+                                       void* output, float* final_state, void* workspace,
+                                       hipStream_t stream) {
+  if (stage != KDA_STAGE_PREP && stage != KDA_STAGE_FWD_INTRA && stage != KDA_STAGE_FWD_SCAN)
+    return kda::set_error(KDA_ERR_INVALID, "chunk_forward_stage: unknown stage %d", stage);
+  return chunk_forward_impl(1 << stage, p, q, k, v, gate, beta_logits, A_log, dt_bias,
+                            initial_state, output, final_state, workspace, stream);
 }

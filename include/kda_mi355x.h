@@ -103,6 +103,35 @@ int kda_chunk_backward(const kda_chunk_problem* p,
                        void* scratch, hipStream_t stream);
 
 /*
+ * Runs one kernel of the chunked forward or backward on buffers that a full
+ * kda_chunk_forward / kda_chunk_backward call with the same arguments has prepared, so a
+ * benchmark can time that kernel alone.  No counterpart in the reference (it exists for
+ * measurement only).  Forward stages: KDA_STAGE_PREP, KDA_STAGE_FWD_INTRA,
+ * KDA_STAGE_FWD_SCAN; backward stages: KDA_STAGE_BWD_SCAN, KDA_STAGE_BWD_DENSE,
+ * KDA_STAGE_BWD_DECAY, KDA_STAGE_BWD_PARAMS.  Arguments are those of the full calls.
+ */
+#define KDA_STAGE_PREP 0
+#define KDA_STAGE_FWD_INTRA 1
+#define KDA_STAGE_FWD_SCAN 2
+#define KDA_STAGE_BWD_SCAN 10
+#define KDA_STAGE_BWD_DENSE 11
+#define KDA_STAGE_BWD_DECAY 12
+#define KDA_STAGE_BWD_PARAMS 13
+int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,
+                            const void* k, const void* v, const void* gate,
+                            const void* beta_logits, const float* A_log, const float* dt_bias,
+                            const float* initial_state, void* output, float* final_state,
+                            void* workspace, hipStream_t stream);
+int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,
+                             const void* k, const void* v, const void* gate,
+                             const void* beta_logits, const float* A_log, const float* dt_bias,
+                             const float* initial_state, const void* workspace,
+                             const void* grad_output, const float* grad_final_state, void* dq,
+                             void* dk, void* dv, void* dgate, void* dbeta_logits, float* dA_log,
+                             float* ddt_bias, float* dinitial_state, void* scratch,
+                             hipStream_t stream);
+
+/*
  * Single-token recurrent step (T == 1).  Replaces torch.ops.nanochat_kda.recurrent_decode
  * (nanochat/mixers/cuda_kda/recurrent_decode.cu:24-181, schema :186-189).
  *   q, k, gate [B,1,H,K] bf16 (gate K3 raw logits), v [B,1,H,V] bf16, beta_logits [B,1,H] bf16
