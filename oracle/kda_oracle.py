@@ -39,6 +39,8 @@ other than its own formula):
 * causal_conv_*: torch.nn.functional.conv1d (grouped) and autograd; decode equals
   full sequence (tests/test_kda_operator.py:167-180).
 * rmsnorm_gate_*: torch.nn.functional.rms_norm and autograd.
+* full_layer: composed only of the functions above and matrix products; checked
+  against the mixer's eager reference mode in tests/test_cpu_api.py.
 """
 
 from __future__ import annotations
@@ -417,3 +419,37 @@ def rmsnorm_gate_backward(x, gate, weight, eps, grad_output):
     dn = dn_w * w
     dx = inv * (dn - n * (dn * n).sum(-1, keepdims=True) / D)
     return dx, dgate, dw
+
+
+# ----------------------------------------------------------------------------
+# full mixer block
+# ----------------------------------------------------------------------------
+
+def full_layer(x, *, q_weight, k_weight, v_weight, q_conv_weight, k_conv_weight, v_conv_weight,
+               forget_a_weight, forget_b_weight, beta_weight, A_log, dt_bias, output_gate_weight,
+               norm_weight, output_weight, num_heads, norm_eps, initial_state=None,
+               lower_bound=-5.0):
+    """Independent composition of the K3 mixer (tests/kda_oracle.py:176-236).
+
+    ``initial_state`` is None or a tuple (memory, q_conv, k_conv, v_conv).  Returns
+    (output [B,T,D], (memory, q_conv, k_conv, v_conv)).
+    """
+    f = lambda a: np.asarray(a, np.float64)  # noqa: E731
+    x = f(x)
+    B, T, _ = x.shape
+    st = (None, None, None, None) if initial_state is None else initial_state
+    qp, kp, vp = x @ f(q_weight).T, x @ f(k_weight).T, x @ f(v_weight).T
+    q, qf = causal_conv_forward(qp, q_conv_weight, st[1])
+    k, kf = causal_conv_forward(kp, k_conv_weight, st[2])
+    v, vf = causal_conv_forward(vp, v_conv_weight, st[3])
+    K = q.shape[-1] // num_heads
+    Vd = v.shape[-1] // num_heads
+    q = q.reshape(B, T, num_heads, K)
+    k = k.reshape(B, T, num_heads, K)
+    v = v.reshape(B, T, num_heads, Vd)
+    raw = ((x @ f(forget_a_weight).T) @ f(forget_b_weight).T).reshape(B, T, num_heads, K)
+    bl = x @ f(beta_weight).T
+    o, mem = kda_forward(q, k, v, raw, bl, A_log, dt_bias, initial_state=st[0], lower_bound=lower_bound)
+    gate = (x @ f(output_gate_weight).T).reshape(B, T, num_heads, Vd)
+    y, _ = rmsnorm_gate_forward(o, gate, norm_weight, norm_eps)
+    return y.reshape(B, T, -1) @ f(output_weight).T, (mem, qf, kf, vf)
