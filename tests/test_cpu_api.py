@@ -132,7 +132,9 @@ def test_contract_errors():
 @pytest.mark.parametrize("mode", ["project_chunk", "chunk", "project_recurrent", "recurrent"])
 def test_accelerated_modes_fail_closed_on_cpu(mode, monkeypatch):
     # no silent fallback to the eager loop, whatever allow_fallback says
-    import experiment_swa_kda_amd.kda as impl
+    import importlib
+
+    impl = importlib.import_module("experiment_swa_kda_amd.kda")
 
     def forbidden(*args, **kwargs):
         raise AssertionError("accelerated call reached the eager loop")
