@@ -29,12 +29,13 @@ FWD_FLOP_PER_TILE = 11_621_717
 # per-kernel algorithmic FLOPs per tile (sum of the products each kernel owns)
 KERNEL_FLOP_PER_TILE = {
     "fwd_intra": 3 * 1_048_576 + 1_048_576 + 87_381,   # A, M', W (2C^2K), U (2C^2V), solve C^3/3
-    "fwd_scan": 3 * 2_097_152 + 1_048_576,             # W S, Qg S, Kd^T delta (2CKV), A delta (2C^2V)
+    "fwd_scan": 2 * 2_097_152,                         # W S, Kd^T delta (2CKV)
+    "fwd_output": 2_097_152 + 1_048_576,               # Qg S (2CKV), A delta (2C^2V)
     "bwd_scan": 3 * 2_097_152 + 1_048_576,             # Kd dS', Qg^T dO, W^T dDelta, A^T dO
     "bwd_dense": 3 * 2_097_152 + 5 * 1_048_576 + 4 * 262_144,  # dQg dKd dW; dA dT(2) dVb dKb; Y dM
     "bwd_decay": 4 * 1_048_576,                        # row/column terms of A and M'
 }
-STAGES = {"fwd_intra": 1, "fwd_scan": 2, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12}
+STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12}
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 

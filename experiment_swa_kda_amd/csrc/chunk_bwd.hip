@@ -59,20 +59,78 @@ struct BwdArgs {
 // ---------------------------------------------------------------------------
 // reverse state-gradient scan
 // ---------------------------------------------------------------------------
+// Same structure as the forward scan, walking the chunks backwards: all global operands
+// of a chunk sit in a register ring kBwdRing chunks ahead, the dO strip is
+// double-buffered in LDS, and each per-step global access is one vector instruction.
+constexpr int kBwdRing = 3;
+
+template <int K>
+struct BwdScanFrag {
+  bf16x8 at[2];            // A^T rows of this wave's dDelta tile
+  bf16x8 kd[K / 32];       // Kd rows of this wave's dDelta tile
+  bf16x8 qgt[K / 64][2];   // Qg^T rows of this wave's dS tiles
+  bf16x8 wt[K / 64][2];    // W^T rows of this wave's dS tiles
+  float4 lam[K / 64];
+  bf16x4 dout;             // this thread's 4 values of the dO strip
+  int dlen;                // chunk length (rows >= dlen of the strip are zero)
+};
+
 template <int K, int V>
 __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
   constexpr int KT = K / 16 / 4;
   constexpr int SP = K + 8;
   constexpr int DP = 64 + 8;
-  __shared__ __attribute__((aligned(16))) bf16 sDS[16 * SP];  // dS' as [v][k]
-  __shared__ __attribute__((aligned(16))) bf16 sDO[16 * DP];  // dO strip as [v][t]
-  __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];  // dDelta strip as [v][t]
+  constexpr int FP = 16 + 4;
+  __shared__ __attribute__((aligned(16))) bf16 sDS[16 * SP];     // dS' as [v][k]
+  __shared__ __attribute__((aligned(16))) float sDSf[K * FP];    // f32 dS' as [k][v]
+  __shared__ __attribute__((aligned(16))) bf16 sDO[2][16 * DP];  // dO strip as [v][t]
+  __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];     // dDelta strip as [v][t]
   const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
   const int H = a.H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+  const int j = 16 * wave + lr;
+  const int dt = tid / 4, dvq = (tid % 4) * 4;  // dO staging: token, 4-wide v group
+
+  // Chunks of one sequence are consecutive 64-token blocks: chunk ci starts at
+  // seq_row0 + 64 ci, so no per-chunk table read sits in front of the dO load.
+  const int n = sq.y;
+  int seq_row0 = 0, seq_end = 0;
+  if (n > 0) {
+    const int4 c_first = chunks[sq.x], c_last = chunks[sq.x + n - 1];
+    seq_row0 = c_first.x;
+    seq_end = c_last.x + c_last.y;
+  }
+  auto load = [&](int chunk, BwdScanFrag<K>& f) {
+    const int row0 = seq_row0 + (chunk - sq.x) * 64;
+    const int len = min(64, seq_end - row0);
+    const size_t tile = (size_t)chunk * H + h;
+    const bf16* AT = (const bf16*)a.ws.p[R_AT] + tile * 64 * 64;
+    const bf16* KD = (const bf16*)a.ws.p[R_KD] + tile * 64 * K;
+    const bf16* QGT = (const bf16*)a.ws.p[R_QGT] + tile * K * 64;
+    const bf16* WT = (const bf16*)a.ws.p[R_WT] + tile * K * 64;
+    const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) f.at[s] = *(const bf16x8*)(AT + j * 64 + 32 * s + 8 * kg);
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) f.kd[s] = *(const bf16x8*)(KD + j * K + 32 * s + 8 * kg);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int kb = 16 * (wave * KT + kt);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        f.qgt[kt][s] = *(const bf16x8*)(QGT + (kb + lr) * 64 + 32 * s + 8 * kg);
+        f.wt[kt][s] = *(const bf16x8*)(WT + (kb + lr) * 64 + 32 * s + 8 * kg);
+      }
+      f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
+    }
+    // rows past the chunk end read row 0 of the chunk and are zeroed when staged
+    const int tr = dt < len ? dt : 0;
+    f.dout = *(const bf16x4*)(a.dout + ((size_t)(row0 + tr) * H + h) * V + v0 + dvq);
+    f.dlen = len;
+  };
 
   f32x4 dS[KT];
 #pragma unroll
@@ -85,97 +143,85 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
       dS[kt] = zero4();
     }
   }
+  BwdScanFrag<K> ring[kBwdRing];
+  if (n > 0) {
+#pragma unroll
+    for (int d = 0; d < kBwdRing; ++d) load(sq.x + max(n - 1 - d, 0), ring[d]);
+  }
 
-  for (int ci = sq.y - 1; ci >= 0; --ci) {
-    const int chunk = sq.x + ci;
-    const int4 ch = chunks[chunk];
+  // step r processes chunk index ci = n - 1 - r
+  auto step = [&](int r, BwdScanFrag<K>& f) {
+    const int chunk = sq.x + n - 1 - r;
     const size_t tile = (size_t)chunk * H + h;
-    const int len = ch.y, row0 = ch.x;
-    // (1) publish dS' (bf16, [v][k]) and stage the dO strip as [v][t]
+    bf16* sO = sDO[r & 1];
+    // (1) publish dS' (bf16 [v][k] operand, f32 [k][v] staging) and the dO strip
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       bf16x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = to_bf16(dS[kt][r]);
+      for (int q = 0; q < 4; ++q) {
+        x[q] = to_bf16(dS[kt][q]);
+        sDSf[(k0 + q) * FP + lr] = dS[kt][q];
+      }
       *(bf16x4*)(sDS + lr * SP + k0) = x;
     }
-    {
-      const int t = tid / 4, vq = (tid % 4) * 4;
-      bf16x4 x;
-      if (t < len) {
-        x = *(const bf16x4*)(a.dout + ((size_t)(row0 + t) * H + h) * V + v0 + vq);
-      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = to_bf16(0.f);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sDO[(vq + r) * DP + t] = x[r];
-    }
+    for (int q = 0; q < 4; ++q) sO[(dvq + q) * DP + dt] = dt < f.dlen ? f.dout[q] : to_bf16(0.f);
     __syncthreads();
-    // (2) f32 dS' history [K][V] for the dense VJP
+    // (2) f32 dS' history [K][V] (fixed-count vector stores)
     {
       float* DSH = (float*)a.sc.p[S_DSH] + tile * K * V;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int k0 = 16 * (wave * KT + kt) + 4 * kg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) DSH[(size_t)(k0 + r) * V + v0 + lr] = dS[kt][r];
+      for (int it = 0; it < K / 64; ++it) {
+        const int idx = tid + 256 * it;
+        const int kk = idx / 4, q4 = (idx % 4) * 4;
+        *(float4*)(DSH + (size_t)kk * V + v0 + q4) = *(const float4*)(sDSf + kk * FP + q4);
       }
     }
     // (3) dDelta rows 16*wave.. = A^T dO + Kd dS'
     {
-      const bf16* AT = (const bf16*)a.ws.p[R_AT] + tile * 64 * 64;
-      const bf16* KD = (const bf16*)a.ws.p[R_KD] + tile * 64 * K;
-      float* DDL = (float*)a.sc.p[S_DDL] + tile * 64 * V;
-      const int j = 16 * wave + lr;
-      f32x4 acc = zero4();
+      f32x4 acc0 = zero4(), acc1 = zero4();
+      acc0 = mfma16(f.at[0], *(const bf16x8*)(sO + lr * DP + 8 * kg), acc0);
+      acc1 = mfma16(f.at[1], *(const bf16x8*)(sO + lr * DP + 32 + 8 * kg), acc1);
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 fa = *(const bf16x8*)(AT + j * 64 + 32 * s + 8 * kg);
-        const bf16x8 fb = *(const bf16x8*)(sDO + lr * DP + 32 * s + 8 * kg);
-        acc = mfma16(fa, fb, acc);
+      for (int s = 0; s < K / 32; s += 2) {
+        acc0 = mfma16(f.kd[s], *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg), acc0);
+        acc1 = mfma16(f.kd[s + 1], *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
       }
-#pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        const bf16x8 fa = *(const bf16x8*)(KD + j * K + 32 * s + 8 * kg);
-        const bf16x8 fb = *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg);
-        acc = mfma16(fa, fb, acc);
-      }
+      float* DDLT = (float*)a.sc.p[S_DDLT] + tile * V * 64;
+      const f32x4 d = acc0 + acc1;
+      *(float4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = make_float4(d[0], d[1], d[2], d[3]);
       bf16x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * wave + 4 * kg + r;
-        DDL[t * V + v0 + lr] = acc[r];
-        x[r] = to_bf16(acc[r]);
-      }
+      for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
       *(bf16x4*)(sDD + lr * DP + 16 * wave + 4 * kg) = x;
     }
     __syncthreads();
     // (4) dS = lam dS' + Qg^T dO - W^T dDelta
-    {
-      const bf16* QGT = (const bf16*)a.ws.p[R_QGT] + tile * K * 64;
-      const bf16* WT = (const bf16*)a.ws.p[R_WT] + tile * K * 64;
-      const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int kb = 16 * (wave * KT + kt);
-        f32x4 pq = zero4(), pw = zero4();
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x4 pq = zero4(), pw = zero4();
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16x8 fq = *(const bf16x8*)(QGT + (kb + lr) * 64 + 32 * s + 8 * kg);
-          const bf16x8 fo = *(const bf16x8*)(sDO + lr * DP + 32 * s + 8 * kg);
-          pq = mfma16(fq, fo, pq);
-          const bf16x8 fw = *(const bf16x8*)(WT + (kb + lr) * 64 + 32 * s + 8 * kg);
-          const bf16x8 fd = *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg);
-          pw = mfma16(fw, fd, pw);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dS[kt][r] = fmaf(lam[kb + 4 * kg + r], dS[kt][r], pq[r] - pw[r]);
+      for (int s = 0; s < 2; ++s) {
+        pq = mfma16(f.qgt[kt][s], *(const bf16x8*)(sO + lr * DP + 32 * s + 8 * kg), pq);
+        pw = mfma16(f.wt[kt][s], *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
       }
+      dS[kt][0] = fmaf(f.lam[kt].x, dS[kt][0], pq[0] - pw[0]);
+      dS[kt][1] = fmaf(f.lam[kt].y, dS[kt][1], pq[1] - pw[1]);
+      dS[kt][2] = fmaf(f.lam[kt].z, dS[kt][2], pq[2] - pw[2]);
+      dS[kt][3] = fmaf(f.lam[kt].w, dS[kt][3], pq[3] - pw[3]);
     }
-    __syncthreads();
+  };
+
+  // unconditional ring loads (index clamped to the first chunk), see the forward scan
+  for (int r0 = 0; r0 < n; r0 += kBwdRing) {
+#pragma unroll
+    for (int d = 0; d < kBwdRing; ++d) {
+      const int r = r0 + d;
+      if (r < n) step(r, ring[d]);
+      load(sq.x + max(n - 1 - (r + kBwdRing), 0), ring[d]);
+    }
   }
   if (a.ds0) {
 #pragma unroll
@@ -190,6 +236,9 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // dense chunk VJP
 // ---------------------------------------------------------------------------
+constexpr int kVjpThreads = 1024;  // 16 waves per (chunk, head): hides global-load latency
+constexpr int kVjpWaves = kVjpThreads / kWave;
+
 template <int K, int V>
 struct DenseSmem {
   static constexpr int MP = 65;
@@ -200,7 +249,9 @@ struct DenseSmem {
   static constexpr size_t off_y = off_dt + 64 * MP * 4;         // f32 [64][65] T^T dT
   static constexpr size_t off_dw = off_y + 64 * MP * 4;         // f32 [64][KP] dW
   static constexpr size_t off_du = off_dw + 64 * KP * 4;        // bf16 [64][VP] dU
-  static constexpr size_t off_b = off_du + 64 * VP * 2;         // f32 [64] beta
+  static constexpr size_t off_dul = off_du + 64 * VP * 2;       // bf16 [64][VP] dU - bf16(dU)
+  static constexpr size_t off_dl = off_dul + 64 * VP * 2;       // bf16 [64][VP] delta
+  static constexpr size_t off_b = off_dl + 64 * VP * 2;         // f32 [64] beta
   static constexpr size_t off_gl = off_b + 64 * 4;              // f32 [4][K] dG_last partials
   static constexpr size_t off_pv = off_gl + 4 * K * 4;          // f32 [V/16][64] dbeta partials
   static constexpr size_t off_pk = off_pv + (V / 16) * 64 * 4;  // f32 [K/16][64]
@@ -209,7 +260,7 @@ struct DenseSmem {
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a) {
   using L = DenseSmem<K, V>;
   constexpr int MP = L::MP, KP = L::KP, VP = L::VP;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -218,6 +269,8 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   float* sY = (float*)(smem + L::off_y);
   float* sDW = (float*)(smem + L::off_dw);
   bf16* sDU = (bf16*)(smem + L::off_du);
+  bf16* sDUl = (bf16*)(smem + L::off_dul);
+  bf16* sDL = (bf16*)(smem + L::off_dl);
   float* sB = (float*)(smem + L::off_b);
   float* sGL = (float*)(smem + L::off_gl);
   float* sPV = (float*)(smem + L::off_pv);
@@ -239,9 +292,9 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
   const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
-  const bf16* DL = (const bf16*)a.ws.p[R_DL] + tile * 64 * V;
+  const bf16* DLT = (const bf16*)a.ws.p[R_DLT] + tile * V * 64;
   const float* DSH = (const float*)a.sc.p[S_DSH] + tile * K * V;
-  const float* DDL = (const float*)a.sc.p[S_DDL] + tile * 64 * V;
+  const float* DDLT = (const float*)a.sc.p[S_DDLT] + tile * V * 64;
   float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
   float* GK = (float*)a.sc.p[S_GK] + tile * 64 * K;
   float* GG = (float*)a.sc.p[S_GG] + tile * 64 * K;
@@ -249,22 +302,27 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
 
   // ---- P0: stage T, dU, beta; clear partials ----
-  for (int idx = tid; idx < 64 * 64; idx += 256) {
+  for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
     const int i = idx / 64, j = idx % 64;
     sT[i * MP + j] = Tg[idx];
     sDT[i * MP + j] = 0.f;
   }
-  for (int idx = tid; idx < 64 * (V / 8); idx += 256) {
-    const int t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
-    const float4* p = (const float4*)(DDL + t * V + c0);
-    const float4 x0 = p[0], x1 = p[1];
-    bf16x8 x;
-    x[0] = to_bf16(x0.x); x[1] = to_bf16(x0.y); x[2] = to_bf16(x0.z); x[3] = to_bf16(x0.w);
-    x[4] = to_bf16(x1.x); x[5] = to_bf16(x1.y); x[6] = to_bf16(x1.z); x[7] = to_bf16(x1.w);
-    *(bf16x8*)(sDU + t * VP + c0) = x;
+  // dU = dDelta (hi/lo bf16 split) and delta, transposed from their [V][64] histories
+  for (int idx = tid; idx < V * 16; idx += kVjpThreads) {
+    const int vv = idx / 16, t4 = (idx % 16) * 4;
+    const float4 d = *(const float4*)(DDLT + (size_t)vv * 64 + t4);
+    const bf16x4 dl = *(const bf16x4*)(DLT + (size_t)vv * 64 + t4);
+    const float dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16 hi = to_bf16(dv[e]);
+      sDU[(t4 + e) * VP + vv] = hi;
+      sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
+      sDL[(t4 + e) * VP + vv] = dl[e];
+    }
   }
   if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
-  for (int idx = tid; idx < 4 * 64; idx += 256) sPM[idx] = 0.f;
+  for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
   __syncthreads();
 
   auto load_dout8 = [&](int i, int c0) -> bf16x8 {
@@ -283,23 +341,23 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
 
   // ---- PA: dQg, dKd, dW over the 64 x K grid ----
   constexpr int NKT = 4 * (K / 16);
-  for (int p = wave; p < NKT; p += 4) {
+  for (int p = wave; p < NKT; p += kVjpWaves) {
     const int rt = p % 4, ct = p / 4;
     const int i = 16 * rt + lr, c = 16 * ct + lr;
     f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
-#pragma unroll
+#pragma unroll 2
     for (int s = 0; s < V / 32; ++s) {
       const int vv = 32 * s + 8 * kg;
-      float xs[8], xd[8], xu[8];
+      float xs[8], xd[8];
       load8f(SH + (size_t)c * V + vv, xs);
       load8f(DSH + (size_t)c * V + vv, xd);
-      load8f(DDL + i * V + vv, xu);
-      bf16x8 sHi, sLo, dHi, dLo, uHi, uLo;
+      bf16x8 sHi, sLo, dHi, dLo;
       split8(xs, sHi, sLo);
       split8(xd, dHi, dLo);
-      split8(xu, uHi, uLo);
+      const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
+      const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
       const bf16x8 aO = load_dout8(i, vv);
-      const bf16x8 aL = *(const bf16x8*)(DL + i * V + vv);
+      const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
       accQ = mfma16(aO, sHi, accQ);
       accQ = mfma16(aO, sLo, accQ);
       accK = mfma16(aL, dHi, accK);
@@ -330,7 +388,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
     if (kg == 0) sGL[rt * K + c] = colsum;
   }
   // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
-  for (int p = wave; p < 16; p += 4) {
+  for (int p = wave; p < 16; p += kVjpWaves) {
     const int ba = p / 4, bb = p % 4;
     if (bb > ba) {
 #pragma unroll
@@ -342,7 +400,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
       const int vv = 32 * s + 8 * kg;
-      acc = mfma16(load_dout8(i, vv), *(const bf16x8*)(DL + j * V + vv), acc);
+      acc = mfma16(load_dout8(i, vv), *(const bf16x8*)(sDL + j * VP + vv), acc);
     }
     const int jj = 16 * bb + lr;
 #pragma unroll
@@ -354,7 +412,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   __syncthreads();
 
   // ---- PB: dT (lower blocks), d(beta v), d(beta kh e^G) ----
-  for (int p = wave; p < 10; p += 4) {
+  for (int p = wave; p < 10; p += kVjpWaves) {
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
@@ -397,7 +455,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
     for (int rr = 0; rr < 4; ++rr) sDT[(16 * ba + 4 * kg + rr) * MP + jj] = acc[rr];
   }
   // d(beta v) = T^T dU  -> dv and beta partials
-  for (int p = wave; p < 4 * (V / 16); p += 4) {
+  for (int p = wave; p < 4 * (V / 16); p += kVjpWaves) {
     const int rt = p % 4, ct = p / 4;
     const int j = 16 * rt + lr, col = 16 * ct + lr;
     f32x4 acc = zero4();
@@ -425,7 +483,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
     }
   }
   // d(beta kh e^G) = T^T dW -> dkh, dG, beta partials (same ownership as PA)
-  for (int p = wave; p < NKT; p += 4) {
+  for (int p = wave; p < NKT; p += kVjpWaves) {
     const int rt = p % 4, ct = p / 4;
     const int j = 16 * rt + lr, c = 16 * ct + lr;
     f32x4 acc = zero4();
@@ -458,7 +516,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   __syncthreads();
 
   // ---- PC: Y = T^T dT ----
-  for (int p = wave; p < 16; p += 4) {
+  for (int p = wave; p < 16; p += kVjpWaves) {
     const int rt = p / 4, ct = p % 4;
     const int i = 16 * rt + lr, jcol = 16 * ct + lr;
     f32x4 acc = zero4();
@@ -478,7 +536,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
   __syncthreads();
 
   // ---- PD: dM = -(Y T^T), strictly lower; dM' = beta_i dM ----
-  for (int p = wave; p < 10; p += 4) {
+  for (int p = wave; p < 10; p += kVjpWaves) {
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
@@ -505,7 +563,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_dense_kernel(BwdArgs a) {
       if (lr == 0) sPM[bb * 64 + ii] = part;
     }
   }
-  for (int idx = tid; idx < 64 * 64; idx += 256) {
+  for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
     const int ii = idx / 64, jj = idx % 64;
     if (jj / 16 > ii / 16) DMP[idx] = 0.f;
   }
@@ -557,7 +615,7 @@ struct DecaySmem {
 };
 
 template <int K>
-__global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a) {
   using L = DecaySmem<K>;
   constexpr int KP = L::KP, MP = L::MP;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -586,7 +644,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
 
   // ---- P0: stage qh, kh, G, dA, dM' ----
   if (tid < 4) sF[tid] = 0;
-  for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+  for (int idx = tid; idx < 64 * (K / 8); idx += kVjpThreads) {
     const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
     float qv[8], kv[8];
     if (t < len) {
@@ -608,7 +666,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
   {
     const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
     const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
-    for (int idx = tid; idx < 64 * 64; idx += 256) {
+    for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
       sDA[(idx / 64) * MP + idx % 64] = DA[idx];
       sDM[(idx / 64) * MP + idx % 64] = DMP[idx];
     }
@@ -624,7 +682,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
 
   constexpr int NKT = 4 * (K / 16);
   // ---- P1: row side  Rq = sum_j dA_ij kh_j e^{G_i-G_j},  Rk = sum_j dM'_ij kh_j e^{G_i-G_j} ----
-  for (int p = wave; p < NKT; p += 4) {
+  for (int p = wave; p < NKT; p += kVjpWaves) {
     const int ba = p % 4, ct = p / 4;
     const int r = 16 * ba;
     const int c = 16 * ct + lr;
@@ -683,7 +741,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
     }
   }
   // ---- P2: column side  C = sum_i (dA_ij qh_i + dM'_ij kh_i) e^{G_i-G_j}  (same ownership) ----
-  for (int p = wave; p < NKT; p += 4) {
+  for (int p = wave; p < NKT; p += kVjpWaves) {
     const int bb = p % 4, ct = p / 4;
     const int rp = 16 * bb + 15;
     const int c = 16 * ct + lr;
@@ -773,7 +831,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
   // ---- P4: L2-norm chains -> dq, dk ----
   {
     constexpr int LPR = K / 8;
-    constexpr int RPP = 256 / LPR;
+    constexpr int RPP = kVjpThreads / LPR;
     const int c0 = (tid % LPR) * 8;
     for (int t = tid / LPR; t < 64; t += RPP) {
       if (t >= len) continue;  // uniform per LPR lane group
@@ -813,27 +871,42 @@ __global__ __launch_bounds__(256) void chunk_bwd_decay_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // gate parameter reduction (fixed order)
 // ---------------------------------------------------------------------------
+constexpr int kParamThreads = 1024;
+
+// Thread (part, c) sums the chunks part, part + P, ... (P = kParamThreads / K) in order;
+// the P partials and then the K channels are combined in a fixed order.
 template <int K>
-__global__ __launch_bounds__(K) void chunk_bwd_params_kernel(BwdArgs a, int max_chunks) {
-  __shared__ float s_red[K];
-  const int h = blockIdx.x, c = threadIdx.x;
+__global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs a, int max_chunks) {
+  constexpr int P = kParamThreads / K;
+  __shared__ float s0[P][K], s1[P][K];
+  const int h = blockIdx.x, c = threadIdx.x % K, part = threadIdx.x / K;
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
   const float* PP = (const float*)a.sc.p[S_PP];
   float p0 = 0.f, p1 = 0.f;
-  for (int chn = 0; chn < max_chunks; ++chn) {
+  for (int chn = part; chn < max_chunks; chn += P) {
     if (chunks[chn].y <= 0) continue;
     const size_t tile = (size_t)chn * a.H + h;
     p0 += PP[tile * 2 * K + c];
     p1 += PP[tile * 2 * K + K + c];
   }
-  a.ddt_bias[h * K + c] = p0;
-  s_red[c] = p1;
+  s0[part][c] = p0;
+  s1[part][c] = p1;
+  __syncthreads();
+  if (part == 0) {
+    float t0 = 0.f, t1 = 0.f;
+    for (int q = 0; q < P; ++q) {
+      t0 += s0[q][c];
+      t1 += s1[q][c];
+    }
+    a.ddt_bias[h * K + c] = t0;
+    s1[0][c] = t1;
+  }
   __syncthreads();
   for (int w = K / 2; w >= 1; w >>= 1) {
-    if (c < w) s_red[c] += s_red[c + w];
+    if (part == 0 && c < w) s1[0][c] += s1[0][c + w];
     __syncthreads();
   }
-  if (c == 0) a.dA_log[h] = s_red[0];
+  if (threadIdx.x == 0) a.dA_log[h] = s1[0][0];
 }
 
 template <int K, int V>
@@ -859,18 +932,18 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     }
     if (stages & (1 << (KDA_STAGE_BWD_DENSE - 10))) {
       auto dense = chunk_bwd_dense_kernel<K, V>;
-      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(256), smem_d, stream, a);
+      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(kVjpThreads), smem_d, stream, a);
       KDA_LAUNCH_CHECK("chunk_backward dense");
     }
     if (stages & (1 << (KDA_STAGE_BWD_DECAY - 10))) {
       auto decay = chunk_bwd_decay_kernel<K>;
-      hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(256), smem_e, stream, a);
+      hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(kVjpThreads), smem_e, stream, a);
       KDA_LAUNCH_CHECK("chunk_backward decay");
     }
   }
   if (p->gate_mode == KDA_GATE_K3 && (stages & (1 << (KDA_STAGE_BWD_PARAMS - 10)))) {
     auto params = chunk_bwd_params_kernel<K>;
-    hipLaunchKernelGGL(params, dim3(p->heads), dim3(K), 0, stream, a, g.max_chunks);
+    hipLaunchKernelGGL(params, dim3(p->heads), dim3(kParamThreads), 0, stream, a, g.max_chunks);
     KDA_LAUNCH_CHECK("chunk_backward params");
   }
   return KDA_OK;

@@ -109,11 +109,14 @@ struct IntraSmem {
   static constexpr size_t bytes = off_f + 16;
 };
 
+constexpr int kIntraThreads = 1024;
+constexpr int kIntraWaves = kIntraThreads / kWave;
+
 __device__ __constant__ int kPairA[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
 __device__ __constant__ int kPairB[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
 
 template <int K, int V>
-__global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs a) {
   using L = IntraSmem<K, V>;
   constexpr int KP = L::KP, VP = L::VP, MP = L::MP;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -137,12 +140,12 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
   const int lr = lane % 16, kg = lane / 16;
 
   if (tid < 4) sF[tid] = 0;
-  for (int i = tid; i < 64 * MP; i += 256) sT[i] = 0.f;
+  for (int i = tid; i < 64 * MP; i += kIntraThreads) sT[i] = 0.f;
 
   // ---- phase 1: load, normalise, activate ----
   {
     constexpr int LPR = K / 8;
-    constexpr int RPP = 256 / LPR;
+    constexpr int RPP = kIntraThreads / LPR;
     const int c0 = (tid % LPR) * 8;
     const float* A_log = a.A_log;
     for (int t = tid / LPR; t < 64; t += RPP) {
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
   }
   __syncthreads();
   // beta * v (bf16) and the in-chunk cumulative decay
-  for (int idx = tid; idx < 64 * (V / 8); idx += 256) {
+  for (int idx = tid; idx < 64 * (V / 8); idx += kIntraThreads) {
     const int t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
     float vv[8];
     if (t < len) {
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
   bf16* Aout = (bf16*)a.ws.p[R_A] + tile * 64 * 64;
   bf16* ATout = (bf16*)a.ws.p[R_AT] + tile * 64 * 64;
   float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
-  for (int p = wave; p < 10; p += 4) {
+  for (int p = wave; p < 10; p += kIntraWaves) {
     const int ba = kPairA[p], bb = kPairB[p];
     const int r = 16 * ba;
     f32x4 accA = zero4(), accM = zero4();
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
     }
   }
   // strictly-upper 16x16 blocks are zero
-  for (int idx = tid; idx < 64 * 64; idx += 256) {
+  for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) {
     const int ii = idx / 64, jj = idx % 64;
     if (jj / 16 > ii / 16) {
       Aout[ii * 64 + jj] = to_bf16(0.f);
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
   }
   __syncthreads();
   for (int ba = 1; ba < 4; ++ba) {
-    for (int idx = tid; idx < ba * 256; idx += 256) {
+    for (int idx = tid; idx < ba * 256; idx += kIntraThreads) {
       const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
       const float bi = sB[16 * ba + i];
       float s = 0.f;
@@ -321,7 +324,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
       sX[(bb * 16 + i) * 17 + j] = bi * s;
     }
     __syncthreads();
-    for (int idx = tid; idx < ba * 256; idx += 256) {
+    for (int idx = tid; idx < ba * 256; idx += kIntraThreads) {
       const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
       float s = 0.f;
 #pragma unroll
@@ -333,16 +336,16 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
   }
   {
     float* Tout = (float*)a.ws.p[R_T] + tile * 64 * 64;
-    for (int idx = tid; idx < 64 * 64; idx += 256) Tout[idx] = sT[(idx / 64) * MP + idx % 64];
+    for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) Tout[idx] = sT[(idx / 64) * MP + idx % 64];
   }
 
   // ---- phase 4: U = T (beta v), W = T (beta kh exp(G)) ----
   {
-    bf16* Uout = (bf16*)a.ws.p[R_U] + tile * 64 * V;
+    bf16* UTout = (bf16*)a.ws.p[R_UT] + tile * V * 64;
     bf16* Wout = (bf16*)a.ws.p[R_W] + tile * 64 * K;
     bf16* WTout = (bf16*)a.ws.p[R_WT] + tile * K * 64;
     constexpr int NU = 4 * (V / 16), NW = 4 * (K / 16);
-    for (int p = wave; p < NU + NW; p += 4) {
+    for (int p = wave; p < NU + NW; p += kIntraWaves) {
       const bool isU = p < NU;
       const int q = isU ? p : p - NU;
       const int rt = q % 4, ct = q / 4;
@@ -361,15 +364,19 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
         }
         acc = mfma16(fa, fb, acc);
       }
+      if (isU) {
+        bf16x4 x;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = 16 * rt + 4 * kg + rr;
-        if (isU) {
-          Uout[ii * V + col] = to_bf16(acc[rr]);
-        } else {
-          Wout[ii * K + col] = to_bf16(acc[rr]);
-          WTout[col * 64 + ii] = to_bf16(acc[rr]);
+        for (int rr = 0; rr < 4; ++rr) x[rr] = to_bf16(acc[rr]);
+        *(bf16x4*)(UTout + col * 64 + 16 * rt + 4 * kg) = x;
+      } else {
+        bf16x4 x;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          x[rr] = to_bf16(acc[rr]);
+          Wout[(16 * rt + 4 * kg + rr) * K + col] = x[rr];
         }
+        *(bf16x4*)(WTout + col * 64 + 16 * rt + 4 * kg) = x;
       }
     }
   }
@@ -380,7 +387,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
     bf16* KD = (bf16*)a.ws.p[R_KD] + tile * 64 * K;
     bf16* QGT = (bf16*)a.ws.p[R_QGT] + tile * K * 64;
     bf16* KDT = (bf16*)a.ws.p[R_KDT] + tile * K * 64;
-    for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+    for (int idx = tid; idx < 64 * (K / 8); idx += kIntraThreads) {
       const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
       float qg[8], kd[8];
 #pragma unroll
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
       store8(QG + t * K + c0, qg);
       store8(KD + t * K + c0, kd);
     }
-    for (int idx = tid; idx < K * 8; idx += 256) {
+    for (int idx = tid; idx < K * 8; idx += kIntraThreads) {
       const int c = idx / 8, t0 = (idx % 8) * 8;
       float qg[8], kd[8];
       const float gl = sG[63 * KP + c];
@@ -409,21 +416,57 @@ __global__ __launch_bounds__(256) void chunk_fwd_intra_kernel(FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// inter-chunk state scan fused with the output
+// inter-chunk state scan
 // ---------------------------------------------------------------------------
+// One 256-thread workgroup per (sequence, head, 16-wide V strip).  The critical path
+// per chunk is: publish S (LDS) -> delta = U - W S -> publish delta (LDS) ->
+// S <- lam S + Kd^T delta, two barriers.  All global operands of a chunk are loaded
+// into a register ring kFwdRing chunks ahead, so the HBM latency (~1-2 us) overlaps
+// several chunk steps.  Every per-step global access is one vector instruction (CDNA
+// counts loads and stores on the same vmcnt, which must stay below 64 in flight).
+constexpr int kFwdRing = 4;
+
+template <int K>
+struct FwdScanFrag {
+  bf16x8 w[K / 32];      // W rows of this wave's delta tile
+  bf16x4 ut;             // U^T: 4 tokens of this lane's delta outputs
+  bf16x8 kdt[K / 64][2]; // Kd^T rows of this wave's state tiles
+  float4 lam[K / 64];    // exp(G_last) of this lane's state rows
+};
+
 template <int K, int V>
 __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
   constexpr int KT = K / 16 / 4;  // 16-row key tiles of the state per wave
   constexpr int SP = K + 8;
   constexpr int DP = 64 + 8;
-  __shared__ __attribute__((aligned(16))) bf16 sS[2][16 * SP];
-  __shared__ __attribute__((aligned(16))) bf16 sD[16 * DP];
+  constexpr int FP = 16 + 4;
+  __shared__ __attribute__((aligned(16))) bf16 sS[2][16 * SP];  // bf16 S as [v][k]
+  __shared__ __attribute__((aligned(16))) float sSf[K * FP];    // f32 S as [k][v]
+  __shared__ __attribute__((aligned(16))) bf16 sD[16 * DP];     // delta as [v][t]
   const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
   const int H = a.H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
-  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+  const int i = 16 * wave + lr;
+
+  auto load = [&](int chunk, FwdScanFrag<K>& f) {
+    const size_t tile = (size_t)chunk * H + h;
+    const bf16* Wt = (const bf16*)a.ws.p[R_W] + tile * 64 * K;
+    const bf16* UT = (const bf16*)a.ws.p[R_UT] + tile * V * 64;
+    const bf16* KDT = (const bf16*)a.ws.p[R_KDT] + tile * K * 64;
+    const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) f.w[s] = *(const bf16x8*)(Wt + i * K + 32 * s + 8 * kg);
+    f.ut = *(const bf16x4*)(UT + (v0 + lr) * 64 + 16 * wave + 4 * kg);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int kb = 16 * (wave * KT + kt);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) f.kdt[kt][s] = *(const bf16x8*)(KDT + (kb + lr) * 64 + 32 * s + 8 * kg);
+      f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
+    }
+  };
 
   f32x4 S[KT];
 #pragma unroll
@@ -436,100 +479,92 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
       S[kt] = zero4();
     }
   }
+  const int n = sq.y;
+  FwdScanFrag<K> ring[kFwdRing];
+  if (n > 0) {
+#pragma unroll
+    for (int d = 0; d < kFwdRing; ++d) load(sq.x + min(d, n - 1), ring[d]);
+  }
 
-  int p = 0;
-  for (int ci = 0; ci < sq.y; ++ci) {
+  auto step = [&](int ci, FwdScanFrag<K>& f) {
     const int chunk = sq.x + ci;
-    const int4 ch = chunks[chunk];
     const size_t tile = (size_t)chunk * H + h;
-    const int len = ch.y, row0 = ch.x;
-    bf16* sSp = sS[p];
-    // (1) publish the bf16 state slice as the MFMA B operand [v][k]
+    bf16* sSp = sS[ci & 1];
+    // (1) publish S: bf16 [v][k] (MFMA operand) and f32 [k][v] (history staging)
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       bf16x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = to_bf16(S[kt][r]);
+      for (int r = 0; r < 4; ++r) {
+        x[r] = to_bf16(S[kt][r]);
+        sSf[(k0 + r) * FP + lr] = S[kt][r];
+      }
       *(bf16x4*)(sSp + lr * SP + k0) = x;
     }
     __syncthreads();
-    // (2) f32 state history [K][V] for the backward pass
+    // (2) state histories: f32 [K][V] and bf16 [V][K] (fixed-count vector stores)
     {
       float* SH = (float*)a.ws.p[R_SH] + tile * K * V;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int k0 = 16 * (wave * KT + kt) + 4 * kg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) SH[(size_t)(k0 + r) * V + v0 + lr] = S[kt][r];
+      for (int it = 0; it < K / 64; ++it) {
+        const int idx = tid + 256 * it;
+        const int kk = idx / 4, q4 = (idx % 4) * 4;
+        *(float4*)(SH + (size_t)kk * V + v0 + q4) = *(const float4*)(sSf + kk * FP + q4);
+      }
+      bf16* SHB = (bf16*)a.ws.p[R_SHB] + tile * V * K;
+      constexpr int E = K / 16;  // bf16 per thread
+      const int vv = tid / (K / E), ke = (tid % (K / E)) * E;
+      if constexpr (E == 8) {
+        *(bf16x8*)(SHB + (size_t)(v0 + vv) * K + ke) = *(const bf16x8*)(sSp + vv * SP + ke);
+      } else {
+        *(bf16x4*)(SHB + (size_t)(v0 + vv) * K + ke) = *(const bf16x4*)(sSp + vv * SP + ke);
       }
     }
-    // (3) delta rows 16*wave.. : U - W S
-    const int i = 16 * wave + lr;
+    // (3) delta rows 16*wave.. = U - W S  (two accumulators halve the MFMA chain)
     {
-      const bf16* Wt = (const bf16*)a.ws.p[R_W] + tile * 64 * K;
-      const bf16* Ut = (const bf16*)a.ws.p[R_U] + tile * 64 * V;
-      bf16* DL = (bf16*)a.ws.p[R_DL] + tile * 64 * V;
-      f32x4 acc = zero4();
+      f32x4 acc0 = zero4(), acc1 = zero4();
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        const bf16x8 fa = *(const bf16x8*)(Wt + i * K + 32 * s + 8 * kg);
-        const bf16x8 fb = *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg);
-        acc = mfma16(fa, fb, acc);
+      for (int s = 0; s < K / 32; s += 2) {
+        acc0 = mfma16(f.w[s], *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg), acc0);
+        acc1 = mfma16(f.w[s + 1], *(const bf16x8*)(sSp + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
       }
       bf16x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * wave + 4 * kg + r;
-        const float d = to_f32(Ut[t * V + v0 + lr]) - acc[r];
-        x[r] = to_bf16(d);
-        DL[t * V + v0 + lr] = x[r];
-      }
+      for (int r = 0; r < 4; ++r) x[r] = to_bf16(to_f32(f.ut[r]) - (acc0[r] + acc1[r]));
       *(bf16x4*)(sD + lr * DP + 16 * wave + 4 * kg) = x;
     }
     __syncthreads();
-    // (4a) S <- lam S + Kd^T delta
+    // (3b) delta^T history [V][64]
     {
-      const bf16* KDT = (const bf16*)a.ws.p[R_KDT] + tile * K * 64;
-      const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int kb = 16 * (wave * KT + kt);
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16x8 fa = *(const bf16x8*)(KDT + (kb + lr) * 64 + 32 * s + 8 * kg);
-          const bf16x8 fb = *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg);
-          acc = mfma16(fa, fb, acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) S[kt][r] = fmaf(lam[kb + 4 * kg + r], S[kt][r], acc[r]);
-      }
+      bf16* DLT = (bf16*)a.ws.p[R_DLT] + tile * V * 64;
+      const int vv = tid / 16, t4 = (tid % 16) * 4;
+      *(bf16x4*)(DLT + (size_t)(v0 + vv) * 64 + t4) = *(const bf16x4*)(sD + vv * DP + t4);
     }
-    // (4b) O = Qg S + A delta for rows 16*wave..
-    {
-      const bf16* QG = (const bf16*)a.ws.p[R_QG] + tile * 64 * K;
-      const bf16* AM = (const bf16*)a.ws.p[R_A] + tile * 64 * 64;
-      f32x4 o = zero4();
+    // (4) S <- lam S + Kd^T delta
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        const bf16x8 fa = *(const bf16x8*)(QG + i * K + 32 * s + 8 * kg);
-        const bf16x8 fb = *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg);
-        o = mfma16(fa, fb, o);
-      }
+    for (int kt = 0; kt < KT; ++kt) {
+      f32x4 acc = zero4();
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 fa = *(const bf16x8*)(AM + i * 64 + 32 * s + 8 * kg);
-        const bf16x8 fb = *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg);
-        o = mfma16(fa, fb, o);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * wave + 4 * kg + r;
-        if (t < len) a.out[((size_t)(row0 + t) * H + h) * V + v0 + lr] = to_bf16(o[r]);
-      }
+      for (int s = 0; s < 2; ++s)
+        acc = mfma16(f.kdt[kt][s], *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg), acc);
+      S[kt][0] = fmaf(f.lam[kt].x, S[kt][0], acc[0]);
+      S[kt][1] = fmaf(f.lam[kt].y, S[kt][1], acc[1]);
+      S[kt][2] = fmaf(f.lam[kt].z, S[kt][2], acc[2]);
+      S[kt][3] = fmaf(f.lam[kt].w, S[kt][3], acc[3]);
     }
-    p ^= 1;
+  };
+
+  // Ring loads are unconditional (the index is clamped to the last chunk) so no register
+  // of the ring is redefined under control flow; otherwise the compiler must wait for
+  // every load in flight at each join.
+  for (int c0 = 0; c0 < n; c0 += kFwdRing) {
+#pragma unroll
+    for (int d = 0; d < kFwdRing; ++d) {
+      const int ci = c0 + d;
+      if (ci < n) step(ci, ring[d]);
+      load(sq.x + min(ci + kFwdRing, n - 1), ring[d]);
+    }
   }
   if (a.sfin) {
 #pragma unroll
@@ -537,6 +572,49 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       *(float4*)(a.sfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
           make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// output:  O = Qg S + A delta  (chunk-parallel, after the scan)
+// ---------------------------------------------------------------------------
+// One 256-thread workgroup per (chunk, head); wave w owns the 16-token row tile w and
+// walks the V/16 column tiles, so its Qg and A operands are loaded once.
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int len = ch.y;
+  if (len <= 0) return;
+  const int H = a.H, h = blockIdx.y;
+  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+  const int i = 16 * wave + lr;
+  const bf16* QG = (const bf16*)a.ws.p[R_QG] + tile * 64 * K;
+  const bf16* AM = (const bf16*)a.ws.p[R_A] + tile * 64 * 64;
+  const bf16* SHB = (const bf16*)a.ws.p[R_SHB] + tile * V * K;
+  const bf16* DLT = (const bf16*)a.ws.p[R_DLT] + tile * V * 64;
+  bf16x8 fq[K / 32], fa[2];
+#pragma unroll
+  for (int s = 0; s < K / 32; ++s) fq[s] = *(const bf16x8*)(QG + i * K + 32 * s + 8 * kg);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) fa[s] = *(const bf16x8*)(AM + i * 64 + 32 * s + 8 * kg);
+#pragma unroll 2
+  for (int ct = 0; ct < V / 16; ++ct) {
+    const int vcol = 16 * ct + lr;
+    f32x4 o0 = zero4(), o1 = zero4();
+#pragma unroll
+    for (int s = 0; s < K / 32; s += 2) {
+      o0 = mfma16(fq[s], *(const bf16x8*)(SHB + (size_t)vcol * K + 32 * s + 8 * kg), o0);
+      o1 = mfma16(fq[s + 1], *(const bf16x8*)(SHB + (size_t)vcol * K + 32 * (s + 1) + 8 * kg), o1);
+    }
+    o0 = mfma16(fa[0], *(const bf16x8*)(DLT + (size_t)vcol * 64 + 8 * kg), o0);
+    o1 = mfma16(fa[1], *(const bf16x8*)(DLT + (size_t)vcol * 64 + 32 + 8 * kg), o1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * kg + r;
+      if (t < len) a.out[((size_t)(ch.x + t) * H + h) * V + vcol] = to_bf16(o0[r] + o1[r]);
     }
   }
 }
@@ -587,15 +665,19 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
       attr = true;
     }
     auto intra = chunk_fwd_intra_kernel<K, V>;
-    hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(256),
+    hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(kIntraThreads),
                        smem, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward intra");
   }
   if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
     auto scan = chunk_fwd_scan_kernel<K, V>;
-    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16),
-                       dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16), dim3(256), 0, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward scan");
+  }
+  if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_OUTPUT))) {
+    auto outk = chunk_fwd_output_kernel<K, V>;
+    hipLaunchKernelGGL(outk, dim3(g.max_chunks, p->heads), dim3(256), 0, stream, a);
+    KDA_LAUNCH_CHECK("chunk_forward output");
   }
   return KDA_OK;
 }
@@ -679,7 +761,8 @@ extern "C" int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p
                                        const float* dt_bias, const float* initial_state,
                                        void* output, float* final_state, void* workspace,
                                        hipStream_t stream) {
-  if (stage != KDA_STAGE_PREP && stage != KDA_STAGE_FWD_INTRA && stage != KDA_STAGE_FWD_SCAN)
+  if (stage != KDA_STAGE_PREP && stage != KDA_STAGE_FWD_INTRA && stage != KDA_STAGE_FWD_SCAN &&
+      stage != KDA_STAGE_FWD_OUTPUT)
     return kda::set_error(KDA_ERR_INVALID, "chunk_forward_stage: unknown stage %d", stage);
   return chunk_forward_impl(1 << stage, p, q, k, v, gate, beta_logits, A_log, dt_bias,
                             initial_state, output, final_state, workspace, stream);

@@ -20,7 +20,7 @@ enum WsRegion {
   R_KDT,         // bf16 [tile][K][64]  transpose of R_KD
   R_W,           // bf16 [tile][64][K]  W = T (beta k_hat exp(G))
   R_WT,          // bf16 [tile][K][64]  transpose of R_W
-  R_U,           // bf16 [tile][64][V]  U = T (beta v)
+  R_UT,          // bf16 [tile][V][64]  U^T, U = T (beta v)
   R_A,           // bf16 [tile][64][64] A (lower, incl. diagonal)
   R_AT,          // bf16 [tile][64][64] transpose of R_A
   R_T,           // f32  [tile][64][64] T = (I + diag(beta) M')^-1
@@ -31,13 +31,14 @@ enum WsRegion {
   R_RK,          // f32  [tile][64]     1 / max(||k||, 1e-12)
   R_BETA,        // f32  [tile][64]     sigmoid(beta_logits)
   R_SH,          // f32  [tile][K][V]   state entering the chunk (written by the scan)
-  R_DL,          // bf16 [tile][64][V]  delta = U - W S (written by the scan)
+  R_SHB,         // bf16 [tile][V][K]   the same state as the bf16 MFMA operand of the scan
+  R_DLT,         // bf16 [tile][V][64]  delta^T, delta = U - W S (written by the scan)
   R_COUNT
 };
 
 enum ScRegion {
   S_DSH = 0,  // f32  [tile][K][V]   dL/dS at the chunk end
-  S_DDL,      // f32  [tile][64][V]  dL/d delta
+  S_DDLT,     // f32  [tile][V][64]  (dL/d delta)^T
   S_DA,       // f32  [tile][64][64] dL/dA (masked lower)
   S_DMP,      // f32  [tile][64][64] dL/dM' (strictly lower, beta folded in)
   S_GQ,       // f32  [tile][64][K]  accumulated dL/dq_hat
@@ -63,14 +64,15 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
     case R_CHUNKS: return (size_t)g.max_chunks * 16;
     case R_SEQS: return (size_t)g.num_seqs * 8;
     case R_QG: case R_QGT: case R_KD: case R_KDT: case R_W: case R_WT: return nt * 64 * K * 2;
-    case R_U: return nt * 64 * V * 2;
+    case R_UT: return nt * 64 * V * 2;
     case R_A: case R_AT: return nt * 64 * 64 * 2;
     case R_T: case R_MP: return nt * 64 * 64 * 4;
     case R_G: return nt * 64 * K * 4;
     case R_LAM: return nt * K * 4;
     case R_RQ: case R_RK: case R_BETA: return nt * 64 * 4;
     case R_SH: return nt * K * V * 4;
-    case R_DL: return nt * 64 * V * 2;
+    case R_SHB: return nt * K * V * 2;
+    case R_DLT: return nt * 64 * V * 2;
     default: return 0;
   }
 }
@@ -80,7 +82,7 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   const size_t K = g.K, V = g.V;
   switch (r) {
     case S_DSH: return nt * K * V * 4;
-    case S_DDL: return nt * 64 * V * 4;
+    case S_DDLT: return nt * 64 * V * 4;
     case S_DA: case S_DMP: return nt * 64 * 64 * 4;
     case S_GQ: case S_GK: case S_GG: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;

@@ -107,12 +107,13 @@ int kda_chunk_backward(const kda_chunk_problem* p,
  * kda_chunk_forward / kda_chunk_backward call with the same arguments has prepared, so a
  * benchmark can time that kernel alone.  No counterpart in the reference (it exists for
  * measurement only).  Forward stages: KDA_STAGE_PREP, KDA_STAGE_FWD_INTRA,
- * KDA_STAGE_FWD_SCAN; backward stages: KDA_STAGE_BWD_SCAN, KDA_STAGE_BWD_DENSE,
+ * KDA_STAGE_FWD_SCAN, KDA_STAGE_FWD_OUTPUT; backward stages: KDA_STAGE_BWD_SCAN, KDA_STAGE_BWD_DENSE,
  * KDA_STAGE_BWD_DECAY, KDA_STAGE_BWD_PARAMS.  Arguments are those of the full calls.
  */
 #define KDA_STAGE_PREP 0
 #define KDA_STAGE_FWD_INTRA 1
 #define KDA_STAGE_FWD_SCAN 2
+#define KDA_STAGE_FWD_OUTPUT 3
 #define KDA_STAGE_BWD_SCAN 10
 #define KDA_STAGE_BWD_DENSE 11
 #define KDA_STAGE_BWD_DECAY 12
