@@ -32,6 +32,7 @@ namespace kda {
 
 struct BwdArgs {
   int H;
+  int num_seqs;
   int gate_mode;
   float lb;
   float scale;
@@ -85,8 +86,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sDSf[K * FP];    // f32 dS' as [k][v]
   __shared__ __attribute__((aligned(16))) bf16 sDO[2][16 * DP];  // dO strip as [v][t]
   __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];     // dDelta strip as [v][t]
-  const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
   const int H = a.H;
+  int rec, strip;
+  if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
+  const int seq = rec / H, h = rec % H, v0 = strip * 16;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
@@ -914,7 +917,9 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
                            hipStream_t stream, int stages) {
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     auto scan = chunk_bwd_scan_kernel<K, V>;
-    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16), dim3(256), 0, stream, a);
+    const int nrec = p->num_seqs * p->heads;
+    const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
+    hipLaunchKernelGGL(scan, dim3(grid), dim3(256), 0, stream, a);
     KDA_LAUNCH_CHECK("chunk_backward scan");
   }
   if (g.max_chunks > 0) {
@@ -976,6 +981,7 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
   const ChunkGeom g = make_geom(p);
   BwdArgs a;
   a.H = p->heads;
+  a.num_seqs = p->num_seqs;
   a.gate_mode = p->gate_mode;
   a.lb = p->lower_bound;
   a.scale = p->scale;

@@ -34,6 +34,7 @@ namespace kda {
 
 struct FwdArgs {
   int H;
+  int num_seqs;
   int gate_mode;
   float lb;
   float scale;
@@ -443,8 +444,10 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sS[2][16 * SP];  // bf16 S as [v][k]
   __shared__ __attribute__((aligned(16))) float sSf[K * FP];    // f32 S as [k][v]
   __shared__ __attribute__((aligned(16))) bf16 sD[16 * DP];     // delta as [v][t]
-  const int seq = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 16;
   const int H = a.H;
+  int rec, strip;
+  if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
+  const int seq = rec / H, h = rec % H, v0 = strip * 16;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
@@ -671,7 +674,9 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
   }
   if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
     auto scan = chunk_fwd_scan_kernel<K, V>;
-    hipLaunchKernelGGL(scan, dim3(p->num_seqs, p->heads, V / 16), dim3(256), 0, stream, a);
+    const int nrec = p->num_seqs * p->heads;
+    const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
+    hipLaunchKernelGGL(scan, dim3(grid), dim3(256), 0, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward scan");
   }
   if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_OUTPUT))) {
@@ -722,6 +727,7 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   const ChunkGeom g = make_geom(p);
   FwdArgs a;
   a.H = p->heads;
+  a.num_seqs = p->num_seqs;
   a.gate_mode = p->gate_mode;
   a.lb = p->lower_bound;
   a.scale = p->scale;

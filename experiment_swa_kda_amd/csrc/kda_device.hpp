@@ -67,6 +67,19 @@ __device__ __forceinline__ void store8(bf16* p, const float* in) {
   *reinterpret_cast<bf16x8*>(p) = x;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X (linear id mod 8),
+// each XCD with its own L2.  For a 1-D grid of kXcds * NS * ceil(NR / kXcds) workgroups,
+// this maps linear id -> (recurrence r, strip) so the NS strips of one recurrence, which
+// read identical per-chunk operands, land on the same XCD.  Returns false past NR.
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool xcd_strip_coords(int NR, int NS, int& r, int& strip) {
+  const int L = blockIdx.x;
+  const int x = L % kXcds, rest = L / kXcds;
+  strip = rest % NS;
+  r = (rest / NS) * kXcds + x;
+  return r < NR;
+}
+
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): two MFMAs with (hi, lo) recover
 // ~16 mantissa bits of an f32 operand.
 __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
