@@ -46,6 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
     ap.add_argument("--cpu-sample-len", type=int, default=1024,
                     help="T of the CPU baseline sample (extrapolated linearly to T=4096)")
     return ap.parse_args()
@@ -125,6 +126,44 @@ def kernel_times(torch, t, do, gate, reps=20):
         torch.cuda.synchronize()
         res[name] = s.elapsed_time(e) / reps
     return res
+
+
+def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42):
+    """6-layer all-KDA decoder, d_model 384, H3 D128, vocab 32768,
+    B2 T4096, 4 gradient-accumulation microsteps per update (32,768 tokens), uniform
+    random token ids, AdamW update.  Returns tokens/s as the median over the timed
+    updates (the reference scores the median of steps 2-6, docs/BENCHMARK.md:33-36)."""
+    from experiment_swa_kda_amd.model import GPT, GPTConfig, make_optimizer
+
+    torch.manual_seed(seed)
+    cfg = GPTConfig(sequence_len=4096, vocab_size=32768, n_layer=6, n_head=3, n_embd=384)
+    model = GPT(cfg).cuda()
+    model.init_weights()
+    opt = make_optimizer(model)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B, T = 2, 4096
+    data = [torch.randint(0, cfg.vocab_size, (B, T + 1), device="cuda", generator=g) for _ in range(accum)]
+
+    def update():
+        for mb in data:
+            loss = model(mb[:, :-1], mb[:, 1:]) / accum
+            loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    times = []
+    for i in range(warmup + updates):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loss = update()
+        torch.cuda.synchronize()
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    return {"tok_per_s": round(B * T * accum / (ms * 1e-3), 1), "ms_per_update": round(ms, 3),
+            "tokens_per_update": B * T * accum, "updates_timed": updates, "loss": round(float(loss) * accum, 4),
+            "optimizer": "AdamW", "reference_gb10_tok_per_s": 44942}
 
 
 def cpu_baseline(sample_len):
@@ -210,6 +249,8 @@ def main():
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": None},
         "reference_gb10_ms_fwd_bwd": 3.916,
     }
+    if not args.no_train:
+        line["train_6layer"] = train_throughput(torch)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_sample_len)
     print(json.dumps(line), flush=True)

@@ -388,6 +388,9 @@ class ShortConvolution(nn.Conv1d):
                          padding=kernel_size - 1)
 
     def forward(self, x, state=None, *, output_final_state=False, backend="fla_triton"):
+        """``backend``: "project_cuda" / "fla_triton" run the HIP kernels on device tensors
+        (the latter names the reference's comparator slot); "reference" runs the eager
+        PyTorch form on any device."""
         if x.ndim != 3 or x.shape[-1] != self.in_channels:
             raise ValueError(f"x must have shape [B,T,{self.in_channels}]")
         batch, length, channels = x.shape
@@ -403,7 +406,7 @@ class ShortConvolution(nn.Conv1d):
             return x.new_empty(batch, 0, channels), current if output_final_state else None
         if backend == "project_cuda" and not x.is_cuda:
             raise RuntimeError("project CUDA causal convolution cannot fall back on CPU")
-        if x.is_cuda:
+        if x.is_cuda and backend != "reference":
             if backend not in {"fla_triton", "project_cuda"}:
                 raise ValueError(f"unknown CUDA short-convolution backend: {backend}")
             output, final_state = _ProjectConvolutionAutograd.apply(
@@ -412,7 +415,8 @@ class ShortConvolution(nn.Conv1d):
                 output_final_state)
             _record("causal_convolution_forward")
             return _record_backward(output, "causal_convolution_backward"), final_state
-        # CPU tensors: the reference's own eager form (kda.py:192-212)
+        # CPU tensors or an explicit backend="reference": the reference's eager form
+        # (kda.py:192-212)
         sequence = x.transpose(1, 2)
         convolution_input = torch.cat((current[..., 1:], sequence), dim=-1)
         output = F.silu(F.conv1d(convolution_input, self.weight.to(dtype=x.dtype), groups=channels)).transpose(1, 2)
@@ -469,7 +473,8 @@ class KimiDeltaAttention(nn.Module):
         k_state = None if state is None else state.k_conv
         v_state = None if state is None else state.v_conv
         memory = None if state is None else state.memory
-        conv_backend = "project_cuda" if requested_mode.startswith("project_") else "fla_triton"
+        conv_backend = ("project_cuda" if requested_mode.startswith("project_")
+                        else "reference" if requested_mode == "reference" else "fla_triton")
         q, q_final = self.q_conv1d(self.q_proj(hidden_states), q_state, output_final_state=want_state,
                                    backend=conv_backend)
         k, k_final = self.k_conv1d(self.k_proj(hidden_states), k_state, output_final_state=want_state,

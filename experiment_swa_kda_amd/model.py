@@ -1,0 +1,135 @@
+"""All-KDA nanochat-style decoder used to measure training throughput.
+
+Restates the structure of the reference model for the ``window_pattern="K"`` case
+(nanochat/gpt.py: ``Block`` :159-205, ``GPT.__init__`` :208-260, ``init_weights``
+:262-330, ``forward`` :543-600): bf16 token embedding, RMS norms, smear gate,
+per-layer residual / x0 scalars, KDA mixer + ReLU^2 MLP blocks, mid-depth backout,
+soft-capped logits and cross entropy.  Master weights stay f32 and are cast to the
+activation dtype inside ``Linear`` (nanochat/gpt.py:52-57).  The KDA mixer is the HIP
+``KimiDeltaAttention`` of this package in ``project_chunk`` mode (conv, KDA core and
+output norm-gate on the gfx950 kernels; projections are PyTorch GEMMs).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .kda import KimiDeltaAttention, Linear
+
+
+@dataclass
+class GPTConfig:
+    sequence_len: int = 4096
+    vocab_size: int = 32768
+    n_layer: int = 6
+    n_head: int = 3
+    n_embd: int = 384
+    mode: str = "project_chunk"
+
+
+def norm(x):
+    return F.rms_norm(x, (x.size(-1),))
+
+
+class MLP(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.c_fc = Linear(d, 4 * d, bias=False)
+        self.c_proj = Linear(4 * d, d, bias=False)
+
+    def forward(self, x):
+        return self.c_proj(F.relu(self.c_fc(x)).square())
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: GPTConfig, layer_idx: int):
+        super().__init__()
+        self.attn = KimiDeltaAttention(cfg.n_embd, cfg.n_head, cfg.n_embd // cfg.n_head, conv_size=4,
+                                       layer_idx=layer_idx, mode=cfg.mode, allow_fallback=False)
+        self.mlp = MLP(cfg.n_embd)
+
+    def forward(self, x):
+        mixed, _ = self.attn(norm(x), state=None, output_final_state=False)
+        x = x + mixed
+        return x + self.mlp(norm(x))
+
+
+class GPT(nn.Module):
+    def __init__(self, cfg: GPTConfig, pad_vocab_size_to: int = 64):
+        super().__init__()
+        self.config = cfg
+        padded = ((cfg.vocab_size + pad_vocab_size_to - 1) // pad_vocab_size_to) * pad_vocab_size_to
+        self.padded_vocab = padded
+        self.transformer = nn.ModuleDict({
+            "wte": nn.Embedding(padded, cfg.n_embd),
+            "h": nn.ModuleList([Block(cfg, i) for i in range(cfg.n_layer)]),
+        })
+        self.lm_head = Linear(cfg.n_embd, padded, bias=False)
+        self.resid_lambdas = nn.Parameter(torch.ones(cfg.n_layer))
+        self.x0_lambdas = nn.Parameter(torch.zeros(cfg.n_layer))
+        self.smear_gate = Linear(24, 1, bias=False)
+        self.smear_lambda = nn.Parameter(torch.zeros(1))
+        self.backout_lambda = nn.Parameter(0.2 * torch.ones(1))
+
+    @torch.no_grad()
+    def init_weights(self, generator=None):
+        """Initialisation of nanochat/gpt.py:262-330 for KDA blocks."""
+        d = self.config.n_embd
+        s = 3 ** 0.5 * d ** -0.5
+        nn.init.normal_(self.transformer.wte.weight, 0.0, 0.8, generator=generator)
+        nn.init.normal_(self.lm_head.weight, 0.0, 0.001, generator=generator)
+        for block in self.transformer.h:
+            m = block.attn
+            for proj in (m.q_proj, m.k_proj, m.v_proj, m.f_a_proj, m.f_b_proj, m.b_proj, m.g_proj):
+                nn.init.uniform_(proj.weight, -s, s, generator=generator)
+            for conv in (m.q_conv1d, m.k_conv1d, m.v_conv1d):
+                nn.init.uniform_(conv.weight, -s, s, generator=generator)
+            nn.init.zeros_(m.A_log)
+            dt = torch.exp(torch.rand(m.dt_bias.shape, generator=generator, device=m.dt_bias.device)
+                           * (math.log(0.1) - math.log(0.001)) + math.log(0.001)).clamp(min=1e-4)
+            m.dt_bias.copy_(dt + torch.log(-torch.expm1(-dt)))
+            nn.init.ones_(m.o_norm.weight)
+            nn.init.zeros_(m.o_proj.weight)
+            nn.init.uniform_(block.mlp.c_fc.weight, -s * 0.4, s * 0.4, generator=generator)
+            nn.init.zeros_(block.mlp.c_proj.weight)
+        n = self.config.n_layer
+        for i in range(n):
+            self.resid_lambdas[i] = 1.15 - 0.10 * i / max(n - 1, 1)
+            self.x0_lambdas[i] = 0.20 - 0.15 * i / max(n - 1, 1)
+        nn.init.zeros_(self.smear_lambda)
+        nn.init.constant_(self.backout_lambda, 0.2)
+        nn.init.uniform_(self.smear_gate.weight, 0.0, 0.02, generator=generator)
+        self.transformer.wte.to(dtype=torch.bfloat16)
+
+    def forward(self, idx, targets=None):
+        x = norm(self.transformer.wte(idx).to(torch.bfloat16))
+        gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, 1:, :24]))
+        x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
+        x0 = x
+        backout_layer = self.config.n_layer // 2
+        x_backout = None
+        for i, block in enumerate(self.transformer.h):
+            x = self.resid_lambdas[i] * x + self.x0_lambdas[i] * x0
+            x = block(x.to(torch.bfloat16))
+            if i == backout_layer:
+                x_backout = x
+        if x_backout is not None:
+            x = x - self.backout_lambda.to(x.dtype) * x_backout
+        x = norm(x)
+        logits = self.lm_head(x)[..., : self.config.vocab_size].float()
+        logits = 15 * torch.tanh(logits / 15)
+        if targets is None:
+            return logits
+        return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1), ignore_index=-1)
+
+
+def make_optimizer(model: GPT, lr: float = 3e-3):
+    """AdamW over all parameters (the reference uses MuonAdamW, nanochat/optim.py; the
+    optimizer is outside the KDA path and only has to run every update)."""
+    return torch.optim.AdamW(model.parameters(), lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0,
+                             fused=True)
