@@ -166,6 +166,74 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42):
             "optimizer": "AdamW", "reference_gb10_tok_per_s": 44942}
 
 
+def graph_time_us(torch, fn, n=50, reps=5):
+    """Per-call GPU time of fn (microseconds): n calls captured in one HIP graph, replayed
+    between events, so host launch overhead is excluded."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(n):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (n * reps)
+
+
+def hbm_kernels(torch):
+    """Conv+SiLU, RMSNorm*gate (config 2 shapes) and the decode step (config 3): per-call
+    time, compulsory HBM bytes and the fraction of the 8 TB/s HBM peak."""
+    from experiment_swa_kda_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(42)
+    out = {}
+
+    def rec(name, us, nbytes):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_per_s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+
+    B, T, C, W = 2, 4096, 384, 4
+    x = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
+    w = torch.randn(C, W, device="cuda", generator=g).bfloat16()
+    dy = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
+    rec("conv_fwd", graph_time_us(torch, lambda: ops.causal_conv_forward(x, w, None, False)), 2 * x.numel() * 2)
+    rec("conv_bwd", graph_time_us(torch, lambda: ops.causal_conv_backward(x, w, None, dy, None)), 3 * x.numel() * 2)
+    o = torch.randn(B, T, 3, 128, device="cuda", generator=g).bfloat16()
+    gt = torch.randn(B, T, 3, 128, device="cuda", generator=g).bfloat16()
+    nw = torch.ones(128, device="cuda")
+    _, inv = ops.rmsnorm_gate_forward(o, gt, nw, 1e-5)
+    rows = B * T * 3
+    rec("norm_gate_fwd", graph_time_us(torch, lambda: ops.rmsnorm_gate_forward(o, gt, nw, 1e-5)),
+        3 * o.numel() * 2 + rows * 4)
+    rec("norm_gate_bwd", graph_time_us(torch, lambda: ops.rmsnorm_gate_backward(o, gt, nw, inv, dy.view_as(o), 1e-5)),
+        5 * o.numel() * 2 + rows * 4)
+    # decode (config 3): B64 H3 D128, f32 state updated in place
+    Bd, H, D = 64, 3, 128
+    q, k, raw = (torch.randn(Bd, 1, H, D, device="cuda", generator=g).bfloat16() for _ in range(3))
+    v = torch.randn(Bd, 1, H, D, device="cuda", generator=g).bfloat16()
+    bl = torch.randn(Bd, 1, H, device="cuda", generator=g).bfloat16()
+    A_log = torch.zeros(H, device="cuda")
+    dt = torch.zeros(H * D, device="cuda")
+    state = torch.randn(Bd, H, D, D, device="cuda", generator=g) * 0.05
+    us = graph_time_us(torch, lambda: ops.recurrent_decode(q, k, v, raw, bl, A_log, dt, state, True, -5.0,
+                                                           D ** -0.5, out_state=state), n=256, reps=3)
+    rec("decode_step", us, 2 * state.numel() * 4 + (4 * q.numel() + bl.numel()) * 2)
+    out["decode_step"]["config"] = "config3: B64 H3 D128, one token per step, 256 steps in one graph, state in place"
+    return out
+
+
 def cpu_baseline(sample_len):
     """The reference's eager f32 CPU path (restated in oracle/reference_path.py), fwd+bwd."""
     import torch
@@ -249,6 +317,7 @@ def main():
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": None},
         "reference_gb10_ms_fwd_bwd": 3.916,
     }
+    line["hbm_kernels"] = hbm_kernels(torch)
     if not args.no_train:
         line["train_6layer"] = train_throughput(torch)
     if not args.no_cpu_baseline:

@@ -6,27 +6,39 @@
 // including the current token):  pre[t] = sum_j xp[t + j] * w[j],  y = silu(pre),
 // final_state = xp[T-1 .. T+W-2].
 //
-// HBM-bound.  One thread owns 8 consecutive channels (one 16-byte bf16x8 vector) and a
-// tile of kTile tokens; adjacent threads own adjacent channel groups so each token row
-// [C] bf16 is read with fully coalesced 16-byte loads.  The W-1 token halo is re-read
-// from L2.  Arithmetic is f32; products are not rounded to bf16 before accumulation.
-// The weight gradient is written as per-tile partials and summed over tiles in a fixed
-// order (deterministic, no atomics).
+// HBM-bound.  A thread owns 8 consecutive channels (one 16-byte bf16x8 vector) and
+// kTok consecutive tokens; a 256-thread workgroup covers kGroups channel groups x
+// kSlices token slices, so adjacent lanes read adjacent 16-byte vectors of a token row.
+// The W-1 token halo is re-read through L1/L2.  Arithmetic is f32 (products are not
+// rounded to bf16 before accumulation).  The weight gradient is reduced inside the
+// workgroup through LDS, written as one partial per workgroup and summed over
+// workgroups in a fixed order (deterministic, no atomics).
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
 namespace kda {
 
-constexpr int kConvTile = 16;  // tokens per thread
+constexpr int kTok = 4;       // tokens per thread
+constexpr int kGroups = 8;    // channel groups (of 8 channels) per workgroup
+constexpr int kSlices = 32;   // token slices per workgroup (256 threads)
+constexpr int kBlockTok = kTok * kSlices;
+
+struct ConvGeom {
+  int B, T, C, CG, ncb, ntb;  // channel groups, channel blocks, token blocks
+  __host__ __device__ ConvGeom(int B_, int T_, int C_)
+      : B(B_), T(T_), C(C_), CG(C_ / 8), ncb((C_ / 8 + kGroups - 1) / kGroups),
+        ntb((T_ + kBlockTok - 1) / kBlockTok) {}
+  __host__ __device__ int blocks() const { return B * ntb * ncb; }
+};
 
 template <int W>
 __device__ __forceinline__ void load_xp8(const bf16* __restrict__ x, const bf16* __restrict__ st,
                                          int b, int T, int C, int c0, int p, float* out) {
   // xp[p] for 8 channels: p >= W-1 -> x[p-(W-1)], else state[.., p+1]
   const int t = p - (W - 1);
-  if (t >= 0) {
+  if (t >= 0 && t < T) {
     load8(x + ((size_t)b * T + t) * C + c0, out);
-  } else if (st) {
+  } else if (t < 0 && st) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[e] = to_f32(st[((size_t)b * C + c0 + e) * W + p + 1]);
   } else {
@@ -35,44 +47,41 @@ __device__ __forceinline__ void load_xp8(const bf16* __restrict__ x, const bf16*
   }
 }
 
+__device__ __forceinline__ float silu_grad(float pre) {
+  float s = sigmoid_acc(pre);
+  return s * (1.f + pre * (1.f - s));
+}
+
 template <int W>
-__global__ __launch_bounds__(256) void conv_fwd_kernel(int B, int T, int C,
-                                                       const bf16* __restrict__ x,
+__global__ __launch_bounds__(256) void conv_fwd_kernel(ConvGeom g, const bf16* __restrict__ x,
                                                        const bf16* __restrict__ w,
                                                        const bf16* __restrict__ st,
                                                        bf16* __restrict__ y) {
-  const int CG = C / 8;
-  const int NTB = (T + kConvTile - 1) / kConvTile;
-  const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= (long)B * NTB * CG) return;
-  const int cg = item % CG;
-  const int tb = (item / CG) % NTB;
-  const int b = item / ((long)CG * NTB);
-  const int c0 = cg * 8, t0 = tb * kConvTile;
+  const int cb = blockIdx.x % g.ncb, tb = (blockIdx.x / g.ncb) % g.ntb, b = blockIdx.x / (g.ncb * g.ntb);
+  const int cg = cb * kGroups + threadIdx.x % kGroups;
+  const int t0 = tb * kBlockTok + (threadIdx.x / kGroups) * kTok;
+  if (cg >= g.CG || t0 >= g.T) return;
+  const int c0 = cg * 8;
   float wt[8][W];
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int j = 0; j < W; ++j) wt[e][j] = to_f32(w[(c0 + e) * W + j]);
-  float win[W][8];  // win[j] = xp[t + j] for the current t
+  float xp[kTok + W - 1][8];  // xp[t0 .. t0+kTok+W-2]
 #pragma unroll
-  for (int j = 0; j < W - 1; ++j) load_xp8<W>(x, st, b, T, C, c0, t0 + j, win[j]);
-  const int t1 = min(T, t0 + kConvTile);
-  for (int t = t0; t < t1; ++t) {
-    load8(x + ((size_t)b * T + t) * C + c0, win[W - 1]);
+  for (int i = 0; i < kTok + W - 1; ++i) load_xp8<W>(x, st, b, g.T, g.C, c0, t0 + i, xp[i]);
+#pragma unroll
+  for (int u = 0; u < kTok; ++u) {
+    if (t0 + u >= g.T) break;
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float pre = 0.f;
 #pragma unroll
-      for (int j = 0; j < W; ++j) pre = fmaf(win[j][e], wt[e][j], pre);
+      for (int j = 0; j < W; ++j) pre = fmaf(xp[u + j][e], wt[e][j], pre);
       o[e] = pre * sigmoid_acc(pre);
     }
-    store8(y + ((size_t)b * T + t) * C + c0, o);
-#pragma unroll
-    for (int j = 0; j < W - 1; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+    store8(y + ((size_t)b * g.T + t0 + u) * g.C + c0, o);
   }
 }
 
@@ -94,123 +103,118 @@ __global__ void conv_final_state_kernel(int B, int T, int C, const bf16* __restr
   fin[i] = to_bf16(val);
 }
 
-__device__ __forceinline__ float silu_grad(float pre) {
-  float s = sigmoid_acc(pre);
-  return s * (1.f + pre * (1.f - s));
-}
-
+// dx[t] = sum_j dpre[t + W-1-j] w[j] (+ grad of the final state); dpre = dy * silu'(pre).
+// dweight[c][j] = sum_t dpre[t] xp[t + j]: per-thread sums over its kTok tokens, reduced
+// over the workgroup's token slices in LDS, one partial per workgroup.
 template <int W>
-__global__ __launch_bounds__(256) void conv_bwd_kernel(int B, int T, int C,
-                                                       const bf16* __restrict__ x,
+__global__ __launch_bounds__(256) void conv_bwd_kernel(ConvGeom g, const bf16* __restrict__ x,
                                                        const bf16* __restrict__ w,
                                                        const bf16* __restrict__ st,
                                                        const bf16* __restrict__ dy,
                                                        const bf16* __restrict__ dfin,
                                                        bf16* __restrict__ dx,
                                                        float* __restrict__ dw_part) {
-  const int CG = C / 8;
-  const int NTB = (T + kConvTile - 1) / kConvTile;
-  const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= (long)B * NTB * CG) return;
-  const int cg = item % CG;
-  const int tb = (item / CG) % NTB;
-  const int b = item / ((long)CG * NTB);
-  const int c0 = cg * 8, t0 = tb * kConvTile;
-  float wt[8][W];
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-#pragma unroll
-    for (int j = 0; j < W; ++j) wt[e][j] = to_f32(w[(c0 + e) * W + j]);
+  __shared__ float s_dw[256 / kWave][kGroups * 8 * W];
+  const int cb = blockIdx.x % g.ncb, tb = (blockIdx.x / g.ncb) % g.ntb, b = blockIdx.x / (g.ncb * g.ntb);
+  const int lg = threadIdx.x % kGroups, slice = threadIdx.x / kGroups;
+  const int cg = cb * kGroups + lg;
+  const int t0 = tb * kBlockTok + slice * kTok;
   float dwacc[8][W];
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int j = 0; j < W; ++j) dwacc[e][j] = 0.f;
-
-  // dp[j] = dpre[t + j] for the current t (j = 0..W-1); win[j] = xp[s + j] for s = t+W-1
-  float dp[W][8];
-  float win[W][8];
+  if (cg < g.CG && t0 < g.T) {
+    const int c0 = cg * 8;
+    float wt[8][W];
 #pragma unroll
-  for (int j = 0; j < W; ++j)
+    for (int e = 0; e < 8; ++e)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dp[j][e] = 0.f;
-  // prime: dpre for tokens t0 .. t0+W-2
+      for (int j = 0; j < W; ++j) wt[e][j] = to_f32(w[(c0 + e) * W + j]);
+    // dpre for tokens t0 .. t0+kTok+W-2 needs xp[t0 .. t0+kTok+2W-3]
+    constexpr int NP = kTok + W - 1;
+    float xp[NP + W - 1][8];
 #pragma unroll
-  for (int j = 0; j < W - 1; ++j) load_xp8<W>(x, st, b, T, C, c0, t0 + j, win[j]);
-  const int t1 = min(T, t0 + kConvTile);
-  // helper computing dpre at token s given win holding xp[s .. s+W-1]
-  auto dpre_at = [&](int s, float* out) {
-    if (s >= T) {
+    for (int i = 0; i < NP + W - 1; ++i) load_xp8<W>(x, st, b, g.T, g.C, c0, t0 + i, xp[i]);
+    float dp[NP][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = 0.f;
-      return;
+    for (int i = 0; i < NP; ++i) {
+      const int s = t0 + i;
+      if (s < g.T) {
+        float gy[8];
+        load8(dy + ((size_t)b * g.T + s) * g.C + c0, gy);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float pre = 0.f;
+#pragma unroll
+          for (int j = 0; j < W; ++j) pre = fmaf(xp[i + j][e], wt[e][j], pre);
+          dp[i][e] = gy[e] * silu_grad(pre);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dp[i][e] = 0.f;
+      }
     }
-    float g[8];
-    load8(dy + ((size_t)b * T + s) * C + c0, g);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float pre = 0.f;
-#pragma unroll
-      for (int j = 0; j < W; ++j) pre = fmaf(win[j][e], wt[e][j], pre);
-      out[e] = g[e] * silu_grad(pre);
-    }
-  };
-  // Walk s from t0 to t1+W-2 computing dpre[s]; win slides over xp.
-  // dx[t] = sum_j dpre[t+W-1-j] w[j]  (+ grad of final state)
-  for (int s = t0; s < t1 + W - 1; ++s) {
-    // load xp[s + W - 1]
-    if (s < T)
-      load8(x + ((size_t)b * T + s) * C + c0, win[W - 1]);
-    // dpre at s (zero beyond T)
-    float cur[8];
-    dpre_at(s, cur);
-    if (s < t1) {
+    for (int u = 0; u < kTok; ++u) {
+      const int t = t0 + u;
+      if (t >= g.T) break;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int j = 0; j < W; ++j) dwacc[e][j] = fmaf(cur[e], win[j][e], dwacc[e][j]);
-    }
-    // shift dp: dp[j] holds dpre[s - (W-1) + j]
-#pragma unroll
-    for (int j = 0; j < W - 1; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dp[j][e] = dp[j + 1][e];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dp[W - 1][e] = cur[e];
-    const int t = s - (W - 1);
-    if (t >= t0) {
+        for (int j = 0; j < W; ++j) dwacc[e][j] = fmaf(dp[u][e], xp[u + j][e], dwacc[e][j]);
       float o[8];
-      const int jf = t + W - T;  // final-state slot fed by xp[t+W-1]
+      const int jf = t + W - g.T;  // final-state slot fed by xp[t+W-1]
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < W; ++j) acc = fmaf(dp[W - 1 - j][e], wt[e][j], acc);
-        if (dfin && jf >= 0 && jf < W) acc += to_f32(dfin[((size_t)b * C + c0 + e) * W + jf]);
+        for (int j = 0; j < W; ++j) acc = fmaf(dp[u + W - 1 - j][e], wt[e][j], acc);
+        if (dfin && jf >= 0 && jf < W) acc += to_f32(dfin[((size_t)b * g.C + c0 + e) * W + jf]);
         o[e] = acc;
       }
-      store8(dx + ((size_t)b * T + t) * C + c0, o);
+      store8(dx + ((size_t)b * g.T + t) * g.C + c0, o);
     }
-#pragma unroll
-    for (int j = 0; j < W - 1; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
   }
-  float* part = dw_part + ((size_t)b * NTB + tb) * C * W;
+  // reduce the 8 token slices of each wave with shuffles, then the 4 waves through LDS
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
-    for (int j = 0; j < W; ++j) part[(c0 + e) * W + j] = dwacc[e][j];
+    for (int j = 0; j < W; ++j) {
+      float v = dwacc[e][j];
+      v += __shfl_xor(v, 8, kWave);
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      if (lane < kGroups) s_dw[wave][(lg * 8 + e) * W + j] = v;
+    }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kGroups * 8 * W; i += 256) {
+    float acc = 0.f;
+    for (int s = 0; s < 256 / kWave; ++s) acc += s_dw[s][i];
+    const int c = cb * kGroups * 8 + i / W;
+    if (c < g.C) dw_part[(size_t)(b * g.ntb + tb) * g.C * W + (size_t)c * W + i % W] = acc;
+  }
 }
 
-// dweight[c][j] = sum over (b, tile) of partials, fixed order.
-__global__ void conv_dw_reduce_kernel(int tiles, int CW, const float* __restrict__ part,
-                                      bf16* __restrict__ dw) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= CW) return;
+// dweight[c][j] = sum over (b, token block) partials.  Workgroup j owns 8 outputs; thread
+// (part, i) sums partials part, part + 32, ... in order, then the 32 part-sums are
+// combined in order through LDS (deterministic, no atomics).
+__global__ __launch_bounds__(256) void conv_dw_reduce_kernel(int tiles, int CW,
+                                                             const float* __restrict__ part,
+                                                             bf16* __restrict__ dw) {
+  __shared__ float s_red[32][8];
+  const int i = blockIdx.x * 8 + threadIdx.x % 8, q = threadIdx.x / 8;
   float acc = 0.f;
-  for (int t = 0; t < tiles; ++t) acc += part[(size_t)t * CW + i];
-  dw[i] = to_bf16(acc);
+  if (i < CW)
+    for (int t = q; t < tiles; t += 32) acc += part[(size_t)t * CW + i];
+  s_red[q][threadIdx.x % 8] = acc;
+  __syncthreads();
+  if (threadIdx.x < 8 && i < CW) {
+    float t = 0.f;
+    for (int k = 0; k < 32; ++k) t += s_red[k][threadIdx.x];
+    dw[i] = to_bf16(t);
+  }
 }
 
 // dstate[b][c][i] = dxp[i-1] for i >= 1 (0 for i = 0); dxp[p] = sum_j dpre[p-j] w[j]
@@ -260,11 +264,10 @@ __global__ void conv_dstate_kernel(int B, int T, int C, const bf16* __restrict__
 template <int W>
 static int conv_forward_w(int B, int T, int C, const void* x, const void* w, const void* st,
                           void* y, void* fin, hipStream_t stream) {
-  const int NTB = (T + kConvTile - 1) / kConvTile;
-  const long items = (long)B * NTB * (C / 8);
-  if (items > 0) {
-    hipLaunchKernelGGL(conv_fwd_kernel<W>, dim3((items + 255) / 256), dim3(256), 0, stream, B,
-                       T, C, (const bf16*)x, (const bf16*)w, (const bf16*)st, (bf16*)y);
+  const ConvGeom g(B, T, C);
+  if (T > 0 && B > 0) {
+    hipLaunchKernelGGL(conv_fwd_kernel<W>, dim3(g.blocks()), dim3(256), 0, stream, g,
+                       (const bf16*)x, (const bf16*)w, (const bf16*)st, (bf16*)y);
     KDA_LAUNCH_CHECK("causal_conv_forward");
   }
   if (fin) {
@@ -280,18 +283,18 @@ template <int W>
 static int conv_backward_w(int B, int T, int C, const void* x, const void* w, const void* st,
                            const void* dy, const void* dfin, void* dx, void* dw, void* dst,
                            void* scratch, hipStream_t stream) {
-  const int NTB = (T + kConvTile - 1) / kConvTile;
-  const long items = (long)B * NTB * (C / 8);
+  const ConvGeom g(B, T, C);
   float* part = (float*)scratch;
-  if (items > 0) {
-    hipLaunchKernelGGL(conv_bwd_kernel<W>, dim3((items + 255) / 256), dim3(256), 0, stream, B, T,
-                       C, (const bf16*)x, (const bf16*)w, (const bf16*)st, (const bf16*)dy,
+  const int tiles = B * g.ntb;
+  if (T > 0 && B > 0) {
+    hipLaunchKernelGGL(conv_bwd_kernel<W>, dim3(g.blocks()), dim3(256), 0, stream, g,
+                       (const bf16*)x, (const bf16*)w, (const bf16*)st, (const bf16*)dy,
                        (const bf16*)dfin, (bf16*)dx, part);
     KDA_LAUNCH_CHECK("causal_conv_backward");
   }
   const int CW = C * W;
-  hipLaunchKernelGGL(conv_dw_reduce_kernel, dim3((CW + 255) / 256), dim3(256), 0, stream,
-                     B * NTB, CW, (const float*)part, (bf16*)dw);
+  hipLaunchKernelGGL(conv_dw_reduce_kernel, dim3((CW + 7) / 8), dim3(256), 0, stream,
+                     (T > 0 && B > 0) ? tiles : 0, CW, (const float*)part, (bf16*)dw);
   KDA_LAUNCH_CHECK("causal_conv_dweight_reduce");
   if (dst) {
     const long n = (long)B * C;
@@ -335,8 +338,8 @@ extern "C" int kda_causal_conv_forward(int32_t batch, int32_t seq_len, int32_t c
 
 extern "C" size_t kda_causal_conv_backward_scratch_bytes(int32_t batch, int32_t seq_len,
                                                          int32_t channels, int32_t width) {
-  const size_t ntb = (size_t)(seq_len + kda::kConvTile - 1) / kda::kConvTile;
-  return kda::align256((size_t)batch * ntb * channels * width * sizeof(float)) + 256;
+  const kda::ConvGeom g(batch, seq_len, channels);
+  return kda::align256((size_t)batch * g.ntb * channels * width * sizeof(float)) + 256;
 }
 
 extern "C" int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t channels,

@@ -23,12 +23,27 @@ __global__ __launch_bounds__(256) void decode_kernel(
     float* final_state) {
   constexpr int LPR = K / 4;          // lanes per V row
   constexpr int RPP = kWave / LPR;    // rows per wave pass
+  constexpr int NPASS = kDecodeRowsPerBlock / (4 * RPP);  // rows per thread
   __shared__ float s_q[K], s_kd[K], s_k[K], s_eg[K];
   __shared__ float s_beta;
   const int bh = blockIdx.x;
   const int h = bh % heads;
   const int tid = threadIdx.x;
   const size_t tok = (size_t)bh;  // [B,1,H,*] flattened: (b*H + h)
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int sub = lane / LPR, kl = lane % LPR;
+  const int k0 = kl * 4;
+  const int row_base = blockIdx.y * kDecodeRowsPerBlock;
+
+  // issue the state loads first: they are independent of the per-key prologue
+  float4 sv4[NPASS];
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int row = row_base + ps * 4 * RPP + wave * RPP + sub;
+    const size_t off = ((size_t)bh * V + row) * K + k0;
+    sv4[ps] = (initial_state && row < V) ? *reinterpret_cast<const float4*>(initial_state + off)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 
   if (tid < kWave) {
     // wave 0 prepares the per-key quantities (K <= 128 -> two keys per lane)
@@ -68,9 +83,6 @@ __global__ __launch_bounds__(256) void decode_kernel(
   }
   __syncthreads();
 
-  const int wave = tid / kWave, lane = tid % kWave;
-  const int sub = lane / LPR, kl = lane % LPR;
-  const int k0 = kl * 4;
   const float beta = s_beta;
   float qk[4], kk[4], kd[4], eg[4];
 #pragma unroll
@@ -80,19 +92,16 @@ __global__ __launch_bounds__(256) void decode_kernel(
     kd[e] = s_kd[k0 + e];
     eg[e] = s_eg[k0 + e];
   }
-  const int row_base = blockIdx.y * kDecodeRowsPerBlock;
-  for (int rr = wave * RPP + sub; rr < kDecodeRowsPerBlock; rr += 4 * RPP) {
-    const int row = row_base + rr;
-    if (row >= V) break;
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int row = row_base + ps * 4 * RPP + wave * RPP + sub;
     const size_t off = ((size_t)bh * V + row) * K + k0;
-    float4 s = initial_state ? *reinterpret_cast<const float4*>(initial_state + off)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-    float sv[4] = {s.x, s.y, s.z, s.w};
+    float sv[4] = {sv4[ps].x, sv4[ps].y, sv4[ps].z, sv4[ps].w};
     float pred = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) pred += kd[e] * sv[e];
     pred = group_sum<LPR>(pred);
-    const float r = to_f32(v[tok * V + row]) - pred;
+    const float r = (row < V ? to_f32(v[tok * V + row]) : 0.f) - pred;
     float o = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -100,9 +109,11 @@ __global__ __launch_bounds__(256) void decode_kernel(
       o += qk[e] * sv[e];
     }
     o = group_sum<LPR>(o);
-    if (final_state)
-      *reinterpret_cast<float4*>(final_state + off) = make_float4(sv[0], sv[1], sv[2], sv[3]);
-    if (kl == 0) out[tok * V + row] = to_bf16(o);
+    if (row < V) {
+      if (final_state)
+        *reinterpret_cast<float4*>(final_state + off) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      if (kl == 0) out[tok * V + row] = to_bf16(o);
+    }
   }
 }
 

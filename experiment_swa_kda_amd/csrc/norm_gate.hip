@@ -12,7 +12,7 @@
 
 namespace kda {
 
-constexpr int kNormBlocksMax = 2048;
+constexpr int kNormBlocksMax = 512;
 
 template <int D>
 __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf16* __restrict__ x,
@@ -93,13 +93,25 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
   }
 }
 
-__global__ void norm_dw_reduce_kernel(int blocks, int D, const float* __restrict__ part,
-                                      float* __restrict__ dw) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= D) return;
+// dweight[c] = sum over workgroup partials.  Workgroup j owns 8 channels; thread
+// (part, c) sums partials part, part + 32, ... in order and the 32 part-sums are combined
+// in order through LDS (deterministic, no atomics).
+constexpr int kRedParts = 32;
+__global__ __launch_bounds__(256) void norm_dw_reduce_kernel(int blocks, int D,
+                                                             const float* __restrict__ part,
+                                                             float* __restrict__ dw) {
+  __shared__ float s_red[kRedParts][8];
+  const int c = blockIdx.x * 8 + threadIdx.x % 8, q = threadIdx.x / 8;
   float acc = 0.f;
-  for (int b = 0; b < blocks; ++b) acc += part[(size_t)b * D + c];
-  dw[c] = acc;
+  if (c < D)
+    for (int b = q; b < blocks; b += kRedParts) acc += part[(size_t)b * D + c];
+  s_red[q][threadIdx.x % 8] = acc;
+  __syncthreads();
+  if (threadIdx.x < 8 && c < D) {
+    float t = 0.f;
+    for (int k = 0; k < kRedParts; ++k) t += s_red[k][threadIdx.x];
+    dw[c] = t;
+  }
 }
 
 static int norm_blocks(long rows, int dim) {
@@ -162,7 +174,7 @@ extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* 
                          (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, part);
     KDA_LAUNCH_CHECK("rmsnorm_gate_backward");
   }
-  hipLaunchKernelGGL(norm_dw_reduce_kernel, dim3(1), dim3(128), 0, stream, rows > 0 ? nb : 0, dim,
+  hipLaunchKernelGGL(norm_dw_reduce_kernel, dim3((dim + 7) / 8), dim3(256), 0, stream, rows > 0 ? nb : 0, dim,
                      (const float*)part, dweight);
   KDA_LAUNCH_CHECK("rmsnorm_gate_dweight_reduce");
   return KDA_OK;
