@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run each kernel once (plus a 64 MiB calibration copy) for rocprofv3 --pmc; no timing")
     ap.add_argument("--cpu-sample-len", type=int, default=1024,
                     help="T of the CPU baseline sample (extrapolated linearly to T=4096)")
     return ap.parse_args()
@@ -166,6 +168,19 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42):
             "optimizer": "AdamW", "reference_gb10_tok_per_s": 44942}
 
 
+def load_traffic():
+    """HBM bytes per dispatch from the committed rocprofv3 --pmc summary, or {}."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_config2.txt")
+    out = {}
+    if os.path.exists(path):
+        for line in open(path):
+            if line.startswith("#") or not line.strip():
+                continue
+            name, fb, wb = line.split()[:3]
+            out[name] = int(fb) + int(wb)
+    return out
+
+
 def graph_time_us(torch, fn, n=50, reps=5):
     """Per-call GPU time of fn (microseconds): n calls captured in one HIP graph, replayed
     between events, so host launch overhead is excluded."""
@@ -252,6 +267,36 @@ def cpu_baseline(sample_len):
                       f"extrapolated linearly to T=4096"}
 
 
+def pmc_workload(torch):
+    """One launch of every kernel of the path at config 2/3 shapes, preceded by a copy of
+    known size (64 MiB read + 64 MiB written) that calibrates FETCH_SIZE / WRITE_SIZE."""
+    from experiment_swa_kda_amd import kda, ops
+
+    src = torch.ones(32 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    t, do = make_inputs(torch, gate="precomputed")
+    out, _ = kda(t["q"], t["k"], t["v"], t["g"], t["beta"], t["A_log"], t["dt_bias"], mode="project_chunk",
+                 gate="precomputed", allow_fallback=False)
+    out.backward(do)
+    torch.cuda.synchronize()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x, dy, gt = (torch.randn(2, 4096, 384, device="cuda", generator=g).bfloat16() for _ in range(3))
+    w = torch.randn(384, 4, device="cuda", generator=g).bfloat16()
+    ops.causal_conv_forward(x, w, None, False)
+    ops.causal_conv_backward(x, w, None, dy, None)
+    o, gto, dyo = (t.view(2, 4096, 3, 128) for t in (x, gt, dy))
+    _, inv = ops.rmsnorm_gate_forward(o, gto, torch.ones(128, device="cuda"), 1e-5)
+    ops.rmsnorm_gate_backward(o, gto, torch.ones(128, device="cuda"), inv, dyo, 1e-5)
+    q = torch.randn(64, 1, 3, 128, device="cuda", generator=g).bfloat16()
+    st = torch.randn(64, 3, 128, 128, device="cuda", generator=g)
+    ops.recurrent_decode(q, q, q, q, q[..., 0], torch.zeros(3, device="cuda"), torch.zeros(384, device="cuda"),
+                         st, True, -5.0, 128 ** -0.5, out_state=st)
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -262,6 +307,9 @@ def main():
 
     from experiment_swa_kda_amd import kda
 
+    if args.pmc_workload:
+        pmc_workload(torch)
+        return
     B, T, H, K, V = 2, 4096, 3, 128, 128
     tiles = B * (T // 64) * H
     flop = 3 * tiles * FWD_FLOP_PER_TILE  # fwd + bwd (bwd := 2 x fwd)
@@ -289,6 +337,7 @@ def main():
 
     ms, ms_fwd, t, do = results["precomputed"]
     kt = kernel_times(torch, t, do, "precomputed")
+    traffic = load_traffic()
     dom = max(kt, key=kt.get)
     achieved = tiles * KERNEL_FLOP_PER_TILE[dom] / (kt[dom] * 1e-3) / 1e12
     line = {
@@ -314,7 +363,8 @@ def main():
         "kernel_ms": {n: round(v, 4) for n, v in kt.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom)},
+        "hbm_traffic_bytes": traffic or None,
         "reference_gb10_ms_fwd_bwd": 3.916,
     }
     line["hbm_kernels"] = hbm_kernels(torch)
