@@ -110,22 +110,22 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
     const int row0 = seq_row0 + (chunk - sq.x) * 64;
     const int len = min(64, seq_end - row0);
     const size_t tile = (size_t)chunk * H + h;
-    const bf16* AT = (const bf16*)a.ws.p[R_AT] + tile * 64 * 64;
-    const bf16* KD = (const bf16*)a.ws.p[R_KD] + tile * 64 * K;
-    const bf16* QGT = (const bf16*)a.ws.p[R_QGT] + tile * K * 64;
-    const bf16* WT = (const bf16*)a.ws.p[R_WT] + tile * K * 64;
+    const bf16* ATF = (const bf16*)a.ws.p[R_ATF] + tile * 64 * 64;
+    const bf16* KDF = (const bf16*)a.ws.p[R_KDF] + tile * 64 * K;
+    const bf16* QGTF = (const bf16*)a.ws.p[R_QGTF] + tile * K * 64;
+    const bf16* WTF = (const bf16*)a.ws.p[R_WTF] + tile * K * 64;
     const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) f.at[s] = *(const bf16x8*)(AT + j * 64 + 32 * s + 8 * kg);
+    for (int s = 0; s < 2; ++s) f.at[s] = *(const bf16x8*)(ATF + frag_off(64, wave, s, lane));
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) f.kd[s] = *(const bf16x8*)(KD + j * K + 32 * s + 8 * kg);
+    for (int s = 0; s < K / 32; ++s) f.kd[s] = *(const bf16x8*)(KDF + frag_off(K, wave, s, lane));
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int kb = 16 * (wave * KT + kt);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        f.qgt[kt][s] = *(const bf16x8*)(QGT + (kb + lr) * 64 + 32 * s + 8 * kg);
-        f.wt[kt][s] = *(const bf16x8*)(WT + (kb + lr) * 64 + 32 * s + 8 * kg);
+        f.qgt[kt][s] = *(const bf16x8*)(QGTF + frag_off(64, wave * KT + kt, s, lane));
+        f.wt[kt][s] = *(const bf16x8*)(WTF + frag_off(64, wave * KT + kt, s, lane));
       }
       f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
     }
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
   const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
-  const bf16* DLT = (const bf16*)a.ws.p[R_DLT] + tile * V * 64;
+  const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
   const float* DSH = (const float*)a.sc.p[S_DSH] + tile * K * V;
   const float* DDLT = (const float*)a.sc.p[S_DDLT] + tile * V * 64;
   float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
@@ -314,15 +314,21 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   for (int idx = tid; idx < V * 16; idx += kVjpThreads) {
     const int vv = idx / 16, t4 = (idx % 16) * 4;
     const float4 d = *(const float4*)(DDLT + (size_t)vv * 64 + t4);
-    const bf16x4 dl = *(const bf16x4*)(DLT + (size_t)vv * 64 + t4);
     const float dv[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bf16 hi = to_bf16(dv[e]);
       sDU[(t4 + e) * VP + vv] = hi;
       sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
-      sDL[(t4 + e) * VP + vv] = dl[e];
     }
+  }
+  // delta from its B-operand fragments [strip][2][64 lanes][8]: (t = 32 s + 8 (l/16) + e, v)
+  for (int idx = tid; idx < 64 * V / 8; idx += kVjpThreads) {
+    const int lane_ = idx % 64, sl = (idx / 64) % 2, strip = idx / 128;
+    const bf16x8 x = *(const bf16x8*)(DLF + (size_t)idx * 8);
+    const int vv = 16 * strip + lane_ % 16, t0 = 32 * sl + 8 * (lane_ / 16);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sDL[(t0 + e) * VP + vv] = x[e];
   }
   if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;

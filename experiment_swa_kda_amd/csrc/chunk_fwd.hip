@@ -95,7 +95,7 @@ __global__ void chunk_prep_kernel(int B, int T, int num_seqs, const int* __restr
 // ---------------------------------------------------------------------------
 template <int K, int V>
 struct IntraSmem {
-  static constexpr int KP = K + 4;  // f32 row stride (breaks power-of-two bank strides)
+  static constexpr int KP = K + 1;  // f32 row stride (odd: conflict-free column access)
   static constexpr int VP = V + 8;  // bf16 row stride
   static constexpr int MP = 65;
   static constexpr size_t off_q = 0;
@@ -107,8 +107,26 @@ struct IntraSmem {
   static constexpr size_t off_v = off_x + 3 * 16 * 17 * 4;
   static constexpr size_t off_b = off_v + 64 * VP * 2;
   static constexpr size_t off_f = off_b + 64 * 4;
-  static constexpr size_t bytes = off_f + 16;
+  static constexpr size_t off_as = off_f + 16;                 // bf16 [64][AP] A staging
+  static constexpr int AP = 64 + 8;
+  static constexpr size_t bytes = off_as + 64 * AP * 2;
+  // W staging (bf16 [64][K + 8]) reuses the q_hat region once Qg has been emitted
+  static_assert(64 * (K + 8) * 2 <= 64 * KP * 4, "W staging must fit the q_hat region");
 };
+
+// Writes the MFMA A-operand fragments of an R x C matrix whose element (r, c) is val(r, c)
+// (see frag_off); one 16-byte piece per thread iteration, contiguous across threads.
+template <int R, int C, int NT, typename F>
+__device__ __forceinline__ void emit_frags(bf16* dst, int tid, F val) {
+  for (int idx = tid; idx < R * C / 8; idx += NT) {
+    const int lane = idx % 64, s = (idx / 64) % (C / 32), rt = idx / (64 * (C / 32));
+    const int r = 16 * rt + lane % 16, c0 = 32 * s + 8 * (lane / 16);
+    bf16x8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = val(r, c0 + e);
+    *(bf16x8*)(dst + (size_t)idx * 8) = x;
+  }
+}
 
 constexpr int kIntraThreads = 1024;
 constexpr int kIntraWaves = kIntraThreads / kWave;
@@ -130,6 +148,9 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
   bf16* sV = (bf16*)(smem + L::off_v);
   float* sB = (float*)(smem + L::off_b);
   int* sF = (int*)(smem + L::off_f);
+  bf16* sAs = (bf16*)(smem + L::off_as);
+  bf16* sWs = (bf16*)(smem + L::off_q);  // after Qg/Kd fragments are written
+  constexpr int AP = L::AP, WP = K + 8;
 
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
   const int len = ch.y;
@@ -229,8 +250,6 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
   __syncthreads();
 
   // ---- phase 2: A and M' (16x16 tiles of the lower triangle) ----
-  bf16* Aout = (bf16*)a.ws.p[R_A] + tile * 64 * 64;
-  bf16* ATout = (bf16*)a.ws.p[R_AT] + tile * 64 * 64;
   float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
   for (int p = wave; p < 10; p += kIntraWaves) {
     const int ba = kPairA[p], bb = kPairB[p];
@@ -279,8 +298,7 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
       const int ii = 16 * ba + 4 * kg + rr;
       const float av = jj <= ii ? accA[rr] : 0.f;
       const float mv = jj < ii ? accM[rr] : 0.f;
-      Aout[ii * 64 + jj] = to_bf16(av);
-      ATout[jj * 64 + ii] = to_bf16(av);
+      sAs[ii * AP + jj] = to_bf16(av);
       sM[ii * MP + jj] = mv;
       MPout[ii * 64 + jj] = mv;
     }
@@ -289,13 +307,34 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
   for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) {
     const int ii = idx / 64, jj = idx % 64;
     if (jj / 16 > ii / 16) {
-      Aout[ii * 64 + jj] = to_bf16(0.f);
-      ATout[jj * 64 + ii] = to_bf16(0.f);
+      sAs[ii * AP + jj] = to_bf16(0.f);
       sM[ii * MP + jj] = 0.f;
       MPout[ii * 64 + jj] = 0.f;
     }
   }
   __syncthreads();
+
+  // ---- A, Qg = qh exp(G), Kd = kh exp(G_last - G) as MFMA fragments (+ transposes) ----
+  {
+    constexpr int NT = kIntraThreads;
+    emit_frags<64, 64, NT>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
+                           [&](int r, int c) { return sAs[r * AP + c]; });
+    emit_frags<64, 64, NT>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
+                           [&](int r, int c) { return sAs[c * AP + r]; });
+    const float* gl = sG + 63 * KP;
+    emit_frags<64, K, NT>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid, [&](int r, int c) {
+      return to_bf16(sQ[r * KP + c] * expf(sG[r * KP + c]));
+    });
+    emit_frags<K, 64, NT>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid, [&](int r, int c) {
+      return to_bf16(sQ[c * KP + r] * expf(sG[c * KP + r]));
+    });
+    emit_frags<64, K, NT>((bf16*)a.ws.p[R_KDF] + tile * 64 * K, tid, [&](int r, int c) {
+      return to_bf16(sK[r * KP + c] * expf(gl[c] - sG[r * KP + c]));
+    });
+    emit_frags<K, 64, NT>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, [&](int r, int c) {
+      return to_bf16(sK[c * KP + r] * expf(gl[r] - sG[c * KP + r]));
+    });
+  }
 
   // ---- phase 3: T = (I + diag(beta) M')^-1, blocked forward substitution ----
   if (tid < 64) {
@@ -342,9 +381,7 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
 
   // ---- phase 4: U = T (beta v), W = T (beta kh exp(G)) ----
   {
-    bf16* UTout = (bf16*)a.ws.p[R_UT] + tile * V * 64;
-    bf16* Wout = (bf16*)a.ws.p[R_W] + tile * 64 * K;
-    bf16* WTout = (bf16*)a.ws.p[R_WT] + tile * K * 64;
+    bf16* Uout = (bf16*)a.ws.p[R_UF] + tile * 64 * V;
     constexpr int NU = 4 * (V / 16), NW = 4 * (K / 16);
     for (int p = wave; p < NU + NW; p += kIntraWaves) {
       const bool isU = p < NU;
@@ -366,54 +403,23 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
         acc = mfma16(fa, fb, acc);
       }
       if (isU) {
+        // C layout kept as is: [strip = ct][row tile][lane][4]
         bf16x4 x;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) x[rr] = to_bf16(acc[rr]);
-        *(bf16x4*)(UTout + col * 64 + 16 * rt + 4 * kg) = x;
+        *(bf16x4*)(Uout + ((size_t)(ct * 4 + rt) * 64 + lane) * 4) = x;
       } else {
-        bf16x4 x;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          x[rr] = to_bf16(acc[rr]);
-          Wout[(16 * rt + 4 * kg + rr) * K + col] = x[rr];
-        }
-        *(bf16x4*)(WTout + col * 64 + 16 * rt + 4 * kg) = x;
+        for (int rr = 0; rr < 4; ++rr) sWs[(16 * rt + 4 * kg + rr) * WP + col] = to_bf16(acc[rr]);
       }
     }
   }
+  __syncthreads();
+  emit_frags<64, K, kIntraThreads>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
+                                   [&](int r, int c) { return sWs[r * WP + c]; });
+  emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid,
+                                   [&](int r, int c) { return sWs[c * WP + r]; });
 
-  // ---- phase 5: Qg = qh exp(G), Kd = kh exp(G_last - G) and their transposes ----
-  {
-    bf16* QG = (bf16*)a.ws.p[R_QG] + tile * 64 * K;
-    bf16* KD = (bf16*)a.ws.p[R_KD] + tile * 64 * K;
-    bf16* QGT = (bf16*)a.ws.p[R_QGT] + tile * K * 64;
-    bf16* KDT = (bf16*)a.ws.p[R_KDT] + tile * K * 64;
-    for (int idx = tid; idx < 64 * (K / 8); idx += kIntraThreads) {
-      const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
-      float qg[8], kd[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float g = sG[t * KP + c0 + e];
-        qg[e] = sQ[t * KP + c0 + e] * expf(g);
-        kd[e] = sK[t * KP + c0 + e] * expf(sG[63 * KP + c0 + e] - g);
-      }
-      store8(QG + t * K + c0, qg);
-      store8(KD + t * K + c0, kd);
-    }
-    for (int idx = tid; idx < K * 8; idx += kIntraThreads) {
-      const int c = idx / 8, t0 = (idx % 8) * 8;
-      float qg[8], kd[8];
-      const float gl = sG[63 * KP + c];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float g = sG[(t0 + e) * KP + c];
-        qg[e] = sQ[(t0 + e) * KP + c] * expf(g);
-        kd[e] = sK[(t0 + e) * KP + c] * expf(gl - g);
-      }
-      store8(QGT + c * 64 + t0, qg);
-      store8(KDT + c * 64 + t0, kd);
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -430,7 +436,7 @@ constexpr int kFwdRing = 4;
 template <int K>
 struct FwdScanFrag {
   bf16x8 w[K / 32];      // W rows of this wave's delta tile
-  bf16x4 ut;             // U^T: 4 tokens of this lane's delta outputs
+  bf16x4 ut;             // U: the 4 entries of this lane's delta outputs (C layout)
   bf16x8 kdt[K / 64][2]; // Kd^T rows of this wave's state tiles
   float4 lam[K / 64];    // exp(G_last) of this lane's state rows
 };
@@ -455,18 +461,18 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
 
   auto load = [&](int chunk, FwdScanFrag<K>& f) {
     const size_t tile = (size_t)chunk * H + h;
-    const bf16* Wt = (const bf16*)a.ws.p[R_W] + tile * 64 * K;
-    const bf16* UT = (const bf16*)a.ws.p[R_UT] + tile * V * 64;
-    const bf16* KDT = (const bf16*)a.ws.p[R_KDT] + tile * K * 64;
+    const bf16* WF = (const bf16*)a.ws.p[R_WF] + tile * 64 * K;
+    const bf16* UF = (const bf16*)a.ws.p[R_UF] + tile * 64 * V;
+    const bf16* KDTF = (const bf16*)a.ws.p[R_KDTF] + tile * K * 64;
     const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) f.w[s] = *(const bf16x8*)(Wt + i * K + 32 * s + 8 * kg);
-    f.ut = *(const bf16x4*)(UT + (v0 + lr) * 64 + 16 * wave + 4 * kg);
+    for (int s = 0; s < K / 32; ++s) f.w[s] = *(const bf16x8*)(WF + frag_off(K, wave, s, lane));
+    f.ut = *(const bf16x4*)(UF + ((size_t)(strip * 4 + wave) * 64 + lane) * 4);
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int kb = 16 * (wave * KT + kt);
 #pragma unroll
-      for (int s = 0; s < 2; ++s) f.kdt[kt][s] = *(const bf16x8*)(KDT + (kb + lr) * 64 + 32 * s + 8 * kg);
+      for (int s = 0; s < 2; ++s) f.kdt[kt][s] = *(const bf16x8*)(KDTF + frag_off(64, wave * KT + kt, s, lane));
       f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
     }
   };
@@ -515,13 +521,12 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
         const int kk = idx / 4, q4 = (idx % 4) * 4;
         *(float4*)(SH + (size_t)kk * V + v0 + q4) = *(const float4*)(sSf + kk * FP + q4);
       }
-      bf16* SHB = (bf16*)a.ws.p[R_SHB] + tile * V * K;
-      constexpr int E = K / 16;  // bf16 per thread
-      const int vv = tid / (K / E), ke = (tid % (K / E)) * E;
-      if constexpr (E == 8) {
-        *(bf16x8*)(SHB + (size_t)(v0 + vv) * K + ke) = *(const bf16x8*)(sSp + vv * SP + ke);
-      } else {
-        *(bf16x4*)(SHB + (size_t)(v0 + vv) * K + ke) = *(const bf16x4*)(sSp + vv * SP + ke);
+      // bf16 state as B-operand fragments of this strip (read by the output kernel)
+      bf16* SHBF = (bf16*)a.ws.p[R_SHBF] + tile * V * K + (size_t)strip * 16 * K;
+      if (tid < 16 * K / 8) {
+        const int sl = tid / 64, ln = tid % 64;
+        *(bf16x8*)(SHBF + ((size_t)sl * 64 + ln) * 8) =
+            *(const bf16x8*)(sSp + (ln % 16) * SP + 32 * sl + 8 * (ln / 16));
       }
     }
     // (3) delta rows 16*wave.. = U - W S  (two accumulators halve the MFMA chain)
@@ -538,11 +543,12 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
       *(bf16x4*)(sD + lr * DP + 16 * wave + 4 * kg) = x;
     }
     __syncthreads();
-    // (3b) delta^T history [V][64]
-    {
-      bf16* DLT = (bf16*)a.ws.p[R_DLT] + tile * V * 64;
-      const int vv = tid / 16, t4 = (tid % 16) * 4;
-      *(bf16x4*)(DLT + (size_t)(v0 + vv) * 64 + t4) = *(const bf16x4*)(sD + vv * DP + t4);
+    // (3b) delta as B-operand fragments of this strip [2][64 lanes][8]
+    if (tid < 128) {
+      bf16* DLF = (bf16*)a.ws.p[R_DLF] + tile * 64 * V + (size_t)strip * 16 * 64;
+      const int sl = tid / 64, ln = tid % 64;
+      *(bf16x8*)(DLF + ((size_t)sl * 64 + ln) * 8) =
+          *(const bf16x8*)(sD + (ln % 16) * DP + 32 * sl + 8 * (ln / 16));
     }
     // (4) S <- lam S + Kd^T delta
 #pragma unroll
@@ -594,26 +600,28 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int i = 16 * wave + lr;
-  const bf16* QG = (const bf16*)a.ws.p[R_QG] + tile * 64 * K;
-  const bf16* AM = (const bf16*)a.ws.p[R_A] + tile * 64 * 64;
-  const bf16* SHB = (const bf16*)a.ws.p[R_SHB] + tile * V * K;
-  const bf16* DLT = (const bf16*)a.ws.p[R_DLT] + tile * V * 64;
+  const bf16* QGF = (const bf16*)a.ws.p[R_QGF] + tile * 64 * K;
+  const bf16* AF = (const bf16*)a.ws.p[R_AF] + tile * 64 * 64;
+  const bf16* SHBF = (const bf16*)a.ws.p[R_SHBF] + tile * V * K;
+  const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
   bf16x8 fq[K / 32], fa[2];
 #pragma unroll
-  for (int s = 0; s < K / 32; ++s) fq[s] = *(const bf16x8*)(QG + i * K + 32 * s + 8 * kg);
+  for (int s = 0; s < K / 32; ++s) fq[s] = *(const bf16x8*)(QGF + frag_off(K, wave, s, lane));
 #pragma unroll
-  for (int s = 0; s < 2; ++s) fa[s] = *(const bf16x8*)(AM + i * 64 + 32 * s + 8 * kg);
+  for (int s = 0; s < 2; ++s) fa[s] = *(const bf16x8*)(AF + frag_off(64, wave, s, lane));
 #pragma unroll 2
   for (int ct = 0; ct < V / 16; ++ct) {
     const int vcol = 16 * ct + lr;
+    const bf16* sb = SHBF + (size_t)ct * 16 * K;
+    const bf16* db = DLF + (size_t)ct * 16 * 64;
     f32x4 o0 = zero4(), o1 = zero4();
 #pragma unroll
     for (int s = 0; s < K / 32; s += 2) {
-      o0 = mfma16(fq[s], *(const bf16x8*)(SHB + (size_t)vcol * K + 32 * s + 8 * kg), o0);
-      o1 = mfma16(fq[s + 1], *(const bf16x8*)(SHB + (size_t)vcol * K + 32 * (s + 1) + 8 * kg), o1);
+      o0 = mfma16(fq[s], *(const bf16x8*)(sb + ((size_t)s * 64 + lane) * 8), o0);
+      o1 = mfma16(fq[s + 1], *(const bf16x8*)(sb + ((size_t)(s + 1) * 64 + lane) * 8), o1);
     }
-    o0 = mfma16(fa[0], *(const bf16x8*)(DLT + (size_t)vcol * 64 + 8 * kg), o0);
-    o1 = mfma16(fa[1], *(const bf16x8*)(DLT + (size_t)vcol * 64 + 32 + 8 * kg), o1);
+    o0 = mfma16(fa[0], *(const bf16x8*)(db + (size_t)lane * 8), o0);
+    o1 = mfma16(fa[1], *(const bf16x8*)(db + (size_t)(64 + lane) * 8), o1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * kg + r;

@@ -11,18 +11,27 @@
 
 namespace kda {
 
+// "Fragment-major" arrays hold a matrix in the exact order the MFMA A/B operand registers
+// of v_mfma_f32_16x16x32_bf16 consume it: for a row-major R x C matrix X, fragment
+// (rt, s) is the 16 x 32 block rows 16rt.., columns 32s..; lane l holds
+// X[16rt + l%16][32s + 8(l/16) + e], e = 0..7, and the 64 lanes' 16-byte pieces are
+// contiguous.  A wave loads one operand with one fully coalesced 1 KB access.
+__host__ __device__ inline size_t frag_off(int C, int rt, int s, int lane) {
+  return ((((size_t)rt * (C / 32) + s) * 64) + lane) * 8;
+}
+
 enum WsRegion {
   R_CHUNKS = 0,  // int4 [max_chunks]   {row0, len, seq, index_in_seq}
   R_SEQS,        // int2 [num_seqs]     {first_chunk, n_chunks}
-  R_QG,          // bf16 [tile][64][K]  q_hat * exp(G)              (q_hat includes the scale)
-  R_QGT,         // bf16 [tile][K][64]  transpose of R_QG
-  R_KD,          // bf16 [tile][64][K]  k_hat * exp(G_last - G)
-  R_KDT,         // bf16 [tile][K][64]  transpose of R_KD
-  R_W,           // bf16 [tile][64][K]  W = T (beta k_hat exp(G))
-  R_WT,          // bf16 [tile][K][64]  transpose of R_W
-  R_UT,          // bf16 [tile][V][64]  U^T, U = T (beta v)
-  R_A,           // bf16 [tile][64][64] A (lower, incl. diagonal)
-  R_AT,          // bf16 [tile][64][64] transpose of R_A
+  R_QGF,         // bf16 fragments of Qg = q_hat exp(G) (64 x K; q_hat includes the scale)
+  R_QGTF,        // bf16 fragments of Qg^T (K x 64)
+  R_KDF,         // bf16 fragments of Kd = k_hat exp(G_last - G) (64 x K)
+  R_KDTF,        // bf16 fragments of Kd^T (K x 64)
+  R_WF,          // bf16 fragments of W = T (beta k_hat exp(G)) (64 x K)
+  R_WTF,         // bf16 fragments of W^T (K x 64)
+  R_UF,          // bf16 U = T (beta v) in MFMA C layout: [V/16 strip][4 row tile][64 lane][4]
+  R_AF,          // bf16 fragments of A (64 x 64, lower incl. diagonal)
+  R_ATF,         // bf16 fragments of A^T
   R_T,           // f32  [tile][64][64] T = (I + diag(beta) M')^-1
   R_MP,          // f32  [tile][64][64] M' (strictly lower, without beta)
   R_G,           // f32  [tile][64][K]  G = inclusive cumsum of g in the chunk
@@ -31,8 +40,8 @@ enum WsRegion {
   R_RK,          // f32  [tile][64]     1 / max(||k||, 1e-12)
   R_BETA,        // f32  [tile][64]     sigmoid(beta_logits)
   R_SH,          // f32  [tile][K][V]   state entering the chunk (written by the scan)
-  R_SHB,         // bf16 [tile][V][K]   the same state as the bf16 MFMA operand of the scan
-  R_DLT,         // bf16 [tile][V][64]  delta^T, delta = U - W S (written by the scan)
+  R_SHBF,        // bf16 the same state as B-operand fragments [V/16 strip][K/32][64][8]
+  R_DLF,         // bf16 delta = U - W S as B-operand fragments [V/16 strip][2][64][8] (scan)
   R_COUNT
 };
 
@@ -63,16 +72,16 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
   switch (r) {
     case R_CHUNKS: return (size_t)g.max_chunks * 16;
     case R_SEQS: return (size_t)g.num_seqs * 8;
-    case R_QG: case R_QGT: case R_KD: case R_KDT: case R_W: case R_WT: return nt * 64 * K * 2;
-    case R_UT: return nt * 64 * V * 2;
-    case R_A: case R_AT: return nt * 64 * 64 * 2;
+    case R_QGF: case R_QGTF: case R_KDF: case R_KDTF: case R_WF: case R_WTF: return nt * 64 * K * 2;
+    case R_UF: return nt * 64 * V * 2;
+    case R_AF: case R_ATF: return nt * 64 * 64 * 2;
     case R_T: case R_MP: return nt * 64 * 64 * 4;
     case R_G: return nt * 64 * K * 4;
     case R_LAM: return nt * K * 4;
     case R_RQ: case R_RK: case R_BETA: return nt * 64 * 4;
     case R_SH: return nt * K * V * 4;
-    case R_SHB: return nt * K * V * 2;
-    case R_DLT: return nt * 64 * V * 2;
+    case R_SHBF: return nt * K * V * 2;
+    case R_DLF: return nt * 64 * V * 2;
     default: return 0;
   }
 }
