@@ -255,10 +255,8 @@ struct DenseSmem {
   static constexpr size_t off_dul = off_du + 64 * VP * 2;       // bf16 [64][VP] dU - bf16(dU)
   static constexpr size_t off_dl = off_dul + 64 * VP * 2;       // bf16 [64][VP] delta
   static constexpr size_t off_b = off_dl + 64 * VP * 2;         // f32 [64] beta
-  static constexpr size_t off_gl = off_b + 64 * 4;              // f32 [4][K] dG_last partials
-  static constexpr size_t off_pv = off_gl + 4 * K * 4;          // f32 [V/16][64] dbeta partials
-  static constexpr size_t off_pk = off_pv + (V / 16) * 64 * 4;  // f32 [K/16][64]
-  static constexpr size_t off_pm = off_pk + (K / 16) * 64 * 4;  // f32 [4][64]
+  static constexpr size_t off_pv = off_b + 64 * 4;              // f32 [V/16][64] dbeta partials
+  static constexpr size_t off_pm = off_pv + (V / 16) * 64 * 4;  // f32 [4][64]
   static constexpr size_t bytes = off_pm + 4 * 64 * 4;
 };
 
@@ -275,9 +273,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   bf16* sDUl = (bf16*)(smem + L::off_dul);
   bf16* sDL = (bf16*)(smem + L::off_dl);
   float* sB = (float*)(smem + L::off_b);
-  float* sGL = (float*)(smem + L::off_gl);
   float* sPV = (float*)(smem + L::off_pv);
-  float* sPK = (float*)(smem + L::off_pk);
   float* sPM = (float*)(smem + L::off_pm);
 
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
@@ -292,15 +288,14 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   const float* Tg = (const float*)a.ws.p[R_T] + tile * 64 * 64;
   const float* MPg = (const float*)a.ws.p[R_MP] + tile * 64 * 64;
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
-  const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
   const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
   const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
   const float* DSH = (const float*)a.sc.p[S_DSH] + tile * K * V;
   const float* DDLT = (const float*)a.sc.p[S_DDLT] + tile * V * 64;
-  float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
-  float* GK = (float*)a.sc.p[S_GK] + tile * 64 * K;
-  float* GG = (float*)a.sc.p[S_GG] + tile * 64 * K;
+  float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
+  float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
+  float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
   float* DA = (float*)a.sc.p[S_DA] + tile * 64 * 64;
   float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
 
@@ -375,26 +370,11 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       accW = mfma16(uHi, sLo, accW);
       accW = mfma16(uLo, sHi, accW);
     }
-    float colsum = 0.f;
-    const float GL = Gg[63 * K + c];
+    // raw dQg, dKd in C-layout item order (consumed with the same lane ownership)
+    *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = accQ;
+    *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int ii = 16 * rt + 4 * kg + rr;
-      const float G = Gg[ii * K + c];
-      const bool valid = ii < len;
-      const float qh = valid ? to_f32(a.q[((size_t)(row0 + ii) * H + h) * K + c]) * RQ[ii] : 0.f;
-      const float kh = valid ? to_f32(a.k[((size_t)(row0 + ii) * H + h) * K + c]) * RK[ii] : 0.f;
-      const float eG = expf(G), eKd = expf(GL - G);
-      const float Kd = kh * eKd;
-      GQ[ii * K + c] = accQ[rr] * eG;
-      GK[ii * K + c] = accK[rr] * eKd;
-      GG[ii * K + c] = accQ[rr] * qh * eG - accK[rr] * Kd;
-      colsum += accK[rr] * Kd;
-      sDW[ii * KP + c] = -accW[rr];
-    }
-    colsum += __shfl_xor(colsum, 16, kWave);
-    colsum += __shfl_xor(colsum, 32, kWave);
-    if (kg == 0) sGL[rt * K + c] = colsum;
+    for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = -accW[rr];
   }
   // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
   for (int p = wave; p < 16; p += kVjpWaves) {
@@ -491,7 +471,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       if (lr == 0) sPV[ct * 64 + jj] = part;
     }
   }
-  // d(beta kh e^G) = T^T dW -> dkh, dG, beta partials (same ownership as PA)
+  // d(beta kh e^G) = T^T dW, raw in C-layout item order (the decay kernel applies it)
   for (int p = wave; p < NKT; p += kVjpWaves) {
     const int rt = p % 4, ct = p / 4;
     const int j = 16 * rt + lr, c = 16 * ct + lr;
@@ -506,21 +486,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       }
       acc = mfma16(fa, fb, acc);
     }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int jj = 16 * rt + 4 * kg + rr;
-      float part = 0.f;
-      if (jj < len) {
-        const float kh = to_f32(a.k[((size_t)(row0 + jj) * H + h) * K + c]) * RK[jj];
-        const float eG = expf(Gg[jj * K + c]);
-        const float bt = sB[jj];
-        part = acc[rr] * kh * eG;
-        GK[jj * K + c] += bt * eG * acc[rr];
-        GG[jj * K + c] += acc[rr] * bt * kh * eG;
-      }
-      part = group_sum<16>(part);
-      if (lr == 0) sPK[ct * 64 + jj] = part;
-    }
+    *(f32x4*)(DKB + ((size_t)p * 64 + lane) * 4) = acc;
   }
   __syncthreads();
 
@@ -578,17 +544,12 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   }
   __syncthreads();
 
-  // ---- PE: dbeta_logits and dG_last ----
+  // ---- PE: dbeta partial (U and M' terms) and lam * dL/dlam ----
   if (tid < 64) {
-    const int t = tid;
-    if (t < len) {
-      float db = 0.f;
-      for (int c = 0; c < V / 16; ++c) db += sPV[c * 64 + t];
-      for (int c = 0; c < K / 16; ++c) db += sPK[c * 64 + t];
-      for (int b = 0; b < 4; ++b) db += sPM[b * 64 + t];
-      const float bt = sB[t];
-      a.dbeta[(size_t)(row0 + t) * H + h] = to_bf16(db * bt * (1.f - bt));
-    }
+    float db = 0.f;
+    for (int c = 0; c < V / 16; ++c) db += sPV[c * 64 + tid];
+    for (int b = 0; b < 4; ++b) db += sPM[b * 64 + tid];
+    ((float*)a.sc.p[S_DBETA])[tile * 64 + tid] = db;
   }
   if (tid < K) {
     const int c = tid;
@@ -601,9 +562,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       for (int e = 0; e < 8; ++e) dl = fmaf(s[e], d[e], dl);
     }
     const float lam = ((const float*)a.ws.p[R_LAM])[tile * K + c];
-    float gl = dl * lam;
-    for (int rt = 0; rt < 4; ++rt) gl += sGL[rt * K + c];
-    ((float*)a.sc.p[S_DGL])[tile * K + c] = gl;
+    ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lam;
   }
 }
 
@@ -614,25 +573,56 @@ template <int K>
 struct DecaySmem {
   static constexpr int KP = K + 4;
   static constexpr int MP = 65;
-  static constexpr size_t off_q = 0;
-  static constexpr size_t off_k = off_q + 64 * KP * 4;
-  static constexpr size_t off_g = off_k + 64 * KP * 4;
-  static constexpr size_t off_da = off_g + 64 * KP * 4;
-  static constexpr size_t off_dm = off_da + 64 * MP * 4;
-  static constexpr size_t off_f = off_dm + 64 * MP * 4;
+  static constexpr int NSEG = kVjpThreads / K;                   // cumsum segments per column
+  static constexpr size_t off_q = 0;                             // f32 [64][KP] qh, later dq
+  static constexpr size_t off_k = off_q + 64 * KP * 4;           // f32 [64][KP] kh, later dk
+  static constexpr size_t off_g = off_k + 64 * KP * 4;           // f32 [64][KP] G, later dG
+  static constexpr size_t off_da = off_g + 64 * KP * 4;          // f32 [64][65] dA
+  static constexpr size_t off_dm = off_da + 64 * MP * 4;         // f32 [64][65] dM'
+  static constexpr size_t off_pb = off_dm + 64 * MP * 4;         // f32 [K/16][64] dbeta partials
+  static constexpr size_t off_pq = off_pb + (K / 16) * 64 * 4;   // f32 [K/16][64] qh . dqh
+  static constexpr size_t off_pk = off_pq + (K / 16) * 64 * 4;   // f32 [K/16][64] kh . dkh
+  static constexpr size_t off_gl = off_pk + (K / 16) * 64 * 4;   // f32 [4][K] dG_last partials
+  static constexpr size_t off_row = off_gl + 4 * K * 4;          // f32 [5][64] beta, rq, rk, fq, fk
+  static constexpr size_t off_f = off_row + 5 * 64 * 4;          // int [4] unsafe-block flags
   static constexpr size_t bytes = off_f + 16;
+  // after the item phase the dA/dM' region holds the cumsum segments and parameter partials
+  static constexpr size_t off_seg = off_da;                      // f32 [NSEG][K]
+  static constexpr size_t off_p0 = off_seg + NSEG * K * 4;       // f32 [NSEG][K]
+  static constexpr size_t off_p1 = off_p0 + NSEG * K * 4;        // f32 [NSEG][K]
+  static_assert(off_p1 + NSEG * K * 4 <= off_pb, "cumsum scratch must fit in the dA/dM' region");
 };
 
+// Decay-structured VJP: gathers every dependence of the loss on qh, kh and G for one
+// (chunk, head), applies the L2-norm, beta and gate chains and writes dq, dk, dbeta, dgate.
+//   dqh = dQg e^G + Rq
+//   dkh = dKd e^{GL-G} + beta e^G dKb + Rk + Cq + Ck
+//   dG  = dQg Qg - dKd Kd + dKb Kb + qh Rq + kh Rk - kh (Cq + Ck),   dGL += sum_i dKd Kd
+// with Rq = sum_j dA_ij kh_j e^{G_i-G_j}, Rk = sum_j dM'_ij kh_j e^{G_i-G_j} (row side) and
+// Cq = sum_i dA_ij qh_i e^{G_i-G_j}, Ck = sum_i dM'_ij kh_i e^{G_i-G_j} (column side).
+// Each 16 x 16 (row tile, key tile) item is owned by one wave in MFMA C layout, the layout in
+// which the dense kernel stored dQg, dKd and dKb, so every per-element term stays in registers.
 template <int K>
 __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a) {
   using L = DecaySmem<K>;
-  constexpr int KP = L::KP, MP = L::MP;
+  constexpr int KP = L::KP, MP = L::MP, NSEG = L::NSEG;
+  constexpr int NKT = 4 * (K / 16);
+  constexpr int IPW = (NKT + kVjpWaves - 1) / kVjpWaves;  // items per wave
   extern __shared__ __attribute__((aligned(16))) char smem[];
   float* sQ = (float*)(smem + L::off_q);
   float* sK = (float*)(smem + L::off_k);
   float* sG = (float*)(smem + L::off_g);
   float* sDA = (float*)(smem + L::off_da);
   float* sDM = (float*)(smem + L::off_dm);
+  float* sPB = (float*)(smem + L::off_pb);
+  float* sPQ = (float*)(smem + L::off_pq);
+  float* sPK = (float*)(smem + L::off_pk);
+  float* sGL = (float*)(smem + L::off_gl);
+  float* sBeta = (float*)(smem + L::off_row);
+  float* sRq = sBeta + 64;
+  float* sRk = sBeta + 128;
+  float* sFq = sBeta + 192;
+  float* sFk = sBeta + 256;
   int* sF = (int*)(smem + L::off_f);
 
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
@@ -645,16 +635,17 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   const int lr = lane % 16, kg = lane / 16;
 
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
-  const float* RQ = (const float*)a.ws.p[R_RQ] + tile * 64;
-  const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
-  float* GQ = (float*)a.sc.p[S_GQ] + tile * 64 * K;
-  float* GK = (float*)a.sc.p[S_GK] + tile * 64 * K;
-  float* GG = (float*)a.sc.p[S_GG] + tile * 64 * K;
+  // dQg/dKd/dKb of this tile; they are overwritten with dqh, dkh and dG (same lane, same
+  // address) to carry them across the barrier that completes the per-row dot products
+  float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
+  float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
+  float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
 
-  // ---- P0: stage qh, kh, G, dA, dM' ----
+  // ---- P0: stage qh, kh, G, dA, dM', beta and the per-row norm factors ----
   if (tid < 4) sF[tid] = 0;
-  for (int idx = tid; idx < 64 * (K / 8); idx += kVjpThreads) {
-    const int t = idx / (K / 8), c0 = (idx % (K / 8)) * 8;
+  if (tid < 64 * (K / 8)) {
+    constexpr int LPR = K / 8;
+    const int t = tid / LPR, c0 = (tid % LPR) * 8;
     float qv[8], kv[8];
     if (t < len) {
       const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
@@ -664,20 +655,41 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
 #pragma unroll
       for (int e = 0; e < 8; ++e) qv[e] = kv[e] = 0.f;
     }
-    const float rq = RQ[t], rk = RK[t];
+    const float rq = ((const float*)a.ws.p[R_RQ])[tile * 64 + t];
+    const float rk = ((const float*)a.ws.p[R_RK])[tile * 64 + t];
+    float sq = 0.f, sk = 0.f;
+    float gv[8];
+    load8f(Gg + t * K + c0, gv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
+      sq += qv[e] * qv[e];
+      sk += kv[e] * kv[e];
       sQ[t * KP + c0 + e] = qv[e] * rq;
       sK[t * KP + c0 + e] = kv[e] * rk;
-      sG[t * KP + c0 + e] = Gg[t * K + c0 + e];
+      sG[t * KP + c0 + e] = gv[e];
+    }
+    sq = group_sum<LPR>(sq);
+    sk = group_sum<LPR>(sk);
+    if (c0 == 0) {
+      // dx = r (g - xhat (xhat . g)) with xhat = x/||x||; expressed through qh = r x:
+      // dx = r g - qh (qh . g) / (||x||^2 r); clamped norms pass r g through
+      sRq[t] = rq;
+      sRk[t] = rk;
+      sFq[t] = sqrtf(sq) > 1e-12f ? 1.f / (sq * rq) : 0.f;
+      sFk[t] = sqrtf(sk) > 1e-12f ? 1.f / (sk * rk) : 0.f;
+      sBeta[t] = ((const float*)a.ws.p[R_BETA])[tile * 64 + t];
     }
   }
   {
     const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
     const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
-    for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
-      sDA[(idx / 64) * MP + idx % 64] = DA[idx];
-      sDM[(idx / 64) * MP + idx % 64] = DMP[idx];
+    for (int idx = tid * 4; idx < 64 * 64; idx += kVjpThreads * 4) {
+      const float4 x = *(const float4*)(DA + idx);
+      const float4 y = *(const float4*)(DMP + idx);
+      float* da = sDA + (idx / 64) * MP + idx % 64;
+      float* dm = sDM + (idx / 64) * MP + idx % 64;
+      da[0] = x.x; da[1] = x.y; da[2] = x.z; da[3] = x.w;
+      dm[0] = y.x; dm[1] = y.y; dm[2] = y.z; dm[3] = y.w;
     }
   }
   __syncthreads();
@@ -689,22 +701,36 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   }
   __syncthreads();
 
-  constexpr int NKT = 4 * (K / 16);
-  // ---- P1: row side  Rq = sum_j dA_ij kh_j e^{G_i-G_j},  Rk = sum_j dM'_ij kh_j e^{G_i-G_j} ----
-  for (int p = wave; p < NKT; p += kVjpWaves) {
-    const int ba = p % 4, ct = p / 4;
-    const int r = 16 * ba;
+  // ---- P1: per item, row side + column side + all per-element terms ----
+#pragma unroll 1
+  for (int n = 0; n < IPW; ++n) {
+    const int p = wave + n * kVjpWaves;
+    if (p >= NKT) break;
+    const int rt = p % 4, ct = p / 4;
+    // lane coordinates made opaque per item: keeps the compiler from hoisting dozens of
+    // lane-dependent LDS addresses out of the item loop (they would be spilled)
+    int lr = lane % 16, kg = lane / 16;
+    asm volatile("" : "+v"(lr), "+v"(kg));
     const int c = 16 * ct + lr;
+    const bool unsafe = sF[rt] != 0;
+    // the raw dQg/dKd/dKb items are not needed before the per-element terms: their loads
+    // overlap the MFMA work below
+    const f32x4 rdQ = *(const f32x4*)(DQG + ((size_t)p * 64 + lane) * 4);
+    const f32x4 rdK = *(const f32x4*)(DKD + ((size_t)p * 64 + lane) * 4);
+    const f32x4 rdB = *(const f32x4*)(DKB + ((size_t)p * 64 + lane) * 4);
+    // row side  Rq = sum_j dA_ij kh_j e^{G_i-G_j},  Rk = sum_j dM'_ij kh_j e^{G_i-G_j}
     f32x4 rq = zero4(), rk = zero4();
-    if (!sF[ba]) {
-      const int i = 16 * ba + lr;
-      const int jmax = 16 * ba + 15;
-      const int nsteps = jmax / 32 + 1;
-      for (int s = 0; s < nsteps; ++s) {
+    // column side  Cq + Ck = sum_i (dA_ij qh_i + dM'_ij kh_i) e^{G_i-G_j}
+    f32x4 cq = zero4(), ck = zero4();
+    if (!unsafe) {
+      const int r = 16 * rt;
+      const int i = 16 * rt + lr;
+      const int jmax = 16 * rt + 15;
+      const float gr = sG[r * KP + c];
+      for (int s = 0; s <= jmax / 32; ++s) {
         const int j0 = 32 * s + 8 * kg;
         bf16x8 fa, fm, fbh, fbl;
         float xb[8];
-        const float gr = sG[r * KP + c];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int j = j0 + e;
@@ -712,7 +738,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
           fm[e] = to_bf16(sDM[i * MP + j]);
           xb[e] = j <= jmax ? sK[j * KP + c] * __expf(gr - sG[j * KP + c]) : 0.f;
         }
-        // the decay-scaled key operand is split (hi + lo): its rounding is systematic
+        // the decay-scaled operands are split (hi + lo): their rounding is systematic
         // across the row/column terms of dG, which nearly cancel
         split8(xb, fbh, fbl);
         rq = mfma16(fa, fbh, rq);
@@ -720,57 +746,21 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
         rk = mfma16(fm, fbh, rk);
         rk = mfma16(fm, fbl, rk);
       }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = 16 * ba + 4 * kg + rr;
-        const float f = __expf(sG[ii * KP + c] - sG[r * KP + c]);
-        rq[rr] *= f;
-        rk[rr] *= f;
-      }
-    } else {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = 16 * ba + 4 * kg + rr;
-        float sq = 0.f, sk = 0.f;
-        for (int j = 0; j <= ii; ++j) {
-          const float kj = sK[j * KP + c] * expf(sG[ii * KP + c] - sG[j * KP + c]);
-          sq = fmaf(sDA[ii * MP + j], kj, sq);
-          sk = fmaf(sDM[ii * MP + j], kj, sk);
-        }
-        rq[rr] = sq;
-        rk[rr] = sk;
-      }
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int ii = 16 * ba + 4 * kg + rr;
-      GQ[ii * K + c] += rq[rr];
-      GK[ii * K + c] += rk[rr];
-      GG[ii * K + c] += sQ[ii * KP + c] * rq[rr] + sK[ii * KP + c] * rk[rr];
-    }
-  }
-  // ---- P2: column side  C = sum_i (dA_ij qh_i + dM'_ij kh_i) e^{G_i-G_j}  (same ownership) ----
-  for (int p = wave; p < NKT; p += kVjpWaves) {
-    const int bb = p % 4, ct = p / 4;
-    const int rp = 16 * bb + 15;
-    const int c = 16 * ct + lr;
-    f32x4 cq = zero4(), ck = zero4();
-    if (!sF[bb]) {
-      const int j = 16 * bb + lr;
-      const float gr = sG[rp * KP + c];
-      for (int s = (16 * bb) / 32; s < 2; ++s) {
+      const int rp = 16 * rt + 15;
+      const int j = 16 * rt + lr;
+      const float gp = sG[rp * KP + c];
+      for (int s = (16 * rt) / 32; s < 2; ++s) {
         const int i0 = 32 * s + 8 * kg;
         bf16x8 fa, fm, bqh, bql, bkh, bkl;
         float xq[8], xk[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int i = i0 + e;
-          const bool ok = i >= 16 * bb;
-          const float f = ok ? __expf(sG[i * KP + c] - gr) : 0.f;
-          fa[e] = to_bf16(sDA[i * MP + j]);
-          fm[e] = to_bf16(sDM[i * MP + j]);
-          xq[e] = sQ[i * KP + c] * f;
-          xk[e] = sK[i * KP + c] * f;
+          const int ii = i0 + e;
+          const float f = ii >= 16 * rt ? __expf(sG[ii * KP + c] - gp) : 0.f;
+          fa[e] = to_bf16(sDA[ii * MP + j]);
+          fm[e] = to_bf16(sDM[ii * MP + j]);
+          xq[e] = sQ[ii * KP + c] * f;
+          xk[e] = sK[ii * KP + c] * f;
         }
         split8(xq, bqh, bql);
         split8(xk, bkh, bkl);
@@ -781,98 +771,190 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
       }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int jj = 16 * bb + 4 * kg + rr;
-        const float f = __expf(gr - sG[jj * KP + c]);
-        cq[rr] *= f;
-        ck[rr] *= f;
+        const int ii = 16 * rt + 4 * kg + rr;
+        const float gi = sG[ii * KP + c];
+        const float fr = __expf(gi - gr), fc = __expf(gp - gi);
+        rq[rr] *= fr;
+        rk[rr] *= fr;
+        cq[rr] *= fc;
+        ck[rr] *= fc;
       }
     } else {
+      // a block whose decay spans more than 80 nats: exact per-pair factors
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int jj = 16 * bb + 4 * kg + rr;
+        const int ii = 16 * rt + 4 * kg + rr;
+        const float gi = sG[ii * KP + c];
         float sq = 0.f, sk = 0.f;
-        for (int i = jj; i < 64; ++i) {
-          const float e = expf(sG[i * KP + c] - sG[jj * KP + c]);
-          sq = fmaf(sDA[i * MP + jj], sQ[i * KP + c] * e, sq);
-          sk = fmaf(sDM[i * MP + jj], sK[i * KP + c] * e, sk);
+        for (int j = 0; j <= ii; ++j) {
+          const float kj = sK[j * KP + c] * expf(gi - sG[j * KP + c]);
+          sq = fmaf(sDA[ii * MP + j], kj, sq);
+          sk = fmaf(sDM[ii * MP + j], kj, sk);
         }
-        cq[rr] = sq;
-        ck[rr] = sk;
+        float tq = 0.f, tk = 0.f;
+        for (int i = ii; i < 64; ++i) {
+          const float e = expf(sG[i * KP + c] - gi);
+          tq = fmaf(sDA[i * MP + ii], sQ[i * KP + c] * e, tq);
+          tk = fmaf(sDM[i * MP + ii], sK[i * KP + c] * e, tk);
+        }
+        rq[rr] = sq;
+        rk[rr] = sk;
+        cq[rr] = tq;
+        ck[rr] = tk;
       }
     }
+    const float GL = sG[63 * KP + c];
+    float glp = 0.f;
+    f32x4 dqs, dks, dgs;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int jj = 16 * bb + 4 * kg + rr;
+      const int ii = 16 * rt + 4 * kg + rr;
+      const float qh = sQ[ii * KP + c], kh = sK[ii * KP + c], G = sG[ii * KP + c];
+      const float bt = sBeta[ii];
+      const float eG = expf(G), eKd = expf(GL - G);
+      const float dQg = rdQ[rr], dKd = rdK[rr], dKb = rdB[rr];
       const float cc = cq[rr] + ck[rr];
-      GK[jj * K + c] += cc;
-      GG[jj * K + c] -= sK[jj * KP + c] * cc;
+      const float dqh = fmaf(dQg, eG, rq[rr]);
+      const float dkh = dKd * eKd + bt * eG * dKb + rk[rr] + cc;
+      const float kdd = dKd * kh * eKd;
+      const float kbb = dKb * kh * eG;  // dbeta partial (the beta factor of Kb removed)
+      dgs[rr] = dQg * qh * eG - kdd + bt * kbb + qh * rq[rr] + kh * rk[rr] - kh * cc;
+      dqs[rr] = dqh;
+      dks[rr] = dkh;
+      glp += kdd;
+      const float pb = group_sum<16>(kbb);
+      const float pq = group_sum<16>(qh * dqh);
+      const float pk = group_sum<16>(kh * dkh);
+      if (lr == 0) {
+        sPB[ct * 64 + ii] = pb;
+        sPQ[ct * 64 + ii] = pq;
+        sPK[ct * 64 + ii] = pk;
+      }
+    }
+    *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = dqs;
+    *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = dks;
+    *(f32x4*)(DKB + ((size_t)p * 64 + lane) * 4) = dgs;
+    glp += __shfl_xor(glp, 16, kWave);
+    glp += __shfl_xor(glp, 32, kWave);
+    if (kg == 0) sGL[rt * K + c] = glp;
+  }
+  __syncthreads();
+
+  // per-row dot products (fixed order) and dbeta
+  if (tid < 64) {
+    const int t = tid;
+    float dotq = 0.f, dotk = 0.f, db = ((const float*)a.sc.p[S_DBETA])[tile * 64 + t];
+#pragma unroll
+    for (int q = 0; q < K / 16; ++q) {
+      dotq += sPQ[q * 64 + t];
+      dotk += sPK[q * 64 + t];
+      db += sPB[q * 64 + t];
+    }
+    sPQ[t] = dotq * sFq[t];
+    sPK[t] = dotk * sFk[t];
+    if (t < len) {
+      const float bt = sBeta[t];
+      a.dbeta[(size_t)(row0 + t) * H + h] = to_bf16(db * bt * (1.f - bt));
     }
   }
   __syncthreads();
 
-  // ---- P3: dg = reverse cumsum of dG (+ dG_last), gate chain, parameter partials ----
-  if (tid < K) {
-    const int c = tid;
-    float acc = ((const float*)a.sc.p[S_DGL])[tile * K + c];
-    float p0 = 0.f, p1 = 0.f;
-    const float ea = a.gate_mode == KDA_GATE_K3 ? expf(a.A_log[h]) : 0.f;
-    const float bias = a.gate_mode == KDA_GATE_K3 ? a.dt_bias[h * K + c] : 0.f;
-    for (int t = len - 1; t >= 0; --t) {
-      acc += GG[t * K + c];
-      const size_t off = ((size_t)(row0 + t) * H + h) * K + c;
-      if (a.gate_mode == KDA_GATE_K3) {
-        const float pre = to_f32(((const bf16*)a.gate)[off]) + bias;
-        const float s = sigmoid_acc(ea * pre);
-        const float dz = acc * a.lb * s * (1.f - s) * ea;
-        ((bf16*)a.dgate)[off] = to_bf16(dz);
-        p0 += dz;
-        p1 = fmaf(dz, pre, p1);
-      } else {
-        ((float*)a.dgate)[off] = acc;
-      }
+  // ---- P2: L2-norm chains; dq, dk, dG into LDS (qh/kh/G are consumed) ----
+#pragma unroll
+  for (int n = 0; n < IPW; ++n) {
+    const int p = wave + n * kVjpWaves;
+    if (p >= NKT) break;
+    const int rt = p % 4, ct = p / 4;
+    const int c = 16 * ct + lr;
+    const f32x4 dqs = *(const f32x4*)(DQG + ((size_t)p * 64 + lane) * 4);
+    const f32x4 dks = *(const f32x4*)(DKD + ((size_t)p * 64 + lane) * 4);
+    const f32x4 dgs = *(const f32x4*)(DKB + ((size_t)p * 64 + lane) * 4);
+    float dqv[4], dkv[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * rt + 4 * kg + rr;
+      dqv[rr] = sRq[ii] * dqs[rr] - sQ[ii * KP + c] * sPQ[ii];
+      dkv[rr] = sRk[ii] * dks[rr] - sK[ii * KP + c] * sPK[ii];
     }
-    if (a.gate_mode == KDA_GATE_K3) {
-      float* PP = (float*)a.sc.p[S_PP] + tile * 2 * K;
-      PP[c] = p0;
-      PP[K + c] = p1;
+    // every read of this element's qh/kh happened in this lane; write back in place
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int ii = 16 * rt + 4 * kg + rr;
+      sQ[ii * KP + c] = dqv[rr];
+      sK[ii * KP + c] = dkv[rr];
+      sG[ii * KP + c] = ii < len ? dgs[rr] : 0.f;
     }
   }
-  // ---- P4: L2-norm chains -> dq, dk ----
+  __syncthreads();
+
+  // ---- P3: coalesced dq, dk writes ----
   {
     constexpr int LPR = K / 8;
-    constexpr int RPP = kVjpThreads / LPR;
-    const int c0 = (tid % LPR) * 8;
-    for (int t = tid / LPR; t < 64; t += RPP) {
-      if (t >= len) continue;  // uniform per LPR lane group
+    for (int idx = tid; idx < 64 * LPR; idx += kVjpThreads) {
+      const int t = idx / LPR, c0 = (idx % LPR) * 8;
+      if (t >= len) continue;
       const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
-      float qv[8], kv[8], gq[8], gk[8];
-      load8(a.q + base, qv);
-      load8(a.k + base, kv);
-      float sq = 0.f, sk = 0.f, dq_dot = 0.f, dk_dot = 0.f;
+      store8(a.dq + base, sQ + t * KP + c0);
+      store8(a.dk + base, sK + t * KP + c0);
+    }
+  }
+
+  // ---- P4: dg = reverse cumsum of dG (+ dG_last) in NSEG segments per key, gate chain ----
+  constexpr int RPS = 64 / NSEG;
+  float* sSeg = (float*)(smem + L::off_seg);
+  float* sP0 = (float*)(smem + L::off_p0);
+  float* sP1 = (float*)(smem + L::off_p1);
+  const int c = tid % K, seg = tid / K;
+  {
+    float sum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        gq[e] = GQ[t * K + c0 + e];
-        gk[e] = GK[t * K + c0 + e];
-        sq += qv[e] * qv[e];
-        sk += kv[e] * kv[e];
-        dq_dot += qv[e] * gq[e];
-        dk_dot += kv[e] * gk[e];
-      }
-      sq = group_sum<LPR>(sq);
-      sk = group_sum<LPR>(sk);
-      dq_dot = group_sum<LPR>(dq_dot);
-      dk_dot = group_sum<LPR>(dk_dot);
-      const float nq = sqrtf(sq), nk = sqrtf(sk);
-      const float rq = RQ[t], rk = RK[t];
-      float oq[8], ok[8];
+    for (int r = 0; r < RPS; ++r) sum += sG[(seg * RPS + r) * KP + c];
+    sSeg[seg * K + c] = sum;
+  }
+  __syncthreads();
+  {
+    float acc = ((const float*)a.sc.p[S_DGL])[tile * K + c];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // dx = r * (g - xhat (xhat . g)), xhat = x / ||x||; clamped norms pass g * r through
-        oq[e] = nq > 1e-12f ? rq * (gq[e] - qv[e] * dq_dot / sq) : rq * gq[e];
-        ok[e] = nk > 1e-12f ? rk * (gk[e] - kv[e] * dk_dot / sk) : rk * gk[e];
+    for (int q = 0; q < 4; ++q) acc += sGL[q * K + c];
+    for (int s = NSEG - 1; s > seg; --s) acc += sSeg[s * K + c];
+    float p0 = 0.f, p1 = 0.f;
+    const bool k3 = a.gate_mode == KDA_GATE_K3;
+    const float ea = k3 ? expf(a.A_log[h]) : 0.f;
+    const float bias = k3 ? a.dt_bias[h * K + c] : 0.f;
+#pragma unroll
+    for (int r = RPS - 1; r >= 0; --r) {
+      const int t = seg * RPS + r;
+      acc += sG[t * KP + c];
+      if (t < len) {
+        const size_t off = ((size_t)(row0 + t) * H + h) * K + c;
+        if (k3) {
+          const float pre = to_f32(((const bf16*)a.gate)[off]) + bias;
+          const float s = sigmoid_acc(ea * pre);
+          const float dz = acc * a.lb * s * (1.f - s) * ea;
+          ((bf16*)a.dgate)[off] = to_bf16(dz);
+          p0 += dz;
+          p1 = fmaf(dz, pre, p1);
+        } else {
+          ((float*)a.dgate)[off] = acc;
+        }
       }
-      store8(a.dq + base, oq);
-      store8(a.dk + base, ok);
+    }
+    if (k3) {
+      sP0[seg * K + c] = p0;
+      sP1[seg * K + c] = p1;
+    }
+  }
+  if (a.gate_mode == KDA_GATE_K3) {
+    __syncthreads();
+    if (tid < K) {
+      float p0 = 0.f, p1 = 0.f;
+      for (int s = 0; s < NSEG; ++s) {
+        p0 += sP0[s * K + tid];
+        p1 += sP1[s * K + tid];
+      }
+      float* PP = (float*)a.sc.p[S_PP] + tile * 2 * K;
+      PP[tid] = p0;
+      PP[K + tid] = p1;
     }
   }
 }

@@ -50,11 +50,12 @@ enum ScRegion {
   S_DDLT,     // f32  [tile][V][64]  (dL/d delta)^T
   S_DA,       // f32  [tile][64][64] dL/dA (masked lower)
   S_DMP,      // f32  [tile][64][64] dL/dM' (strictly lower, beta folded in)
-  S_GQ,       // f32  [tile][64][K]  accumulated dL/dq_hat
-  S_GK,       // f32  [tile][64][K]  accumulated dL/dk_hat
-  S_GG,       // f32  [tile][64][K]  accumulated dL/dG
+  S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
+  S_DKD,      // f32  [tile][item][64 lane][4]  dL/dKd  (same layout)
+  S_DKB,      // f32  [tile][item][64 lane][4]  dL/d(beta kh exp(G))  (same layout)
   S_PP,       // f32  [tile][2][K]   gate parameter partials {sum draw, sum draw*(z+b)}
-  S_DGL,      // f32  [tile][K]      dL/dG_last (state-decay and Kd column terms)
+  S_DGL,      // f32  [tile][K]      lam * dL/dlam (the state-decay part of dL/dG_last)
+  S_DBETA,    // f32  [tile][64]     dL/dbeta from the dense VJP (U, M' terms)
   S_COUNT
 };
 
@@ -93,9 +94,10 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
     case S_DSH: return nt * K * V * 4;
     case S_DDLT: return nt * 64 * V * 4;
     case S_DA: case S_DMP: return nt * 64 * 64 * 4;
-    case S_GQ: case S_GK: case S_GG: return nt * 64 * K * 4;
+    case S_DQG: case S_DKD: case S_DKB: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
     case S_DGL: return nt * K * 4;
+    case S_DBETA: return nt * 64 * 4;
     default: return 0;
   }
 }
