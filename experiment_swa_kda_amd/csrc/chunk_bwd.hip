@@ -834,8 +834,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
     *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = dqs;
     *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = dks;
     *(f32x4*)(DKB + ((size_t)p * 64 + lane) * 4) = dgs;
-    glp += __shfl_xor(glp, 16, kWave);
-    glp += __shfl_xor(glp, 32, kWave);
+    glp = lane_stride_sum<16>(glp);
     if (kg == 0) sGL[rt * K + c] = glp;
   }
   __syncthreads();
@@ -1060,6 +1059,8 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
   KDA_REQUIRE(empty || (q && k && v && gate && beta_logits && grad_output && dq && dk && dv &&
                         dgate && dbeta_logits),
               "chunk_backward: null input/output pointer");
+  KDA_REQUIRE(aligned16(q, k, v, gate, grad_output, dq, dk, dv, dgate),
+              "chunk_backward: q, k, v, gate, grad_output and the gradients must be 16-byte aligned");
   KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || (A_log && dt_bias && dA_log && ddt_bias),
               "chunk_backward: K3 gate needs A_log, dt_bias, dA_log and ddt_bias");
   KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,

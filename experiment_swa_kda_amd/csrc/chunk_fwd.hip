@@ -728,6 +728,8 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   const bool empty = (size_t)p->batch * p->seq_len == 0;
   KDA_REQUIRE(empty || (q && k && v && gate && beta_logits && output),
               "chunk_forward: null input/output pointer");
+  KDA_REQUIRE(aligned16(q, k, v, gate, output, initial_state, final_state),
+              "chunk_forward: q, k, v, gate, output and the states must be 16-byte aligned");
   KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || (A_log && dt_bias),
               "chunk_forward: K3 gate needs A_log and dt_bias");
   KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,

@@ -6,82 +6,138 @@
 // including the current token):  pre[t] = sum_j xp[t + j] * w[j],  y = silu(pre),
 // final_state = xp[T-1 .. T+W-2].
 //
-// HBM-bound.  A thread owns 8 consecutive channels (one 16-byte bf16x8 vector) and
-// kTok consecutive tokens; a 256-thread workgroup covers kGroups channel groups x
-// kSlices token slices, so adjacent lanes read adjacent 16-byte vectors of a token row.
-// The W-1 token halo is re-read through L1/L2.  Arithmetic is f32 (products are not
-// rounded to bf16 before accumulation).  The weight gradient is reduced inside the
-// workgroup through LDS, written as one partial per workgroup and summed over
-// workgroups in a fixed order (deterministic, no atomics).
+// HBM-bound.  A thread owns 8 consecutive channels (one 16-byte bf16x8 vector) and kTok
+// consecutive tokens.  A 256-thread workgroup is kCgs channel groups x kSlices token
+// slices with the channel group fastest, so each load instruction of a wave covers
+// 256 / kCgs contiguous 256-byte row segments.  Every thread issues all of its row loads
+// (clamped to valid rows, no branches) before it consumes any of them, so the loads of a
+// thread are in flight together; rows outside [0, T) are replaced afterwards by the
+// initial state or zero.  The W-1 token halo is re-read through L1/L2.  Arithmetic is
+// f32 (products are not rounded to bf16 before accumulation).  The weight gradient is
+// reduced inside the workgroup (shuffles, then LDS), written as one partial per
+// workgroup and summed over workgroups in a fixed order (deterministic, no atomics).
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
 namespace kda {
 
-constexpr int kTok = 4;       // tokens per thread
-constexpr int kGroups = 8;    // channel groups (of 8 channels) per workgroup
-constexpr int kSlices = 32;   // token slices per workgroup (256 threads)
-constexpr int kBlockTok = kTok * kSlices;
+// Tile shapes (tokens per thread, channel groups per workgroup); the token slices per
+// workgroup are 256 / channel groups.  Overridable at build time for tuning sweeps.
+#ifndef KDA_CONV_FWD_TOK
+#define KDA_CONV_FWD_TOK 8
+#endif
+#ifndef KDA_CONV_FWD_CGS
+#define KDA_CONV_FWD_CGS 16
+#endif
+#ifndef KDA_CONV_BWD_TOK
+#define KDA_CONV_BWD_TOK 4
+#endif
+#ifndef KDA_CONV_BWD_CGS
+#define KDA_CONV_BWD_CGS 8
+#endif
 
+// `halo` is the overlap of consecutive token blocks (the backward's W-1; 0 forward).
+template <int TOK, int CGS>
 struct ConvGeom {
+  static constexpr int kTok = TOK, kCgs = CGS, kSlices = 256 / CGS, kBlockTok = TOK * kSlices;
   int B, T, C, CG, ncb, ntb;  // channel groups, channel blocks, token blocks
-  __host__ __device__ ConvGeom(int B_, int T_, int C_)
-      : B(B_), T(T_), C(C_), CG(C_ / 8), ncb((C_ / 8 + kGroups - 1) / kGroups),
-        ntb((T_ + kBlockTok - 1) / kBlockTok) {}
+  __host__ __device__ ConvGeom(int B_, int T_, int C_, int halo = 0)
+      : B(B_), T(T_), C(C_), CG(C_ / 8), ncb((C_ / 8 + kCgs - 1) / kCgs),
+        ntb((T_ + kBlockTok - halo - 1) / (kBlockTok - halo)) {}
   __host__ __device__ int blocks() const { return B * ntb * ncb; }
 };
+using FwdGeom = ConvGeom<KDA_CONV_FWD_TOK, KDA_CONV_FWD_CGS>;
+using BwdGeom = ConvGeom<KDA_CONV_BWD_TOK, KDA_CONV_BWD_CGS>;
 
+// Workgroup -> (batch, token block, channel block); thread -> (channel group, slice).
+struct ConvPos {
+  int b, tb, cb, cg, slice, t0, c0;
+  template <typename G>
+  __device__ ConvPos(const G& g) {
+    cb = blockIdx.x % g.ncb;
+    tb = (blockIdx.x / g.ncb) % g.ntb;
+    b = blockIdx.x / (g.ncb * g.ntb);
+    cg = cb * G::kCgs + threadIdx.x % G::kCgs;
+    slice = threadIdx.x / G::kCgs;
+    t0 = tb * G::kBlockTok + slice * G::kTok;
+    c0 = cg * 8;
+  }
+};
+
+// W taps of 8 channels: w[c0 + e][j] = 8*W contiguous bf16 (16-byte aligned, c0 % 8 == 0).
 template <int W>
-__device__ __forceinline__ void load_xp8(const bf16* __restrict__ x, const bf16* __restrict__ st,
-                                         int b, int T, int C, int c0, int p, float* out) {
-  // xp[p] for 8 channels: p >= W-1 -> x[p-(W-1)], else state[.., p+1]
-  const int t = p - (W - 1);
-  if (t >= 0 && t < T) {
-    load8(x + ((size_t)b * T + t) * C + c0, out);
-  } else if (t < 0 && st) {
+__device__ __forceinline__ void load_taps(const bf16* __restrict__ w, int c0, float (&wt)[8][W]) {
+  bf16x8 v[W];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = to_f32(st[((size_t)b * C + c0 + e) * W + p + 1]);
-  } else {
+  for (int i = 0; i < W; ++i) v[i] = *reinterpret_cast<const bf16x8*>(w + (size_t)c0 * W + 8 * i);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = 0.f;
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int j = 0; j < W; ++j) wt[e][j] = (float)v[(e * W + j) / 8][(e * W + j) % 8];
+}
+
+// N rows of 8 channels of x at tokens t = p0 - (W-1) + i (i < N), i.e. xp[p0 + i].  All
+// loads are issued first (row index clamped into [0, T-1]); rows with t < 0 then come
+// from the initial state (or zero), rows with t >= T are zero.
+template <int W, int N>
+__device__ __forceinline__ void load_xp_rows(const bf16* __restrict__ x, const bf16* __restrict__ st,
+                                             int b, int T, int C, int c0, int p0,
+                                             bf16x8 (&raw)[N]) {
+  const bf16* base = x + (size_t)b * T * C + c0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    int t = p0 - (W - 1) + i;
+    t = t < 0 ? 0 : (t >= T ? T - 1 : t);
+    raw[i] = *reinterpret_cast<const bf16x8*>(base + (size_t)t * C);
+  }
+  const bf16 zero = (bf16)0.f;
+  if (p0 < W - 1 || p0 - (W - 1) + N > T) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int t = p0 - (W - 1) + i;
+      if (t < 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          raw[i][e] = st ? st[((size_t)b * C + c0 + e) * W + (p0 + i) + 1] : zero;
+      } else if (t >= T) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) raw[i][e] = zero;
+      }
+    }
   }
 }
 
 __device__ __forceinline__ float silu_grad(float pre) {
-  float s = sigmoid_acc(pre);
+  float s = sigmoid_fast(pre);
   return s * (1.f + pre * (1.f - s));
 }
 
 template <int W>
-__global__ __launch_bounds__(256) void conv_fwd_kernel(ConvGeom g, const bf16* __restrict__ x,
+__global__ __launch_bounds__(256) void conv_fwd_kernel(FwdGeom g, const bf16* __restrict__ x,
                                                        const bf16* __restrict__ w,
                                                        const bf16* __restrict__ st,
                                                        bf16* __restrict__ y) {
-  const int cb = blockIdx.x % g.ncb, tb = (blockIdx.x / g.ncb) % g.ntb, b = blockIdx.x / (g.ncb * g.ntb);
-  const int cg = cb * kGroups + threadIdx.x % kGroups;
-  const int t0 = tb * kBlockTok + (threadIdx.x / kGroups) * kTok;
-  if (cg >= g.CG || t0 >= g.T) return;
-  const int c0 = cg * 8;
+  const ConvPos P(g);
+  if (P.cg >= g.CG || P.t0 >= g.T) return;
+  constexpr int kTok = FwdGeom::kTok;
+  constexpr int NX = kTok + W - 1;  // xp[t0 .. t0 + kTok + W - 2]
+  bf16x8 xr[NX];
+  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, P.c0, P.t0, xr);
   float wt[8][W];
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-#pragma unroll
-    for (int j = 0; j < W; ++j) wt[e][j] = to_f32(w[(c0 + e) * W + j]);
-  float xp[kTok + W - 1][8];  // xp[t0 .. t0+kTok+W-2]
-#pragma unroll
-  for (int i = 0; i < kTok + W - 1; ++i) load_xp8<W>(x, st, b, g.T, g.C, c0, t0 + i, xp[i]);
+  load_taps<W>(w, P.c0, wt);
+  bf16* yb = y + ((size_t)P.b * g.T + P.t0) * g.C + P.c0;
 #pragma unroll
   for (int u = 0; u < kTok; ++u) {
-    if (t0 + u >= g.T) break;
+    if (P.t0 + u >= g.T) break;
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float pre = 0.f;
 #pragma unroll
-      for (int j = 0; j < W; ++j) pre = fmaf(xp[u + j][e], wt[e][j], pre);
-      o[e] = pre * sigmoid_acc(pre);
+      for (int j = 0; j < W; ++j) pre = fmaf((float)xr[u + j][e], wt[e][j], pre);
+      o[e] = pre * sigmoid_fast(pre);
     }
-    store8(y + ((size_t)b * g.T + t0 + u) * g.C + c0, o);
+    store8(yb + (size_t)u * g.C, o);
   }
 }
 
@@ -103,117 +159,131 @@ __global__ void conv_final_state_kernel(int B, int T, int C, const bf16* __restr
   fin[i] = to_bf16(val);
 }
 
-// dx[t] = sum_j dpre[t + W-1-j] w[j] (+ grad of the final state); dpre = dy * silu'(pre).
-// dweight[c][j] = sum_t dpre[t] xp[t + j]: per-thread sums over its kTok tokens, reduced
-// over the workgroup's token slices in LDS, one partial per workgroup.
+// Backward.  dpre[s] = dy[s] * silu'(pre[s]);  dx[t] = sum_j dpre[t + W-1-j] w[j] (+ the
+// final-state gradient);  dweight[c][j] = sum_s dpre[s] xp[s + j].
+// A workgroup computes dpre for a block of kBlockTok tokens (each thread for its own kTok
+// tokens: no recomputation inside the block) and shares it through LDS; it writes dx
+// and accumulates dweight for the first kOut = kBlockTok - (W-1) tokens, so consecutive
+// blocks overlap by the W-1 tokens whose dpre the last outputs need.  dweight is reduced
+// over the workgroup (shuffles within a wave, LDS across waves) into one partial per
+// workgroup.
 template <int W>
-__global__ __launch_bounds__(256) void conv_bwd_kernel(ConvGeom g, const bf16* __restrict__ x,
+__global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __restrict__ x,
                                                        const bf16* __restrict__ w,
                                                        const bf16* __restrict__ st,
                                                        const bf16* __restrict__ dy,
                                                        const bf16* __restrict__ dfin,
                                                        bf16* __restrict__ dx,
                                                        float* __restrict__ dw_part) {
-  __shared__ float s_dw[256 / kWave][kGroups * 8 * W];
-  const int cb = blockIdx.x % g.ncb, tb = (blockIdx.x / g.ncb) % g.ntb, b = blockIdx.x / (g.ncb * g.ntb);
-  const int lg = threadIdx.x % kGroups, slice = threadIdx.x / kGroups;
-  const int cg = cb * kGroups + lg;
-  const int t0 = tb * kBlockTok + slice * kTok;
+  constexpr int kTok = BwdGeom::kTok, kCgs = BwdGeom::kCgs, kBlk = BwdGeom::kBlockTok;
+  constexpr int kOut = kBlk - (W - 1);
+  static_assert(kWave % kCgs == 0, "a wave must hold whole token slices");
+  static_assert(kOut > 0, "token block shorter than the filter");
+  // dpre in LDS as [u][half][thread] float4 (u < kTok, half = channels 0-3 / 4-7): a
+  // wave's store of one (u, half) is 64 consecutive 16-byte words (no bank conflicts).
+  __shared__ __attribute__((aligned(16))) float4 s_dp[kTok * 2 * 256];
+  __shared__ float s_dw[256 / kWave][kCgs * 8 * W];
+  const int cb = blockIdx.x % g.ncb, tb = (blockIdx.x / g.ncb) % g.ntb;
+  const int b = blockIdx.x / (g.ncb * g.ntb);
+  const int lg = threadIdx.x % kCgs, slice = threadIdx.x / kCgs;
+  const int cg = cb * kCgs + lg, c0 = cg * 8;
+  const int l0 = slice * kTok;          // first local token of this thread
+  const int s0 = tb * kOut + l0;        // its global token
+  const bool active = cg < g.CG;
   float dwacc[8][W];
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int j = 0; j < W; ++j) dwacc[e][j] = 0.f;
-  if (cg < g.CG && t0 < g.T) {
-    const int c0 = cg * 8;
-    float wt[8][W];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int j = 0; j < W; ++j) wt[e][j] = to_f32(w[(c0 + e) * W + j]);
-    // dpre for tokens t0 .. t0+kTok+W-2 needs xp[t0 .. t0+kTok+2W-3]
-    constexpr int NP = kTok + W - 1;
-    float xp[NP + W - 1][8];
-#pragma unroll
-    for (int i = 0; i < NP + W - 1; ++i) load_xp8<W>(x, st, b, g.T, g.C, c0, t0 + i, xp[i]);
-    float dp[NP][8];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int s = t0 + i;
-      if (s < g.T) {
-        float gy[8];
-        load8(dy + ((size_t)b * g.T + s) * g.C + c0, gy);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float pre = 0.f;
-#pragma unroll
-          for (int j = 0; j < W; ++j) pre = fmaf(xp[i + j][e], wt[e][j], pre);
-          dp[i][e] = gy[e] * silu_grad(pre);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dp[i][e] = 0.f;
-      }
-    }
+  float wt[8][W];
+  if (active) {
+    // dpre[s] for s = s0 .. s0+kTok-1 needs xp[s .. s+W-1], i.e. xp[s0 .. s0+kTok+W-2]
+    constexpr int NX = kTok + W - 1;
+    bf16x8 xr[NX], gr[kTok];
+    load_xp_rows<W, NX>(x, st, b, g.T, g.C, c0, s0, xr);
+    const bf16* dyb = dy + (size_t)b * g.T * g.C + c0;
 #pragma unroll
     for (int u = 0; u < kTok; ++u) {
-      const int t = t0 + u;
-      if (t >= g.T) break;
+      const int sc = s0 + u < g.T ? s0 + u : g.T - 1;
+      gr[u] = *reinterpret_cast<const bf16x8*>(dyb + (size_t)sc * g.C);
+    }
+    load_taps<W>(w, c0, wt);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
+    for (int u = 0; u < kTok; ++u) {
+      const bool live = s0 + u < g.T;
+      const bool owned = live && l0 + u < kOut;
+      float dp[8];
 #pragma unroll
-        for (int j = 0; j < W; ++j) dwacc[e][j] = fmaf(dp[u][e], xp[u + j][e], dwacc[e][j]);
+      for (int e = 0; e < 8; ++e) {
+        float xv[W];
+#pragma unroll
+        for (int j = 0; j < W; ++j) xv[j] = (float)xr[u + j][e];
+        float pre = 0.f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) pre = fmaf(xv[j], wt[e][j], pre);
+        dp[e] = live ? (float)gr[u][e] * silu_grad(pre) : 0.f;
+        const float dpo = owned ? dp[e] : 0.f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) dwacc[e][j] = fmaf(dpo, xv[j], dwacc[e][j]);
+      }
+      s_dp[(u * 2) * 256 + threadIdx.x] = make_float4(dp[0], dp[1], dp[2], dp[3]);
+      s_dp[(u * 2 + 1) * 256 + threadIdx.x] = make_float4(dp[4], dp[5], dp[6], dp[7]);
+    }
+  }
+  __syncthreads();
+  if (active) {
+    // dx for this thread's owned tokens: dpre rows l0 .. l0+kTok+W-2 (all inside the block
+    // for owned tokens, since l0 + u < kOut)
+    constexpr int ND = kTok + W - 1;
+    float dpw[ND][8];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      // local token l0 + i was computed by slice (l0 + i) / kTok as its token (i % kTok)
+      int src = threadIdx.x + (i / kTok) * kCgs;
+      src = src < 256 ? src : 255;  // only read for tokens a thread does not output
+      const float4 a = s_dp[((i % kTok) * 2) * 256 + src];
+      const float4 c = s_dp[((i % kTok) * 2 + 1) * 256 + src];
+      dpw[i][0] = a.x; dpw[i][1] = a.y; dpw[i][2] = a.z; dpw[i][3] = a.w;
+      dpw[i][4] = c.x; dpw[i][5] = c.y; dpw[i][6] = c.z; dpw[i][7] = c.w;
+    }
+    bf16* dxb = dx + ((size_t)b * g.T + s0) * g.C + c0;
+#pragma unroll
+    for (int u = 0; u < kTok; ++u) {
+      const int t = s0 + u;
+      if (l0 + u >= kOut || t >= g.T) break;
       float o[8];
-      const int jf = t + W - g.T;  // final-state slot fed by xp[t+W-1]
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < W; ++j) acc = fmaf(dp[u + W - 1 - j][e], wt[e][j], acc);
-        if (dfin && jf >= 0 && jf < W) acc += to_f32(dfin[((size_t)b * g.C + c0 + e) * W + jf]);
+        for (int j = 0; j < W; ++j) acc = fmaf(dpw[u + W - 1 - j][e], wt[e][j], acc);
         o[e] = acc;
       }
-      store8(dx + ((size_t)b * g.T + t) * g.C + c0, o);
+      const int jf = t + W - g.T;  // final-state slot fed by xp[t+W-1]
+      if (dfin && jf >= 0 && jf < W) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += to_f32(dfin[((size_t)b * g.C + c0 + e) * W + jf]);
+      }
+      store8(dxb + (size_t)u * g.C, o);
     }
   }
-  // reduce the 8 token slices of each wave with shuffles, then the 4 waves through LDS
+  // reduce the kWave/kCgs token slices of each wave across lanes, then the waves via LDS
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
     for (int j = 0; j < W; ++j) {
       float v = dwacc[e][j];
-      v += __shfl_xor(v, 8, kWave);
-      v += __shfl_xor(v, 16, kWave);
-      v += __shfl_xor(v, 32, kWave);
-      if (lane < kGroups) s_dw[wave][(lg * 8 + e) * W + j] = v;
+      v = lane_stride_sum<kCgs>(v);
+      if (lane < kCgs) s_dw[wave][(lg * 8 + e) * W + j] = v;
     }
   __syncthreads();
-  for (int i = threadIdx.x; i < kGroups * 8 * W; i += 256) {
+  for (int i = threadIdx.x; i < kCgs * 8 * W; i += 256) {
     float acc = 0.f;
+#pragma unroll
     for (int s = 0; s < 256 / kWave; ++s) acc += s_dw[s][i];
-    const int c = cb * kGroups * 8 + i / W;
+    const int c = cb * kCgs * 8 + i / W;
     if (c < g.C) dw_part[(size_t)(b * g.ntb + tb) * g.C * W + (size_t)c * W + i % W] = acc;
-  }
-}
-
-// dweight[c][j] = sum over (b, token block) partials.  Workgroup j owns 8 outputs; thread
-// (part, i) sums partials part, part + 32, ... in order, then the 32 part-sums are
-// combined in order through LDS (deterministic, no atomics).
-__global__ __launch_bounds__(256) void conv_dw_reduce_kernel(int tiles, int CW,
-                                                             const float* __restrict__ part,
-                                                             bf16* __restrict__ dw) {
-  __shared__ float s_red[32][8];
-  const int i = blockIdx.x * 8 + threadIdx.x % 8, q = threadIdx.x / 8;
-  float acc = 0.f;
-  if (i < CW)
-    for (int t = q; t < tiles; t += 32) acc += part[(size_t)t * CW + i];
-  s_red[q][threadIdx.x % 8] = acc;
-  __syncthreads();
-  if (threadIdx.x < 8 && i < CW) {
-    float t = 0.f;
-    for (int k = 0; k < 32; ++k) t += s_red[k][threadIdx.x];
-    dw[i] = to_bf16(t);
   }
 }
 
@@ -264,7 +334,7 @@ __global__ void conv_dstate_kernel(int B, int T, int C, const bf16* __restrict__
 template <int W>
 static int conv_forward_w(int B, int T, int C, const void* x, const void* w, const void* st,
                           void* y, void* fin, hipStream_t stream) {
-  const ConvGeom g(B, T, C);
+  const FwdGeom g(B, T, C);
   if (T > 0 && B > 0) {
     hipLaunchKernelGGL(conv_fwd_kernel<W>, dim3(g.blocks()), dim3(256), 0, stream, g,
                        (const bf16*)x, (const bf16*)w, (const bf16*)st, (bf16*)y);
@@ -283,7 +353,7 @@ template <int W>
 static int conv_backward_w(int B, int T, int C, const void* x, const void* w, const void* st,
                            const void* dy, const void* dfin, void* dx, void* dw, void* dst,
                            void* scratch, hipStream_t stream) {
-  const ConvGeom g(B, T, C);
+  const BwdGeom g(B, T, C, W - 1);
   float* part = (float*)scratch;
   const int tiles = B * g.ntb;
   if (T > 0 && B > 0) {
@@ -293,7 +363,7 @@ static int conv_backward_w(int B, int T, int C, const void* x, const void* w, co
     KDA_LAUNCH_CHECK("causal_conv_backward");
   }
   const int CW = C * W;
-  hipLaunchKernelGGL(conv_dw_reduce_kernel, dim3((CW + 7) / 8), dim3(256), 0, stream,
+  hipLaunchKernelGGL(dw_reduce_kernel<bf16>, dim3((CW * kDwRedLanes + 255) / 256), dim3(256), 0, stream,
                      (T > 0 && B > 0) ? tiles : 0, CW, (const float*)part, (bf16*)dw);
   KDA_LAUNCH_CHECK("causal_conv_dweight_reduce");
   if (dst) {
@@ -330,6 +400,7 @@ extern "C" int kda_causal_conv_forward(int32_t batch, int32_t seq_len, int32_t c
   KDA_REQUIRE(channels % 8 == 0, "causal_conv_forward: channels must be a multiple of 8");
   KDA_REQUIRE(width >= 1 && width <= 8, "causal_conv_forward: width must be in [1, 8]");
   KDA_REQUIRE(weight && (seq_len == 0 || (x && output)), "causal_conv_forward: null pointer");
+  KDA_REQUIRE(aligned16(x, weight, output), "causal_conv_forward: x, weight and output must be 16-byte aligned");
 #define CALL(W) conv_forward_w<W>(batch, seq_len, channels, x, weight, initial_state, output, final_state, stream)
   KDA_CONV_DISPATCH(width, CALL)
 #undef CALL
@@ -338,7 +409,8 @@ extern "C" int kda_causal_conv_forward(int32_t batch, int32_t seq_len, int32_t c
 
 extern "C" size_t kda_causal_conv_backward_scratch_bytes(int32_t batch, int32_t seq_len,
                                                          int32_t channels, int32_t width) {
-  const kda::ConvGeom g(batch, seq_len, channels);
+  if (width < 1 || width > 8) return 256;
+  const kda::BwdGeom g(batch, seq_len, channels, width - 1);
   return kda::align256((size_t)batch * g.ntb * channels * width * sizeof(float)) + 256;
 }
 
@@ -354,6 +426,8 @@ extern "C" int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t 
   KDA_REQUIRE(width >= 1 && width <= 8, "causal_conv_backward: width must be in [1, 8]");
   KDA_REQUIRE(weight && dweight && scratch, "causal_conv_backward: null pointer");
   KDA_REQUIRE(seq_len == 0 || (x && grad_output && dx), "causal_conv_backward: null pointer");
+  KDA_REQUIRE(aligned16(x, weight, grad_output, dx, scratch),
+              "causal_conv_backward: x, weight, grad_output, dx and scratch must be 16-byte aligned");
   KDA_REQUIRE(!dinitial_state || initial_state,
               "causal_conv_backward: dinitial_state requires initial_state");
 #define CALL(W) conv_backward_w<W>(batch, seq_len, channels, x, weight, initial_state, grad_output, grad_final_state, dx, dweight, dinitial_state, scratch, stream)

@@ -5,14 +5,23 @@
 //
 // State layout is V-first [B,H,V,K] f32, so one V row is K contiguous floats.  A
 // workgroup owns 32 V rows of one (b,h); a row is covered by K/4 lanes holding a float4
-// each, so every state access is a coalesced 16-byte load/store and the two row
-// reductions are in-wave shuffles.  Grid: (B*H) x (V/32) workgroups of 256 threads.
+// each, so every state access is a coalesced 16-byte load/store and the row reductions
+// are in-wave shuffles.  Every lane loads what it needs (its 4 keys of q, k, gate, the
+// state rows and their v) before it consumes anything, and derives its own keys'
+// normalised q, k and decay itself: the L2 norms are reductions over the K/4 lanes of a
+// row group, so there is no LDS and no barrier.  Grid: (B*H) x (V/32) workgroups of 256.
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
 namespace kda {
 
 constexpr int kDecodeRowsPerBlock = 32;
+
+__device__ __forceinline__ void load4bf(const bf16* p, float* out) {
+  const bf16x4 x = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (float)x[e];
+}
 
 template <int K>
 __global__ __launch_bounds__(256) void decode_kernel(
@@ -24,8 +33,6 @@ __global__ __launch_bounds__(256) void decode_kernel(
   constexpr int LPR = K / 4;          // lanes per V row
   constexpr int RPP = kWave / LPR;    // rows per wave pass
   constexpr int NPASS = kDecodeRowsPerBlock / (4 * RPP);  // rows per thread
-  __shared__ float s_q[K], s_kd[K], s_k[K], s_eg[K];
-  __shared__ float s_beta;
   const int bh = blockIdx.x;
   const int h = bh % heads;
   const int tid = threadIdx.x;
@@ -35,62 +42,52 @@ __global__ __launch_bounds__(256) void decode_kernel(
   const int k0 = kl * 4;
   const int row_base = blockIdx.y * kDecodeRowsPerBlock;
 
-  // issue the state loads first: they are independent of the per-key prologue
+  // every load first: state rows, their v, and this lane's 4 keys
   float4 sv4[NPASS];
+  float vr[NPASS];
 #pragma unroll
   for (int ps = 0; ps < NPASS; ++ps) {
     const int row = row_base + ps * 4 * RPP + wave * RPP + sub;
-    const size_t off = ((size_t)bh * V + row) * K + k0;
-    sv4[ps] = (initial_state && row < V) ? *reinterpret_cast<const float4*>(initial_state + off)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int rc = row < V ? row : V - 1;
+    const size_t off = ((size_t)bh * V + rc) * K + k0;
+    sv4[ps] = initial_state ? *reinterpret_cast<const float4*>(initial_state + off)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[ps] = (float)v[tok * V + rc];
   }
-
-  if (tid < kWave) {
-    // wave 0 prepares the per-key quantities (K <= 128 -> two keys per lane)
-    float qv[2], kv[2];
-    float sq = 0.f, sk = 0.f;
+  float qv[4], kv[4], gv[4];
+  load4bf(q + tok * K + k0, qv);
+  load4bf(k + tok * K + k0, kv);
+  const float bl = (float)beta_logits[tok];
+  if (gate_mode == KDA_GATE_K3) {
+    float raw[4];
+    load4bf(reinterpret_cast<const bf16*>(gate) + tok * K + k0, raw);
+    const float4 db = *reinterpret_cast<const float4*>(dt_bias + (size_t)h * K + k0);
+    const float ea = expf(A_log[h]);
+    const float dbv[4] = {db.x, db.y, db.z, db.w};
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int c = tid + j * kWave;
-      qv[j] = c < K ? to_f32(q[tok * K + c]) : 0.f;
-      kv[j] = c < K ? to_f32(k[tok * K + c]) : 0.f;
-      sq += qv[j] * qv[j];
-      sk += kv[j] * kv[j];
-    }
-    sq = wave_sum(sq);
-    sk = wave_sum(sk);
-    const float rq = scale / fmaxf(sqrtf(sq), 1e-12f);
-    const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int c = tid + j * kWave;
-      if (c < K) {
-        float g;
-        if (gate_mode == KDA_GATE_K3) {
-          float raw = to_f32(reinterpret_cast<const bf16*>(gate)[tok * K + c]);
-          g = lb * sigmoid_acc(expf(A_log[h]) * (raw + dt_bias[h * K + c]));
-        } else {
-          g = reinterpret_cast<const float*>(gate)[tok * K + c];
-        }
-        float eg = expf(g);
-        s_q[c] = qv[j] * rq;
-        s_k[c] = kv[j] * rk;
-        s_eg[c] = eg;
-        s_kd[c] = kv[j] * rk * eg;
-      }
-    }
-    if (tid == 0) s_beta = sigmoid_acc(to_f32(beta_logits[tok]));
+    for (int e = 0; e < 4; ++e) gv[e] = lb * sigmoid_acc(ea * (raw[e] + dbv[e]));
+  } else {
+    const float4 g4 = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(gate) + tok * K + k0);
+    gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
   }
-  __syncthreads();
-
-  const float beta = s_beta;
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sq = fmaf(qv[e], qv[e], sq);
+    sk = fmaf(kv[e], kv[e], sk);
+  }
+  sq = group_sum<LPR>(sq);
+  sk = group_sum<LPR>(sk);
+  const float rq = scale / fmaxf(sqrtf(sq), 1e-12f);
+  const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+  const float beta = sigmoid_acc(bl);
   float qk[4], kk[4], kd[4], eg[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    qk[e] = s_q[k0 + e];
-    kk[e] = s_k[k0 + e];
-    kd[e] = s_kd[k0 + e];
-    eg[e] = s_eg[k0 + e];
+    eg[e] = expf(gv[e]);
+    qk[e] = qv[e] * rq;
+    kk[e] = kv[e] * rk;
+    kd[e] = kk[e] * eg[e];
   }
 #pragma unroll
   for (int ps = 0; ps < NPASS; ++ps) {
@@ -99,14 +96,14 @@ __global__ __launch_bounds__(256) void decode_kernel(
     float sv[4] = {sv4[ps].x, sv4[ps].y, sv4[ps].z, sv4[ps].w};
     float pred = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pred += kd[e] * sv[e];
+    for (int e = 0; e < 4; ++e) pred = fmaf(kd[e], sv[e], pred);
     pred = group_sum<LPR>(pred);
-    const float r = (row < V ? to_f32(v[tok * V + row]) : 0.f) - pred;
+    const float r = vr[ps] - pred;
     float o = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sv[e] = eg[e] * sv[e] + beta * kk[e] * r;
-      o += qk[e] * sv[e];
+      o = fmaf(qk[e], sv[e], o);
     }
     o = group_sum<LPR>(o);
     if (row < V) {
@@ -135,6 +132,8 @@ extern "C" int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_di
   KDA_REQUIRE(q && k && v && gate && beta_logits && output, "recurrent_decode: null pointer");
   KDA_REQUIRE(gate_mode != KDA_GATE_K3 || (A_log && dt_bias),
               "recurrent_decode: K3 gate needs A_log and dt_bias");
+  KDA_REQUIRE(aligned16(q, k, gate, dt_bias, initial_state, final_state),
+              "recurrent_decode: q, k, gate, dt_bias and the states must be 16-byte aligned");
   if (batch == 0) return KDA_OK;
   dim3 grid(batch * heads, (value_dim + kDecodeRowsPerBlock - 1) / kDecodeRowsPerBlock);
   auto args = [&](auto kern) {

@@ -36,6 +36,14 @@ __device__ __forceinline__ f32x4 zero4() {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Sigmoid from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; each about 1 ulp):
+// five VALU instructions, no branch.  For elementwise kernels whose results are rounded to
+// bf16, where the accurate form below would make them VALU-bound.  Saturates correctly:
+// exp(-x) -> inf gives 0, exp(-x) -> 0 gives 1.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
 // Full-precision sigmoid used where the value feeds a gradient chain.
 __device__ __forceinline__ float sigmoid_acc(float x) {
   if (x >= 0.f) return 1.0f / (1.0f + expf(-x));
@@ -43,11 +51,49 @@ __device__ __forceinline__ float sigmoid_acc(float x) {
   return e / (1.0f + e);
 }
 
+// Cross-lane sums without LDS round trips.  Within a 16-lane row, DPP modifiers fold the
+// partner's value into a VALU add (quad_perm, row mirrors, row rotates); across rows,
+// gfx950's v_permlane16_swap / v_permlane32_swap exchange whole rows.  Every step adds two
+// values commutatively, so all lanes of a group end with bit-identical sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+// v(lane) + v(lane ^ 16)
+__device__ __forceinline__ float swap16_sum(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+// v(lane) + v(lane ^ 32)
+__device__ __forceinline__ float swap32_sum(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-  // sum over aligned groups of W lanes (W power of two, W <= 64)
-#pragma unroll
-  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  // sum over aligned groups of W lanes (W power of two, W <= 64), result in every lane
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  if constexpr (W >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (W >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (W >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror: quad 0 <-> quad 1
+  if constexpr (W >= 16) v += dpp_mov<0x140>(v); // row_mirror: half-row 0 <-> half-row 1
+  if constexpr (W >= 32) v = swap16_sum(v);
+  if constexpr (W >= 64) v = swap32_sum(v);
+  return v;
+}
+
+// Sum over the lanes congruent to this lane modulo S (S in {8, 16, 32, 64}): lanes that
+// hold the same column of a [64/S][S] lane grid.  Result in every such lane.
+template <int S>
+__device__ __forceinline__ float lane_stride_sum(float v) {
+  static_assert(S == 8 || S == 16 || S == 32 || S == 64, "stride");
+  if constexpr (S <= 8) v += dpp_mov<0x128>(v);  // row_ror:8 within 16 lanes: lane ^ 8
+  if constexpr (S <= 16) v = swap16_sum(v);
+  if constexpr (S <= 32) v = swap32_sum(v);
   return v;
 }
 
@@ -95,6 +141,34 @@ __device__ __forceinline__ void load8f(const float* p, float* out) {
   const float4 b = *reinterpret_cast<const float4*>(p + 4);
   out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
   out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
+// Weight-gradient finish: out[i] = sum over `parts` partials (row-major [parts][n]),
+// launched with kDwRedLanes threads per output.  Lane l of an output loads partials l,
+// l + kDwRedLanes, ... (a batch of loads issued before any is added), sums them in order,
+// and the lanes combine through group_sum's fixed tree (deterministic, no atomics).
+constexpr int kDwRedLanes = 32;
+template <typename OutT>
+__global__ __launch_bounds__(256) void dw_reduce_kernel(int parts, int n,
+                                                        const float* __restrict__ part,
+                                                        OutT* __restrict__ out) {
+  constexpr int kRedLanes = kDwRedLanes, kBatch = 8;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int i = gid / kRedLanes, l = gid % kRedLanes;
+  const int ic = i < n ? i : n - 1;
+  float acc = 0.f;
+  for (int p0 = l; p0 < parts; p0 += kBatch * kRedLanes) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int p = p0 + u * kRedLanes;
+      v[u] = p < parts ? part[(size_t)p * n + ic] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) acc += v[u];
+  }
+  acc = group_sum<kRedLanes>(acc);
+  if (l == 0 && i < n) out[i] = (OutT)acc;
 }
 
 }  // namespace kda

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 
 #include "../../include/kda_mi355x.h"
@@ -20,6 +21,13 @@ inline int check_launch(const char* what) {
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// True when every pointer is null or 16-byte aligned (the kernels move 16-byte vectors).
+inline bool aligned16() { return true; }
+template <typename P, typename... R>
+inline bool aligned16(P p, R... rest) {
+  return ((uintptr_t)p % 16) == 0 && aligned16(rest...);
+}
 
 }  // namespace kda
 

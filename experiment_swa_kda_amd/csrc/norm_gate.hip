@@ -2,17 +2,18 @@
 // Reference: nanochat/mixers/cuda_kda/rmsnorm_gate.cu:31-184; semantics
 // nanochat/mixers/kda.py:46-59 (F.rms_norm(x, weight) * sigmoid(gate)).
 //
-// HBM-bound.  D/8 lanes own one row (one 16-byte bf16x8 vector each), so a wave covers
-// 64/(D/8) rows per pass with coalesced loads and an in-wave shuffle reduction.  The
-// grid is a fixed number of workgroups striding over rows, so the per-workgroup weight
-// gradient partials are summed in a fixed order (deterministic).  Arithmetic is f32 with
-// one rounding to bf16 at the store.
+// HBM-bound.  D/8 lanes own one row (one 16-byte bf16x8 vector each); a thread handles
+// kRows rows spaced one row-pass apart, so every load instruction of a wave is coalesced
+// and all of a thread's loads are issued before any is consumed.  A workgroup owns a
+// contiguous block of 256 / (D/8) * kRows rows; reductions over a row are in-wave
+// shuffles.  The per-workgroup weight-gradient partials are summed in a fixed order
+// (deterministic).  Arithmetic is f32 with one rounding to bf16 at the store.
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
 namespace kda {
 
-constexpr int kNormBlocksMax = 512;
+constexpr int kRows = 4;  // rows per thread
 
 template <int D>
 __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf16* __restrict__ x,
@@ -21,25 +22,35 @@ __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf1
                                                             float eps, bf16* __restrict__ y,
                                                             float* __restrict__ inv_rms) {
   constexpr int LPR = D / 8;
-  constexpr int RPB = 256 / LPR;
+  constexpr int RPP = 256 / LPR;  // rows per pass of the workgroup
   const int lane = threadIdx.x % LPR;
   const int c0 = lane * 8;
-  float w[8];
+  const long r0 = (long)blockIdx.x * RPP * kRows + threadIdx.x / LPR;
+  bf16x8 xr[kRows], gr[kRows];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) w[e] = weight[c0 + e];
-  for (long r = (long)blockIdx.x * RPB + threadIdx.x / LPR; r < rows; r += (long)gridDim.x * RPB) {
-    float xv[8], gv[8], o[8];
-    load8(x + r * D + c0, xv);
-    load8(gate + r * D + c0, gv);
+  for (int i = 0; i < kRows; ++i) {
+    long r = r0 + (long)i * RPP;
+    r = r < rows ? r : rows - 1;
+    xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
+    gr[i] = *reinterpret_cast<const bf16x8*>(gate + r * D + c0);
+  }
+  float w[8];
+  load8f(weight + c0, w);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const long r = r0 + (long)i * RPP;
     float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+    for (int e = 0; e < 8; ++e) ss = fmaf((float)xr[i][e], (float)xr[i][e], ss);
     ss = group_sum<LPR>(ss);
     const float inv = rsqrtf(ss / D + eps);
+    float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = xv[e] * inv * w[e] * sigmoid_acc(gv[e]);
-    store8(y + r * D + c0, o);
-    if (lane == 0) inv_rms[r] = inv;
+    for (int e = 0; e < 8; ++e) o[e] = (float)xr[i][e] * inv * w[e] * sigmoid_fast((float)gr[i][e]);
+    if (r < rows) {
+      store8(y + r * D + c0, o);
+      if (lane == 0) inv_rms[r] = inv;
+    }
   }
 }
 
@@ -50,74 +61,72 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     const bf16* __restrict__ dy, bf16* __restrict__ dx, bf16* __restrict__ dgate,
     float* __restrict__ dw_part) {
   constexpr int LPR = D / 8;
-  constexpr int RPB = 256 / LPR;
-  __shared__ float s_dw[RPB][D + 1];
+  constexpr int RPP = 256 / LPR;
+  __shared__ float s_dw[256 / kWave][D];
   const int lane = threadIdx.x % LPR;
-  const int slot = threadIdx.x / LPR;
   const int c0 = lane * 8;
-  float w[8], dwacc[8];
+  const long r0 = (long)blockIdx.x * RPP * kRows + threadIdx.x / LPR;
+  bf16x8 xr[kRows], gr[kRows], dr[kRows];
+  float ir[kRows];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    w[e] = weight[c0 + e];
-    dwacc[e] = 0.f;
+  for (int i = 0; i < kRows; ++i) {
+    long r = r0 + (long)i * RPP;
+    r = r < rows ? r : rows - 1;
+    xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
+    gr[i] = *reinterpret_cast<const bf16x8*>(gate + r * D + c0);
+    dr[i] = *reinterpret_cast<const bf16x8*>(dy + r * D + c0);
+    ir[i] = inv_rms[r];
   }
-  for (long r = (long)blockIdx.x * RPB + slot; r < rows; r += (long)gridDim.x * RPB) {
-    float xv[8], gv[8], g[8], dn[8], n[8], o[8], og[8];
-    load8(x + r * D + c0, xv);
-    load8(gate + r * D + c0, gv);
-    load8(dy + r * D + c0, g);
-    const float inv = inv_rms[r];
+  float w[8], dwacc[8];
+  load8f(weight + c0, w);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dwacc[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const long r = r0 + (long)i * RPP;
+    const bool live = r < rows;
+    const float inv = ir[i];
+    float dn[8], n[8], o[8], og[8];
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float s = sigmoid_acc(gv[e]);
-      n[e] = xv[e] * inv;
-      dn[e] = g[e] * s * w[e];
-      dot += dn[e] * n[e];
-      og[e] = g[e] * n[e] * w[e] * s * (1.f - s);
-      dwacc[e] += g[e] * s * n[e];
+      const float g = live ? (float)dr[i][e] : 0.f;
+      const float s = sigmoid_fast((float)gr[i][e]);
+      n[e] = (float)xr[i][e] * inv;
+      dn[e] = g * s * w[e];
+      dot = fmaf(dn[e], n[e], dot);
+      og[e] = g * n[e] * w[e] * s * (1.f - s);
+      dwacc[e] = fmaf(g * s, n[e], dwacc[e]);
     }
     dot = group_sum<LPR>(dot) / D;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = inv * (dn[e] - n[e] * dot);
-    store8(dx + r * D + c0, o);
-    store8(dgate + r * D + c0, og);
+    if (live) {
+      store8(dx + r * D + c0, o);
+      store8(dgate + r * D + c0, og);
+    }
   }
+  // rows of one channel slot: reduce the wave's kWave/LPR row slots across lanes, then
+  // the waves through LDS, in a fixed order
+  const int wave = threadIdx.x / kWave;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s_dw[slot][c0 + e] = dwacc[e];
+  for (int e = 0; e < 8; ++e) {
+    float v = dwacc[e];
+    v = lane_stride_sum<LPR>(v);
+    if (threadIdx.x % kWave < LPR) s_dw[wave][c0 + e] = v;
+  }
   __syncthreads();
   if (threadIdx.x < D) {
     float acc = 0.f;
-    for (int s = 0; s < RPB; ++s) acc += s_dw[s][threadIdx.x];
+#pragma unroll
+    for (int s = 0; s < 256 / kWave; ++s) acc += s_dw[s][threadIdx.x];
     dw_part[(size_t)blockIdx.x * D + threadIdx.x] = acc;
   }
 }
 
-// dweight[c] = sum over workgroup partials.  Workgroup j owns 8 channels; thread
-// (part, c) sums partials part, part + 32, ... in order and the 32 part-sums are combined
-// in order through LDS (deterministic, no atomics).
-constexpr int kRedParts = 32;
-__global__ __launch_bounds__(256) void norm_dw_reduce_kernel(int blocks, int D,
-                                                             const float* __restrict__ part,
-                                                             float* __restrict__ dw) {
-  __shared__ float s_red[kRedParts][8];
-  const int c = blockIdx.x * 8 + threadIdx.x % 8, q = threadIdx.x / 8;
-  float acc = 0.f;
-  if (c < D)
-    for (int b = q; b < blocks; b += kRedParts) acc += part[(size_t)b * D + c];
-  s_red[q][threadIdx.x % 8] = acc;
-  __syncthreads();
-  if (threadIdx.x < 8 && c < D) {
-    float t = 0.f;
-    for (int k = 0; k < kRedParts; ++k) t += s_red[k][threadIdx.x];
-    dw[c] = t;
-  }
-}
-
 static int norm_blocks(long rows, int dim) {
-  const long rpb = 256 / (dim / 8);
+  const long rpb = 256 / (dim / 8) * kRows;
   long nb = (rows + rpb - 1) / rpb;
-  if (nb > kNormBlocksMax) nb = kNormBlocksMax;
   if (nb < 1) nb = 1;
   return (int)nb;
 }
@@ -133,6 +142,8 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
   KDA_REQUIRE(eps > 0.f, "rmsnorm_gate_forward: eps must be positive");
   KDA_REQUIRE(weight && (rows == 0 || (x && gate && output && inv_rms)),
               "rmsnorm_gate_forward: null pointer");
+  KDA_REQUIRE(aligned16(x, gate, weight, output),
+              "rmsnorm_gate_forward: x, gate, weight and output must be 16-byte aligned");
   if (rows == 0) return KDA_OK;
   const int nb = norm_blocks(rows, dim);
   if (dim == 128)
@@ -161,6 +172,8 @@ extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* 
   KDA_REQUIRE(weight && dweight && scratch, "rmsnorm_gate_backward: null pointer");
   KDA_REQUIRE(rows == 0 || (x && gate && inv_rms && grad_output && dx && dgate),
               "rmsnorm_gate_backward: null pointer");
+  KDA_REQUIRE(aligned16(x, gate, weight, grad_output, dx, dgate, scratch),
+              "rmsnorm_gate_backward: x, gate, weight, grad_output, dx, dgate and scratch must be 16-byte aligned");
   const int nb = norm_blocks(rows, dim);
   float* part = (float*)scratch;
   if (rows > 0) {
@@ -174,8 +187,8 @@ extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* 
                          (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, part);
     KDA_LAUNCH_CHECK("rmsnorm_gate_backward");
   }
-  hipLaunchKernelGGL(norm_dw_reduce_kernel, dim3((dim + 7) / 8), dim3(256), 0, stream, rows > 0 ? nb : 0, dim,
-                     (const float*)part, dweight);
+  hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3((dim * kDwRedLanes + 255) / 256), dim3(256), 0, stream,
+                     rows > 0 ? nb : 0, dim, (const float*)part, dweight);
   KDA_LAUNCH_CHECK("rmsnorm_gate_dweight_reduce");
   return KDA_OK;
 }

@@ -43,7 +43,14 @@ def _require_cuda(what: str, *tensors) -> torch.device:
 
 
 def _c(t):
-    return None if t is None else t.contiguous()
+    """Contiguous and 16-byte aligned (the kernels move 16-byte vectors): a view with an
+    unaligned storage offset is copied."""
+    if t is None:
+        return None
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
 
 
 def _check_dtype(what, t, dtype, name):

@@ -114,10 +114,12 @@ def test_decode_in_place_and_input_preserved():
     assert torch.equal(o1, o2) and torch.equal(f1, s)
 
 
-@pytest.mark.parametrize("T,state,W", [(1, True, 4), (3, True, 4), (50, False, 4), (257, True, 4), (33, True, 3)])
-def test_conv_forward_backward(T, state, W):
+@pytest.mark.parametrize("T,state,W,C", [(1, True, 4, 384), (3, True, 4, 384), (50, False, 4, 384),
+                                         (257, True, 4, 384), (33, True, 3, 384), (128, True, 4, 136),
+                                         (129, False, 2, 8), (255, True, 8, 264), (7, True, 1, 128)])
+def test_conv_forward_backward(T, state, W, C):
     g = torch.Generator().manual_seed(T)
-    B, C = 2, 384
+    B = 2
     x = torch.randn(B, T, C, generator=g).bfloat16()
     w = (torch.randn(C, W, generator=g) * 0.5).bfloat16()
     st = torch.randn(B, C, W, generator=g).bfloat16() if state else None
@@ -134,15 +136,29 @@ def test_conv_forward_backward(T, state, W):
         assert rel_err(dst, edst) < 5e-3
 
 
-def test_rmsnorm_gate_forward_backward():
+@pytest.mark.parametrize("T,D", [(100, 128), (37, 64), (1, 128)])
+def test_rmsnorm_gate_forward_backward(T, D):
     g = torch.Generator().manual_seed(1)
-    x = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
-    gt = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
-    w = torch.randn(128, generator=g).float()
-    dy = torch.randn(2, 100, 3, 128, generator=g).bfloat16()
+    x = torch.randn(2, T, 3, D, generator=g).bfloat16()
+    gt = torch.randn(2, T, 3, D, generator=g).bfloat16()
+    w = torch.randn(D, generator=g).float()
+    dy = torch.randn(2, T, 3, D, generator=g).bfloat16()
     y, inv = ops.rmsnorm_gate_forward(x.cuda(), gt.cuda(), w.cuda(), 1e-5)
     ey, einv = O.rmsnorm_gate_forward(np64(x), np64(gt), np64(w), 1e-5)
     assert rel_err(y, ey) < 5e-3 and rel_err(inv, einv.reshape(-1)) < 1e-5
     dx, dg, dw = ops.rmsnorm_gate_backward(x.cuda(), gt.cuda(), w.cuda(), inv, dy.cuda(), 1e-5)
     edx, edg, edw = O.rmsnorm_gate_backward(np64(x), np64(gt), np64(w), 1e-5, np64(dy))
     assert rel_err(dx, edx) < 5e-3 and rel_err(dg, edg) < 5e-3 and rel_err(dw, edw) < 1e-4
+
+
+def test_unaligned_views_are_copied_before_the_kernels():
+    """A contiguous view at an odd element offset is not 16-byte aligned; the host layer
+    copies it, so results equal those of the aligned tensor."""
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn(2 * 64 * 128 + 1, generator=g).bfloat16().cuda()
+    x = base[1:].view(2, 64, 128)
+    assert x.data_ptr() % 16 != 0
+    w = (torch.randn(128, 4, generator=g) * 0.5).bfloat16().cuda()
+    y, _ = ops.causal_conv_forward(x, w, None, False)
+    y2, _ = ops.causal_conv_forward(x.clone(), w, None, False)
+    assert torch.equal(y, y2)
