@@ -23,6 +23,11 @@ LIB_NAME = "libkda_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
 SOURCES = ["capi.cpp", "decode.hip", "conv.hip", "norm_gate.hip", "chunk_fwd.hip", "chunk_bwd.hip"]
+# Per-source extra flags.  The chunk kernels keep MFMA accumulators in VGPRs: their
+# accumulators feed VALU work every step, and the AGPR form costs a copy per element.
+EXTRA_FLAGS = {
+    "chunk_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 ARCH = "gfx950"
 
 
@@ -49,7 +54,7 @@ def _flags() -> list[str]:
 def _compile(src: str) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [_hipcc(), *_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [_hipcc(), *_flags(), *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")

@@ -317,13 +317,14 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
     }
   }
-  // delta from its B-operand fragments [strip][2][64 lanes][8]: (t = 32 s + 8 (l/16) + e, v)
+  // delta from its B-operand fragments [strip][2][64 lanes][8] in the scan's permuted
+  // token order: element e of lane l is t = 32 s + 16 (e/4) + 4 (l/16) + e%4
   for (int idx = tid; idx < 64 * V / 8; idx += kVjpThreads) {
     const int lane_ = idx % 64, sl = (idx / 64) % 2, strip = idx / 128;
     const bf16x8 x = *(const bf16x8*)(DLF + (size_t)idx * 8);
-    const int vv = 16 * strip + lane_ % 16, t0 = 32 * sl + 8 * (lane_ / 16);
+    const int vv = 16 * strip + lane_ % 16, t0 = 32 * sl + 4 * (lane_ / 16);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sDL[(t0 + e) * VP + vv] = x[e];
+    for (int e = 0; e < 8; ++e) sDL[(t0 + 16 * (e / 4) + e % 4) * VP + vv] = x[e];
   }
   if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;

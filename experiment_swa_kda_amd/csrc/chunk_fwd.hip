@@ -11,7 +11,7 @@
 //
 // MI355X design:
 //  * kda_chunk_prep: builds the chunk / sequence tables (B x T or packed cu_seqlens).
-//  * intra kernel: one 256-thread workgroup per (chunk, head) tile, everything staged in
+//  * intra kernel: one 1024-thread workgroup per (chunk, head) tile, everything staged in
 //    LDS (f32 qh/kh/G).  The 64x64 A and M' are built as 16x16 MFMA tiles
 //    (v_mfma_f32_16x16x32_bf16).  Pairwise decays exp(G_i - G_j) are factorised around
 //    the first row r of the row block: exp(G_i - G_r) <= 1 and, for j < r,
@@ -21,10 +21,10 @@
 //    U and W by MFMA.  Factors are written once to the workspace in both row- and
 //    column-major form so every later MFMA operand is a contiguous 16-byte load.
 //  * scan kernel: one workgroup per (sequence, head, 16-wide V strip) walks the chunks
-//    in order holding its 128x16 f32 state slice in VGPRs as MFMA accumulators; the V
-//    columns of the state evolve independently, so strips never communicate.  Each step
-//    computes delta = U - W S, the output tile, and S <- lam S + Kd^T delta, and records
-//    the bf16 state and delta for the backward pass.
+//    in order; one wave holds the K x 16 f32 state slice in MFMA accumulators and runs
+//    delta = U - W S and S <- lam S + Kd^T delta from registers, fed by two loader waves
+//    (direct global->LDS ring) and drained by a store wave (state / delta histories).
+//  * output kernel: O = Qg S + A delta, chunk-parallel after the scan.
 // Every reduction has a fixed order, so the forward is bitwise deterministic.
 #include "chunk_host.hpp"
 #include "kda_device.hpp"
@@ -114,16 +114,25 @@ struct IntraSmem {
   static_assert(64 * (K + 8) * 2 <= 64 * KP * 4, "W staging must fit the q_hat region");
 };
 
+// Column of element e held by lane group kg in 32-wide step s of a fragment: natural
+// (32s + 8kg + e) or permuted to match two MFMA accumulator tiles (32s + 16(e/4) + 4kg +
+// e%4: a lane's accumulator rows of tiles 2s and 2s+1), see the scan kernel.
+template <bool PERM>
+__device__ __forceinline__ int frag_col(int s, int kg, int e) {
+  return PERM ? 32 * s + 16 * (e / 4) + 4 * kg + (e % 4) : 32 * s + 8 * kg + e;
+}
+
 // Writes the MFMA A-operand fragments of an R x C matrix whose element (r, c) is val(r, c)
-// (see frag_off); one 16-byte piece per thread iteration, contiguous across threads.
-template <int R, int C, int NT, typename F>
+// (see frag_off; PERM selects the permuted column order of frag_col); one 16-byte piece
+// per thread iteration, contiguous across threads.
+template <int R, int C, int NT, bool PERM = false, typename F>
 __device__ __forceinline__ void emit_frags(bf16* dst, int tid, F val) {
   for (int idx = tid; idx < R * C / 8; idx += NT) {
     const int lane = idx % 64, s = (idx / 64) % (C / 32), rt = idx / (64 * (C / 32));
-    const int r = 16 * rt + lane % 16, c0 = 32 * s + 8 * (lane / 16);
+    const int r = 16 * rt + lane % 16, kg = lane / 16;
     bf16x8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = val(r, c0 + e);
+    for (int e = 0; e < 8; ++e) x[e] = val(r, frag_col<PERM>(s, kg, e));
     *(bf16x8*)(dst + (size_t)idx * 8) = x;
   }
 }
@@ -317,12 +326,12 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
   // ---- A, Qg = qh exp(G), Kd = kh exp(G_last - G) as MFMA fragments (+ transposes) ----
   {
     constexpr int NT = kIntraThreads;
-    emit_frags<64, 64, NT>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
+    emit_frags<64, 64, NT, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
                            [&](int r, int c) { return sAs[r * AP + c]; });
     emit_frags<64, 64, NT>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
                            [&](int r, int c) { return sAs[c * AP + r]; });
     const float* gl = sG + 63 * KP;
-    emit_frags<64, K, NT>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid, [&](int r, int c) {
+    emit_frags<64, K, NT, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid, [&](int r, int c) {
       return to_bf16(sQ[r * KP + c] * expf(sG[r * KP + c]));
     });
     emit_frags<K, 64, NT>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid, [&](int r, int c) {
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
     emit_frags<64, K, NT>((bf16*)a.ws.p[R_KDF] + tile * 64 * K, tid, [&](int r, int c) {
       return to_bf16(sK[r * KP + c] * expf(gl[c] - sG[r * KP + c]));
     });
-    emit_frags<K, 64, NT>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, [&](int r, int c) {
+    emit_frags<K, 64, NT, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, [&](int r, int c) {
       return to_bf16(sK[c * KP + r] * expf(gl[r] - sG[c * KP + r]));
     });
   }
@@ -415,8 +424,8 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
     }
   }
   __syncthreads();
-  emit_frags<64, K, kIntraThreads>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
-                                   [&](int r, int c) { return sWs[r * WP + c]; });
+  emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
+                                         [&](int r, int c) { return (bf16)(-(float)sWs[r * WP + c]); });
   emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid,
                                    [&](int r, int c) { return sWs[c * WP + r]; });
 
@@ -425,62 +434,175 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
 // ---------------------------------------------------------------------------
 // inter-chunk state scan
 // ---------------------------------------------------------------------------
-// One 256-thread workgroup per (sequence, head, 16-wide V strip).  The critical path
-// per chunk is: publish S (LDS) -> delta = U - W S -> publish delta (LDS) ->
-// S <- lam S + Kd^T delta, two barriers.  All global operands of a chunk are loaded
-// into a register ring kFwdRing chunks ahead, so the HBM latency (~1-2 us) overlaps
-// several chunk steps.  Every per-step global access is one vector instruction (CDNA
-// counts loads and stores on the same vmcnt, which must stay below 64 in flight).
-constexpr int kFwdRing = 4;
-
-template <int K>
-struct FwdScanFrag {
-  bf16x8 w[K / 32];      // W rows of this wave's delta tile
-  bf16x4 ut;             // U: the 4 entries of this lane's delta outputs (C layout)
-  bf16x8 kdt[K / 64][2]; // Kd^T rows of this wave's state tiles
-  float4 lam[K / 64];    // exp(G_last) of this lane's state rows
-};
+// One workgroup per (sequence, head, 16-wide V strip): a compute wave, two loader waves and
+// a store wave.  The V columns of the state evolve independently, so strips never
+// communicate.
+//
+// The compute wave holds the K x 16 f32 state slice as K/16 MFMA accumulator tiles (lane
+// l: rows 16kt + 4(l/16) + r, column l%16) and runs each chunk step from registers:
+//   delta = U + (-W) S     (S as the B operand; U is the accumulator input),
+//   S     = lam S + Kd^T delta  (delta as B; lam S is the accumulator input).
+// The B operand of a 32-deep MFMA step wants 8 values per lane; the two accumulator tiles
+// 2s and 2s+1 give a lane exactly 8 values of its column, so the intra kernel stores W and
+// Qg with their key columns (and Kd^T and A with their token columns) in the matching
+// permuted order (frag_col<true>): an accumulator becomes the next product's operand with
+// one conversion.  The per-step critical path is pack -> 16 MFMAs -> pack -> 16 MFMAs.
+//
+// The loader waves stream each chunk's -W and Kd^T fragments, U strip and lam into a
+// kScanRing-deep LDS ring with direct global->LDS loads, kScanRing - 1 chunks ahead.  The
+// compute wave writes its histories (f32 and bf16 state, delta) to a double-buffered LDS
+// staging area, which the store wave copies to HBM one step later, so no global access
+// sits in the compute wave's instruction stream.  Per chunk the four waves meet at one
+// barrier: before it the loaders wait (vmcnt) for the slot of that chunk and the compute
+// and store waves for their LDS accesses (lgkmcnt); after it the loaders refill the slot
+// the compute wave released.
+constexpr int kScanRing = 3;
+constexpr int kScanThreads = 4 * kWave;
 
 template <int K, int V>
-__global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
-  constexpr int KT = K / 16 / 4;  // 16-row key tiles of the state per wave
-  constexpr int SP = K + 8;
-  constexpr int DP = 64 + 8;
-  constexpr int FP = 16 + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sS[2][16 * SP];  // bf16 S as [v][k]
-  __shared__ __attribute__((aligned(16))) float sSf[K * FP];    // f32 S as [k][v]
-  __shared__ __attribute__((aligned(16))) bf16 sD[16 * DP];     // delta as [v][t]
+struct ScanLds {
+  static constexpr int off_w = 0;                       // -W fragments, 64 x K bf16
+  static constexpr int off_kdt = off_w + 64 * K * 2;    // Kd^T fragments, K x 64 bf16
+  static constexpr int off_u = off_kdt + K * 64 * 2;    // U strip, C layout, 64 x 16 bf16
+  static constexpr int off_lam = off_u + 64 * 16 * 2;   // lam, K f32
+  static constexpr int slot = off_lam + K * 4;
+  static constexpr int n_load0 = (64 * K * 2) / 1024 + 2;  // loader 0: W blocks + U strip
+  static constexpr int n_load1 = (K * 64 * 2) / 1024 + 1;  // loader 1: Kd^T blocks + lam
+  // staging (x2): f32 state in accumulator order, bf16 state and delta fragments
+  static constexpr int st_sf = 0;
+  static constexpr int st_sb = st_sf + 16 * K * 4;
+  static constexpr int st_dl = st_sb + 16 * K * 2;
+  static constexpr int stage = st_dl + 16 * 64 * 2;
+  static constexpr int off_stage = kScanRing * slot;
+  static constexpr int bytes = off_stage + 2 * stage;
+};
+
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void* src, char* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt, lgkmcnt left open)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier that orders the surrounding memory accesses for the compiler only; the
+// hardware waits the ring protocol needs (vmcnt / lgkmcnt) are issued explicitly.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ bf16x8 pack_tiles(const f32x4& lo, const f32x4& hi) {
+  bf16x8 x;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[r] = to_bf16(lo[r]);
+    x[4 + r] = to_bf16(hi[r]);
+  }
+  return x;
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a) {
+  using L = ScanLds<K, V>;
+  constexpr int KT = K / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int H = a.H;
   int rec, strip;
   if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
   const int seq = rec / H, h = rec % H, v0 = strip * 16;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
-  const int i = 16 * wave + lr;
-
-  auto load = [&](int chunk, FwdScanFrag<K>& f) {
-    const size_t tile = (size_t)chunk * H + h;
-    const bf16* WF = (const bf16*)a.ws.p[R_WF] + tile * 64 * K;
-    const bf16* UF = (const bf16*)a.ws.p[R_UF] + tile * 64 * V;
-    const bf16* KDTF = (const bf16*)a.ws.p[R_KDTF] + tile * K * 64;
-    const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) f.w[s] = *(const bf16x8*)(WF + frag_off(K, wave, s, lane));
-    f.ut = *(const bf16x4*)(UF + ((size_t)(strip * 4 + wave) * 64 + lane) * 4);
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      const int kb = 16 * (wave * KT + kt);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) f.kdt[kt][s] = *(const bf16x8*)(KDTF + frag_off(64, wave * KT + kt, s, lane));
-      f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
+  const int n = sq.y;
+  if (n <= 0) {
+    if (wave == 0 && a.sfin) {
+      for (int kt = 0; kt < KT; ++kt) {
+        const size_t o = (((size_t)seq * H + h) * V + v0 + lr) * K + 16 * kt + 4 * kg;
+        *(float4*)(a.sfin + o) = a.s0 ? *(const float4*)(a.s0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
-  };
+    return;
+  }
 
+  if (wave == 1 || wave == 2) {
+    // ---- loader waves ----
+    const int lw = wave - 1;
+    auto issue = [&](int ci) {
+      const int c = ci < n ? ci : n - 1;  // fixed load count per chunk (clamped index)
+      const size_t tile = (size_t)(sq.x + c) * H + h;
+      char* slot = smem + (ci % kScanRing) * L::slot;
+      if (lw == 0) {
+        const char* w = (const char*)((const bf16*)a.ws.p[R_WF] + tile * 64 * K) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (64 * K * 2) / 1024; ++b) dma16(w + b * 1024, slot + L::off_w + b * 1024);
+        const char* u = (const char*)((const bf16*)a.ws.p[R_UF] + tile * 64 * V + (size_t)strip * 64 * 16) +
+                        lane * 16;
+        dma16(u, slot + L::off_u);
+        dma16(u + 1024, slot + L::off_u + 1024);
+      } else {
+        const char* kd = (const char*)((const bf16*)a.ws.p[R_KDTF] + tile * K * 64) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(kd + b * 1024, slot + L::off_kdt + b * 1024);
+        if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < kScanRing - 1; ++d) issue(d);
+    for (int ci = 0; ci < n; ++ci) {
+      // the slot of chunk ci is complete once at most (ring - 2) chunks' loads are newer
+      if (lw == 0)
+        wait_vmcnt<(kScanRing - 2) * L::n_load0>();
+      else
+        wait_vmcnt<(kScanRing - 2) * L::n_load1>();
+      ring_barrier();
+      issue(ci + kScanRing - 1);
+    }
+    ring_barrier();   // the store wave's hand-over of the last chunk
+    wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
+    return;
+  }
+
+  if (wave == 3) {
+    // ---- store wave: histories of chunk ci - 1 after barrier ci ----
+    for (int ci = 0; ci <= n; ++ci) {
+      ring_barrier();
+      if (ci == 0) continue;
+      const size_t tile = (size_t)(sq.x + ci - 1) * H + h;
+      const char* st = smem + L::off_stage + ((ci - 1) & 1) * L::stage;
+      // f32 state [K][V]: lane covers (k, 4 columns); element (k, v) was staged by lane
+      // v + 16 ((k % 16) / 4) of tile k / 16 as its value k % 4
+      float* SH = (float*)a.ws.p[R_SH] + tile * K * V + v0;
+#pragma unroll
+      for (int it = 0; it < K / 16; ++it) {
+        const int idx = it * 64 + lane, k = idx / 4, c4 = (idx % 4) * 4;
+        const float* sf = (const float*)(st + L::st_sf) + ((k / 16) * 64 + 16 * ((k % 16) / 4) + c4) * 4 + k % 4;
+        *(float4*)(SH + (size_t)k * V + c4) = make_float4(sf[0], sf[4], sf[8], sf[12]);
+      }
+      bf16* SHBF = (bf16*)a.ws.p[R_SHBF] + tile * V * K + (size_t)strip * 16 * K;
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s)
+        *(bf16x8*)(SHBF + ((size_t)s * 64 + lane) * 8) = *(const bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16);
+      bf16* DLF = (bf16*)a.ws.p[R_DLF] + tile * 64 * V + (size_t)strip * 16 * 64;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        *(bf16x8*)(DLF + ((size_t)s * 64 + lane) * 8) = *(const bf16x8*)(st + L::st_dl + (s * 64 + lane) * 16);
+      wait_lgkm0();
+    }
+    return;
+  }
+
+  // ---- compute wave ----
   f32x4 S[KT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
-    const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+    const int k0 = 16 * kt + 4 * kg;
     if (a.s0) {
       const float4 s = *(const float4*)(a.s0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
       S[kt][0] = s.x; S[kt][1] = s.y; S[kt][2] = s.z; S[kt][3] = s.w;
@@ -488,97 +610,75 @@ __global__ __launch_bounds__(256) void chunk_fwd_scan_kernel(FwdArgs a) {
       S[kt] = zero4();
     }
   }
-  const int n = sq.y;
-  FwdScanFrag<K> ring[kFwdRing];
-  if (n > 0) {
+  for (int ci = 0; ci < n; ++ci) {
+    ring_barrier();
+    const char* slot = smem + (ci % kScanRing) * L::slot;
+    char* st = smem + L::off_stage + (ci & 1) * L::stage;
+    // LDS operands: -W and U first; the Kd^T and lam reads are issued between the delta
+    // MFMAs so they arrive while those run (sched_barrier keeps this order)
+    bf16x8 wf[4][K / 32], kf[KT][2];
+    bf16x4 uf[4];
+    float4 lamf[KT];
 #pragma unroll
-    for (int d = 0; d < kFwdRing; ++d) load(sq.x + min(d, n - 1), ring[d]);
-  }
-
-  auto step = [&](int ci, FwdScanFrag<K>& f) {
-    const int chunk = sq.x + ci;
-    const size_t tile = (size_t)chunk * H + h;
-    bf16* sSp = sS[ci & 1];
-    // (1) publish S: bf16 [v][k] (MFMA operand) and f32 [k][v] (history staging)
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s)
+        wf[tt][s] = *(const bf16x8*)(slot + L::off_w + ((tt * (K / 32) + s) * 64 + lane) * 16);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) uf[tt] = *(const bf16x4*)(slot + L::off_u + (tt * 64 + lane) * 8);
+    __builtin_amdgcn_sched_barrier(0);
+    // state entering the chunk as B operands (permuted key order)
+    bf16x8 Bs[K / 32];
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) Bs[s] = pack_tiles(S[2 * s], S[2 * s + 1]);
+    // delta = U + (-W) S: four independent 16-row tiles, their K/32-deep chains interleaved
+    f32x4 dl[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dl[tt][r] = to_f32(uf[tt][r]);
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) dl[tt] = mfma16(wf[tt][s], Bs[s], dl[tt]);
+#pragma unroll
+      for (int kt = s * KT / (K / 32); kt < (s + 1) * KT / (K / 32); ++kt) {
+        kf[kt][0] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2) * 64 + lane) * 16);
+        kf[kt][1] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2 + 1) * 64 + lane) * 16);
+        lamf[kt] = *(const float4*)(slot + L::off_lam + (16 * kt + 4 * kg) * 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // histories of the state entering the chunk (staged for the store wave; the f32 state
+    // in accumulator order [kt][lane][4], which the store wave transposes)
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+      *(float4*)(st + L::st_sf + (kt * 64 + lane) * 16) = make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) *(bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16) = Bs[s];
+    const bf16x8 D0 = pack_tiles(dl[0], dl[1]), D1 = pack_tiles(dl[2], dl[3]);
+    *(bf16x8*)(st + L::st_dl + lane * 16) = D0;
+    *(bf16x8*)(st + L::st_dl + (64 + lane) * 16) = D1;
+    // S = lam S + Kd^T delta
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
-      bf16x4 x;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = to_bf16(S[kt][r]);
-        sSf[(k0 + r) * FP + lr] = S[kt][r];
-      }
-      *(bf16x4*)(sSp + lr * SP + k0) = x;
+      f32x4 acc;
+      acc[0] = lamf[kt].x * S[kt][0];
+      acc[1] = lamf[kt].y * S[kt][1];
+      acc[2] = lamf[kt].z * S[kt][2];
+      acc[3] = lamf[kt].w * S[kt][3];
+      S[kt] = mfma16(kf[kt][0], D0, acc);
     }
-    __syncthreads();
-    // (2) state histories: f32 [K][V] and bf16 [V][K] (fixed-count vector stores)
-    {
-      float* SH = (float*)a.ws.p[R_SH] + tile * K * V;
 #pragma unroll
-      for (int it = 0; it < K / 64; ++it) {
-        const int idx = tid + 256 * it;
-        const int kk = idx / 4, q4 = (idx % 4) * 4;
-        *(float4*)(SH + (size_t)kk * V + v0 + q4) = *(const float4*)(sSf + kk * FP + q4);
-      }
-      // bf16 state as B-operand fragments of this strip (read by the output kernel)
-      bf16* SHBF = (bf16*)a.ws.p[R_SHBF] + tile * V * K + (size_t)strip * 16 * K;
-      if (tid < 16 * K / 8) {
-        const int sl = tid / 64, ln = tid % 64;
-        *(bf16x8*)(SHBF + ((size_t)sl * 64 + ln) * 8) =
-            *(const bf16x8*)(sSp + (ln % 16) * SP + 32 * sl + 8 * (ln / 16));
-      }
-    }
-    // (3) delta rows 16*wave.. = U - W S  (two accumulators halve the MFMA chain)
-    {
-      f32x4 acc0 = zero4(), acc1 = zero4();
-#pragma unroll
-      for (int s = 0; s < K / 32; s += 2) {
-        acc0 = mfma16(f.w[s], *(const bf16x8*)(sSp + lr * SP + 32 * s + 8 * kg), acc0);
-        acc1 = mfma16(f.w[s + 1], *(const bf16x8*)(sSp + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
-      }
-      bf16x4 x;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = to_bf16(to_f32(f.ut[r]) - (acc0[r] + acc1[r]));
-      *(bf16x4*)(sD + lr * DP + 16 * wave + 4 * kg) = x;
-    }
-    __syncthreads();
-    // (3b) delta as B-operand fragments of this strip [2][64 lanes][8]
-    if (tid < 128) {
-      bf16* DLF = (bf16*)a.ws.p[R_DLF] + tile * 64 * V + (size_t)strip * 16 * 64;
-      const int sl = tid / 64, ln = tid % 64;
-      *(bf16x8*)(DLF + ((size_t)sl * 64 + ln) * 8) =
-          *(const bf16x8*)(sD + (ln % 16) * DP + 32 * sl + 8 * (ln / 16));
-    }
-    // (4) S <- lam S + Kd^T delta
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        acc = mfma16(f.kdt[kt][s], *(const bf16x8*)(sD + lr * DP + 32 * s + 8 * kg), acc);
-      S[kt][0] = fmaf(f.lam[kt].x, S[kt][0], acc[0]);
-      S[kt][1] = fmaf(f.lam[kt].y, S[kt][1], acc[1]);
-      S[kt][2] = fmaf(f.lam[kt].z, S[kt][2], acc[2]);
-      S[kt][3] = fmaf(f.lam[kt].w, S[kt][3], acc[3]);
-    }
-  };
-
-  // Ring loads are unconditional (the index is clamped to the last chunk) so no register
-  // of the ring is redefined under control flow; otherwise the compiler must wait for
-  // every load in flight at each join.
-  for (int c0 = 0; c0 < n; c0 += kFwdRing) {
-#pragma unroll
-    for (int d = 0; d < kFwdRing; ++d) {
-      const int ci = c0 + d;
-      if (ci < n) step(ci, ring[d]);
-      load(sq.x + min(ci + kFwdRing, n - 1), ring[d]);
-    }
+    for (int kt = 0; kt < KT; ++kt) S[kt] = mfma16(kf[kt][1], D1, S[kt]);
+    // the slot and the staging buffer are handed over at the next barrier
+    wait_lgkm0();
   }
+  ring_barrier();
   if (a.sfin) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      const int k0 = 16 * kt + 4 * kg;
       *(float4*)(a.sfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
           make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
     }
@@ -682,9 +782,17 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
   }
   if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
     auto scan = chunk_fwd_scan_kernel<K, V>;
+    constexpr size_t smem = ScanLds<K, V>::bytes;
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e = hipFuncSetAttribute((const void*)scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_forward: scan LDS attribute: %s", hipGetErrorString(e));
+      attr = true;
+    }
     const int nrec = p->num_seqs * p->heads;
     const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
-    hipLaunchKernelGGL(scan, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), smem, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward scan");
   }
   if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_OUTPUT))) {

@@ -20,17 +20,21 @@ __host__ __device__ inline size_t frag_off(int C, int rt, int s, int lane) {
   return ((((size_t)rt * (C / 32) + s) * 64) + lane) * 8;
 }
 
+// Arrays marked "permuted" keep their fragment shape but order each 32-wide step of the
+// contraction index as 32s + 16(e/4) + 4(l/16) + e%4 for element e of lane l (instead of
+// 32s + 8(l/16) + e): the order in which a lane holds two stacked MFMA accumulator tiles,
+// so the scan feeds accumulators straight back in as operands.
 enum WsRegion {
   R_CHUNKS = 0,  // int4 [max_chunks]   {row0, len, seq, index_in_seq}
   R_SEQS,        // int2 [num_seqs]     {first_chunk, n_chunks}
-  R_QGF,         // bf16 fragments of Qg = q_hat exp(G) (64 x K; q_hat includes the scale)
+  R_QGF,         // bf16 fragments of Qg = q_hat exp(G) (64 x K; q_hat includes the scale), permuted
   R_QGTF,        // bf16 fragments of Qg^T (K x 64)
   R_KDF,         // bf16 fragments of Kd = k_hat exp(G_last - G) (64 x K)
-  R_KDTF,        // bf16 fragments of Kd^T (K x 64)
-  R_WF,          // bf16 fragments of W = T (beta k_hat exp(G)) (64 x K)
+  R_KDTF,        // bf16 fragments of Kd^T (K x 64), permuted
+  R_WF,          // bf16 fragments of -W, W = T (beta k_hat exp(G)) (64 x K), permuted
   R_WTF,         // bf16 fragments of W^T (K x 64)
   R_UF,          // bf16 U = T (beta v) in MFMA C layout: [V/16 strip][4 row tile][64 lane][4]
-  R_AF,          // bf16 fragments of A (64 x 64, lower incl. diagonal)
+  R_AF,          // bf16 fragments of A (64 x 64, lower incl. diagonal), permuted
   R_ATF,         // bf16 fragments of A^T
   R_T,           // f32  [tile][64][64] T = (I + diag(beta) M')^-1
   R_MP,          // f32  [tile][64][64] M' (strictly lower, without beta)
@@ -40,8 +44,8 @@ enum WsRegion {
   R_RK,          // f32  [tile][64]     1 / max(||k||, 1e-12)
   R_BETA,        // f32  [tile][64]     sigmoid(beta_logits)
   R_SH,          // f32  [tile][K][V]   state entering the chunk (written by the scan)
-  R_SHBF,        // bf16 the same state as B-operand fragments [V/16 strip][K/32][64][8]
-  R_DLF,         // bf16 delta = U - W S as B-operand fragments [V/16 strip][2][64][8] (scan)
+  R_SHBF,        // bf16 the same state as B-operand fragments [V/16 strip][K/32][64][8], permuted
+  R_DLF,         // bf16 delta = U - W S as B-operand fragments [V/16 strip][2][64][8] (scan), permuted
   R_COUNT
 };
 
