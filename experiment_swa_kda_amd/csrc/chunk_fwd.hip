@@ -93,27 +93,6 @@ __global__ void chunk_prep_kernel(int B, int T, int num_seqs, const int* __restr
 // ---------------------------------------------------------------------------
 // intra-chunk kernel
 // ---------------------------------------------------------------------------
-template <int K, int V>
-struct IntraSmem {
-  static constexpr int KP = K + 1;  // f32 row stride (odd: conflict-free column access)
-  static constexpr int VP = V + 8;  // bf16 row stride
-  static constexpr int MP = 65;
-  static constexpr size_t off_q = 0;
-  static constexpr size_t off_k = off_q + 64 * KP * 4;
-  static constexpr size_t off_g = off_k + 64 * KP * 4;
-  static constexpr size_t off_m = off_g + 64 * KP * 4;
-  static constexpr size_t off_t = off_m + 64 * MP * 4;
-  static constexpr size_t off_x = off_t + 64 * MP * 4;
-  static constexpr size_t off_v = off_x + 3 * 16 * 17 * 4;
-  static constexpr size_t off_b = off_v + 64 * VP * 2;
-  static constexpr size_t off_f = off_b + 64 * 4;
-  static constexpr size_t off_as = off_f + 16;                 // bf16 [64][AP] A staging
-  static constexpr int AP = 64 + 8;
-  static constexpr size_t bytes = off_as + 64 * AP * 2;
-  // W staging (bf16 [64][K + 8]) reuses the q_hat region once Qg has been emitted
-  static_assert(64 * (K + 8) * 2 <= 64 * KP * 4, "W staging must fit the q_hat region");
-};
-
 // Column of element e held by lane group kg in 32-wide step s of a fragment: natural
 // (32s + 8kg + e) or permuted to match two MFMA accumulator tiles (32s + 16(e/4) + 4kg +
 // e%4: a lane's accumulator rows of tiles 2s and 2s+1), see the scan kernel.
@@ -137,29 +116,108 @@ __device__ __forceinline__ void emit_frags(bf16* dst, int tid, F val) {
   }
 }
 
-constexpr int kIntraThreads = 1024;
-constexpr int kIntraWaves = kIntraThreads / kWave;
-
-__device__ __constant__ int kPairA[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-__device__ __constant__ int kPairB[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+// ---------------------------------------------------------------------------
+// intra-chunk kernel
+// ---------------------------------------------------------------------------
+// One 256-thread workgroup per (chunk, head) tile; wave w owns the 16-row block w.  Lane
+// (lr, kg) holds row 16w + lr on the channels 32s + 8kg + e (s < K/32, e < 8): exactly
+// the A-operand fragments of its row block, so the bf16 MFMA operands of A and M' are
+// formed in registers.  The in-chunk cumulative decay is a DPP scan across the 16 rows of
+// a wave plus a 3-term prefix of the block totals; row norms are two permlane swaps.
+// LDS stays under 80 KB so two tiles share a CU.
+constexpr int kIntraThreads = 256;
 
 template <int K, int V>
-__global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs a) {
-  using L = IntraSmem<K, V>;
-  constexpr int KP = L::KP, VP = L::VP, MP = L::MP;
+struct IntraLds {
+  static constexpr int NS = K / 32;
+  static constexpr int RS = K + 8;   // bf16 row stride of [64][K] staging
+  static constexpr int TS = 64 + 8;  // bf16 row stride of [*][64] staging
+  static constexpr int cmax(int a, int b) { return a > b ? a : b; }
+  // X1: Fq / Fk fragments (A, M') -> (beta v)^T, (beta kh e^G)^T (U, W) -> Qg, Kd staging
+  static constexpr int x1 = 0;
+  static constexpr int x1_bytes = cmax(cmax(2 * 64 * K * 2, (V + K) * TS * 2), 2 * 64 * RS * 2);
+  // X3: M' f32 [64][65] -> W bf16 [64][RS]
+  static constexpr int x3 = x1 + x1_bytes;
+  static constexpr int x3_bytes = cmax(64 * 65 * 4, 64 * RS * 2);
+  // X4: A bf16 [64][TS] -> T f32 [64][65]
+  static constexpr int x4 = x3 + x3_bytes;
+  static constexpr int x4_bytes = cmax(64 * TS * 2, 64 * 65 * 4);
+  // per-wave 16 x 17 f32 product scratch (T solve)
+  static constexpr int scr = x4 + x4_bytes;
+  static constexpr int scr_bytes = 4 * 16 * 17 * 4;
+  static constexpr int gref = scr + scr_bytes;   // f32 [5][K]: G of rows 0, 16, 32, 48 and 63
+  static constexpr int tot = gref + 5 * K * 4;   // f32 [4][K]: block totals of g
+  static constexpr int beta = tot + 4 * K * 4;   // f32 [64]
+  static constexpr int bytes = beta + 64 * 4;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_shr(float v) {
+  // row_shr with bound_ctrl: lanes shifted in from outside the 16-lane row read 0
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// Inclusive prefix sum across the 16 lanes of each DPP row (lane order = row order).
+__device__ __forceinline__ float row_prefix16(float x) {
+  x += dpp_shr<0x111>(x);
+  x += dpp_shr<0x112>(x);
+  x += dpp_shr<0x114>(x);
+  x += dpp_shr<0x118>(x);
+  return x;
+}
+
+// Exact A / M' entries of a diagonal block whose decay span is too large for the
+// factorised MFMA form: lane (lr, kg) computes (i = 16w + 4kg + r, j = 16w + lr), r < 4,
+// from the global inputs and the G rows this workgroup already wrote.
+template <int K>
+__device__ void intra_exact_block(const FwdArgs& a, int w, int lane, int row0, int len, int h,
+                                  const float* G, const float* RQ, const float* RK, f32x4& accA,
+                                  f32x4& accM) {
+  const int lr = lane % 16, kg = lane / 16, H = a.H;
+  const int j = 16 * w + lr;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 16 * w + 4 * kg + r;
+    float sa = 0.f, sm = 0.f;
+    if (j <= i && i < len) {
+      const size_t bi = ((size_t)(row0 + i) * H + h) * K, bj = ((size_t)(row0 + j) * H + h) * K;
+      const float rqi = RQ[i], rki = RK[i], rkj = RK[j];
+      for (int c0 = 0; c0 < K; c0 += 8) {
+        float qi[8], ki[8], kj[8];
+        load8(a.q + bi + c0, qi);
+        load8(a.k + bi + c0, ki);
+        load8(a.k + bj + c0, kj);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = expf(G[i * K + c0 + e] - G[j * K + c0 + e]) * kj[e] * rkj;
+          sa = fmaf(qi[e] * rqi, d, sa);
+          sm = fmaf(ki[e] * rki, d, sm);
+        }
+      }
+    }
+    accA[r] = sa;
+    accM[r] = sm;
+  }
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdArgs a) {
+  using L = IntraLds<K, V>;
+  constexpr int NS = K / 32, NV = V / 32, RS = L::RS, TS = L::TS;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  float* sQ = (float*)(smem + L::off_q);
-  float* sK = (float*)(smem + L::off_k);
-  float* sG = (float*)(smem + L::off_g);
-  float* sM = (float*)(smem + L::off_m);
-  float* sT = (float*)(smem + L::off_t);
-  float* sX = (float*)(smem + L::off_x);
-  bf16* sV = (bf16*)(smem + L::off_v);
-  float* sB = (float*)(smem + L::off_b);
-  int* sF = (int*)(smem + L::off_f);
-  bf16* sAs = (bf16*)(smem + L::off_as);
-  bf16* sWs = (bf16*)(smem + L::off_q);  // after Qg/Kd fragments are written
-  constexpr int AP = L::AP, WP = K + 8;
+  bf16* sF = (bf16*)(smem + L::x1);        // Fq / Fk fragments
+  bf16* sVT = (bf16*)(smem + L::x1);       // (beta v)^T [V][TS]
+  bf16* sBT = sVT + V * TS;                // (beta kh e^G)^T [K][TS]
+  bf16* sQg = (bf16*)(smem + L::x1);       // Qg [64][RS]
+  bf16* sKd = sQg + 64 * RS;               // Kd [64][RS]
+  float* sM = (float*)(smem + L::x3);      // M' [64][65]
+  bf16* sW = (bf16*)(smem + L::x3);        // W [64][RS]
+  bf16* sA = (bf16*)(smem + L::x4);        // A [64][TS]
+  float* sT = (float*)(smem + L::x4);      // T [64][65]
+  float* sScr = (float*)(smem + L::scr);
+  float* sGref = (float*)(smem + L::gref);
+  float* sTot = (float*)(smem + L::tot);
+  float* sBeta = (float*)(smem + L::beta);
 
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
   const int len = ch.y;
@@ -167,268 +225,314 @@ __global__ __launch_bounds__(kIntraThreads) void chunk_fwd_intra_kernel(FwdArgs 
   const int H = a.H, h = blockIdx.y;
   const size_t tile = (size_t)blockIdx.x * H + h;
   const int row0 = ch.x;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
+  const int i = 16 * w + lr;
+  const bool live = i < len;
+  const size_t rbase = (size_t)(row0 + (live ? i : len - 1)) * H + h;
 
-  if (tid < 4) sF[tid] = 0;
-  for (int i = tid; i < 64 * MP; i += kIntraThreads) sT[i] = 0.f;
+  // ---- phase 1: loads (all issued first), norms, gate, beta, cumulative decay ----
+  bf16x8 qr[NS], kr[NS], vr[NV];
+  float g[NS][8];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    qr[s] = *(const bf16x8*)(a.q + rbase * K + 32 * s + 8 * kg);
+    kr[s] = *(const bf16x8*)(a.k + rbase * K + 32 * s + 8 * kg);
+  }
+#pragma unroll
+  for (int s = 0; s < NV; ++s) vr[s] = *(const bf16x8*)(a.v + rbase * V + 32 * s + 8 * kg);
+  const float bl = (float)a.beta[rbase];
+  if (a.gate_mode == KDA_GATE_K3) {
+    const float ea = expf(a.A_log[h]);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int c0 = 32 * s + 8 * kg;
+      const bf16x8 raw = *(const bf16x8*)((const bf16*)a.gate + rbase * K + c0);
+      float db[8];
+      load8f(a.dt_bias + h * K + c0, db);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[s][e] = a.lb * sigmoid_fast(ea * ((float)raw[e] + db[e]));
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) load8f((const float*)a.gate + rbase * K + 32 * s + 8 * kg, g[s]);
+  }
+  float qh[NS][8], kh[NS][8];
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qh[s][e] = live ? (float)qr[s][e] : 0.f;
+      kh[s][e] = live ? (float)kr[s][e] : 0.f;
+      if (!live) g[s][e] = 0.f;
+      sq = fmaf(qh[s][e], qh[s][e], sq);
+      sk = fmaf(kh[s][e], kh[s][e], sk);
+    }
+  sq = swap32_sum(swap16_sum(sq));
+  sk = swap32_sum(swap16_sum(sk));
+  const float rq = a.scale / fmaxf(sqrtf(sq), 1e-12f);
+  const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+  const float beta = live ? sigmoid_acc(bl) : 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qh[s][e] *= rq;
+      kh[s][e] *= rk;
+      g[s][e] = row_prefix16(g[s][e]);  // inclusive in-block prefix over the 16 rows
+    }
+  if (kg == 0) {
+    sBeta[i] = beta;
+    ((float*)a.ws.p[R_RQ])[tile * 64 + i] = rq;
+    ((float*)a.ws.p[R_RK])[tile * 64 + i] = rk;
+    ((float*)a.ws.p[R_BETA])[tile * 64 + i] = beta;
+  }
+  if (lr == 15) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float* t = sTot + w * K + 32 * s + 8 * kg;
+      *(float4*)t = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
+      *(float4*)(t + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
+    }
+  }
+  __syncthreads();
+  // G = in-block prefix + totals of the preceding blocks (fixed order)
+  for (int b = 0; b < w; ++b) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float t[8];
+      load8f(sTot + b * K + 32 * s + 8 * kg, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[s][e] += t[e];
+    }
+  }
+  float* Gout = (float*)a.ws.p[R_G] + tile * 64 * K;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    float* o = Gout + i * K + 32 * s + 8 * kg;
+    *(float4*)o = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
+    *(float4*)(o + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
+    if (lr == 0 || i == 63) {
+      float* r = sGref + (lr == 0 ? w : 4) * K + 32 * s + 8 * kg;
+      *(float4*)r = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
+      *(float4*)(r + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
+    }
+    if (i == 63) {
+      float* lam = (float*)a.ws.p[R_LAM] + tile * K + 32 * s + 8 * kg;
+      *(float4*)lam = make_float4(expf(g[s][0]), expf(g[s][1]), expf(g[s][2]), expf(g[s][3]));
+      *(float4*)(lam + 4) = make_float4(expf(g[s][4]), expf(g[s][5]), expf(g[s][6]), expf(g[s][7]));
+    }
+  }
+  __syncthreads();
 
-  // ---- phase 1: load, normalise, activate ----
+  // ---- phase 2: A and M' = (factorised) 16 x 16 blocks; row factors e^{G_i - G_r} ----
+  bool wide = false;  // this wave's diagonal block spans more than 80 nats on some channel
   {
-    constexpr int LPR = K / 8;
-    constexpr int RPP = kIntraThreads / LPR;
-    const int c0 = (tid % LPR) * 8;
-    const float* A_log = a.A_log;
-    for (int t = tid / LPR; t < 64; t += RPP) {
-      float qv[8], kv[8], gv[8];
-      if (t < len) {
-        const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
-        load8(a.q + base, qv);
-        load8(a.k + base, kv);
-        if (a.gate_mode == KDA_GATE_K3) {
-          float raw[8];
-          load8((const bf16*)a.gate + base, raw);
-          const float ea = expf(A_log[h]);
+    float gr[NS][8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            gv[e] = a.lb * sigmoid_acc(ea * (raw[e] + a.dt_bias[h * K + c0 + e]));
-        } else {
-          const float4* gp = (const float4*)((const float*)a.gate + base);
-          float4 g0 = gp[0], g1 = gp[1];
-          gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
-          gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
-        }
-      } else {
+    for (int s = 0; s < NS; ++s) load8f(sGref + w * K + 32 * s + 8 * kg, gr[s]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[e] = kv[e] = gv[e] = 0.f;
-      }
-      float sq = 0.f, sk = 0.f;
+    for (int s = 0; s < NS; ++s) {
+      bf16x8 fq, fk;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        sq += qv[e] * qv[e];
-        sk += kv[e] * kv[e];
+        const float f = __expf(g[s][e] - gr[s][e]);
+        fq[e] = (bf16)(qh[s][e] * f);
+        fk[e] = (bf16)(kh[s][e] * f);
+        wide |= (lr == 15) && (gr[s][e] - g[s][e] > 80.f);
       }
-      sq = group_sum<LPR>(sq);
-      sk = group_sum<LPR>(sk);
-      const float rq = a.scale / fmaxf(sqrtf(sq), 1e-12f);
-      const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sQ[t * KP + c0 + e] = qv[e] * rq;
-        sK[t * KP + c0 + e] = kv[e] * rk;
-        sG[t * KP + c0 + e] = gv[e];
-      }
-      if (tid % LPR == 0) {
-        const float bt = t < len ? sigmoid_acc(to_f32(a.beta[(size_t)(row0 + t) * H + h])) : 0.f;
-        sB[t] = bt;
-        ((float*)a.ws.p[R_RQ])[tile * 64 + t] = rq;
-        ((float*)a.ws.p[R_RK])[tile * 64 + t] = rk;
-        ((float*)a.ws.p[R_BETA])[tile * 64 + t] = bt;
-      }
+      *(bf16x8*)(sF + ((size_t)(w * NS + s) * 64 + lane) * 8) = fq;
+      *(bf16x8*)(sF + ((size_t)((4 + w) * NS + s) * 64 + lane) * 8) = fk;
     }
   }
+  wide = __builtin_amdgcn_ballot_w64(wide) != 0;
   __syncthreads();
-  // beta * v (bf16) and the in-chunk cumulative decay
-  for (int idx = tid; idx < 64 * (V / 8); idx += kIntraThreads) {
-    const int t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
-    float vv[8];
-    if (t < len) {
-      load8(a.v + ((size_t)(row0 + t) * H + h) * V + c0, vv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vv[e] = 0.f;
-    }
-    const float bt = sB[t];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sV[t * VP + c0 + e] = to_bf16(bt * vv[e]);
-  }
-  if (tid < K) {
-    const int c = tid;
-    float* Gout = (float*)a.ws.p[R_G] + tile * 64 * K;
-    float acc = 0.f;
-    for (int t = 0; t < 64; ++t) {
-      acc += sG[t * KP + c];
-      sG[t * KP + c] = acc;
-      Gout[t * K + c] = acc;
-    }
-    ((float*)a.ws.p[R_LAM])[tile * K + c] = expf(acc);
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      if (sG[(16 * b) * KP + c] - sG[(16 * b + 15) * KP + c] > 80.f) atomicOr(&sF[b], 1);
-  }
-  __syncthreads();
-
-  // ---- phase 2: A and M' (16x16 tiles of the lower triangle) ----
-  float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
-  for (int p = wave; p < 10; p += kIntraWaves) {
-    const int ba = kPairA[p], bb = kPairB[p];
-    const int r = 16 * ba;
+  // wave w = column block bb computes the pairs (ba, bb) for ba >= w
+  for (int ba = w; ba < 4; ++ba) {
     f32x4 accA = zero4(), accM = zero4();
-    if (!(ba == bb && sF[ba])) {
-      const int i = 16 * ba + lr, j = 16 * bb + lr;
-#pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        const int c = 32 * s + 8 * kg;
-        bf16x8 fq, fk, fb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float gr = sG[r * KP + c + e];
-          const float ei = __expf(sG[i * KP + c + e] - gr);
-          const float ej = __expf(gr - sG[j * KP + c + e]);
-          fq[e] = to_bf16(sQ[i * KP + c + e] * ei);
-          fk[e] = to_bf16(sK[i * KP + c + e] * ei);
-          fb[e] = to_bf16(sK[j * KP + c + e] * ej);
-        }
-        accA = mfma16(fq, fb, accA);
-        accM = mfma16(fk, fb, accM);
-      }
+    if (ba == w && wide) {
+      __threadfence_block();
+      intra_exact_block<K>(a, w, lane, row0, len, h, Gout, (const float*)a.ws.p[R_RQ] + tile * 64,
+                           (const float*)a.ws.p[R_RK] + tile * 64, accA, accM);
     } else {
-      // exact pairwise path for a diagonal block with a large decay span
-      const int jj = 16 * bb + lr;
+      float gr[NS][8];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = 16 * ba + 4 * kg + rr;
-        float sa = 0.f, sm = 0.f;
-        if (jj <= ii) {
-          for (int c = 0; c < K; ++c) {
-            const float e = expf(sG[ii * KP + c] - sG[jj * KP + c]);
-            const float kj = sK[jj * KP + c] * e;
-            sa = fmaf(sQ[ii * KP + c], kj, sa);
-            sm = fmaf(sK[ii * KP + c], kj, sm);
-          }
-        }
-        accA[rr] = sa;
-        accM[rr] = sm;
+      for (int s = 0; s < NS; ++s) load8f(sGref + ba * K + 32 * s + 8 * kg, gr[s]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        bf16x8 cf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cf[e] = (bf16)(kh[s][e] * __expf(gr[s][e] - g[s][e]));
+        accA = mfma16(*(const bf16x8*)(sF + ((size_t)(ba * NS + s) * 64 + lane) * 8), cf, accA);
+        accM = mfma16(*(const bf16x8*)(sF + ((size_t)((4 + ba) * NS + s) * 64 + lane) * 8), cf, accM);
       }
     }
-    const int jj = 16 * bb + lr;
+    const int jj = 16 * w + lr;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int ii = 16 * ba + 4 * kg + rr;
-      const float av = jj <= ii ? accA[rr] : 0.f;
-      const float mv = jj < ii ? accM[rr] : 0.f;
-      sAs[ii * AP + jj] = to_bf16(av);
-      sM[ii * MP + jj] = mv;
-      MPout[ii * 64 + jj] = mv;
+    for (int r = 0; r < 4; ++r) {
+      const int ii = 16 * ba + 4 * kg + r;
+      sA[ii * TS + jj] = (bf16)(jj <= ii ? accA[r] : 0.f);
+      sM[ii * 65 + jj] = jj < ii ? accM[r] : 0.f;
     }
   }
-  // strictly-upper 16x16 blocks are zero
-  for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) {
-    const int ii = idx / 64, jj = idx % 64;
-    if (jj / 16 > ii / 16) {
-      sAs[ii * AP + jj] = to_bf16(0.f);
-      sM[ii * MP + jj] = 0.f;
-      MPout[ii * 64 + jj] = 0.f;
+  for (int ba = 0; ba < w; ++ba) {  // blocks above the diagonal are zero
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ii = 16 * ba + 4 * kg + r, jj = 16 * w + lr;
+      sA[ii * TS + jj] = (bf16)0.f;
+      sM[ii * 65 + jj] = 0.f;
     }
   }
   __syncthreads();
 
-  // ---- A, Qg = qh exp(G), Kd = kh exp(G_last - G) as MFMA fragments (+ transposes) ----
+  // ---- phase 2b: A fragments, M' to HBM, (beta v)^T and (beta kh e^G)^T to LDS ----
+  emit_frags<64, 64, kIntraThreads, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
+                                          [&](int r, int c) { return sA[r * TS + c]; });
+  emit_frags<64, 64, kIntraThreads>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
+                                    [&](int r, int c) { return sA[c * TS + r]; });
   {
-    constexpr int NT = kIntraThreads;
-    emit_frags<64, 64, NT, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
-                           [&](int r, int c) { return sAs[r * AP + c]; });
-    emit_frags<64, 64, NT>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
-                           [&](int r, int c) { return sAs[c * AP + r]; });
-    const float* gl = sG + 63 * KP;
-    emit_frags<64, K, NT, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid, [&](int r, int c) {
-      return to_bf16(sQ[r * KP + c] * expf(sG[r * KP + c]));
-    });
-    emit_frags<K, 64, NT>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid, [&](int r, int c) {
-      return to_bf16(sQ[c * KP + r] * expf(sG[c * KP + r]));
-    });
-    emit_frags<64, K, NT>((bf16*)a.ws.p[R_KDF] + tile * 64 * K, tid, [&](int r, int c) {
-      return to_bf16(sK[r * KP + c] * expf(gl[c] - sG[r * KP + c]));
-    });
-    emit_frags<K, 64, NT, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, [&](int r, int c) {
-      return to_bf16(sK[c * KP + r] * expf(gl[r] - sG[c * KP + r]));
-    });
+    float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
+    for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) MPout[idx] = sM[(idx / 64) * 65 + idx % 64];
   }
+#pragma unroll
+  for (int s = 0; s < NV; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sVT[(32 * s + 8 * kg + e) * TS + i] = (bf16)(beta * (live ? (float)vr[s][e] : 0.f));
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sBT[(32 * s + 8 * kg + e) * TS + i] = (bf16)(beta * kh[s][e] * __expf(g[s][e]));
+  // Qg = qh e^G and Kd = kh e^{G_last - G} (bf16) are all that phase 5 needs of this row;
+  // Kd's natural fragments are exactly what this lane holds
+  bf16x8 xq[NS], xk[NS];
+  {
+    bf16* KDF = (bf16*)a.ws.p[R_KDF] + tile * 64 * K;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float gl[8];
+      load8f(sGref + 4 * K + 32 * s + 8 * kg, gl);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xq[s][e] = (bf16)(qh[s][e] * __expf(g[s][e]));
+        xk[s][e] = (bf16)(kh[s][e] * __expf(gl[e] - g[s][e]));
+      }
+      *(bf16x8*)(KDF + frag_off(K, w, s, lane)) = xk[s];
+    }
+  }
+  __syncthreads();
 
-  // ---- phase 3: T = (I + diag(beta) M')^-1, blocked forward substitution ----
-  if (tid < 64) {
-    const int blk = tid / 16, j = tid % 16;
-    const int o = 16 * blk;
+  // ---- phase 3: T = (I + diag(beta) M')^-1 ----
+  // diagonal blocks by forward substitution, one column per lane (lanes of group kg = 0)
+  {
+    const int o = 16 * w, j = lr;
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float s = (i == j) ? 1.f : 0.f;
-      const float bi = sB[o + i];
+    for (int ii = 0; ii < 16; ++ii) {
+      float sacc = (ii == j) ? 1.f : 0.f;
+      const float bi = sBeta[o + ii];
 #pragma unroll
-      for (int m = 0; m < i; ++m)
-        if (m >= j) s -= bi * sM[(o + i) * MP + o + m] * x[m];
-      x[i] = (i < j) ? 0.f : s;
+      for (int m = 0; m < ii; ++m) sacc = fmaf(-bi * sM[(o + ii) * 65 + o + m], x[m], sacc);
+      x[ii] = (ii < j) ? 0.f : sacc;
     }
+    __syncthreads();  // sA (aliasing sT) is no longer read
+    if (kg == 0) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sT[(o + i) * MP + o + j] = x[i];
+      for (int ii = 0; ii < 16; ++ii) sT[(o + ii) * 65 + o + j] = x[ii];
+    }
+    for (int idx = lane; idx < 16 * 16 * (3 - w); idx += kWave) {  // zero blocks right of the diagonal
+      const int cb = w + 1 + idx / 256, rr = (idx % 256) / 16, cc = idx % 16;
+      sT[(o + rr) * 65 + 16 * cb + cc] = 0.f;
+    }
   }
   __syncthreads();
-  for (int ba = 1; ba < 4; ++ba) {
-    for (int idx = tid; idx < ba * 256; idx += kIntraThreads) {
-      const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
-      const float bi = sB[16 * ba + i];
-      float s = 0.f;
-      for (int m = 16 * bb; m < 16 * ba; ++m)
-        s = fmaf(sM[(16 * ba + i) * MP + m], sT[m * MP + 16 * bb + j], s);
-      sX[(bb * 16 + i) * 17 + j] = bi * s;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < ba * 256; idx += kIntraThreads) {
-      const int bb = idx / 256, i = (idx % 256) / 16, j = idx % 16;
-      float s = 0.f;
+  // off-diagonal blocks by levels: T_ab = -D_a sum_{m=b}^{a-1} N_am T_mb, N = diag(beta) M'.
+  // 16 x 16 x 16 f32 products on v_mfma_f32_16x16x4_f32 (A[lr][kg], B[kg][lr] per 4-step).
+  auto prod_NT = [&](int ra, int cm, int cb, f32x4 acc) {  // acc += N[ra-block][cm-block] T[cm][cb]
 #pragma unroll
-      for (int m = 0; m < 16; ++m)
-        s = fmaf(sT[(16 * ba + i) * MP + 16 * ba + m], sX[(bb * 16 + m) * 17 + j], s);
-      sT[(16 * ba + i) * MP + 16 * bb + j] = -s;
+    for (int st = 0; st < 4; ++st) {
+      const int kk = 4 * st + kg;
+      const float av = sBeta[16 * ra + lr] * sM[(16 * ra + lr) * 65 + 16 * cm + kk];
+      const float bv = sT[(16 * cm + kk) * 65 + 16 * cb + lr];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    }
+    return acc;
+  };
+  float* scr = sScr + w * 16 * 17;
+  for (int lvl = 1; lvl < 4; ++lvl) {
+    const int b = w, ra = w + lvl;
+    if (ra < 4) {
+      f32x4 z = zero4();
+      for (int m = b; m < ra; ++m) z = prod_NT(ra, m, b, z);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) scr[(4 * kg + r) * 17 + lr] = z[r];
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave reads its own scratch next
+      f32x4 t = zero4();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kk = 4 * st + kg;
+        t = __builtin_amdgcn_mfma_f32_16x16x4f32(sT[(16 * ra + lr) * 65 + 16 * ra + kk], scr[kk * 17 + lr], t, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sT[(16 * ra + 4 * kg + r) * 65 + 16 * b + lr] = -t[r];
     }
     __syncthreads();
   }
   {
     float* Tout = (float*)a.ws.p[R_T] + tile * 64 * 64;
-    for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) Tout[idx] = sT[(idx / 64) * MP + idx % 64];
+    for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) Tout[idx] = sT[(idx / 64) * 65 + idx % 64];
   }
 
-  // ---- phase 4: U = T (beta v), W = T (beta kh exp(G)) ----
+  // ---- phase 4: U = T (beta v), W = T (beta kh e^G); wave w = row tile ----
   {
+    const int rt = w, nst = (16 * rt + 15) / 32 + 1;
+    bf16x8 fa[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      bf16x8 x;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (bf16)sT[(16 * rt + lr) * 65 + 32 * st + 8 * kg + e];
+      fa[st] = x;
+    }
     bf16* Uout = (bf16*)a.ws.p[R_UF] + tile * 64 * V;
-    constexpr int NU = 4 * (V / 16), NW = 4 * (K / 16);
-    for (int p = wave; p < NU + NW; p += kIntraWaves) {
-      const bool isU = p < NU;
-      const int q = isU ? p : p - NU;
-      const int rt = q % 4, ct = q / 4;
-      const int i = 16 * rt + lr, col = 16 * ct + lr;
+    for (int ct = 0; ct < V / 16; ++ct) {
       f32x4 acc = zero4();
-      const int nsteps = (16 * rt + 15) / 32 + 1;
-      for (int s = 0; s < nsteps; ++s) {
-        const int j0 = 32 * s + 8 * kg;
-        bf16x8 fa, fb;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          fa[e] = to_bf16(sT[i * MP + j0 + e]);
-          const int j = j0 + e;
-          fb[e] = isU ? sV[j * VP + col]
-                      : to_bf16(sB[j] * sK[j * KP + col] * __expf(sG[j * KP + col]));
-        }
-        acc = mfma16(fa, fb, acc);
-      }
-      if (isU) {
-        // C layout kept as is: [strip = ct][row tile][lane][4]
-        bf16x4 x;
+      for (int st = 0; st < 2; ++st)  // T is lower triangular: row tile rt needs nst steps
+        if (st < nst) acc = mfma16(fa[st], *(const bf16x8*)(sVT + (16 * ct + lr) * TS + 32 * st + 8 * kg), acc);
+      bf16x4 x;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) x[rr] = to_bf16(acc[rr]);
-        *(bf16x4*)(Uout + ((size_t)(ct * 4 + rt) * 64 + lane) * 4) = x;
-      } else {
+      for (int r = 0; r < 4; ++r) x[r] = (bf16)acc[r];
+      *(bf16x4*)(Uout + ((size_t)(ct * 4 + rt) * 64 + lane) * 4) = x;
+    }
+    __syncthreads();  // M' (aliasing W) is no longer read
+    for (int ct = 0; ct < K / 16; ++ct) {
+      f32x4 acc = zero4();
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sWs[(16 * rt + 4 * kg + rr) * WP + col] = to_bf16(acc[rr]);
-      }
+      for (int st = 0; st < 2; ++st)
+        if (st < nst) acc = mfma16(fa[st], *(const bf16x8*)(sBT + (16 * ct + lr) * TS + 32 * st + 8 * kg), acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sW[(16 * rt + 4 * kg + r) * RS + 16 * ct + lr] = (bf16)acc[r];
     }
   }
   __syncthreads();
+  // -W and W^T fragments; Qg and Kd staged for their transposed / permuted fragments
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
-                                         [&](int r, int c) { return (bf16)(-(float)sWs[r * WP + c]); });
+                                         [&](int r, int c) { return (bf16)(-(float)sW[r * RS + c]); });
   emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid,
-                                   [&](int r, int c) { return sWs[c * WP + r]; });
-
+                                   [&](int r, int c) { return sW[c * RS + r]; });
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    *(bf16x8*)(sQg + i * RS + 32 * s + 8 * kg) = xq[s];
+    *(bf16x8*)(sKd + i * RS + 32 * s + 8 * kg) = xk[s];
+  }
+  __syncthreads();
+  emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid,
+                                         [&](int r, int c) { return sQg[r * RS + c]; });
+  emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid,
+                                   [&](int r, int c) { return sQg[c * RS + r]; });
+  emit_frags<K, 64, kIntraThreads, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid,
+                                         [&](int r, int c) { return sKd[c * RS + r]; });
 }
 
 // ---------------------------------------------------------------------------
@@ -766,7 +870,7 @@ template <int K, int V>
 static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArgs& a,
                           hipStream_t stream, int stages) {
   if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_INTRA))) {
-    constexpr size_t smem = IntraSmem<K, V>::bytes;
+    constexpr size_t smem = IntraLds<K, V>::bytes;
     static bool attr = false;
     if (!attr) {
       hipError_t e = hipFuncSetAttribute((const void*)chunk_fwd_intra_kernel<K, V>,
@@ -776,8 +880,7 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
       attr = true;
     }
     auto intra = chunk_fwd_intra_kernel<K, V>;
-    hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(kIntraThreads),
-                       smem, stream, a);
+    hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(kIntraThreads), smem, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward intra");
   }
   if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
