@@ -345,37 +345,64 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   };
 
   // ---- PA: dQg, dKd, dW over the 64 x K grid ----
+  // Wave w owns key tile ct and RPW row tiles: the f32 state rows S[c][.] and dS'[c][.] of
+  // its 16 keys are loaded once (all loads issued first), split into hi + lo bf16 once, and
+  // reused for every row tile.  The same rows give dlam = lam * sum_v S dS'.
   constexpr int NKT = 4 * (K / 16);
-  for (int p = wave; p < NKT; p += kVjpWaves) {
-    const int rt = p % 4, ct = p / 4;
-    const int i = 16 * rt + lr, c = 16 * ct + lr;
-    f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
-#pragma unroll 2
-    for (int s = 0; s < V / 32; ++s) {
-      const int vv = 32 * s + 8 * kg;
-      float xs[8], xd[8];
-      load8f(SH + (size_t)c * V + vv, xs);
-      load8f(DSH + (size_t)c * V + vv, xd);
-      bf16x8 sHi, sLo, dHi, dLo;
-      split8(xs, sHi, sLo);
-      split8(xd, dHi, dLo);
-      const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
-      const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
-      const bf16x8 aO = load_dout8(i, vv);
-      const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
-      accQ = mfma16(aO, sHi, accQ);
-      accQ = mfma16(aO, sLo, accQ);
-      accK = mfma16(aL, dHi, accK);
-      accK = mfma16(aL, dLo, accK);
-      accW = mfma16(uHi, sHi, accW);
-      accW = mfma16(uHi, sLo, accW);
-      accW = mfma16(uLo, sHi, accW);
-    }
-    // raw dQg, dKd in C-layout item order (consumed with the same lane ownership)
-    *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = accQ;
-    *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
+  {
+    constexpr int RPW = NKT / kVjpWaves;  // row tiles per wave (2 for K = 128, 1 for K = 64)
+    constexpr int NVS = V / 32;
+    static_assert(RPW >= 1 && 4 % RPW == 0, "row tiles per wave");
+    const int ct = wave / (4 / RPW), rt0 = (wave % (4 / RPW)) * RPW;
+    const int c = 16 * ct + lr;
+    float xs[NVS][8], xd[NVS][8];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = -accW[rr];
+    for (int sv = 0; sv < NVS; ++sv) {
+      load8f(SH + (size_t)c * V + 32 * sv + 8 * kg, xs[sv]);
+      load8f(DSH + (size_t)c * V + 32 * sv + 8 * kg, xd[sv]);
+    }
+    bf16x8 aO[RPW][NVS];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q)
+#pragma unroll
+      for (int sv = 0; sv < NVS; ++sv) aO[q][sv] = load_dout8(16 * (rt0 + q) + lr, 32 * sv + 8 * kg);
+    const float lamc = ((const float*)a.ws.p[R_LAM])[tile * K + c];
+    bf16x8 sHi[NVS], sLo[NVS], dHi[NVS], dLo[NVS];
+    float dl = 0.f;
+#pragma unroll
+    for (int sv = 0; sv < NVS; ++sv) {
+      split8(xs[sv], sHi[sv], sLo[sv]);
+      split8(xd[sv], dHi[sv], dLo[sv]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dl = fmaf(xs[sv][e], xd[sv][e], dl);
+    }
+    dl = swap32_sum(swap16_sum(dl));
+    if (rt0 == 0 && kg == 0) ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lamc;
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rt = rt0 + q, i = 16 * rt + lr;
+      const int p = rt + 4 * ct;
+      f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
+#pragma unroll
+      for (int sv = 0; sv < NVS; ++sv) {
+        const int vv = 32 * sv + 8 * kg;
+        const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
+        const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
+        const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
+        accQ = mfma16(aO[q][sv], sHi[sv], accQ);
+        accQ = mfma16(aO[q][sv], sLo[sv], accQ);
+        accK = mfma16(aL, dHi[sv], accK);
+        accK = mfma16(aL, dLo[sv], accK);
+        accW = mfma16(uHi, sHi[sv], accW);
+        accW = mfma16(uHi, sLo[sv], accW);
+        accW = mfma16(uLo, sHi[sv], accW);
+      }
+      // raw dQg, dKd in C-layout item order (consumed with the same lane ownership)
+      *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = accQ;
+      *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = -accW[rr];
+    }
   }
   // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
   for (int p = wave; p < 16; p += kVjpWaves) {
@@ -545,25 +572,12 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   }
   __syncthreads();
 
-  // ---- PE: dbeta partial (U and M' terms) and lam * dL/dlam ----
+  // ---- PE: dbeta partial (U and M' terms); lam * dL/dlam was written in PA ----
   if (tid < 64) {
     float db = 0.f;
     for (int c = 0; c < V / 16; ++c) db += sPV[c * 64 + tid];
     for (int b = 0; b < 4; ++b) db += sPM[b * 64 + tid];
     ((float*)a.sc.p[S_DBETA])[tile * 64 + tid] = db;
-  }
-  if (tid < K) {
-    const int c = tid;
-    float dl = 0.f;
-    for (int vv = 0; vv < V; vv += 8) {
-      float s[8], d[8];
-      load8f(SH + (size_t)c * V + vv, s);
-      load8f(DSH + (size_t)c * V + vv, d);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dl = fmaf(s[e], d[e], dl);
-    }
-    const float lam = ((const float*)a.ws.p[R_LAM])[tile * K + c];
-    ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lam;
   }
 }
 
