@@ -330,12 +330,15 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
   __syncthreads();
 
+  // branch-free: the row is clamped for the load and zeroed after it, so loads issued
+  // together stay in flight together
   auto load_dout8 = [&](int i, int c0) -> bf16x8 {
-    if (i < len) return *(const bf16x8*)(a.dout + ((size_t)(row0 + i) * H + h) * V + c0);
-    bf16x8 z;
+    const int ic = i < len ? i : len - 1;
+    bf16x8 x = *(const bf16x8*)(a.dout + ((size_t)(row0 + ic) * H + h) * V + c0);
+    const bf16 z = to_bf16(0.f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) z[e] = to_bf16(0.f);
-    return z;
+    for (int e = 0; e < 8; ++e) x[e] = i < len ? x[e] : z;
+    return x;
   };
   auto f2b8 = [&](const float* p) -> bf16x8 {
     bf16x8 x;
@@ -433,39 +436,34 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
-    f32x4 acc = zero4();
-    const float bj = sB[j];
     const bool jv = j < len;
+    // all global operands of the pair first (row clamped, zeroed by the select below)
+    const size_t rj = (size_t)(row0 + (jv ? j : len - 1)) * H + h;
+    bf16x8 vrow[V / 32], krow[K / 32];
+    float grow[K / 32][8];
 #pragma unroll
-    for (int s = 0; s < V / 32; ++s) {
-      const int vv = 32 * s + 8 * kg;
-      bf16x8 fb;
-      if (jv) {
-        float x[8];
-        load8(a.v + ((size_t)(row0 + j) * H + h) * V + vv, x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * x[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(0.f);
-      }
-      acc = mfma16(*(const bf16x8*)(sDU + i * VP + vv), fb, acc);
-    }
-    const float rkj = RK[j];
+    for (int s = 0; s < V / 32; ++s) vrow[s] = *(const bf16x8*)(a.v + rj * V + 32 * s + 8 * kg);
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) {
-      const int cc = 32 * s + 8 * kg;
+      krow[s] = *(const bf16x8*)(a.k + rj * K + 32 * s + 8 * kg);
+      load8f(Gg + j * K + 32 * s + 8 * kg, grow[s]);
+    }
+    const float bj = jv ? sB[j] : 0.f;
+    const float bk = bj * RK[j];
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
       bf16x8 fb;
-      if (jv) {
-        float x[8];
-        load8(a.k + ((size_t)(row0 + j) * H + h) * K + cc, x);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * x[e] * rkj * expf(Gg[j * K + cc + e]));
-      } else {
+      for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * to_f32(vrow[s][e]));
+      acc = mfma16(*(const bf16x8*)(sDU + i * VP + 32 * s + 8 * kg), fb, acc);
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) fb[e] = to_bf16(0.f);
-      }
-      acc = mfma16(f2b8(sDW + i * KP + cc), fb, acc);
+    for (int s = 0; s < K / 32; ++s) {
+      bf16x8 fb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bk * to_f32(krow[s][e]) * __expf(grow[s][e]));
+      acc = mfma16(f2b8(sDW + i * KP + 32 * s + 8 * kg), fb, acc);
     }
     const int jj = 16 * bb + lr;
 #pragma unroll
@@ -543,6 +541,9 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
+    float mp[4];  // M' entries of this lane's outputs, needed after the MFMAs
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) mp[rr] = MPg[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr];
     f32x4 acc = zero4();
     const int nsteps = (16 * bb + 15) / 32 + 1;
     for (int s = 0; s < nsteps; ++s) {
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       const int ii = 16 * ba + 4 * kg + rr;
       const float dm = jj < ii ? -acc[rr] : 0.f;
       DMP[ii * 64 + jj] = sB[ii] * dm;
-      float part = dm * MPg[ii * 64 + jj];
+      float part = dm * mp[rr];
       part = group_sum<16>(part);
       if (lr == 0) sPM[bb * 64 + ii] = part;
     }

@@ -117,3 +117,29 @@ def test_backward_extreme_gates_finite():
     do, dsT = cotangents(d, 6)
     for a in gpu_grads(d, "k3", do, dsT):
         assert torch.isfinite(a).all()
+
+
+@pytest.mark.parametrize("T,KV", [(1100, (64, 64)), (600, (128, 128))])
+def test_long_sequences_states_and_gradients(T, KV):
+    """Multi-chunk sequences with a ragged last chunk: initial state in, final state out and
+    every gradient including dS0, against the float64 oracle."""
+    K, V = KV
+    d = make_kda_inputs(2, T, 2, K, V, seed=T, gate="precomputed", state=True, dist="baseline")
+    o, fin, _ = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], d["s0"],
+                                  True, -5.0, K ** -0.5, gate="precomputed")
+    eo, ef = O.kda_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
+                           np64(d["A_log"]), np64(d["dt_bias"]), initial_state=np64(d["s0"]), gate_mode="logdecay")
+    assert rel_err(o, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+    do, dsT = cotangents(d, 9)
+    check(gpu_grads(d, "precomputed", do, dsT), oracle_grads(d, "precomputed", do, dsT))
+
+
+def test_varlen_mixed_lengths():
+    """Packed sequences of 1, 3, 58 and 2 chunks, each with its own initial state."""
+    lens = [40, 150, 3700, 100]
+    T = sum(lens)
+    d = make_kda_inputs(1, T, 2, 64, 64, seed=77, state=True)
+    cu = torch.tensor(np.cumsum([0] + lens), dtype=torch.int32, device="cuda")
+    d["s0"] = torch.randn(len(lens), 2, 64, 64, generator=torch.Generator().manual_seed(3)).cuda() * 0.05
+    do, dsT = cotangents(d, 11, n_states=len(lens))
+    check(gpu_grads(d, "k3", do, dsT, cu), oracle_grads(d, "k3", do, dsT, cu))
