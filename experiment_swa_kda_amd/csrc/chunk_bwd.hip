@@ -242,33 +242,45 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
 constexpr int kVjpThreads = 1024;  // 16 waves per (chunk, head): hides global-load latency
 constexpr int kVjpWaves = kVjpThreads / kWave;
 
+// 512 threads and under 80 KB of LDS, so two tiles share a CU and one tile's global-load
+// latency overlaps the other's work.  T, dT, T^T dT and dW only ever feed bf16 MFMA
+// operands and are stored as bf16; T, dT and T^T dT reuse the (dU lo, delta) region once the
+// dQg / dKd / dW / dA phase is done.
+constexpr int kDenseThreads = 512;
+constexpr int kDenseWaves = kDenseThreads / kWave;
+
 template <int K, int V>
 struct DenseSmem {
-  static constexpr int MP = 65;
-  static constexpr int KP = K + 4;
+  static constexpr int TP = 64 + 8;   // bf16 row stride of the 64 x 64 matrices
+  static constexpr int KP = K + 8;    // bf16 row stride of dW
   static constexpr int VP = V + 8;
-  static constexpr size_t off_t = 0;                            // f32 [64][65] T
-  static constexpr size_t off_dt = off_t + 64 * MP * 4;         // f32 [64][65] dT
-  static constexpr size_t off_y = off_dt + 64 * MP * 4;         // f32 [64][65] T^T dT
-  static constexpr size_t off_dw = off_y + 64 * MP * 4;         // f32 [64][KP] dW
-  static constexpr size_t off_du = off_dw + 64 * KP * 4;        // bf16 [64][VP] dU
+  static constexpr size_t off_du = 0;                           // bf16 [64][VP] dU
   static constexpr size_t off_dul = off_du + 64 * VP * 2;       // bf16 [64][VP] dU - bf16(dU)
   static constexpr size_t off_dl = off_dul + 64 * VP * 2;       // bf16 [64][VP] delta
-  static constexpr size_t off_b = off_dl + 64 * VP * 2;         // f32 [64] beta
+  static constexpr size_t off_dw = off_dl + 64 * VP * 2;        // bf16 [64][KP] dW
+  static constexpr size_t off_b = off_dw + 64 * KP * 2;         // f32 [64] beta
   static constexpr size_t off_pv = off_b + 64 * 4;              // f32 [V/16][64] dbeta partials
   static constexpr size_t off_pm = off_pv + (V / 16) * 64 * 4;  // f32 [4][64]
-  static constexpr size_t bytes = off_pm + 4 * 64 * 4;
+  static constexpr size_t end = off_pm + 4 * 64 * 4;
+  // T, dT, T^T dT (bf16 [64][TP] each, after dA): in the dU-lo / delta region when it is
+  // large enough (V = 128), else behind everything
+  static constexpr bool kAlias = 3 * 64 * TP * 2 <= 2 * 64 * VP * 2;
+  static constexpr size_t off_t = kAlias ? off_dul : end;
+  static constexpr size_t off_dt = off_t + 64 * TP * 2;
+  static constexpr size_t off_y = off_dt + 64 * TP * 2;
+  static constexpr size_t bytes = kAlias ? end : off_y + 64 * TP * 2;
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdArgs a) {
   using L = DenseSmem<K, V>;
-  constexpr int MP = L::MP, KP = L::KP, VP = L::VP;
+  constexpr int MP = L::TP, KP = L::KP, VP = L::VP;
+  constexpr int kVjpThreads = kDenseThreads, kVjpWaves = kDenseWaves;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  float* sT = (float*)(smem + L::off_t);
-  float* sDT = (float*)(smem + L::off_dt);
-  float* sY = (float*)(smem + L::off_y);
-  float* sDW = (float*)(smem + L::off_dw);
+  bf16* sT = (bf16*)(smem + L::off_t);
+  bf16* sDT = (bf16*)(smem + L::off_dt);
+  bf16* sY = (bf16*)(smem + L::off_y);
+  bf16* sDW = (bf16*)(smem + L::off_dw);
   bf16* sDU = (bf16*)(smem + L::off_du);
   bf16* sDUl = (bf16*)(smem + L::off_dul);
   bf16* sDL = (bf16*)(smem + L::off_dl);
@@ -299,12 +311,11 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
   float* DA = (float*)a.sc.p[S_DA] + tile * 64 * 64;
   float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
 
-  // ---- P0: stage T, dU, beta; clear partials ----
-  for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
-    const int i = idx / 64, j = idx % 64;
-    sT[i * MP + j] = Tg[idx];
-    sDT[i * MP + j] = 0.f;
-  }
+  // ---- P0: stage dU, delta, beta; clear partials; T waits in registers until after dA ----
+  static_assert(64 * 64 % (4 * kDenseThreads) == 0, "T staging");
+  float4 treg[64 * 64 / (4 * kDenseThreads)];
+#pragma unroll
+  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
   // dU = dDelta (hi/lo bf16 split) and delta, transposed from their [V][64] histories
   for (int idx = tid; idx < V * 16; idx += kVjpThreads) {
     const int vv = idx / 16, t4 = (idx % 16) * 4;
@@ -349,7 +360,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
 
   // ---- PA: dQg, dKd, dW over the 64 x K grid ----
   // Wave w owns key tile ct and RPW row tiles: the f32 state rows S[c][.] and dS'[c][.] of
-  // its 16 keys are loaded once (all loads issued first), split into hi + lo bf16 once, and
+  // its 16 keys are loaded once (loads issued together), split into hi + lo bf16 once, and
   // reused for every row tile.  The same rows give dlam = lam * sum_v S dS'.
   constexpr int NKT = 4 * (K / 16);
   {
@@ -364,11 +375,6 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       load8f(SH + (size_t)c * V + 32 * sv + 8 * kg, xs[sv]);
       load8f(DSH + (size_t)c * V + 32 * sv + 8 * kg, xd[sv]);
     }
-    bf16x8 aO[RPW][NVS];
-#pragma unroll
-    for (int q = 0; q < RPW; ++q)
-#pragma unroll
-      for (int sv = 0; sv < NVS; ++sv) aO[q][sv] = load_dout8(16 * (rt0 + q) + lr, 32 * sv + 8 * kg);
     const float lamc = ((const float*)a.ws.p[R_LAM])[tile * K + c];
     bf16x8 sHi[NVS], sLo[NVS], dHi[NVS], dLo[NVS];
     float dl = 0.f;
@@ -385,6 +391,9 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
     for (int q = 0; q < RPW; ++q) {
       const int rt = rt0 + q, i = 16 * rt + lr;
       const int p = rt + 4 * ct;
+      bf16x8 aO[NVS];
+#pragma unroll
+      for (int sv = 0; sv < NVS; ++sv) aO[sv] = load_dout8(i, 32 * sv + 8 * kg);
       f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
 #pragma unroll
       for (int sv = 0; sv < NVS; ++sv) {
@@ -392,8 +401,8 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
         const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
         const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
         const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
-        accQ = mfma16(aO[q][sv], sHi[sv], accQ);
-        accQ = mfma16(aO[q][sv], sLo[sv], accQ);
+        accQ = mfma16(aO[sv], sHi[sv], accQ);
+        accQ = mfma16(aO[sv], sLo[sv], accQ);
         accK = mfma16(aL, dHi[sv], accK);
         accK = mfma16(aL, dLo[sv], accK);
         accW = mfma16(uHi, sHi[sv], accW);
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = accQ;
       *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = -accW[rr];
+      for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = to_bf16(-accW[rr]);
     }
   }
   // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
@@ -428,6 +437,16 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       const int ii = 16 * ba + 4 * kg + rr;
       DA[ii * 64 + jj] = jj <= ii ? acc[rr] : 0.f;
     }
+  }
+  __syncthreads();
+  // dU lo and delta are consumed: their region now holds T (bf16) and a zeroed dT
+#pragma unroll
+  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) {
+    const int idx = (q * kDenseThreads + tid) * 4, i = idx / 64, j = idx % 64;
+    bf16* t = sT + i * MP + j;
+    t[0] = to_bf16(treg[q].x); t[1] = to_bf16(treg[q].y); t[2] = to_bf16(treg[q].z); t[3] = to_bf16(treg[q].w);
+    bf16* z = sDT + i * MP + j;
+    z[0] = z[1] = z[2] = z[3] = to_bf16(0.f);
   }
   __syncthreads();
 
@@ -463,11 +482,11 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       bf16x8 fb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bk * to_f32(krow[s][e]) * __expf(grow[s][e]));
-      acc = mfma16(f2b8(sDW + i * KP + 32 * s + 8 * kg), fb, acc);
+      acc = mfma16(*(const bf16x8*)(sDW + i * KP + 32 * s + 8 * kg), fb, acc);
     }
     const int jj = 16 * bb + lr;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) sDT[(16 * ba + 4 * kg + rr) * MP + jj] = acc[rr];
+    for (int rr = 0; rr < 4; ++rr) sDT[(16 * ba + 4 * kg + rr) * MP + jj] = to_bf16(acc[rr]);
   }
   // d(beta v) = T^T dU  -> dv and beta partials
   for (int p = wave; p < 4 * (V / 16); p += kVjpWaves) {
@@ -479,7 +498,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       bf16x8 fa, fb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        fa[e] = to_bf16(sT[(i0 + e) * MP + j]);
+        fa[e] = sT[(i0 + e) * MP + j];
         fb[e] = sDU[(i0 + e) * VP + col];
       }
       acc = mfma16(fa, fb, acc);
@@ -507,8 +526,8 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       bf16x8 fa, fb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        fa[e] = to_bf16(sT[(i0 + e) * MP + j]);
-        fb[e] = to_bf16(sDW[(i0 + e) * KP + c]);
+        fa[e] = sT[(i0 + e) * MP + j];
+        fb[e] = sDW[(i0 + e) * KP + c];
       }
       acc = mfma16(fa, fb, acc);
     }
@@ -526,13 +545,13 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       bf16x8 fa, fb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        fa[e] = to_bf16(sT[(a0 + e) * MP + i]);
-        fb[e] = to_bf16(sDT[(a0 + e) * MP + jcol]);
+        fa[e] = sT[(a0 + e) * MP + i];
+        fb[e] = sDT[(a0 + e) * MP + jcol];
       }
       acc = mfma16(fa, fb, acc);
     }
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) sY[(16 * rt + 4 * kg + rr) * MP + jcol] = acc[rr];
+    for (int rr = 0; rr < 4; ++rr) sY[(16 * rt + 4 * kg + rr) * MP + jcol] = to_bf16(acc[rr]);
   }
   __syncthreads();
 
@@ -551,8 +570,8 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_dense_kernel(BwdArgs a)
       bf16x8 fa, fb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        fa[e] = to_bf16(sY[i * MP + b0 + e]);
-        fb[e] = to_bf16(sT[j * MP + b0 + e]);
+        fa[e] = sY[i * MP + b0 + e];
+        fb[e] = sT[j * MP + b0 + e];
       }
       acc = mfma16(fa, fb, acc);
     }
@@ -1040,7 +1059,7 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     }
     if (stages & (1 << (KDA_STAGE_BWD_DENSE - 10))) {
       auto dense = chunk_bwd_dense_kernel<K, V>;
-      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(kVjpThreads), smem_d, stream, a);
+      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(kDenseThreads), smem_d, stream, a);
       KDA_LAUNCH_CHECK("chunk_backward dense");
     }
     if (stages & (1 << (KDA_STAGE_BWD_DECAY - 10))) {
