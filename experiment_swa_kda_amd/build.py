@@ -27,6 +27,7 @@ SOURCES = ["capi.cpp", "decode.hip", "conv.hip", "norm_gate.hip", "chunk_fwd.hip
 # accumulators feed VALU work every step, and the AGPR form costs a copy per element.
 EXTRA_FLAGS = {
     "chunk_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "chunk_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 ARCH = "gfx950"
 

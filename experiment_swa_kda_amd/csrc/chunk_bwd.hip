@@ -681,20 +681,20 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   if (tid < 64 * (K / 8)) {
     constexpr int LPR = K / 8;
     const int t = tid / LPR, c0 = (tid % LPR) * 8;
-    float qv[8], kv[8];
-    if (t < len) {
-      const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
-      load8(a.q + base, qv);
-      load8(a.k + base, kv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[e] = kv[e] = 0.f;
-    }
+    // every load of the row first (clamped row, zeroed after), so they are in flight together
+    const size_t base = ((size_t)(row0 + (t < len ? t : len - 1)) * H + h) * K + c0;
+    const bf16x8 qr = *(const bf16x8*)(a.q + base), kr = *(const bf16x8*)(a.k + base);
     const float rq = ((const float*)a.ws.p[R_RQ])[tile * 64 + t];
     const float rk = ((const float*)a.ws.p[R_RK])[tile * 64 + t];
-    float sq = 0.f, sk = 0.f;
     float gv[8];
     load8f(Gg + t * K + c0, gv);
+    float qv[8], kv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qv[e] = t < len ? (float)qr[e] : 0.f;
+      kv[e] = t < len ? (float)kr[e] : 0.f;
+    }
+    float sq = 0.f, sk = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       sq += qv[e] * qv[e];
