@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from .kda import KimiDeltaAttention, Linear
 
 
@@ -30,6 +31,38 @@ class GPTConfig:
     n_head: int = 3
     n_embd: int = 384
     mode: str = "project_chunk"
+
+
+class _SoftcapCrossEntropy(torch.autograd.Function):
+    """Mean soft-capped cross entropy on the HIP kernels: forward reads the bf16 logits once,
+    backward reads them again and writes the bf16 logit gradient (nanochat/gpt.py:600-608)."""
+
+    @staticmethod
+    def forward(ctx, logits, targets, vocab, softcap, ignore_index):
+        loss_rows, lse = ops.softcap_cross_entropy_forward(logits, targets, vocab, softcap, ignore_index)
+        count = (targets != ignore_index).sum()
+        ctx.save_for_backward(logits, targets, lse, count)
+        ctx.args = (vocab, softcap, ignore_index)
+        return loss_rows.sum() / count
+
+    @staticmethod
+    def backward(ctx, grad):
+        logits, targets, lse, count = ctx.saved_tensors
+        vocab, softcap, ignore_index = ctx.args
+        scale = grad.float() / count
+        dlogits = ops.softcap_cross_entropy_backward(logits, targets, lse, scale, vocab, softcap,
+                                                     ignore_index)
+        return dlogits, None, None, None, None
+
+
+def softcap_cross_entropy(logits, targets, vocab, softcap=15.0, ignore_index=-1):
+    """mean cross_entropy(softcap * tanh(logits[:, :vocab] / softcap), targets) over rows whose
+    target is not ignore_index; logits [rows, padded vocab].  bf16 CUDA logits run the fused
+    HIP kernels, anything else the eager f32 form."""
+    if logits.is_cuda and logits.dtype == torch.bfloat16:
+        return _SoftcapCrossEntropy.apply(logits, targets, vocab, float(softcap), ignore_index)
+    z = softcap * torch.tanh(logits[:, :vocab].float() / softcap)
+    return F.cross_entropy(z, targets, ignore_index=ignore_index)
 
 
 def norm(x):
@@ -121,11 +154,11 @@ class GPT(nn.Module):
         if x_backout is not None:
             x = x - self.backout_lambda.to(x.dtype) * x_backout
         x = norm(x)
-        logits = self.lm_head(x)[..., : self.config.vocab_size].float()
-        logits = 15 * torch.tanh(logits / 15)
+        logits = self.lm_head(x)
         if targets is None:
-            return logits
-        return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1), ignore_index=-1)
+            return 15 * torch.tanh(logits[..., : self.config.vocab_size].float() / 15)
+        return softcap_cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1),
+                                     self.config.vocab_size, 15.0, -1)
 
 
 def make_optimizer(model: GPT, lr: float = 3e-3):

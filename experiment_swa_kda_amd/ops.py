@@ -319,6 +319,41 @@ def rmsnorm_gate_backward(x, gate, weight, inv_rms, grad_output, eps):
 _LIBRARY = None
 
 
+def softcap_cross_entropy_forward(logits, targets, vocab, softcap, ignore_index=-1):
+    """logits [rows, stride] bf16 (stride >= vocab), targets [rows] int64 ->
+    (loss_rows f32 [rows], lse_rows f32 [rows])."""
+    dev = _require_cuda("softcap_cross_entropy_forward", logits, targets)
+    _check_dtype("softcap_cross_entropy_forward", logits, torch.bfloat16, "logits")
+    _check_dtype("softcap_cross_entropy_forward", targets, torch.int64, "targets")
+    if logits.ndim != 2 or targets.shape != logits.shape[:1]:
+        raise RuntimeError("softcap_cross_entropy_forward: logits [rows, stride] and targets [rows]")
+    logits, targets = _c(logits), _c(targets)
+    rows, stride = logits.shape
+    loss = torch.empty(rows, dtype=torch.float32, device=dev)
+    lse = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_softcap_cross_entropy_forward(rows, int(vocab), stride, float(softcap),
+                                                           ptr(logits), ptr(targets), int(ignore_index),
+                                                           ptr(loss), ptr(lse), _stream(dev))
+    check(rc, "kda_softcap_cross_entropy_forward")
+    return loss, lse
+
+
+def softcap_cross_entropy_backward(logits, targets, lse, grad_scale, vocab, softcap, ignore_index=-1):
+    """grad_scale: f32 device scalar (dL/dmean / non-ignored count) -> grad [rows, stride] bf16."""
+    dev = _require_cuda("softcap_cross_entropy_backward", logits, targets, lse, grad_scale)
+    logits, targets, lse = _c(logits), _c(targets), _c(lse)
+    grad_scale = grad_scale.to(torch.float32).reshape(1).contiguous()
+    rows, stride = logits.shape
+    grad = torch.empty_like(logits)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_softcap_cross_entropy_backward(rows, int(vocab), stride, float(softcap),
+                                                            ptr(logits), ptr(targets), int(ignore_index),
+                                                            ptr(lse), ptr(grad_scale), ptr(grad),
+                                                            _stream(dev))
+    check(rc, "kda_softcap_cross_entropy_backward")
+    return grad
+
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):
     out, fin, _ = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,

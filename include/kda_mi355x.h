@@ -196,6 +196,30 @@ int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* x, const vo
                               float eps, void* dx, void* dgate, float* dweight, void* scratch,
                               hipStream_t stream);
 
+/*
+ * Trainer support: soft-capped cross entropy over bf16 logits [rows, stride] (columns
+ * >= vocab are vocabulary padding).  Replaces the eager f32 chain of nanochat/gpt.py:600-608
+ * (logits.float(), softcap * tanh(logits / softcap), F.cross_entropy(ignore_index=-1)),
+ * which the reference fuses with torch.compile (scripts/base_train.py:267).
+ *   loss_rows[r] = lse_r - z[r, t_r] (0 where t_r == ignore_index), lse_rows[r] = log sum_j exp z[r, j]
+ * The mean is sum(loss_rows) / count(t != ignore_index), formed by the caller.
+ */
+int kda_softcap_cross_entropy_forward(int64_t rows, int32_t vocab, int64_t stride, float softcap,
+                                      const void* logits, const int64_t* targets,
+                                      int64_t ignore_index, float* loss_rows, float* lse_rows,
+                                      hipStream_t stream);
+
+/*
+ * Backward of the above: grad_logits [rows, stride] bf16 =
+ *   grad_scale[0] * (softmax(z) - onehot(t)) * (1 - (z / softcap)^2), zero in ignored rows
+ * and padding columns.  grad_scale is a device scalar (dL/dmean / non-ignored count).
+ */
+int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, int64_t stride, float softcap,
+                                       const void* logits, const int64_t* targets,
+                                       int64_t ignore_index, const float* lse_rows,
+                                       const float* grad_scale, void* grad_logits,
+                                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,9 @@ in plain numpy at float64:
                                current token), nanochat/mixers/kda.py:136-212
 * ``rmsnorm_gate_forward/backward`` tests/kda_oracle.py:164-173,
                                nanochat/mixers/kda.py:46-59
+* ``softcap_cross_entropy``    the trainer's loss, nanochat/gpt.py:600-608
+                               (softcap * tanh(logits / softcap), mean cross entropy
+                               with ignore_index=-1)
 
 Pinning (each function is checked by tests/test_oracle.py against something
 other than its own formula):
@@ -39,6 +42,8 @@ other than its own formula):
 * causal_conv_*: torch.nn.functional.conv1d (grouped) and autograd; decode equals
   full sequence (tests/test_kda_operator.py:167-180).
 * rmsnorm_gate_*: torch.nn.functional.rms_norm and autograd.
+* softcap_cross_entropy: torch.nn.functional.cross_entropy (ignore_index, mean) at
+  float64 and autograd through it; a uniform-logit closed form.
 * full_layer: composed only of the functions above and matrix products; checked
   against the mixer's eager reference mode in tests/test_cpu_api.py.
 """
@@ -419,6 +424,32 @@ def rmsnorm_gate_backward(x, gate, weight, eps, grad_output):
     dn = dn_w * w
     dx = inv * (dn - n * (dn * n).sum(-1, keepdims=True) / D)
     return dx, dgate, dw
+
+
+def softcap_cross_entropy(logits, targets, vocab, softcap=15.0, ignore_index=-1):
+    """Mean soft-capped cross entropy and its logit gradient (nanochat/gpt.py:600-608).
+
+    logits [rows, stride] (columns >= vocab are padding), targets [rows].  Returns
+    (loss, loss_rows, lse_rows, dlogits) with dlogits = d loss / d logits (zero in padding
+    columns and ignored rows)."""
+    x = np.asarray(logits, np.float64)
+    t = np.asarray(targets, np.int64)
+    th = np.tanh(x[:, :vocab] / softcap)
+    z = softcap * th
+    m = z.max(-1, keepdims=True)
+    lse = (m + np.log(np.exp(z - m).sum(-1, keepdims=True)))[:, 0]
+    valid = t != ignore_index
+    rows = np.arange(x.shape[0])
+    tz = np.where(valid, z[rows, np.where(valid, t, 0)], 0.0)
+    loss_rows = np.where(valid, lse - tz, 0.0)
+    count = valid.sum()
+    loss = loss_rows.sum() / count if count else np.nan
+    p = np.exp(z - lse[:, None])
+    p[rows[valid], t[valid]] -= 1.0
+    dz = np.where(valid[:, None], p, 0.0) / max(count, 1)
+    d = np.zeros_like(x)
+    d[:, :vocab] = dz * (1.0 - th * th)
+    return loss, loss_rows, lse, d
 
 
 # ----------------------------------------------------------------------------

@@ -1,0 +1,70 @@
+"""GPU parity of the trainer-support kernels (soft-capped cross entropy) against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kda_oracle as O
+from tests.kda_testutil import rel_err
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from experiment_swa_kda_amd import ops
+    from experiment_swa_kda_amd.model import softcap_cross_entropy
+
+
+def _case(rows, vocab, stride, scale, seed, ignore_every=0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, stride, generator=g) * scale).bfloat16()
+    t = torch.randint(0, vocab, (rows,), generator=g)
+    if ignore_every:
+        t[::ignore_every] = -1
+    return x, t
+
+
+@pytest.mark.parametrize("rows,vocab,stride,scale,ignore_every", [
+    (300, 1000, 1024, 3.0, 7),      # padded vocabulary, ignored rows
+    (64, 32768, 32768, 1.0, 0),     # the trainer's vocabulary
+    (33, 4101, 4104, 60.0, 3),      # saturated tanh, ragged vocab tail
+    (5, 8, 8, 1.0, 0),              # one vector per row
+])
+def test_softcap_ce_matches_oracle(rows, vocab, stride, scale, ignore_every):
+    x, t = _case(rows, vocab, stride, scale, seed=rows + vocab, ignore_every=ignore_every)
+    loss_o, rows_o, lse_o, d_o = O.softcap_cross_entropy(x.double().numpy(), t.numpy(), vocab, 15.0, -1)
+    xd, td = x.cuda().requires_grad_(), t.cuda()
+    loss = softcap_cross_entropy(xd, td, vocab, 15.0, -1)
+    loss.backward()
+    # f32 arithmetic with ~1 ulp exp/rcp: the loss to ~1e-6, the bf16 gradient to bf16 rounding
+    assert abs(loss.item() - loss_o) <= 1e-5 * max(1.0, abs(loss_o))
+    lr, lse = ops.softcap_cross_entropy_forward(xd.detach(), td, vocab, 15.0, -1)
+    np.testing.assert_allclose(lse.cpu().double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(lr.cpu().double().numpy(), rows_o, rtol=2e-5, atol=2e-5)
+    d = xd.grad.float().cpu()
+    assert rel_err(d, d_o) < 5e-3
+    assert torch.all(d[:, vocab:] == 0)
+    if ignore_every:
+        assert torch.all(d[::ignore_every] == 0)
+
+
+def test_softcap_ce_deterministic_and_scaled_gradient():
+    x, t = _case(128, 2048, 2048, 2.0, seed=5)
+    xd, td = x.cuda(), t.cuda()
+    _, lse1 = ops.softcap_cross_entropy_forward(xd, td, 2048, 15.0)
+    _, lse2 = ops.softcap_cross_entropy_forward(xd, td, 2048, 15.0)
+    assert torch.equal(lse1, lse2)
+    # the upstream gradient scales the logit gradient linearly
+    g1 = ops.softcap_cross_entropy_backward(xd, td, lse1, torch.tensor(1.0, device="cuda"), 2048, 15.0)
+    g2 = ops.softcap_cross_entropy_backward(xd, td, lse1, torch.tensor(0.25, device="cuda"), 2048, 15.0)
+    assert torch.equal((g1.float() * 0.25).bfloat16(), g2)
+
+
+def test_softcap_ce_rejects_bad_arguments():
+    x = torch.zeros(4, 12, dtype=torch.bfloat16, device="cuda")
+    t = torch.zeros(4, dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError):
+        ops.softcap_cross_entropy_forward(x, t, 10, 15.0)  # stride not a multiple of 8
+    with pytest.raises(RuntimeError):
+        ops.softcap_cross_entropy_forward(x[:, :8], t, 10, 15.0)  # vocab > stride

@@ -253,3 +253,35 @@ def test_rmsnorm_gate_matches_torch():
     gm = O.rmsnorm_gate_backward(x.detach().numpy(), gt.detach().numpy(), w.detach().numpy(), 1e-5, dy)
     for a, m in zip(ga, gm):
         np.testing.assert_allclose(m, a.numpy(), rtol=1e-11, atol=1e-11)
+
+
+# --- soft-capped cross entropy ------------------------------------------------
+
+def test_softcap_cross_entropy_matches_torch():
+    g = torch.Generator().manual_seed(11)
+    rows, vocab, stride = 37, 50, 56
+    x = (torch.randn(rows, stride, generator=g, dtype=torch.float64) * 20).requires_grad_()
+    t = torch.randint(0, vocab, (rows,), generator=g)
+    t[::5] = -1
+    z = 15.0 * torch.tanh(x[:, :vocab] / 15.0)
+    ref = F.cross_entropy(z, t, ignore_index=-1)
+    ref.backward()
+    loss, loss_rows, lse, d = O.softcap_cross_entropy(x.detach().numpy(), t.numpy(), vocab, 15.0, -1)
+    assert abs(loss - ref.item()) < 1e-12
+    np.testing.assert_allclose(d, x.grad.numpy(), rtol=0, atol=1e-14)
+    assert np.all(d[:, vocab:] == 0) and np.all(d[::5] == 0)
+    np.testing.assert_allclose(lse, torch.logsumexp(z, -1).detach().numpy(), rtol=1e-13)
+    assert np.all(loss_rows[::5] == 0)
+
+
+def test_softcap_cross_entropy_uniform_closed_form():
+    # equal logits: every row's loss is log(vocab), the gradient (1/vocab - onehot) / rows
+    rows, vocab = 4, 10
+    x = np.full((rows, vocab), 3.0)
+    t = np.array([0, 3, 9, 2])
+    loss, _, _, d = O.softcap_cross_entropy(x, t, vocab, 15.0)
+    assert abs(loss - np.log(vocab)) < 1e-13
+    sech2 = 1.0 - np.tanh(3.0 / 15.0) ** 2
+    exp = np.full((rows, vocab), 1.0 / vocab)
+    exp[np.arange(rows), t] -= 1.0
+    np.testing.assert_allclose(d, exp / rows * sech2, atol=1e-15)
