@@ -130,29 +130,36 @@ def kernel_times(torch, t, do, gate, reps=20):
     return res
 
 
-def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42):
+def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42, graphed=True):
     """6-layer all-KDA decoder, d_model 384, H3 D128, vocab 32768,
     B2 T4096, 4 gradient-accumulation microsteps per update (32,768 tokens), uniform
     random token ids, AdamW update.  Returns tokens/s as the median over the timed
-    updates (the reference scores the median of steps 2-6, docs/BENCHMARK.md:33-36)."""
-    from experiment_swa_kda_amd.model import GPT, GPTConfig, make_optimizer
+    updates (the reference scores the median of steps 2-6, docs/BENCHMARK.md:33-36).
+    graphed: the whole update (4 x forward + backward, optimizer step) is one HIP graph
+    replay (model.GraphedUpdate); otherwise every op is dispatched eagerly."""
+    from experiment_swa_kda_amd.model import GPT, GPTConfig, GraphedUpdate, make_optimizer
 
     torch.manual_seed(seed)
     cfg = GPTConfig(sequence_len=4096, vocab_size=32768, n_layer=6, n_head=3, n_embd=384)
     model = GPT(cfg).cuda()
     model.init_weights()
-    opt = make_optimizer(model)
+    opt = make_optimizer(model, capturable=graphed)
     g = torch.Generator(device="cuda").manual_seed(seed)
     B, T = 2, 4096
     data = [torch.randint(0, cfg.vocab_size, (B, T + 1), device="cuda", generator=g) for _ in range(accum)]
 
-    def update():
-        for mb in data:
-            loss = model(mb[:, :-1], mb[:, 1:]) / accum
-            loss.backward()
-        opt.step()
-        opt.zero_grad(set_to_none=True)
-        return loss
+    if graphed:
+        step = GraphedUpdate(model, opt, data, warmup=warmup)
+        update = step
+        warmup = 1
+    else:
+        def update():
+            for mb in data:
+                loss = model(mb[:, :-1], mb[:, 1:]) / accum
+                loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            return loss * accum
 
     times = []
     for i in range(warmup + updates):
@@ -164,8 +171,9 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42):
             times.append(time.perf_counter() - t0)
     ms = statistics.median(times) * 1e3
     return {"tok_per_s": round(B * T * accum / (ms * 1e-3), 1), "ms_per_update": round(ms, 3),
-            "tokens_per_update": B * T * accum, "updates_timed": updates, "loss": round(float(loss) * accum, 4),
-            "optimizer": "AdamW", "reference_gb10_tok_per_s": 44942}
+            "tokens_per_update": B * T * accum, "updates_timed": updates,
+            "loss": round(float(loss.detach()), 4), "optimizer": "AdamW",
+            "execution": "hip_graph" if graphed else "eager", "reference_gb10_tok_per_s": 44942}
 
 
 def load_traffic():

@@ -60,6 +60,8 @@ SIGNATURES = {
     "kda_rmsnorm_gate_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P]),
     "kda_softcap_cross_entropy_forward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P]),
     "kda_softcap_cross_entropy_backward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P, _P]),
+    "kda_weight_grad_scratch_bytes": (ctypes.c_size_t, [_L, _I, _I]),
+    "kda_weight_grad": (ctypes.c_int, [_L, _I, _I, _P, _L, _P, _L, _P, _P, _P]),
 }
 
 _lib = None

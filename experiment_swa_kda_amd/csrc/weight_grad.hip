@@ -1,0 +1,277 @@
+// Weight gradient of a linear layer, dW[N, K] (f32) = dy[M, N]^T x[M, K] (bf16), for the
+// trainer's projections (M = batch * tokens, N and K a few hundred).
+//
+// Reference: the weight-gradient GEMM that autograd runs for nanochat's Linear
+// (nanochat/gpt.py:52-57: F.linear on the bf16 cast of an f32 master weight).  Library
+// GEMMs tile this shape (a long contraction, a small output) into a few dozen workgroups;
+// here the contraction is split into 512-row ranges, one workgroup per (output tile, range),
+// and the f32 partials are summed in a fixed order by a second kernel (deterministic, no
+// atomics).
+//
+// Both operands are row-major in M, while an MFMA operand fragment holds 8 consecutive
+// contraction rows of one column.  Each thread loads an 8 x 8 block (8 rows of one 16-byte
+// column group), transposes it in registers and writes 8 16-byte rows of the transposed
+// slab [column][row] to LDS, so every global access and every LDS access is 16 bytes wide.
+// A workgroup covers kWgDepth 128-row steps of the contraction and issues all of their
+// global loads up front; one barrier per step (double-buffered LDS).
+#include "kda_device.hpp"
+#include "kda_host.hpp"
+
+namespace kda {
+
+constexpr int kWgThreads = 256;
+constexpr int kWgTile = 64;          // output tile: 64 (n) x 64 (k)
+constexpr int kWgRows = 128;         // contraction rows per step
+constexpr int kWgDepth = 4;         // contraction steps whose loads are in flight
+constexpr int kWgPitch = kWgRows + 8;  // bf16 per transposed LDS row (+16 B against bank conflicts)
+
+struct WgLds {
+  bf16 dyT[2][kWgTile * kWgPitch];
+  bf16 xT[2][kWgTile * kWgPitch];
+};
+
+// Loads this thread's 8 x 8 block: rows m0 + r (r < 8), columns c .. c + 7 of a row-major
+// [M, ncols] operand with leading dimension ld.  Rows >= m_end and columns >= ncols read
+// as zero.  Every load is issued unconditionally from a clamped address and masked with
+// bit operations afterwards, so no branch separates a load from its use (a branch would
+// make the compiler wait for all outstanding loads at the join).  VEC: ld and the base are
+// 16-byte aligned and ncols % 8 == 0.
+template <bool VEC>
+__device__ __forceinline__ void load_block(const bf16* __restrict__ p, long ld, int ncols, int m0,
+                                           int m_end, int c, bf16x8 (&v)[8]) {
+  if constexpr (VEC) {
+    const bool cok = c < ncols;
+    const int cc = cok ? c : 0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = m0 + r;
+      const int mc = m < m_end ? m : m_end - 1;
+      v[r] = *reinterpret_cast<const bf16x8*>(p + (long)mc * ld + cc);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const unsigned keep = (cok && m0 + r < m_end) ? 0xffffffffu : 0u;
+      uint4 u = __builtin_bit_cast(uint4, v[r]);
+      u.x &= keep; u.y &= keep; u.z &= keep; u.w &= keep;
+      v[r] = __builtin_bit_cast(bf16x8, u);
+    }
+  } else {
+    unsigned short e16[8][8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = m0 + r;
+      const int mc = m < m_end ? m : m_end - 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ce = c + e < ncols ? c + e : ncols - 1;
+        e16[r][e] = reinterpret_cast<const unsigned short*>(p)[(long)mc * ld + ce];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const unsigned short keep = (m0 + r < m_end && c + e < ncols) ? 0xffff : 0;
+        v[r][e] = __builtin_bit_cast(bf16, (unsigned short)(e16[r][e] & keep));
+      }
+  }
+}
+
+// 16-byte chunk c of transposed row `row` lives at chunk c ^ ((row / 8) % 8): the eight
+// threads that write one chunk index into rows 8 cb + j (cb = 0..7) then hit eight
+// different bank groups instead of one.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 3) & 7); }
+
+// Writes the transpose of an 8 x 8 block: LDS row (column c0 + j) gets rows 8 mb .. 8 mb + 7.
+__device__ __forceinline__ void store_transposed(bf16* slab, int col0, int mb, const bf16x8 (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    bf16x8 w;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) w[r] = v[r][j];
+    const int row = col0 + j;
+    *reinterpret_cast<bf16x8*>(slab + row * kWgPitch + 8 * swz(row, mb)) = w;
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(
+    int M, int N, int K, const bf16* __restrict__ dy, long ldd, const bf16* __restrict__ x, long ldx,
+    int rows_per_split, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) WgLds s;
+  // 1-D grid of kXcds * tiles * ceil(splits / kXcds): workgroups are dispatched round-robin
+  // over the XCDs (linear id mod 8), so all tiles of one split (the same dy / x rows) share
+  // an XCD and its L2, and every row range is fetched from HBM about once.
+  const int tiles_k = (K + kWgTile - 1) / kWgTile;
+  const int tiles = tiles_k * ((N + kWgTile - 1) / kWgTile);
+  const int L = blockIdx.x, rest = L / kXcds;
+  const int tile = rest % tiles;
+  const int split = (rest / tiles) * kXcds + L % kXcds;
+  if (split * rows_per_split >= max(M, 1)) return;  // past the last split (grid rounding)
+  const int n0 = (tile / tiles_k) * kWgTile, k0 = (tile % tiles_k) * kWgTile;
+  const int m_begin = split * rows_per_split;
+  const int m_end = min(M, m_begin + rows_per_split);
+  const int tid = threadIdx.x;
+  // loader role: threads 0..127 stage dy, 128..255 stage x; block (mb, cb) of the step
+  const bool is_x = tid >= 128;
+  const int b = tid % 128, mb = b / 8, cb = b % 8;
+  const bf16* src = is_x ? x : dy;
+  const long ld = is_x ? ldx : ldd;
+  const int ncols = is_x ? K : N;
+  const int col = (is_x ? k0 : n0) + 8 * cb;
+  // compute role: wave (wn, wk) owns the 32 x 32 sub-tile (32 wn.., 32 wk..)
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int wn = wave / 2, wk = wave % 2;
+  const int lr = lane % 16, kg = lane / 16;
+
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero4();
+
+  if (m_end <= m_begin) {  // M == 0: the gradient is zero, and there is no row to load
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int k = k0 + 32 * wk + 16 * j + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = n0 + 32 * wn + 16 * i + 4 * kg + r;
+          if (n < N && k < K) out[(size_t)n * K + k] = 0.f;
+        }
+      }
+    return;
+  }
+  // A workgroup runs exactly kWgDepth 128-row steps (rows past m_end are zero), and all of
+  // their global loads are issued before the first step.
+  bf16x8 v[kWgDepth][8];
+#pragma unroll
+  for (int d = 0; d < kWgDepth; ++d)
+    load_block<VEC>(src, ld, ncols, m_begin + d * kWgRows + 8 * mb, m_end, col, v[d]);
+#pragma unroll
+  for (int st = 0; st < kWgDepth; ++st) {
+    const int buf = st & 1;
+    store_transposed(is_x ? s.xT[buf] : s.dyT[buf], 8 * cb, mb, v[st]);
+    __syncthreads();
+    const bf16* A = s.dyT[buf];
+    const bf16* B = s.xT[buf];
+#pragma unroll
+    for (int ks = 0; ks < kWgRows / 32; ++ks) {
+      bf16x8 a[2], bb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = 32 * wn + 16 * i + lr;
+        a[i] = *reinterpret_cast<const bf16x8*>(A + row * kWgPitch + 8 * swz(row, 4 * ks + kg));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = 32 * wk + 16 * j + lr;
+        bb[j] = *reinterpret_cast<const bf16x8*>(B + row * kWgPitch + 8 * swz(row, 4 * ks + kg));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma16(a[i], bb[j], acc[i][j]);
+    }
+  }
+  float* o = out + (size_t)split * N * K;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = k0 + 32 * wk + 16 * j + lr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 32 * wn + 16 * i + 4 * kg + r;
+        if (n < N && k < K) o[(size_t)n * K + k] = acc[i][j][r];
+      }
+    }
+}
+
+// out[i] = sum_p part[p][i] in order p = 0, 1, ...; four outputs per thread, the loads of
+// kSumBatch partials issued before any is added.
+constexpr int kSumBatch = 8;
+__global__ __launch_bounds__(256) void partial_sum_kernel(int parts, long n, const float* __restrict__ part,
+                                                          float* __restrict__ out) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (n % 4 == 0) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int p0 = 0; p0 < parts; p0 += kSumBatch) {
+      float4 v[kSumBatch];
+#pragma unroll
+      for (int u = 0; u < kSumBatch; ++u) {
+        const int p = p0 + u < parts ? p0 + u : parts - 1;
+        v[u] = *reinterpret_cast<const float4*>(part + (size_t)p * n + i);
+      }
+#pragma unroll
+      for (int u = 0; u < kSumBatch; ++u) {
+        if (p0 + u < parts) {
+          acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+        }
+      }
+    }
+    *reinterpret_cast<float4*>(out + i) = acc;
+  } else {
+    for (long e = i; e < i + 4 && e < n; ++e) {
+      float acc = 0.f;
+      for (int p = 0; p < parts; ++p) acc += part[(size_t)p * n + e];
+      out[e] = acc;
+    }
+  }
+}
+
+struct WgPlan {
+  int tiles, splits, rows_per_split;
+};
+
+static WgPlan plan_weight_grad(int M, int N, int K) {
+  WgPlan p;
+  p.tiles = ((N + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
+  p.rows_per_split = kWgDepth * kWgRows;
+  p.splits = max(1, (M + p.rows_per_split - 1) / p.rows_per_split);
+  return p;
+}
+
+}  // namespace kda
+
+extern "C" size_t kda_weight_grad_scratch_bytes(int64_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > 0x7fffffff) return 0;
+  const kda::WgPlan p = kda::plan_weight_grad((int)M, N, K);
+  return p.splits > 1 ? (size_t)p.splits * N * K * sizeof(float) : 0;
+}
+
+extern "C" int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, int64_t ldd,
+                               const void* x, int64_t ldx, float* dweight, void* scratch,
+                               hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(M >= 0 && M <= 0x7fffffff && N > 0 && K > 0, "weight_grad: invalid shape");
+  KDA_REQUIRE(ldd >= N && ldx >= K, "weight_grad: leading dimensions must cover the rows");
+  KDA_REQUIRE(dweight && (M == 0 || (dy && x)), "weight_grad: null pointer");
+  // M == 0: one split with no steps writes the zero gradient (no memset node, so the call
+  // stays capturable)
+  const WgPlan p = M > 0 ? plan_weight_grad((int)M, N, K)
+                         : WgPlan{((N + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile), 1, 1};
+  KDA_REQUIRE(p.splits == 1 || scratch, "weight_grad: scratch required (kda_weight_grad_scratch_bytes)");
+  KDA_REQUIRE(aligned16(scratch, dweight), "weight_grad: dweight and scratch must be 16-byte aligned");
+  const bool vec = aligned16(dy, x) && ldd % 8 == 0 && ldx % 8 == 0 && N % 8 == 0 && K % 8 == 0;
+  float* part = p.splits > 1 ? (float*)scratch : dweight;
+  dim3 grid(kXcds * p.tiles * ((p.splits + kXcds - 1) / kXcds));
+  if (vec)
+    hipLaunchKernelGGL(weight_grad_kernel<true>, grid, dim3(kWgThreads), 0, stream, (int)M, N, K,
+                       (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
+  else
+    hipLaunchKernelGGL(weight_grad_kernel<false>, grid, dim3(kWgThreads), 0, stream, (int)M, N, K,
+                       (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
+  KDA_LAUNCH_CHECK("weight_grad");
+  if (p.splits > 1) {
+    const long n = (long)N * K;
+    const unsigned blocks = (unsigned)((n + 4 * 256 - 1) / (4 * 256));
+    hipLaunchKernelGGL(partial_sum_kernel, dim3(blocks), dim3(256), 0, stream, p.splits, n,
+                       (const float*)part, dweight);
+    KDA_LAUNCH_CHECK("weight_grad reduce");
+  }
+  return KDA_OK;
+}

@@ -49,10 +49,42 @@ class KDAState:
     v_conv: torch.Tensor
 
 
+_SPLIT_WGRAD_MAX = 1 << 21  # weights up to 2M entries take the split-contraction kernel
+
+
+class _LinearBF16(torch.autograd.Function):
+    """y = x W^T with an f32 master weight cast to bf16; the weight gradient comes from the
+    split-contraction HIP kernel straight in f32 (nanochat/gpt.py:52-57)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        w = weight.to(torch.bfloat16)
+        ctx.save_for_backward(x, w)
+        ctx.has_bias = bias is not None
+        return F.linear(x, w, None if bias is None else bias.to(torch.bfloat16))
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, w = ctx.saved_tensors
+        g2 = grad.reshape(-1, grad.shape[-1])
+        dx = (g2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            x2 = x.reshape(-1, x.shape[-1])
+            if w.numel() <= _SPLIT_WGRAD_MAX:
+                dw = ops.weight_grad(g2, x2)
+            else:  # a large output (the lm_head) already fills the GPU as one library GEMM
+                dw = (g2.t() @ x2).float()
+        db = g2.float().sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dx, dw, db
+
+
 class Linear(nn.Linear):
     """Keep master weights in FP32 while matching activation dtype for matmul."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda and x.dtype == torch.bfloat16 and self.weight.dtype == torch.float32:
+            return _LinearBF16.apply(x, self.weight, self.bias)
         bias = None if self.bias is None else self.bias.to(dtype=x.dtype)
         return F.linear(x, self.weight.to(dtype=x.dtype), bias)
 

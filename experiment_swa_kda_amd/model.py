@@ -161,8 +161,55 @@ class GPT(nn.Module):
                                      self.config.vocab_size, 15.0, -1)
 
 
-def make_optimizer(model: GPT, lr: float = 3e-3):
+def make_optimizer(model: GPT, lr: float = 3e-3, capturable: bool = False):
     """AdamW over all parameters (the reference uses MuonAdamW, nanochat/optim.py; the
-    optimizer is outside the KDA path and only has to run every update)."""
+    optimizer is outside the KDA path and only has to run every update).  ``capturable``
+    keeps the step count on the device so that the update can be replayed from a graph."""
     return torch.optim.AdamW(model.parameters(), lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0,
-                             fused=True)
+                             fused=True, capturable=capturable)
+
+
+class GraphedUpdate:
+    """One training update (``len(batches)`` gradient-accumulation microsteps of forward +
+    backward, then the optimizer step) captured once as a HIP graph and replayed.
+
+    The reference compiles the model with torch.compile (scripts/base_train.py:267) to cut
+    per-op overhead; here the same kernels are recorded once and replayed, so one update is
+    one graph launch instead of a few thousand host-side dispatches.  Every kernel of the
+    update runs on each replay.  ``batches`` are static [B, T + 1] token buffers: copy the
+    next data into them before calling.  The optimizer must be capturable
+    (make_optimizer(..., capturable=True)); every launch in the KDA library is
+    stream-ordered and host-synchronisation free, as capture requires.
+    """
+
+    def __init__(self, model: GPT, opt, batches, warmup: int = 2):
+        self.model, self.opt, self.batches = model, opt, batches
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._update()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        opt.zero_grad(set_to_none=True)
+        with torch.cuda.graph(self.graph):
+            self.loss = self._update(zero=False)
+        torch.cuda.synchronize()
+
+    def _update(self, zero: bool = True):
+        n = len(self.batches)
+        total = None
+        for mb in self.batches:
+            loss = self.model(mb[:, :-1], mb[:, 1:]) / n
+            loss.backward()
+            total = loss.detach() if total is None else total + loss.detach()
+        self.opt.step()
+        if zero:
+            self.opt.zero_grad(set_to_none=True)
+        return total
+
+    def __call__(self):
+        """Runs one update; returns the (static) mean loss tensor of the update."""
+        self.graph.replay()
+        return self.loss

@@ -354,6 +354,28 @@ def softcap_cross_entropy_backward(logits, targets, lse, grad_scale, vocab, soft
     check(rc, "kda_softcap_cross_entropy_backward")
     return grad
 
+def weight_grad(grad_output, x):
+    """dW [N, K] f32 = grad_output[M, N]^T x[M, K] (bf16, 2-D, unit column stride)."""
+    dev = _require_cuda("weight_grad", grad_output, x)
+    _check_dtype("weight_grad", grad_output, torch.bfloat16, "grad_output")
+    _check_dtype("weight_grad", x, torch.bfloat16, "x")
+    if grad_output.ndim != 2 or x.ndim != 2 or grad_output.shape[0] != x.shape[0]:
+        raise RuntimeError("weight_grad: grad_output [M, N] and x [M, K] expected")
+    if grad_output.stride(1) != 1 or (grad_output.shape[0] > 1 and grad_output.stride(0) < grad_output.shape[1]):
+        grad_output = grad_output.contiguous()
+    if x.stride(1) != 1 or (x.shape[0] > 1 and x.stride(0) < x.shape[1]):
+        x = x.contiguous()
+    M, N = grad_output.shape
+    K = x.shape[1]
+    lib = _lib.load()
+    scratch = torch.empty(lib.kda_weight_grad_scratch_bytes(M, N, K), dtype=torch.uint8, device=dev)
+    dw = torch.empty(N, K, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.kda_weight_grad(M, N, K, ptr(grad_output), max(grad_output.stride(0), N), ptr(x),
+                                 max(x.stride(0), K), ptr(dw), ptr(scratch), _stream(dev))
+    check(rc, "kda_weight_grad")
+    return dw
+
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):
     out, fin, _ = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,

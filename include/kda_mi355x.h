@@ -220,6 +220,18 @@ int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, int64_t stri
                                        const float* grad_scale, void* grad_logits,
                                        hipStream_t stream);
 
+/* Bytes of scratch kda_weight_grad needs for an (M, N, K) problem (0: none). */
+size_t kda_weight_grad_scratch_bytes(int64_t M, int32_t N, int32_t K);
+
+/*
+ * Trainer support: weight gradient of a linear layer, dweight[N, K] f32 = dy[M, N]^T x[M, K]
+ * (bf16, row-major with leading dimensions ldd, ldx).  Replaces the weight-gradient GEMM
+ * autograd runs for nanochat's Linear (nanochat/gpt.py:52-57).  Split-contraction partials
+ * are summed in a fixed order (deterministic); dweight is overwritten.
+ */
+int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, int64_t ldd, const void* x,
+                    int64_t ldx, float* dweight, void* scratch, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,3 +85,48 @@ def test_tiny_gpt_trains_and_matches_reference_mode_logits():
             b.attn.mode = "reference"
         ref = model(idx[:, :-1])
     assert rel_err(logits, ref) < 2e-2
+
+
+def test_graphed_update_matches_eager_updates():
+    """The captured update replays the eager update: same losses and parameters over
+    several replays with fresh data copied in between (eager work between replays)."""
+    from experiment_swa_kda_amd.model import GraphedUpdate, make_optimizer
+    cfg = GPTConfig(sequence_len=128, vocab_size=512, n_layer=2, n_head=2, n_embd=256)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    data = [[torch.randint(0, 512, (2, 129), device="cuda", generator=g) for _ in range(2)] for _ in range(5)]
+    data[1] = data[0]  # the two warm-up updates of the graphed trainer see the initial buffers
+
+    def fresh():
+        torch.manual_seed(0)
+        m = GPT(cfg).cuda()
+        m.init_weights()
+        with torch.no_grad():
+            for b in m.transformer.h:
+                b.attn.o_proj.weight.normal_(0, 0.02)
+                b.mlp.c_proj.weight.normal_(0, 0.02)
+        return m
+
+    eager = fresh()
+    opt_e = make_optimizer(eager, capturable=True)
+    eager_losses = []
+    for step in range(5):
+        total = 0.0
+        for mb in data[step]:
+            loss = eager(mb[:, :-1], mb[:, 1:]) / 2
+            loss.backward()
+            total += loss.item()
+        opt_e.step()
+        opt_e.zero_grad(set_to_none=True)
+        eager_losses.append(total)
+
+    graphed = fresh()
+    opt_g = make_optimizer(graphed, capturable=True)
+    static = [d.clone() for d in data[0]]
+    update = GraphedUpdate(graphed, opt_g, static, warmup=2)
+    for upd in range(2, 5):
+        for i in range(2):
+            static[i].copy_(data[upd][i])
+        loss = update().item()
+        assert abs(loss - eager_losses[upd]) < 1e-4 * abs(eager_losses[upd]), (upd, loss, eager_losses[upd])
+    for (n, pe), (_, pg) in zip(eager.named_parameters(), graphed.named_parameters()):
+        assert rel_err(pg, pe) < 1e-4, n

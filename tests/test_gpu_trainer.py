@@ -68,3 +68,45 @@ def test_softcap_ce_rejects_bad_arguments():
         ops.softcap_cross_entropy_forward(x, t, 10, 15.0)  # stride not a multiple of 8
     with pytest.raises(RuntimeError):
         ops.softcap_cross_entropy_forward(x[:, :8], t, 10, 15.0)  # vocab > stride
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (8192, 384, 384),   # the trainer's projections
+    (8192, 1536, 384),  # MLP
+    (4097, 128, 384),   # ragged contraction
+    (1000, 3, 384),     # unaligned output rows (element path)
+    (777, 130, 24),     # ragged tile edges
+    (64, 16, 8),        # one step, one split
+])
+def test_weight_grad_matches_matmul(M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    dy = torch.randn(M, N, generator=g).bfloat16()
+    x = torch.randn(M, K, generator=g).bfloat16()
+    exp = dy.double().T @ x.double()
+    dw = ops.weight_grad(dy.cuda(), x.cuda())
+    assert dw.dtype == torch.float32 and dw.shape == (N, K)
+    assert rel_err(dw.cpu(), exp) < 1e-5
+    assert torch.equal(dw, ops.weight_grad(dy.cuda(), x.cuda()))  # fixed-order reduction
+
+
+def test_weight_grad_strided_views_and_empty():
+    g = torch.Generator().manual_seed(9)
+    big = torch.randn(2048, 1024, generator=g).bfloat16().cuda()
+    dy, x = big[:, 8:392], big[:, 512:896]  # leading dimension 1024
+    exp = dy.double().T @ x.double()
+    assert rel_err(ops.weight_grad(dy, x), exp) < 1e-5
+    z = ops.weight_grad(big[:0, :64], big[:0, :32])
+    assert z.shape == (64, 32) and torch.all(z == 0)
+
+
+def test_linear_autograd_uses_f32_weight_gradient():
+    from experiment_swa_kda_amd.kda import Linear
+    torch.manual_seed(0)
+    lin = Linear(384, 256, bias=False).cuda()
+    x = torch.randn(4, 300, 384, device="cuda").bfloat16().requires_grad_()
+    y = lin(x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    w16 = lin.weight.detach().bfloat16().double()
+    assert rel_err(lin.weight.grad, gy.double().reshape(-1, 256).T @ x.detach().double().reshape(-1, 384)) < 1e-5
+    assert rel_err(x.grad, (gy.double() @ w16)) < 1e-2
