@@ -347,12 +347,15 @@ class _ProjectConvolutionAutograd(torch.autograd.Function):
 
 def kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias, *, initial_state=None,
         output_final_state=False, mode="reference", lower_bound=-5.0, scale=None,
-        allow_fallback=True, cu_seqlens=None, gate="k3"):
+        allow_fallback=True, cu_seqlens=None, gate="k3", state_in_place=False):
     """Run KDA through the requested backend (reference kda.py:561-673).
 
     Returns ``(output [B,T,H,V], final_state [N,H,V,K] or None)``.  Accelerated modes
     never fall back to the eager loop; ``allow_fallback`` is accepted for API
-    compatibility only.
+    compatibility only.  ``state_in_place`` (an extension for decode caches): a
+    single-token recurrent step writes the new state into ``initial_state`` and returns
+    that tensor, instead of allocating a new one; by default the initial state is never
+    written, as in the reference.
     """
     del allow_fallback
     if mode not in MODES:
@@ -396,9 +399,11 @@ def kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias, *, initial_state=None,
         _record("chunk_forward")
         return _record_backward(output, "chunk_backward"), final_state
     if q.shape[1] == 1 and cu_seqlens is None:
+        in_place = state_in_place and initial_state is not None and initial_state.is_contiguous()
         output, final_state = ops.recurrent_decode(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
                                                    initial_state, output_final_state,
-                                                   float(lower_bound), resolved_scale, gate=gate)
+                                                   float(lower_bound), resolved_scale, gate=gate,
+                                                   out_state=initial_state if in_place else None)
         _record("recurrent_decode")
         return output, final_state
     output, final_state, _ = ops.chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
@@ -494,7 +499,10 @@ class KimiDeltaAttention(nn.Module):
         self.o_proj = Linear(hidden_size, hidden_size, bias=False)
 
     def forward(self, hidden_states, state: KDAState | None = None, output_final_state: bool = False,
-                mode: str | None = None, allow_fallback: bool | None = None):
+                mode: str | None = None, allow_fallback: bool | None = None,
+                state_in_place: bool = False):
+        """``state_in_place`` (extension): a one-token recurrent step updates
+        ``state.memory`` in place (see ``kda``); the returned state holds that tensor."""
         if hidden_states.ndim != 3 or hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"hidden_states must have shape [B,T,{self.hidden_size}]")
         batch, length, _ = hidden_states.shape
@@ -522,7 +530,7 @@ class KimiDeltaAttention(nn.Module):
         mixed, final_memory = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias,
                                   initial_state=memory, output_final_state=want_state,
                                   mode=requested_mode, lower_bound=self.lower_bound,
-                                  allow_fallback=requested_fallback)
+                                  allow_fallback=requested_fallback, state_in_place=state_in_place)
         output_gate = self.g_proj(hidden_states).reshape(batch, length, self.num_heads, self.head_dim)
         use_fused = (requested_mode != "reference" and mixed.is_cuda and mixed.dtype == torch.bfloat16
                      and output_gate.dtype == torch.bfloat16 and self.head_dim in (64, 128)

@@ -7,7 +7,9 @@ per-layer residual / x0 scalars, KDA mixer + ReLU^2 MLP blocks, mid-depth backou
 soft-capped logits and cross entropy.  Master weights stay f32 and are cast to the
 activation dtype inside ``Linear`` (nanochat/gpt.py:52-57).  The KDA mixer is the HIP
 ``KimiDeltaAttention`` of this package in ``project_chunk`` mode (conv, KDA core and
-output norm-gate on the gfx950 kernels; projections are PyTorch GEMMs).
+output norm-gate on the gfx950 kernels; projections are PyTorch GEMMs).  With a
+``KVCache`` (nanochat/engine.py:92-221) the model prefills through the chunk kernels and
+decodes one token at a time through the recurrent decode kernel.
 """
 
 from __future__ import annotations
@@ -20,7 +22,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .kda import KimiDeltaAttention, Linear
+from .kda import KDAState, KimiDeltaAttention, Linear
 
 
 @dataclass
@@ -31,6 +33,99 @@ class GPTConfig:
     n_head: int = 3
     n_embd: int = 384
     mode: str = "project_chunk"
+
+
+class KVCache:
+    """Decode cache of an all-KDA model (nanochat/engine.py:92-221 with every layer "K").
+
+    Holds one ``KDAState`` per layer (f32 memory [B,H,V,K] and the three conv windows),
+    the position counter and the smear embedding of the previous token; same constructor,
+    methods and errors as the reference for its KDA layers.  Attention layers ("L"/"S")
+    are outside this build and are rejected.  ``inplace_state`` (extension): each
+    one-token step updates the layers' memory tensors in place instead of allocating new
+    ones (one read and one write of the state, no allocation per step).
+    """
+
+    def __init__(self, batch_size, num_heads, seq_len, head_dim, num_layers, device, dtype,
+                 mixer_types=None, conv_size=4, inplace_state=False):
+        self.batch_size = batch_size
+        self.max_seq_len = seq_len
+        self.n_layers = num_layers
+        self.n_heads = num_heads
+        self.head_dim = head_dim
+        self.conv_size = conv_size
+        self.inplace_state = inplace_state
+        self.mixer_types = tuple(mixer_types or ("K",) * num_layers)
+        if len(self.mixer_types) != num_layers or any(kind not in "LSK" for kind in self.mixer_types):
+            raise ValueError("mixer_types must contain one L/S/K entry per layer")
+        if any(kind != "K" for kind in self.mixer_types):
+            raise ValueError("this cache holds KDA layers only; attention layers are not part of this build")
+        self.allocated_kv_layers = ()
+        self.allocated_kda_layers = tuple(range(num_layers))
+        self._kda_states = {index: None for index in self.allocated_kda_layers}
+        self.cache_seqlens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        self.prev_embedding = None
+
+    def reset(self):
+        self.cache_seqlens.zero_()
+        self.prev_embedding = None
+        for index in self.allocated_kda_layers:
+            self._kda_states[index] = None
+
+    def get_pos(self):
+        return self.cache_seqlens[0].item()
+
+    def get_layer_cache(self, layer_idx):
+        raise ValueError(f"layer {layer_idx} is KDA and has no KV cache")
+
+    def get_kda_state(self, layer_idx):
+        if layer_idx not in self.allocated_kda_layers:
+            raise ValueError(f"layer {layer_idx} is attention and has no KDA state")
+        return self._kda_states[layer_idx]
+
+    def set_kda_state(self, layer_idx, state):
+        if layer_idx not in self.allocated_kda_layers:
+            raise ValueError(f"layer {layer_idx} is attention and has no KDA state")
+        if state is not None and not isinstance(state, KDAState):
+            raise TypeError("KDA state must be a KDAState instance")
+        self._kda_states[layer_idx] = state
+
+    def advance(self, num_tokens):
+        self.cache_seqlens += num_tokens
+
+    def prefill(self, other):
+        """Copy another cache's states, expanding a batch-1 prefill to this batch."""
+        if self.get_pos() != 0:
+            raise ValueError("Cannot prefill a non-empty KV cache")
+        if (self.n_layers, self.n_heads, self.head_dim) != (other.n_layers, other.n_heads, other.head_dim):
+            raise ValueError("cache geometry mismatch")
+        if self.mixer_types != other.mixer_types or self.max_seq_len < other.max_seq_len:
+            raise ValueError("cache layout mismatch")
+        for index in self.allocated_kda_layers:
+            state = other.get_kda_state(index)
+            if state is None:
+                self._kda_states[index] = None
+                continue
+
+            def expand(tensor):
+                if tensor.shape[0] not in {1, self.batch_size}:
+                    raise ValueError("source KDA state batch cannot be expanded to destination")
+                return tensor.expand(self.batch_size, *tensor.shape[1:]).clone()
+
+            self._kda_states[index] = KDAState(memory=expand(state.memory), q_conv=expand(state.q_conv),
+                                               k_conv=expand(state.k_conv), v_conv=expand(state.v_conv))
+        self.cache_seqlens.fill_(other.get_pos())
+        if other.prev_embedding is not None:
+            self.prev_embedding = other.prev_embedding.expand(self.batch_size, -1, -1).clone()
+
+    def state_nbytes(self):
+        tensors = []
+        for state in self._kda_states.values():
+            if state is not None:
+                tensors.extend((state.memory, state.q_conv, state.k_conv, state.v_conv))
+        if self.prev_embedding is not None:
+            tensors.append(self.prev_embedding)
+        return sum(t.numel() * t.element_size() for t in tensors)
 
 
 class _SoftcapCrossEntropy(torch.autograd.Function):
@@ -86,8 +181,17 @@ class Block(nn.Module):
                                        layer_idx=layer_idx, mode=cfg.mode, allow_fallback=False)
         self.mlp = MLP(cfg.n_embd)
 
-    def forward(self, x):
-        mixed, _ = self.attn(norm(x), state=None, output_final_state=False)
+    def forward(self, x, kv_cache=None):
+        """nanochat/gpt.py:180-205 for a KDA layer: with a cache, the layer's state is read
+        from and written back to it, and a one-token step runs the recurrent decode kernel."""
+        state = None if kv_cache is None else kv_cache.get_kda_state(self.attn.layer_idx)
+        mode = None
+        if x.is_cuda and self.attn.mode.startswith("project_"):
+            mode = "project_recurrent" if kv_cache is not None and x.shape[1] == 1 else "project_chunk"
+        mixed, state = self.attn(norm(x), state=state, output_final_state=kv_cache is not None, mode=mode,
+                                 state_in_place=kv_cache is not None and kv_cache.inplace_state)
+        if kv_cache is not None:
+            kv_cache.set_kda_state(self.attn.layer_idx, state)
         x = x + mixed
         return x + self.mlp(norm(x))
 
@@ -139,18 +243,33 @@ class GPT(nn.Module):
         nn.init.uniform_(self.smear_gate.weight, 0.0, 0.02, generator=generator)
         self.transformer.wte.to(dtype=torch.bfloat16)
 
-    def forward(self, idx, targets=None):
+    def forward(self, idx, targets=None, kv_cache=None):
         x = norm(self.transformer.wte(idx).to(torch.bfloat16))
-        gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, 1:, :24]))
-        x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
+        T = idx.shape[1]
+        # smear: mix the previous token's embedding into each position (nanochat/gpt.py:564-581);
+        # with a cache the previous token of the first position is the cached embedding
+        if kv_cache is None:
+            gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, 1:, :24]))
+            x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
+        else:
+            x_pre_smear = kv_cache.prev_embedding
+            kv_cache.prev_embedding = x[:, -1:, :]
+            if T > 1:
+                gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, 1:, :24]))
+                x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
+            elif x_pre_smear is not None:
+                gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, :, :24]))
+                x = x + gate * x_pre_smear
         x0 = x
         backout_layer = self.config.n_layer // 2
         x_backout = None
         for i, block in enumerate(self.transformer.h):
             x = self.resid_lambdas[i] * x + self.x0_lambdas[i] * x0
-            x = block(x.to(torch.bfloat16))
+            x = block(x.to(torch.bfloat16), kv_cache)
             if i == backout_layer:
                 x_backout = x
+        if kv_cache is not None:
+            kv_cache.advance(T)
         if x_backout is not None:
             x = x - self.backout_lambda.to(x.dtype) * x_backout
         x = norm(x)

@@ -196,3 +196,27 @@ def test_provenance_names_native_symbols():
     for comp, entry in prov["components"].items():
         assert entry["owner"] == "project"
         assert entry["symbol"] in syms, comp
+
+
+def test_kv_cache_contract_on_cpu():
+    """The decode cache keeps the reference KVCache's KDA-layer contract
+    (nanochat/engine.py:92-221): per-layer KDAState slots, type checks, position, reset."""
+    from experiment_swa_kda_amd.model import KVCache
+    from experiment_swa_kda_amd.kda import KDAState
+    c = KVCache(2, 3, 64, 128, 4, "cpu", torch.bfloat16)
+    assert c.allocated_kda_layers == (0, 1, 2, 3) and c.get_pos() == 0
+    with pytest.raises(TypeError):
+        c.set_kda_state(1, "not a state")
+    with pytest.raises(ValueError):
+        c.get_kda_state(7)
+    with pytest.raises(ValueError):
+        c.get_layer_cache(0)
+    st = KDAState(torch.zeros(2, 3, 128, 128), torch.zeros(2, 384, 4), torch.zeros(2, 384, 4), torch.zeros(2, 384, 4))
+    c.set_kda_state(2, st)
+    c.advance(5)
+    assert c.get_pos() == 5 and c.get_kda_state(2) is st
+    assert c.state_nbytes() == (2 * 3 * 128 * 128 + 3 * 2 * 384 * 4) * 4
+    c.reset()
+    assert c.get_pos() == 0 and c.get_kda_state(2) is None
+    with pytest.raises(ValueError):
+        KVCache(1, 3, 64, 128, 2, "cpu", torch.bfloat16, mixer_types="KS")

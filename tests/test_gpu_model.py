@@ -130,3 +130,57 @@ def test_graphed_update_matches_eager_updates():
         assert abs(loss - eager_losses[upd]) < 1e-4 * abs(eager_losses[upd]), (upd, loss, eager_losses[upd])
     for (n, pe), (_, pg) in zip(eager.named_parameters(), graphed.named_parameters()):
         assert rel_err(pg, pe) < 1e-4, n
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_kv_cache_decode_matches_full_forward(inplace):
+    """Prefill through the chunk kernels, then one-token decode steps through the recurrent
+    kernel: every step's logits equal the full-sequence forward at that position."""
+    from experiment_swa_kda_amd.model import KVCache
+    cfg = GPTConfig(sequence_len=128, vocab_size=512, n_layer=2, n_head=2, n_embd=256)
+    torch.manual_seed(0)
+    model = GPT(cfg).cuda()
+    model.init_weights()
+    with torch.no_grad():
+        for b in model.transformer.h:
+            b.attn.o_proj.weight.normal_(0, 0.02)
+            b.mlp.c_proj.weight.normal_(0, 0.02)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    B, T, P = 2, 48, 37
+    idx = torch.randint(0, 512, (B, T), device="cuda", generator=g)
+    with torch.no_grad():
+        full = model(idx)
+        cache = KVCache(B, 2, T, 128, 2, "cuda", torch.bfloat16, inplace_state=inplace)
+        pre = model(idx[:, :P], kv_cache=cache)
+        assert cache.get_pos() == P
+        assert rel_err(pre, full[:, :P]) < 2e-2
+        mem = [cache.get_kda_state(i).memory for i in range(2)]
+        for t in range(P, T):
+            step = model(idx[:, t:t + 1], kv_cache=cache)
+            assert rel_err(step[:, 0], full[:, t]) < 2e-2, t
+        assert cache.get_pos() == T
+        same = [cache.get_kda_state(i).memory.data_ptr() == mem[i].data_ptr() for i in range(2)]
+        assert all(same) == inplace
+        assert cache.state_nbytes() > 2 * B * 2 * 128 * 128 * 4
+
+
+def test_kv_cache_prefill_expands_batch_one():
+    from experiment_swa_kda_amd.model import KVCache
+    cfg = GPTConfig(sequence_len=64, vocab_size=512, n_layer=2, n_head=2, n_embd=256)
+    torch.manual_seed(0)
+    model = GPT(cfg).cuda()
+    model.init_weights()
+    idx = torch.randint(0, 512, (1, 20), device="cuda")
+    with torch.no_grad():
+        one = KVCache(1, 2, 64, 128, 2, "cuda", torch.bfloat16)
+        model(idx, kv_cache=one)
+        many = KVCache(3, 2, 64, 128, 2, "cuda", torch.bfloat16)
+        many.prefill(one)
+        assert many.get_pos() == 20
+        nxt = torch.randint(0, 512, (1, 1), device="cuda")
+        a = model(nxt, kv_cache=one)
+        b = model(nxt.expand(3, 1).contiguous(), kv_cache=many)
+    for r in range(3):
+        assert torch.equal(b[r], a[0])
+    with pytest.raises(ValueError):
+        KVCache(1, 2, 64, 128, 2, "cuda", torch.bfloat16, mixer_types="KL")
