@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
+    ap.add_argument("--hbm-sweep", action="store_true",
+                    help="print the HBM-peak fraction of conv / norm-gate / copy over batch sizes and exit")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run each kernel once (plus a 64 MiB calibration copy) for rocprofv3 --pmc; no timing")
     ap.add_argument("--cpu-sample-len", type=int, default=1024,
@@ -257,6 +259,36 @@ def hbm_kernels(torch):
     return out
 
 
+def hbm_sweep(torch, batches=(2, 4, 8, 16, 32)):
+    """Fraction of the HBM peak reached by conv, RMSNorm*gate and a plain copy of the same
+    bytes as the batch grows (T = 4096, C = 384): separates launch / ramp cost from kernel
+    efficiency.  One JSON line per batch."""
+    from experiment_swa_kda_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(42)
+    for B in batches:
+        T, C, W = 4096, 384, 4
+        x = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
+        w = torch.randn(C, W, device="cuda", generator=g).bfloat16()
+        dy = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
+        o, gt = x.view(B, T, 3, 128), dy.view(B, T, 3, 128)
+        nw = torch.ones(128, device="cuda")
+        _, inv = ops.rmsnorm_gate_forward(o, gt, nw, 1e-5)
+        c = torch.empty_like(x)
+        n = x.numel() * 2
+        cases = {
+            "conv_fwd": (2 * n, lambda: ops.causal_conv_forward(x, w, None, False)),
+            "conv_bwd": (3 * n, lambda: ops.causal_conv_backward(x, w, None, dy, None)),
+            "norm_gate_fwd": (3 * n, lambda: ops.rmsnorm_gate_forward(o, gt, nw, 1e-5)),
+            "norm_gate_bwd": (5 * n, lambda: ops.rmsnorm_gate_backward(o, gt, nw, inv, gt, 1e-5)),
+            "copy": (2 * n, lambda: c.copy_(x)),
+        }
+        line = {"batch": B}
+        for name, (nbytes, fn) in cases.items():
+            line[name] = round(nbytes / (graph_time_us(torch, fn, n=20) * 1e-6) / 1e9 / PEAK_HBM_GBS, 3)
+        print(json.dumps(line), flush=True)
+
+
 def cpu_baseline(sample_len):
     """The reference's eager f32 CPU path (restated in oracle/reference_path.py), fwd+bwd."""
     import torch
@@ -317,6 +349,9 @@ def main():
 
     if args.pmc_workload:
         pmc_workload(torch)
+        return
+    if args.hbm_sweep:
+        hbm_sweep(torch)
         return
     B, T, H, K, V = 2, 4096, 3, 128, 128
     tiles = B * (T // 64) * H
