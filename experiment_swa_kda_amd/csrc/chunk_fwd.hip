@@ -35,6 +35,7 @@ namespace kda {
 struct FwdArgs {
   int H;
   int num_seqs;
+  int fixed_T;  // > 0: every sequence has this length and the intra kernel fills the tables
   int gate_mode;
   float lb;
   float scale;
@@ -219,7 +220,21 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   float* sTot = (float*)(smem + L::tot);
   float* sBeta = (float*)(smem + L::beta);
 
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  // Fixed-length problems derive their chunk from the index and publish the chunk and
+  // sequence tables for the later kernels (which run after this one on the stream);
+  // variable-length problems read the tables chunk_prep_kernel built.
+  int4 ch;
+  if (a.fixed_T > 0) {
+    const int nc = (a.fixed_T + kChunk - 1) / kChunk;
+    const int sq = blockIdx.x / nc, j = blockIdx.x % nc;
+    ch = make_int4(sq * a.fixed_T + j * kChunk, min(kChunk, a.fixed_T - j * kChunk), sq, j);
+    if (blockIdx.y == 0 && threadIdx.x == 0) {
+      ((int4*)a.ws.p[R_CHUNKS])[blockIdx.x] = ch;
+      if (j == 0) ((int2*)a.ws.p[R_SEQS])[sq] = make_int2(blockIdx.x, nc);
+    }
+  } else {
+    ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  }
   const int len = ch.y;
   if (len <= 0) return;
   const int H = a.H, h = blockIdx.y;
@@ -963,7 +978,9 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   a.out = (bf16*)output;
   a.sfin = final_state;
   a.ws = ws_regions(g, workspace);
-  if (stages & (1 << KDA_STAGE_PREP)) {
+  // fixed-length problems with at least one chunk get their tables from the intra kernel
+  a.fixed_T = (p->cu_seqlens == nullptr && g.max_chunks > 0) ? p->seq_len : 0;
+  if ((stages & (1 << KDA_STAGE_PREP)) && a.fixed_T == 0) {
     rc = launch_chunk_prep(p, g, a.ws, stream);
     if (rc != KDA_OK) return rc;
   }
