@@ -62,6 +62,11 @@ SIGNATURES = {
     "kda_softcap_cross_entropy_backward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P, _P]),
     "kda_weight_grad_scratch_bytes": (ctypes.c_size_t, [_L, _I, _I]),
     "kda_weight_grad": (ctypes.c_int, [_L, _I, _I, _P, _L, _P, _L, _P, _P, _P]),
+    "kda_resid_mix_backward_scratch_bytes": (ctypes.c_size_t, [_L]),
+    "kda_resid_mix_forward": (ctypes.c_int, [_L, _P, _P, _P, _P, _P, _P]),
+    "kda_resid_mix_backward": (ctypes.c_int, [_L] + [_P] * 10 + [_P]),
+    "kda_relu2_forward": (ctypes.c_int, [_L, _P, _P, _P]),
+    "kda_relu2_backward": (ctypes.c_int, [_L, _P, _P, _P, _P]),
 }
 
 _lib = None

@@ -1,0 +1,234 @@
+// Elementwise trainer glue of the all-KDA decoder, fused so each op is one pass over HBM.
+// Reference: nanochat/gpt.py (the per-layer residual mix x = resid_lambdas[i] x +
+// x0_lambdas[i] x0 at :585-587, and the MLP activation relu(x)^2 at :151-156), which the
+// reference fuses with torch.compile (scripts/base_train.py:267).
+//
+// HBM-bound.  Each thread moves 16-byte bf16x8 vectors, kVecs of them in flight, f32 math,
+// one rounding to bf16 per output.  The scalar-weight gradients of the residual mix are
+// per-workgroup partials summed afterwards in a fixed order (deterministic, no atomics).
+#include "kda_device.hpp"
+#include "kda_host.hpp"
+
+namespace kda {
+
+constexpr int kGlueThreads = 256;
+constexpr int kGlueVecs = 4;  // bf16x8 vectors per thread
+constexpr long kGlueBlock = (long)kGlueThreads * kGlueVecs * 8;  // elements per workgroup
+
+__device__ __forceinline__ void unpack8(const bf16x8& v, float (&f)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float (&f)[8]) {
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = to_bf16(f[e]);
+  return v;
+}
+
+// y = a x + b x0 with a = wa[0], b = wb[0] (device scalars)
+__global__ __launch_bounds__(kGlueThreads) void resid_mix_fwd_kernel(long n, const float* __restrict__ wa,
+                                                                     const float* __restrict__ wb,
+                                                                     const bf16* __restrict__ x,
+                                                                     const bf16* __restrict__ x0,
+                                                                     bf16* __restrict__ y) {
+  const float a = wa[0], b = wb[0];
+  const long base = (long)blockIdx.x * kGlueBlock + threadIdx.x * 8;
+  bf16x8 xv[kGlueVecs], zv[kGlueVecs];
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    const long ic = i < n ? i : 0;
+    xv[u] = *reinterpret_cast<const bf16x8*>(x + ic);
+    zv[u] = *reinterpret_cast<const bf16x8*>(x0 + ic);
+  }
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    float fx[8], fz[8], o[8];
+    unpack8(xv[u], fx);
+    unpack8(zv[u], fz);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(a, fx[e], b * fz[e]);
+    if (i < n) *reinterpret_cast<bf16x8*>(y + i) = pack8(o);
+  }
+}
+
+// dx = a g, dx0 = b g; part[block] = {sum g x, sum g x0} over the workgroup's elements
+__global__ __launch_bounds__(kGlueThreads) void resid_mix_bwd_kernel(
+    long n, const float* __restrict__ wa, const float* __restrict__ wb, const bf16* __restrict__ x,
+    const bf16* __restrict__ x0, const bf16* __restrict__ g, bf16* __restrict__ dx,
+    bf16* __restrict__ dx0, float* __restrict__ part) {
+  __shared__ float red[2][kGlueThreads / kWave];
+  const float a = wa[0], b = wb[0];
+  const long base = (long)blockIdx.x * kGlueBlock + threadIdx.x * 8;
+  bf16x8 xv[kGlueVecs], zv[kGlueVecs], gv[kGlueVecs];
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    const long ic = i < n ? i : 0;
+    xv[u] = *reinterpret_cast<const bf16x8*>(x + ic);
+    zv[u] = *reinterpret_cast<const bf16x8*>(x0 + ic);
+    gv[u] = *reinterpret_cast<const bf16x8*>(g + ic);
+  }
+  float sa = 0.f, sb = 0.f;
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    float fx[8], fz[8], fg[8], ox[8], oz[8];
+    unpack8(xv[u], fx);
+    unpack8(zv[u], fz);
+    unpack8(gv[u], fg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ox[e] = a * fg[e];
+      oz[e] = b * fg[e];
+    }
+    if (i < n) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sa = fmaf(fg[e], fx[e], sa);
+        sb = fmaf(fg[e], fz[e], sb);
+      }
+      *reinterpret_cast<bf16x8*>(dx + i) = pack8(ox);
+      *reinterpret_cast<bf16x8*>(dx0 + i) = pack8(oz);
+    }
+  }
+  sa = wave_sum(sa);
+  sb = wave_sum(sb);
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    red[0][wave] = sa;
+    red[1][wave] = sb;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGlueThreads / kWave; ++w) t += red[threadIdx.x][w];
+    part[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = t;
+  }
+}
+
+// y = relu(x)^2
+__global__ __launch_bounds__(kGlueThreads) void relu2_fwd_kernel(long n, const bf16* __restrict__ x,
+                                                                 bf16* __restrict__ y) {
+  const long base = (long)blockIdx.x * kGlueBlock + threadIdx.x * 8;
+  bf16x8 xv[kGlueVecs];
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    xv[u] = *reinterpret_cast<const bf16x8*>(x + (i < n ? i : 0));
+  }
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    float f[8];
+    unpack8(xv[u], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = fmaxf(f[e], 0.f);
+      f[e] = r * r;
+    }
+    if (i < n) *reinterpret_cast<bf16x8*>(y + i) = pack8(f);
+  }
+}
+
+// dx = 2 relu(x) g
+__global__ __launch_bounds__(kGlueThreads) void relu2_bwd_kernel(long n, const bf16* __restrict__ x,
+                                                                 const bf16* __restrict__ g,
+                                                                 bf16* __restrict__ dx) {
+  const long base = (long)blockIdx.x * kGlueBlock + threadIdx.x * 8;
+  bf16x8 xv[kGlueVecs], gv[kGlueVecs];
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    const long ic = i < n ? i : 0;
+    xv[u] = *reinterpret_cast<const bf16x8*>(x + ic);
+    gv[u] = *reinterpret_cast<const bf16x8*>(g + ic);
+  }
+#pragma unroll
+  for (int u = 0; u < kGlueVecs; ++u) {
+    const long i = base + (long)u * kGlueThreads * 8;
+    float f[8], fg[8];
+    unpack8(xv[u], f);
+    unpack8(gv[u], fg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = 2.f * fmaxf(f[e], 0.f) * fg[e];
+    if (i < n) *reinterpret_cast<bf16x8*>(dx + i) = pack8(f);
+  }
+}
+
+inline unsigned glue_blocks(long n) { return (unsigned)((n + kGlueBlock - 1) / kGlueBlock); }
+
+}  // namespace kda
+
+#define KDA_GLUE_CHECK(n, ...)                                                              \
+  do {                                                                                      \
+    KDA_REQUIRE((n) >= 0 && (n) % 8 == 0 && (n) / kda::kGlueBlock < 0x7fffffff,           \
+                "elementwise op: length must be a non-negative multiple of 8");             \
+    KDA_REQUIRE(kda::aligned16(__VA_ARGS__), "elementwise op: tensors must be 16-byte aligned"); \
+  } while (0)
+
+extern "C" size_t kda_resid_mix_backward_scratch_bytes(int64_t n) {
+  return n > 0 ? 2 * (size_t)kda::glue_blocks(n) * sizeof(float) : 0;
+}
+
+extern "C" int kda_resid_mix_forward(int64_t n, const float* a, const float* b, const void* x,
+                                     const void* x0, void* y, hipStream_t stream) {
+  using namespace kda;
+  KDA_GLUE_CHECK(n, x, x0, y);
+  KDA_REQUIRE(a && b && (n == 0 || (x && x0 && y)), "resid_mix_forward: null pointer");
+  if (n == 0) return KDA_OK;
+  hipLaunchKernelGGL(resid_mix_fwd_kernel, dim3(glue_blocks(n)), dim3(kGlueThreads), 0, stream, (long)n, a,
+                     b, (const bf16*)x, (const bf16*)x0, (bf16*)y);
+  KDA_LAUNCH_CHECK("resid_mix_forward");
+  return KDA_OK;
+}
+
+extern "C" int kda_resid_mix_backward(int64_t n, const float* a, const float* b, const void* x,
+                                      const void* x0, const void* grad, void* dx, void* dx0,
+                                      float* da, float* db, void* scratch, hipStream_t stream) {
+  using namespace kda;
+  KDA_GLUE_CHECK(n, x, x0, grad, dx, dx0);
+  KDA_REQUIRE(a && b && da && db && (n == 0 || (x && x0 && grad && dx && dx0 && scratch)),
+              "resid_mix_backward: null pointer");
+  const unsigned blocks = n > 0 ? glue_blocks(n) : 0;
+  float* part = (float*)scratch;
+  if (n > 0) {
+    hipLaunchKernelGGL(resid_mix_bwd_kernel, dim3(blocks), dim3(kGlueThreads), 0, stream, (long)n, a, b,
+                       (const bf16*)x, (const bf16*)x0, (const bf16*)grad, (bf16*)dx, (bf16*)dx0, part);
+    KDA_LAUNCH_CHECK("resid_mix_backward");
+  }
+  // da = sum of the first row of partials, db of the second (fixed order)
+  hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3(1), dim3(256), 0, stream, (int)blocks, 1,
+                     (const float*)part, da);
+  hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3(1), dim3(256), 0, stream, (int)blocks, 1,
+                     (const float*)(part + blocks), db);
+  KDA_LAUNCH_CHECK("resid_mix_backward reduce");
+  return KDA_OK;
+}
+
+extern "C" int kda_relu2_forward(int64_t n, const void* x, void* y, hipStream_t stream) {
+  using namespace kda;
+  KDA_GLUE_CHECK(n, x, y);
+  if (n == 0) return KDA_OK;
+  KDA_REQUIRE(x && y, "relu2_forward: null pointer");
+  hipLaunchKernelGGL(relu2_fwd_kernel, dim3(glue_blocks(n)), dim3(kGlueThreads), 0, stream, (long)n,
+                     (const bf16*)x, (bf16*)y);
+  KDA_LAUNCH_CHECK("relu2_forward");
+  return KDA_OK;
+}
+
+extern "C" int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx,
+                                  hipStream_t stream) {
+  using namespace kda;
+  KDA_GLUE_CHECK(n, x, grad, dx);
+  if (n == 0) return KDA_OK;
+  KDA_REQUIRE(x && grad && dx, "relu2_backward: null pointer");
+  hipLaunchKernelGGL(relu2_bwd_kernel, dim3(glue_blocks(n)), dim3(kGlueThreads), 0, stream, (long)n,
+                     (const bf16*)x, (const bf16*)grad, (bf16*)dx);
+  KDA_LAUNCH_CHECK("relu2_backward");
+  return KDA_OK;
+}

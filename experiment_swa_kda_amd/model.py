@@ -160,6 +160,52 @@ def softcap_cross_entropy(logits, targets, vocab, softcap=15.0, ignore_index=-1)
     return F.cross_entropy(z, targets, ignore_index=ignore_index)
 
 
+class _Relu2(torch.autograd.Function):
+    """relu(x)^2 as one HIP pass forward and one backward (nanochat/gpt.py:151-156)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        ctx.save_for_backward(x)
+        return ops.relu2_forward(x)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (x,) = ctx.saved_tensors
+        return ops.relu2_backward(x, grad)
+
+
+def relu2(x):
+    if x.is_cuda and x.dtype == torch.bfloat16 and x.numel() % 8 == 0:
+        return _Relu2.apply(x)
+    return F.relu(x).square()
+
+
+class _ResidMix(torch.autograd.Function):
+    """x = resid_lambdas[i] x + x0_lambdas[i] x0 (nanochat/gpt.py:585-587) as one HIP pass;
+    the backward forms dx, dx0 and both scalar gradients in one pass plus a fixed-order
+    reduction."""
+
+    @staticmethod
+    def forward(ctx, x, x0, lam_r, lam_0, i):
+        ctx.save_for_backward(x, x0, lam_r, lam_0)
+        ctx.i = i
+        return ops.resid_mix_forward(x, x0, lam_r[i:i + 1], lam_0[i:i + 1])
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, x0, lam_r, lam_0 = ctx.saved_tensors
+        i, n = ctx.i, lam_r.numel()
+        dx, dx0, da, db = ops.resid_mix_backward(x, x0, lam_r[i:i + 1], lam_0[i:i + 1], grad)
+        return dx, dx0, F.pad(da, (i, n - 1 - i)), F.pad(db, (i, n - 1 - i)), None
+
+
+def resid_mix(x, x0, lam_r, lam_0, i):
+    if (x.is_cuda and x.dtype == torch.bfloat16 and x0.dtype == torch.bfloat16
+            and x.shape == x0.shape and x.numel() % 8 == 0):
+        return _ResidMix.apply(x, x0, lam_r, lam_0, i)
+    return lam_r[i] * x + lam_0[i] * x0
+
+
 def norm(x):
     return F.rms_norm(x, (x.size(-1),))
 
@@ -171,7 +217,7 @@ class MLP(nn.Module):
         self.c_proj = Linear(4 * d, d, bias=False)
 
     def forward(self, x):
-        return self.c_proj(F.relu(self.c_fc(x)).square())
+        return self.c_proj(relu2(self.c_fc(x)))
 
 
 class Block(nn.Module):
@@ -264,7 +310,7 @@ class GPT(nn.Module):
         backout_layer = self.config.n_layer // 2
         x_backout = None
         for i, block in enumerate(self.transformer.h):
-            x = self.resid_lambdas[i] * x + self.x0_lambdas[i] * x0
+            x = resid_mix(x, x0, self.resid_lambdas, self.x0_lambdas, i)
             x = block(x.to(torch.bfloat16), kv_cache)
             if i == backout_layer:
                 x_backout = x

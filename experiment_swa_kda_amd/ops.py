@@ -376,6 +376,64 @@ def weight_grad(grad_output, x):
     check(rc, "kda_weight_grad")
     return dw
 
+def _glue_check(what, *tensors):
+    dev = _require_cuda(what, *tensors)
+    for t in tensors:
+        _check_dtype(what, t, torch.bfloat16, "tensor")
+        if t.shape != tensors[0].shape:
+            raise RuntimeError(f"{what}: tensors must share a shape")
+        if t.numel() % 8:
+            raise RuntimeError(f"{what}: element count must be a multiple of 8")
+    return dev
+
+
+def resid_mix_forward(x, x0, a, b):
+    """y = a x + b x0 (bf16); a, b are f32 device scalars (one-element views)."""
+    dev = _glue_check("resid_mix_forward", x, x0)
+    x, x0, a, b = _c(x), _c(x0), _c(a), _c(b)
+    y = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_resid_mix_forward(x.numel(), ptr(a), ptr(b), ptr(x), ptr(x0), ptr(y),
+                                               _stream(dev))
+    check(rc, "kda_resid_mix_forward")
+    return y
+
+
+def resid_mix_backward(x, x0, a, b, grad):
+    """Returns (dx, dx0, da [1] f32, db [1] f32)."""
+    dev = _glue_check("resid_mix_backward", x, x0, grad)
+    x, x0, grad, a, b = _c(x), _c(x0), _c(grad), _c(a), _c(b)
+    lib = _lib.load()
+    scratch = torch.empty(lib.kda_resid_mix_backward_scratch_bytes(x.numel()), dtype=torch.uint8, device=dev)
+    dx, dx0 = torch.empty_like(x), torch.empty_like(x0)
+    da = torch.empty(1, dtype=torch.float32, device=dev)
+    db = torch.empty(1, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.kda_resid_mix_backward(x.numel(), ptr(a), ptr(b), ptr(x), ptr(x0), ptr(grad), ptr(dx),
+                                        ptr(dx0), ptr(da), ptr(db), ptr(scratch), _stream(dev))
+    check(rc, "kda_resid_mix_backward")
+    return dx, dx0, da, db
+
+
+def relu2_forward(x):
+    dev = _glue_check("relu2_forward", x)
+    x = _c(x)
+    y = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_relu2_forward(x.numel(), ptr(x), ptr(y), _stream(dev))
+    check(rc, "kda_relu2_forward")
+    return y
+
+
+def relu2_backward(x, grad):
+    dev = _glue_check("relu2_backward", x, grad)
+    x, grad = _c(x), _c(grad)
+    dx = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_relu2_backward(x.numel(), ptr(x), ptr(grad), ptr(dx), _stream(dev))
+    check(rc, "kda_relu2_backward")
+    return dx
+
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):
     out, fin, _ = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,

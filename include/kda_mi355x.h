@@ -232,6 +232,23 @@ size_t kda_weight_grad_scratch_bytes(int64_t M, int32_t N, int32_t K);
 int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, int64_t ldd, const void* x,
                     int64_t ldx, float* dweight, void* scratch, hipStream_t stream);
 
+/*
+ * Trainer support: fused elementwise glue of the decoder (reference nanochat/gpt.py,
+ * fused there by torch.compile).  bf16 tensors of n elements (n % 8 == 0, 16-byte aligned).
+ *   resid_mix: y = a x + b x0 with device scalars a, b (the per-layer resid / x0 lambdas,
+ *     gpt.py:585-587); backward dx = a g, dx0 = b g, da = sum g x, db = sum g x0 (fixed-order
+ *     reduction through `scratch`, kda_resid_mix_backward_scratch_bytes(n) bytes).
+ *   relu2: y = relu(x)^2 (the MLP activation, gpt.py:151-156); backward dx = 2 relu(x) g.
+ */
+size_t kda_resid_mix_backward_scratch_bytes(int64_t n);
+int kda_resid_mix_forward(int64_t n, const float* a, const float* b, const void* x, const void* x0,
+                          void* y, hipStream_t stream);
+int kda_resid_mix_backward(int64_t n, const float* a, const float* b, const void* x, const void* x0,
+                           const void* grad, void* dx, void* dx0, float* da, float* db,
+                           void* scratch, hipStream_t stream);
+int kda_relu2_forward(int64_t n, const void* x, void* y, hipStream_t stream);
+int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -110,3 +110,32 @@ def test_linear_autograd_uses_f32_weight_gradient():
     w16 = lin.weight.detach().bfloat16().double()
     assert rel_err(lin.weight.grad, gy.double().reshape(-1, 256).T @ x.detach().double().reshape(-1, 384)) < 1e-5
     assert rel_err(x.grad, (gy.double() @ w16)) < 1e-2
+
+
+def test_relu2_and_resid_mix_match_torch():
+    from experiment_swa_kda_amd.model import relu2, resid_mix
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(3, 100, 64, generator=g).bfloat16().cuda().requires_grad_()
+    y = relu2(x)
+    gy = torch.randn(y.shape, generator=g).bfloat16().cuda()
+    y.backward(gy)
+    xr = x.detach().double().requires_grad_()
+    yr = torch.relu(xr).square()
+    yr.backward(gy.double())
+    assert rel_err(y, yr) < 4e-3 and rel_err(x.grad, xr.grad) < 4e-3
+
+    lam_r = torch.tensor([1.1, 0.9, 1.05], device="cuda", requires_grad=True)
+    lam_0 = torch.tensor([0.2, 0.1, 0.05], device="cuda", requires_grad=True)
+    a = torch.randn(2, 300, 128, generator=g).bfloat16().cuda().requires_grad_()
+    a0 = torch.randn(2, 300, 128, generator=g).bfloat16().cuda().requires_grad_()
+    z = resid_mix(a, a0, lam_r, lam_0, 1)
+    gz = torch.randn(z.shape, generator=g).bfloat16().cuda()
+    z.backward(gz)
+    ad, a0d = a.detach().double(), a0.detach().double()
+    zr = 0.9 * ad + 0.1 * a0d
+    assert rel_err(z, zr) < 4e-3
+    assert rel_err(a.grad, 0.9 * gz.double()) < 4e-3 and rel_err(a0.grad, 0.1 * gz.double()) < 4e-3
+    ga = float((gz.double() * ad).sum()); gb = float((gz.double() * a0d).sum())
+    assert lam_r.grad[0] == 0 and lam_r.grad[2] == 0 and lam_0.grad[0] == 0
+    assert abs(float(lam_r.grad[1]) - ga) < 1e-4 * max(1.0, abs(ga))
+    assert abs(float(lam_0.grad[1]) - gb) < 1e-4 * max(1.0, abs(gb))
