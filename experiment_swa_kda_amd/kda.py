@@ -79,6 +79,23 @@ class _LinearBF16(torch.autograd.Function):
         return dx, dw, db
 
 
+class _SplitColumns(torch.autograd.Function):
+    """Splits the last dimension into contiguous column blocks; the backward writes the
+    blocks' gradients back side by side with one concatenation (slicing views instead would
+    make autograd zero-fill and copy a full-width gradient per block)."""
+
+    @staticmethod
+    def forward(ctx, y, sizes):
+        ctx.sizes = sizes
+        return tuple(t.contiguous() for t in torch.split(y, sizes, dim=-1))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        ref = next(g for g in grads if g is not None)
+        full = [g if g is not None else ref.new_zeros(*ref.shape[:-1], n) for g, n in zip(grads, ctx.sizes)]
+        return torch.cat(full, dim=-1), None
+
+
 class Linear(nn.Linear):
     """Keep master weights in FP32 while matching activation dtype for matmul."""
 
@@ -509,6 +526,10 @@ class KimiDeltaAttention(nn.Module):
         requested_mode = self.mode if mode is None else mode
         requested_fallback = self.allow_fallback if allow_fallback is None else allow_fallback
         want_state = output_final_state
+        if (state is None and not want_state and requested_mode in ("project_chunk", "chunk")
+                and hidden_states.is_cuda and hidden_states.dtype == torch.bfloat16 and length > 0
+                and self.q_proj.weight.dtype == torch.float32):
+            return self._forward_batched(hidden_states, requested_mode, requested_fallback), None
         q_state = None if state is None else state.q_conv
         k_state = None if state is None else state.k_conv
         v_state = None if state is None else state.v_conv
@@ -544,6 +565,40 @@ class KimiDeltaAttention(nn.Module):
         output = self.o_proj(mixed.reshape(batch, length, self.hidden_size))
         final_state = KDAState(final_memory, q_final, k_final, v_final) if want_state else None
         return output, final_state
+
+    def _forward_batched(self, hidden_states, mode, allow_fallback):
+        """Stateless training / prefill path: the same computation as ``forward`` with the six
+        projections that read ``hidden_states`` (q, k, v, g, f_a, b) as one GEMM and the three
+        short convolutions as one launch over the concatenated channels.  One weight-gradient
+        and one input-gradient GEMM replace six of each, and the input gradient needs no
+        accumulation of six partial gradients."""
+        batch, length, C = hidden_states.shape
+        H, D = self.num_heads, self.head_dim
+        # zero rows pad the output width to a multiple of 8 (16-byte rows for the kernels)
+        pad = -(4 * C + D + H) % 8
+        weight = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.g_proj.weight,
+                            self.f_a_proj.weight, self.b_proj.weight,
+                            self.q_proj.weight.new_zeros(pad, C)], dim=0)
+        y = _LinearBF16.apply(hidden_states, weight, None)
+        qkv_in, gate_lin, fa, beta_logits, _ = _SplitColumns.apply(y, (3 * C, C, D, H, pad))
+        conv_w = torch.cat([self.q_conv1d.weight, self.k_conv1d.weight, self.v_conv1d.weight], dim=0)
+        qkv, _ = _ProjectConvolutionAutograd.apply("causal_convolution_forward", "causal_convolution_backward",
+                                                   qkv_in, conv_w.squeeze(1).to(torch.bfloat16), None, False)
+        _record("causal_convolution_forward")
+        qkv = _record_backward(qkv, "causal_convolution_backward")
+        q, k, v = (t.view(batch, length, H, D) for t in _SplitColumns.apply(qkv, (C, C, C)))
+        raw_gate = self.f_b_proj(fa).view(batch, length, H, D)
+        mixed, _ = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias, initial_state=None,
+                       output_final_state=False, mode=mode, lower_bound=self.lower_bound,
+                       allow_fallback=allow_fallback)
+        output_gate = gate_lin.view(batch, length, H, D)
+        if D in (64, 128) and self.o_norm.weight.dtype == torch.float32:
+            mixed = _ProjectRMSNormGateAutograd.apply(mixed, output_gate, self.o_norm.weight, self.o_norm.eps)
+            _record("rmsnorm_gate_forward")
+            mixed = _record_backward(mixed, "rmsnorm_gate_backward")
+        else:
+            mixed = self.o_norm(mixed, output_gate)
+        return self.o_proj(mixed.reshape(batch, length, C))
 
 
 __all__ = ["KDAState", "KimiDeltaAttention", "k3_decay_gate", "kda", "prepare_kda_backend",
