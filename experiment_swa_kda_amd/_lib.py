@@ -66,6 +66,8 @@ SIGNATURES = {
     "kda_resid_mix_forward": (ctypes.c_int, [_L, _P, _P, _P, _P, _P, _P]),
     "kda_resid_mix_backward": (ctypes.c_int, [_L] + [_P] * 10 + [_P]),
     "kda_relu2_forward": (ctypes.c_int, [_L, _P, _P, _P]),
+    "kda_rms_norm_forward": (ctypes.c_int, [_L, _I, _F, _P, _P, _P, _P]),
+    "kda_rms_norm_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P]),
     "kda_relu2_backward": (ctypes.c_int, [_L, _P, _P, _P, _P]),
 }
 

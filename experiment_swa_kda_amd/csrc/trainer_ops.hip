@@ -1,4 +1,5 @@
-// Elementwise trainer glue of the all-KDA decoder, fused so each op is one pass over HBM.
+// Elementwise and row-normalisation trainer glue of the all-KDA decoder, fused so each op
+// is one pass over HBM.
 // Reference: nanochat/gpt.py (the per-layer residual mix x = resid_lambdas[i] x +
 // x0_lambdas[i] x0 at :585-587, and the MLP activation relu(x)^2 at :151-156), which the
 // reference fuses with torch.compile (scripts/base_train.py:267).
@@ -162,6 +163,83 @@ __global__ __launch_bounds__(kGlueThreads) void relu2_bwd_kernel(long n, const b
 
 inline unsigned glue_blocks(long n) { return (unsigned)((n + kGlueBlock - 1) / kGlueBlock); }
 
+// RMS normalisation without weight over rows of D = 128 J channels (the decoder's norm(),
+// F.rms_norm(x, (D,)), nanochat/gpt.py:46-48).  16 lanes own a row, each lane J 16-byte
+// vectors (channels 8 l + 128 j), so a wave covers 4 rows with fully coalesced accesses;
+// row sums are 16-lane DPP reductions.  Forward writes y and 1/rms per row; backward
+//   dx = r (g - y mean(g y)),  r = 1/rms.
+constexpr int kNormLanes = 16;
+constexpr int kNormRowsPerBlock = 256 / kNormLanes;
+
+template <int J>
+__global__ __launch_bounds__(256) void rms_norm_fwd_kernel(long rows, float eps, const bf16* __restrict__ x,
+                                                           bf16* __restrict__ y, float* __restrict__ rinv) {
+  constexpr int D = 128 * J;
+  const long row = (long)blockIdx.x * kNormRowsPerBlock + threadIdx.x / kNormLanes;
+  const int l = threadIdx.x % kNormLanes;
+  const long rc = row < rows ? row : rows - 1;
+  bf16x8 xv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) xv[j] = *reinterpret_cast<const bf16x8*>(x + rc * D + 128 * j + 8 * l);
+  float f[J][8], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    unpack8(xv[j], f[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[j][e], f[j][e], ss);
+  }
+  ss = group_sum<kNormLanes>(ss);
+  const float r = rsqrtf(ss / D + eps);
+  if (row < rows) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f[j][e] * r;
+      *reinterpret_cast<bf16x8*>(y + row * D + 128 * j + 8 * l) = pack8(o);
+    }
+    if (l == 0) rinv[row] = r;
+  }
+}
+
+template <int J>
+__global__ __launch_bounds__(256) void rms_norm_bwd_kernel(long rows, const bf16* __restrict__ x,
+                                                           const float* __restrict__ rinv,
+                                                           const bf16* __restrict__ g, bf16* __restrict__ dx) {
+  constexpr int D = 128 * J;
+  const long row = (long)blockIdx.x * kNormRowsPerBlock + threadIdx.x / kNormLanes;
+  const int l = threadIdx.x % kNormLanes;
+  const long rc = row < rows ? row : rows - 1;
+  bf16x8 xv[J], gv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    xv[j] = *reinterpret_cast<const bf16x8*>(x + rc * D + 128 * j + 8 * l);
+    gv[j] = *reinterpret_cast<const bf16x8*>(g + rc * D + 128 * j + 8 * l);
+  }
+  const float r = rinv[rc];
+  float yf[J][8], gf[J][8], dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    unpack8(xv[j], yf[j]);
+    unpack8(gv[j], gf[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      yf[j][e] *= r;
+      dot = fmaf(gf[j][e], yf[j][e], dot);
+    }
+  }
+  dot = group_sum<kNormLanes>(dot) / D;
+  if (row < rows) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = r * (gf[j][e] - yf[j][e] * dot);
+      *reinterpret_cast<bf16x8*>(dx + row * D + 128 * j + 8 * l) = pack8(o);
+    }
+  }
+}
+
 }  // namespace kda
 
 #define KDA_GLUE_CHECK(n, ...)                                                              \
@@ -207,6 +285,54 @@ extern "C" int kda_resid_mix_backward(int64_t n, const float* a, const float* b,
   hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3(1), dim3(256), 0, stream, (int)blocks, 1,
                      (const float*)(part + blocks), db);
   KDA_LAUNCH_CHECK("resid_mix_backward reduce");
+  return KDA_OK;
+}
+
+#define KDA_NORM_DISPATCH(J_, CALL) \
+  switch (J_) {                      \
+    case 1: CALL(1); break;          \
+    case 2: CALL(2); break;          \
+    case 3: CALL(3); break;          \
+    case 4: CALL(4); break;          \
+    case 6: CALL(6); break;          \
+    case 8: CALL(8); break;          \
+    default: break;                  \
+  }
+
+static bool norm_dim_ok(int32_t dim) {
+  const int J = dim / 128;
+  return dim > 0 && dim % 128 == 0 && (J <= 4 || J == 6 || J == 8);
+}
+
+extern "C" int kda_rms_norm_forward(int64_t rows, int32_t dim, float eps, const void* x, void* y,
+                                    float* rinv, hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(rows >= 0 && norm_dim_ok(dim), "rms_norm_forward: dim must be 128 x {1,2,3,4,6,8}");
+  KDA_REQUIRE(aligned16(x, y), "rms_norm_forward: tensors must be 16-byte aligned");
+  if (rows == 0) return KDA_OK;
+  KDA_REQUIRE(x && y && rinv, "rms_norm_forward: null pointer");
+  const unsigned blocks = (unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+#define CALL(J) hipLaunchKernelGGL(rms_norm_fwd_kernel<J>, dim3(blocks), dim3(256), 0, stream, (long)rows, eps, \
+                                   (const bf16*)x, (bf16*)y, rinv)
+  KDA_NORM_DISPATCH(dim / 128, CALL)
+#undef CALL
+  KDA_LAUNCH_CHECK("rms_norm_forward");
+  return KDA_OK;
+}
+
+extern "C" int kda_rms_norm_backward(int64_t rows, int32_t dim, const void* x, const float* rinv,
+                                     const void* grad, void* dx, hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(rows >= 0 && norm_dim_ok(dim), "rms_norm_backward: dim must be 128 x {1,2,3,4,6,8}");
+  KDA_REQUIRE(aligned16(x, grad, dx), "rms_norm_backward: tensors must be 16-byte aligned");
+  if (rows == 0) return KDA_OK;
+  KDA_REQUIRE(x && rinv && grad && dx, "rms_norm_backward: null pointer");
+  const unsigned blocks = (unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+#define CALL(J) hipLaunchKernelGGL(rms_norm_bwd_kernel<J>, dim3(blocks), dim3(256), 0, stream, (long)rows, \
+                                   (const bf16*)x, rinv, (const bf16*)grad, (bf16*)dx)
+  KDA_NORM_DISPATCH(dim / 128, CALL)
+#undef CALL
+  KDA_LAUNCH_CHECK("rms_norm_backward");
   return KDA_OK;
 }
 

@@ -434,6 +434,32 @@ def relu2_backward(x, grad):
     check(rc, "kda_relu2_backward")
     return dx
 
+def rms_norm_forward(x, eps):
+    """y = x / sqrt(mean(x^2) + eps) over the last dim (bf16) -> (y, rinv f32 [rows])."""
+    dev = _require_cuda("rms_norm_forward", x)
+    _check_dtype("rms_norm_forward", x, torch.bfloat16, "x")
+    x = _c(x)
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    y = torch.empty_like(x)
+    rinv = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_rms_norm_forward(rows, D, float(eps), ptr(x), ptr(y), ptr(rinv), _stream(dev))
+    check(rc, "kda_rms_norm_forward")
+    return y, rinv
+
+
+def rms_norm_backward(x, rinv, grad):
+    dev = _require_cuda("rms_norm_backward", x, rinv, grad)
+    x, rinv, grad = _c(x), _c(rinv), _c(grad.to(torch.bfloat16))
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    dx = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_rms_norm_backward(rows, D, ptr(x), ptr(rinv), ptr(grad), ptr(dx), _stream(dev))
+    check(rc, "kda_rms_norm_backward")
+    return dx
+
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):
     out, fin, _ = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,

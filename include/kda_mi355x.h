@@ -247,6 +247,13 @@ int kda_resid_mix_backward(int64_t n, const float* a, const float* b, const void
                            const void* grad, void* dx, void* dx0, float* da, float* db,
                            void* scratch, hipStream_t stream);
 int kda_relu2_forward(int64_t n, const void* x, void* y, hipStream_t stream);
+/* rms_norm (no weight; the decoder's norm(), gpt.py:46-48) over bf16 rows of dim = 128 J
+ * (J in {1,2,3,4,6,8}): y = x / sqrt(mean(x^2) + eps), rinv [rows] f32 = 1/rms;
+ * backward dx = rinv (g - y mean(g y)). */
+int kda_rms_norm_forward(int64_t rows, int32_t dim, float eps, const void* x, void* y, float* rinv,
+                         hipStream_t stream);
+int kda_rms_norm_backward(int64_t rows, int32_t dim, const void* x, const float* rinv,
+                          const void* grad, void* dx, hipStream_t stream);
 int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -108,7 +108,7 @@ def test_graphed_update_matches_eager_updates():
 
     eager = fresh()
     opt_e = make_optimizer(eager, capturable=True)
-    eager_losses = []
+    eager_losses, eager_params = [], []
     for step in range(5):
         total = 0.0
         for mb in data[step]:
@@ -118,6 +118,7 @@ def test_graphed_update_matches_eager_updates():
         opt_e.step()
         opt_e.zero_grad(set_to_none=True)
         eager_losses.append(total)
+        eager_params.append([p.detach().clone() for p in eager.parameters()])
 
     graphed = fresh()
     opt_g = make_optimizer(graphed, capturable=True)
@@ -128,8 +129,9 @@ def test_graphed_update_matches_eager_updates():
             static[i].copy_(data[upd][i])
         loss = update().item()
         assert abs(loss - eager_losses[upd]) < 1e-4 * abs(eager_losses[upd]), (upd, loss, eager_losses[upd])
-    for (n, pe), (_, pg) in zip(eager.named_parameters(), graphed.named_parameters()):
-        assert rel_err(pg, pe) < 1e-4, n
+        # every replay, not only the last, reproduces the eager parameters
+        for (n, pg), pe in zip(graphed.named_parameters(), eager_params[upd]):
+            assert rel_err(pg, pe) < 1e-4, (upd, n)
 
 
 @pytest.mark.parametrize("inplace", [False, True])

@@ -139,3 +139,21 @@ def test_relu2_and_resid_mix_match_torch():
     assert lam_r.grad[0] == 0 and lam_r.grad[2] == 0 and lam_0.grad[0] == 0
     assert abs(float(lam_r.grad[1]) - ga) < 1e-4 * max(1.0, abs(ga))
     assert abs(float(lam_0.grad[1]) - gb) < 1e-4 * max(1.0, abs(gb))
+
+
+@pytest.mark.parametrize("D", [128, 384, 768])
+def test_rms_norm_matches_torch(D):
+    from experiment_swa_kda_amd.model import norm
+    g = torch.Generator().manual_seed(D)
+    x = (torch.randn(5, 77, D, generator=g) * 3).bfloat16().cuda().requires_grad_()
+    y = norm(x)
+    gy = torch.randn(y.shape, generator=g).bfloat16().cuda()
+    y.backward(gy)
+    xr = x.detach().clone().requires_grad_()
+    yr = torch.nn.functional.rms_norm(xr, (D,))   # the reference's norm() on the same device
+    yr.backward(gy)
+    assert rel_err(y, yr) < 4e-3 and rel_err(x.grad, xr.grad) < 1e-2
+    x64 = x.detach().double().requires_grad_()
+    y64 = x64 * torch.rsqrt((x64 * x64).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)
+    y64.backward(gy.double())
+    assert rel_err(y, y64) < 4e-3 and rel_err(x.grad, x64.grad) < 4e-3
