@@ -252,6 +252,8 @@ constexpr int kDenseWaves = kDenseThreads / kWave;
 template <int K, int V>
 struct DenseSmem {
   static constexpr int TP = 64 + 8;   // bf16 row stride of the 64 x 64 matrices
+  static_assert(TP % 8 == 0 && (K + 8) % 4 == 0 && (V + 8) % 4 == 0,
+                "column-fragment reads need 8-byte rows, the PD row reads 16-byte rows");
   static constexpr int KP = K + 8;    // bf16 row stride of dW
   static constexpr int VP = V + 8;
   static constexpr size_t off_du = 0;                           // bf16 [64][VP] dU
@@ -493,16 +495,8 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
     const int rt = p % 4, ct = p / 4;
     const int j = 16 * rt + lr, col = 16 * ct + lr;
     f32x4 acc = zero4();
-    for (int s = (16 * rt) / 32; s < 2; ++s) {
-      const int i0 = 32 * s + 8 * kg;
-      bf16x8 fa, fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fa[e] = sT[(i0 + e) * MP + j];
-        fb[e] = sDU[(i0 + e) * VP + col];
-      }
-      acc = mfma16(fa, fb, acc);
-    }
+    for (int s = (16 * rt) / 32; s < 2; ++s)
+      acc = mfma16(lds_col_frag(sT, MP, 32 * s, 16 * rt, lane), lds_col_frag(sDU, VP, 32 * s, 16 * ct, lane), acc);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int jj = 16 * rt + 4 * kg + rr;
@@ -521,16 +515,8 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
     const int rt = p % 4, ct = p / 4;
     const int j = 16 * rt + lr, c = 16 * ct + lr;
     f32x4 acc = zero4();
-    for (int s = (16 * rt) / 32; s < 2; ++s) {
-      const int i0 = 32 * s + 8 * kg;
-      bf16x8 fa, fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fa[e] = sT[(i0 + e) * MP + j];
-        fb[e] = sDW[(i0 + e) * KP + c];
-      }
-      acc = mfma16(fa, fb, acc);
-    }
+    for (int s = (16 * rt) / 32; s < 2; ++s)
+      acc = mfma16(lds_col_frag(sT, MP, 32 * s, 16 * rt, lane), lds_col_frag(sDW, KP, 32 * s, 16 * ct, lane), acc);
     *(f32x4*)(DKB + ((size_t)p * 64 + lane) * 4) = acc;
   }
   __syncthreads();
@@ -540,16 +526,8 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
     const int rt = p / 4, ct = p % 4;
     const int i = 16 * rt + lr, jcol = 16 * ct + lr;
     f32x4 acc = zero4();
-    for (int s = (16 * rt) / 32; s < 2; ++s) {
-      const int a0 = 32 * s + 8 * kg;
-      bf16x8 fa, fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fa[e] = sT[(a0 + e) * MP + i];
-        fb[e] = sDT[(a0 + e) * MP + jcol];
-      }
-      acc = mfma16(fa, fb, acc);
-    }
+    for (int s = (16 * rt) / 32; s < 2; ++s)
+      acc = mfma16(lds_col_frag(sT, MP, 32 * s, 16 * rt, lane), lds_col_frag(sDT, MP, 32 * s, 16 * ct, lane), acc);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) sY[(16 * rt + 4 * kg + rr) * MP + jcol] = to_bf16(acc[rr]);
   }
@@ -566,14 +544,8 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
     f32x4 acc = zero4();
     const int nsteps = (16 * bb + 15) / 32 + 1;
     for (int s = 0; s < nsteps; ++s) {
-      const int b0 = 32 * s + 8 * kg;
-      bf16x8 fa, fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fa[e] = sY[i * MP + b0 + e];
-        fb[e] = sT[j * MP + b0 + e];
-      }
-      acc = mfma16(fa, fb, acc);
+      const int b0 = 32 * s + 8 * kg;  // rows are 16-byte aligned (MP * 2 = 144 bytes)
+      acc = mfma16(*(const bf16x8*)(sY + i * MP + b0), *(const bf16x8*)(sT + j * MP + b0), acc);
     }
     const int jj = 16 * bb + lr;
 #pragma unroll

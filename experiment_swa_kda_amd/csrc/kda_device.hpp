@@ -126,6 +126,25 @@ __device__ __forceinline__ bool xcd_strip_coords(int NR, int NS, int& r, int& st
   return r < NR;
 }
 
+// MFMA operand fragment holding 8 consecutive rows of one column of a row-major bf16 LDS
+// matrix: lane (l % 16, l / 16) gets m[r0 + 8 (l / 16) + e][c0 + l % 16], e = 0..7 (the
+// contraction runs down the rows).  Two gfx950 transposing reads ds_read_b64_tr_b16: within
+// each 16-lane group, lane j supplies the address of 4 consecutive bf16 and lane i receives
+// element i % 4 of lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12; pointing lane j at row
+// 8 (l / 16) + j / 4, columns 4 (j % 4).. of the block gives the column fragment.  The pitch
+// and c0 must be multiples of 4 elements (8-byte aligned reads).
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ bf16x8 lds_col_frag(const bf16* m, int pitch, int r0, int c0, int lane) {
+  const int lr = lane % 16, kg = lane / 16;
+  const bf16* p = m + (r0 + 8 * kg + lr / 4) * pitch + c0 + 4 * (lr % 4);
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
+  const short4_t hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p + 4 * pitch));
+  // one whole-vector reinterpretation (element-wise casts of the halves miscompile here)
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): two MFMAs with (hi, lo) recover
 // ~16 mantissa bits of an f32 operand.
 __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
