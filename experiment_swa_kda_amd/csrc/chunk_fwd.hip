@@ -134,9 +134,11 @@ struct IntraLds {
   static constexpr int RS = K + 8;   // bf16 row stride of [64][K] staging
   static constexpr int TS = 64 + 8;  // bf16 row stride of [*][64] staging
   static constexpr int cmax(int a, int b) { return a > b ? a : b; }
-  // X1: Fq / Fk fragments (A, M') -> (beta v)^T, (beta kh e^G)^T (U, W) -> Qg, Kd staging
+  static constexpr int VS = V + 8;   // bf16 row stride of [64][V] staging
+  static_assert(RS % 8 == 0 && VS % 8 == 0, "vector rows and transposing reads need 16-byte rows");
+  // X1: Fq / Fk fragments (A, M') -> beta v, beta kh e^G (U, W) -> Qg, Kd staging
   static constexpr int x1 = 0;
-  static constexpr int x1_bytes = cmax(cmax(2 * 64 * K * 2, (V + K) * TS * 2), 2 * 64 * RS * 2);
+  static constexpr int x1_bytes = cmax(cmax(2 * 64 * K * 2, 64 * (VS + RS) * 2), 2 * 64 * RS * 2);
   // X3: M' f32 [64][65] -> W bf16 [64][RS]
   static constexpr int x3 = x1 + x1_bytes;
   static constexpr int x3_bytes = cmax(64 * 65 * 4, 64 * RS * 2);
@@ -207,8 +209,9 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   constexpr int NS = K / 32, NV = V / 32, RS = L::RS, TS = L::TS;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* sF = (bf16*)(smem + L::x1);        // Fq / Fk fragments
-  bf16* sVT = (bf16*)(smem + L::x1);       // (beta v)^T [V][TS]
-  bf16* sBT = sVT + V * TS;                // (beta kh e^G)^T [K][TS]
+  constexpr int VS = L::VS;
+  bf16* sBV = (bf16*)(smem + L::x1);       // beta v [64][VS]
+  bf16* sBK = sBV + 64 * VS;               // beta kh e^G [64][RS]
   bf16* sQg = (bf16*)(smem + L::x1);       // Qg [64][RS]
   bf16* sKd = sQg + 64 * RS;               // Kd [64][RS]
   float* sM = (float*)(smem + L::x3);      // M' [64][65]
@@ -401,7 +404,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   }
   __syncthreads();
 
-  // ---- phase 2b: A fragments, M' to HBM, (beta v)^T and (beta kh e^G)^T to LDS ----
+  // ---- phase 2b: A fragments, M' to HBM, beta v and beta kh e^G (natural rows) to LDS ----
   emit_frags<64, 64, kIntraThreads, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
                                           [&](int r, int c) { return sA[r * TS + c]; });
   emit_frags<64, 64, kIntraThreads>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
@@ -411,13 +414,19 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) MPout[idx] = sM[(idx / 64) * 65 + idx % 64];
   }
 #pragma unroll
-  for (int s = 0; s < NV; ++s)
+  for (int s = 0; s < NV; ++s) {
+    bf16x8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sVT[(32 * s + 8 * kg + e) * TS + i] = (bf16)(beta * (live ? (float)vr[s][e] : 0.f));
+    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * (live ? (float)vr[s][e] : 0.f));
+    *(bf16x8*)(sBV + i * VS + 32 * s + 8 * kg) = x;
+  }
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < NS; ++s) {
+    bf16x8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sBT[(32 * s + 8 * kg + e) * TS + i] = (bf16)(beta * kh[s][e] * __expf(g[s][e]));
+    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * kh[s][e] * __expf(g[s][e]));
+    *(bf16x8*)(sBK + i * RS + 32 * s + 8 * kg) = x;
+  }
   // Qg = qh e^G and Kd = kh e^{G_last - G} (bf16) are all that phase 5 needs of this row;
   // Kd's natural fragments are exactly what this lane holds
   bf16x8 xq[NS], xk[NS];
@@ -514,7 +523,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
       f32x4 acc = zero4();
 #pragma unroll
       for (int st = 0; st < 2; ++st)  // T is lower triangular: row tile rt needs nst steps
-        if (st < nst) acc = mfma16(fa[st], *(const bf16x8*)(sVT + (16 * ct + lr) * TS + 32 * st + 8 * kg), acc);
+        if (st < nst) acc = mfma16(fa[st], lds_col_frag(sBV, VS, 32 * st, 16 * ct, lane), acc);
       bf16x4 x;
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = (bf16)acc[r];
@@ -525,7 +534,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
       f32x4 acc = zero4();
 #pragma unroll
       for (int st = 0; st < 2; ++st)
-        if (st < nst) acc = mfma16(fa[st], *(const bf16x8*)(sBT + (16 * ct + lr) * TS + 32 * st + 8 * kg), acc);
+        if (st < nst) acc = mfma16(fa[st], lds_col_frag(sBK, RS, 32 * st, 16 * ct, lane), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) sW[(16 * rt + 4 * kg + r) * RS + 16 * ct + lr] = (bf16)acc[r];
     }
