@@ -738,12 +738,21 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
         const int j0 = 32 * s + 8 * kg;
         bf16x8 fa, fm, fbh, fbl;
         float xb[8];
+        // every operand is read unconditionally (all rows are in bounds) and the causal
+        // mask is a select: a masked read would become a branch that waits on each load
+        float kj[8], gj[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int j = j0 + e;
           fa[e] = to_bf16(sDA[i * MP + j]);
           fm[e] = to_bf16(sDM[i * MP + j]);
-          xb[e] = j <= jmax ? sK[j * KP + c] * __expf(gr - sG[j * KP + c]) : 0.f;
+          kj[e] = sK[j * KP + c];
+          gj[e] = sG[j * KP + c];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = kj[e] * __expf(gr - gj[e]);
+          xb[e] = j0 + e <= jmax ? x : 0.f;
         }
         // the decay-scaled operands are split (hi + lo): their rounding is systematic
         // across the row/column terms of dG, which nearly cancel
@@ -760,14 +769,22 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
         const int i0 = 32 * s + 8 * kg;
         bf16x8 fa, fm, bqh, bql, bkh, bkl;
         float xq[8], xk[8];
+        float gi[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int ii = i0 + e;
-          const float f = ii >= 16 * rt ? __expf(sG[ii * KP + c] - gp) : 0.f;
           fa[e] = to_bf16(sDA[ii * MP + j]);
           fm[e] = to_bf16(sDM[ii * MP + j]);
-          xq[e] = sQ[ii * KP + c] * f;
-          xk[e] = sK[ii * KP + c] * f;
+          xq[e] = sQ[ii * KP + c];
+          xk[e] = sK[ii * KP + c];
+          gi[e] = sG[ii * KP + c];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = __expf(gi[e] - gp);
+          const float f = i0 + e >= 16 * rt ? x : 0.f;
+          xq[e] *= f;
+          xk[e] *= f;
         }
         split8(xq, bqh, bql);
         split8(xk, bkh, bkl);

@@ -562,30 +562,36 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
 // ---------------------------------------------------------------------------
 // inter-chunk state scan
 // ---------------------------------------------------------------------------
-// One workgroup per (sequence, head, 16-wide V strip): a compute wave, two loader waves and
-// a store wave.  The V columns of the state evolve independently, so strips never
+// One workgroup per (sequence, head, 16-wide V strip): four compute waves, two loader waves
+// and a store wave.  The V columns of the state evolve independently, so strips never
 // communicate.
 //
-// The compute wave holds the K x 16 f32 state slice as K/16 MFMA accumulator tiles (lane
-// l: rows 16kt + 4(l/16) + r, column l%16) and runs each chunk step from registers:
+// The K x 16 f32 state slice is held as K/16 MFMA accumulator tiles (lane l: rows
+// 16kt + 4(l/16) + r, column l%16), split evenly over the compute waves; each chunk step is
 //   delta = U + (-W) S     (S as the B operand; U is the accumulator input),
 //   S     = lam S + Kd^T delta  (delta as B; lam S is the accumulator input).
+// Compute wave c owns the 16-token delta row tile c and state tiles c K/64 .. (c+1) K/64 - 1.
 // The B operand of a 32-deep MFMA step wants 8 values per lane; the two accumulator tiles
 // 2s and 2s+1 give a lane exactly 8 values of its column, so the intra kernel stores W and
 // Qg with their key columns (and Kd^T and A with their token columns) in the matching
 // permuted order (frag_col<true>): an accumulator becomes the next product's operand with
-// one conversion.  The per-step critical path is pack -> 16 MFMAs -> pack -> 16 MFMAs.
+// one conversion.  The waves exchange the packed state and the delta tiles through LDS and
+// meet at two barriers per chunk:
+//   B1(ci): slot ci loaded, state entering chunk ci staged -> each wave's delta tile
+//           (one K/32-deep MFMA chain)
+//   B2(ci): every delta tile staged -> each wave's state tiles (two MFMAs each).
+// Split over four SIMDs the step's dependent chain is K/32 + 2 MFMAs deep instead of the
+// single-wave 16 + 16.
 //
 // The loader waves stream each chunk's -W and Kd^T fragments, U strip and lam into a
-// kScanRing-deep LDS ring with direct global->LDS loads, kScanRing - 1 chunks ahead.  The
-// compute wave writes its histories (f32 and bf16 state, delta) to a double-buffered LDS
-// staging area, which the store wave copies to HBM one step later, so no global access
-// sits in the compute wave's instruction stream.  Per chunk the four waves meet at one
-// barrier: before it the loaders wait (vmcnt) for the slot of that chunk and the compute
-// and store waves for their LDS accesses (lgkmcnt); after it the loaders refill the slot
-// the compute wave released.
-constexpr int kScanRing = 3;
-constexpr int kScanThreads = 4 * kWave;
+// kScanRing-deep LDS ring with direct global->LDS loads, kScanRing - 1 chunks ahead (the
+// step is bound by memory latency: a deeper ring measured faster).  The compute waves write
+// the f32 state history straight to HBM (nothing in their stream waits on those stores);
+// the store wave copies the bf16 state and delta histories out of the double-buffered
+// exchange one step later.
+constexpr int kScanRing = 4;
+constexpr int kScanCompute = 4;                 // compute waves (one 16-token delta tile each)
+constexpr int kScanThreads = (kScanCompute + 3) * kWave;  // + two loader waves and a store wave
 
 template <int K, int V>
 struct ScanLds {
@@ -597,8 +603,7 @@ struct ScanLds {
   static constexpr int n_load0 = (64 * K * 2) / 1024 + 2;  // loader 0: W blocks + U strip
   static constexpr int n_load1 = (K * 64 * 2) / 1024 + 1;  // loader 1: Kd^T blocks + lam
   // staging (x2): f32 state in accumulator order, bf16 state and delta fragments
-  static constexpr int st_sf = 0;
-  static constexpr int st_sb = st_sf + 16 * K * 4;
+  static constexpr int st_sb = 0;
   static constexpr int st_dl = st_sb + 16 * K * 2;
   static constexpr int stage = st_dl + 16 * 64 * 2;
   static constexpr int off_stage = kScanRing * slot;
@@ -639,7 +644,8 @@ __device__ __forceinline__ bf16x8 pack_tiles(const f32x4& lo, const f32x4& hi) {
 template <int K, int V>
 __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a) {
   using L = ScanLds<K, V>;
-  constexpr int KT = K / 16;
+  constexpr int KT = K / 16, NB = K / 32, KPW = KT / kScanCompute;
+  static_assert(KT % kScanCompute == 0, "state tiles split evenly over the compute waves");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int H = a.H;
   int rec, strip;
@@ -659,9 +665,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a)
     return;
   }
 
-  if (wave == 1 || wave == 2) {
+  if (wave == kScanCompute || wave == kScanCompute + 1) {
     // ---- loader waves ----
-    const int lw = wave - 1;
+    const int lw = wave - kScanCompute;
     auto issue = [&](int ci) {
       const int c = ci < n ? ci : n - 1;  // fixed load count per chunk (clamped index)
       const size_t tile = (size_t)(sq.x + c) * H + h;
@@ -689,126 +695,134 @@ __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a)
         wait_vmcnt<(kScanRing - 2) * L::n_load0>();
       else
         wait_vmcnt<(kScanRing - 2) * L::n_load1>();
-      ring_barrier();
+      ring_barrier();  // B1(ci): every read of slot ci - 1 finished before B2(ci - 1)
       issue(ci + kScanRing - 1);
+      ring_barrier();  // B2(ci)
     }
-    ring_barrier();   // the store wave's hand-over of the last chunk
+    ring_barrier();   // B1(n)
     wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
     return;
   }
 
-  if (wave == 3) {
-    // ---- store wave: histories of chunk ci - 1 after barrier ci ----
+  if (wave == kScanCompute + 2) {
+    // ---- store wave: histories of chunk ci - 1, read between B1(ci) and B2(ci) (the
+    // compute waves refill that staging buffer after B2(ci)), written to HBM after ----
     for (int ci = 0; ci <= n; ++ci) {
-      ring_barrier();
+      ring_barrier();  // B1(ci)
+      bf16x8 sb[NB], dl[2];
+      if (ci > 0) {
+        const char* st = smem + L::off_stage + ((ci - 1) & 1) * L::stage;
+#pragma unroll
+        for (int s = 0; s < NB; ++s) sb[s] = *(const bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) dl[s] = *(const bf16x8*)(st + L::st_dl + (s * 64 + lane) * 16);
+        wait_lgkm0();
+      }
+      if (ci < n) ring_barrier();  // B2(ci)
       if (ci == 0) continue;
       const size_t tile = (size_t)(sq.x + ci - 1) * H + h;
-      const char* st = smem + L::off_stage + ((ci - 1) & 1) * L::stage;
-      // f32 state [K][V]: lane covers (k, 4 columns); element (k, v) was staged by lane
-      // v + 16 ((k % 16) / 4) of tile k / 16 as its value k % 4
-      float* SH = (float*)a.ws.p[R_SH] + tile * K * V + v0;
-#pragma unroll
-      for (int it = 0; it < K / 16; ++it) {
-        const int idx = it * 64 + lane, k = idx / 4, c4 = (idx % 4) * 4;
-        const float* sf = (const float*)(st + L::st_sf) + ((k / 16) * 64 + 16 * ((k % 16) / 4) + c4) * 4 + k % 4;
-        *(float4*)(SH + (size_t)k * V + c4) = make_float4(sf[0], sf[4], sf[8], sf[12]);
-      }
       bf16* SHBF = (bf16*)a.ws.p[R_SHBF] + tile * V * K + (size_t)strip * 16 * K;
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s)
-        *(bf16x8*)(SHBF + ((size_t)s * 64 + lane) * 8) = *(const bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16);
+      for (int s = 0; s < NB; ++s) *(bf16x8*)(SHBF + ((size_t)s * 64 + lane) * 8) = sb[s];
       bf16* DLF = (bf16*)a.ws.p[R_DLF] + tile * 64 * V + (size_t)strip * 16 * 64;
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-        *(bf16x8*)(DLF + ((size_t)s * 64 + lane) * 8) = *(const bf16x8*)(st + L::st_dl + (s * 64 + lane) * 16);
-      wait_lgkm0();
+      for (int s = 0; s < 2; ++s) *(bf16x8*)(DLF + ((size_t)s * 64 + lane) * 8) = dl[s];
     }
     return;
   }
 
-  // ---- compute wave ----
-  f32x4 S[KT];
+  // ---- compute wave c: delta row tile c, state tiles c*KPW .. c*KPW + KPW - 1 ----
+  const int cw = wave;
+  f32x4 S[KPW];
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-    const int k0 = 16 * kt + 4 * kg;
+  for (int j = 0; j < KPW; ++j) {
+    const int k0 = 16 * (cw * KPW + j) + 4 * kg;
     if (a.s0) {
       const float4 s = *(const float4*)(a.s0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
-      S[kt][0] = s.x; S[kt][1] = s.y; S[kt][2] = s.z; S[kt][3] = s.w;
+      S[j][0] = s.x; S[j][1] = s.y; S[j][2] = s.z; S[j][3] = s.w;
     } else {
-      S[kt] = zero4();
+      S[j] = zero4();
     }
   }
+  // the bf16 state (B operand of the delta product) lives in the staging buffer of the
+  // chunk it enters: fragment s packs state tiles 2s (low half) and 2s + 1 (high half)
+  auto put_state = [&](char* st) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int kt = cw * KPW + j;
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = to_bf16(S[j][r]);
+      *(bf16x4*)(st + L::st_sb + ((kt / 2) * 64 + lane) * 16 + (kt % 2) * 8) = x;
+    }
+  };
+  put_state(smem + L::off_stage);
+  wait_lgkm0();
   for (int ci = 0; ci < n; ++ci) {
-    ring_barrier();
+    ring_barrier();  // B1(ci): slot ci loaded, the state entering chunk ci staged
     const char* slot = smem + (ci % kScanRing) * L::slot;
     char* st = smem + L::off_stage + (ci & 1) * L::stage;
-    // LDS operands: -W and U first; the Kd^T and lam reads are issued between the delta
-    // MFMAs so they arrive while those run (sched_barrier keeps this order)
-    bf16x8 wf[4][K / 32], kf[KT][2];
-    bf16x4 uf[4];
-    float4 lamf[KT];
+    bf16x8 wf[NB], Bs[NB], kf[KPW][2];
+    float4 lamf[KPW];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int s = 0; s < K / 32; ++s)
-        wf[tt][s] = *(const bf16x8*)(slot + L::off_w + ((tt * (K / 32) + s) * 64 + lane) * 16);
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) uf[tt] = *(const bf16x4*)(slot + L::off_u + (tt * 64 + lane) * 8);
-    __builtin_amdgcn_sched_barrier(0);
-    // state entering the chunk as B operands (permuted key order)
-    bf16x8 Bs[K / 32];
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) Bs[s] = pack_tiles(S[2 * s], S[2 * s + 1]);
-    // delta = U + (-W) S: four independent 16-row tiles, their K/32-deep chains interleaved
-    f32x4 dl[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dl[tt][r] = to_f32(uf[tt][r]);
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) dl[tt] = mfma16(wf[tt][s], Bs[s], dl[tt]);
-#pragma unroll
-      for (int kt = s * KT / (K / 32); kt < (s + 1) * KT / (K / 32); ++kt) {
-        kf[kt][0] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2) * 64 + lane) * 16);
-        kf[kt][1] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2 + 1) * 64 + lane) * 16);
-        lamf[kt] = *(const float4*)(slot + L::off_lam + (16 * kt + 4 * kg) * 4);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int s = 0; s < NB; ++s) {
+      wf[s] = *(const bf16x8*)(slot + L::off_w + ((cw * NB + s) * 64 + lane) * 16);
+      Bs[s] = *(const bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16);
     }
-    // histories of the state entering the chunk (staged for the store wave; the f32 state
-    // in accumulator order [kt][lane][4], which the store wave transposes)
+    const bf16x4 uf = *(const bf16x4*)(slot + L::off_u + (cw * 64 + lane) * 8);
+    __builtin_amdgcn_sched_barrier(0);
+    // delta tile c = U + (-W) S: one K/32-deep chain
+    f32x4 dl;
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt)
-      *(float4*)(st + L::st_sf + (kt * 64 + lane) * 16) = make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+    for (int r = 0; r < 4; ++r) dl[r] = to_f32(uf[r]);
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) *(bf16x8*)(st + L::st_sb + (s * 64 + lane) * 16) = Bs[s];
-    const bf16x8 D0 = pack_tiles(dl[0], dl[1]), D1 = pack_tiles(dl[2], dl[3]);
-    *(bf16x8*)(st + L::st_dl + lane * 16) = D0;
-    *(bf16x8*)(st + L::st_dl + (64 + lane) * 16) = D1;
+    for (int s = 0; s < NB; ++s) dl = mfma16(wf[s], Bs[s], dl);
+    // meanwhile: the f32 history of the entering state (straight to HBM: nothing in this
+    // wave waits on its stores), and this wave's Kd^T rows and lam
+    float* SH = (float*)a.ws.p[R_SH] + ((size_t)(sq.x + ci) * H + h) * K * V + v0 + lr;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int kt = cw * KPW + j;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) SH[(size_t)(16 * kt + 4 * kg + r) * V] = S[j][r];
+      kf[j][0] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2) * 64 + lane) * 16);
+      kf[j][1] = *(const bf16x8*)(slot + L::off_kdt + ((kt * 2 + 1) * 64 + lane) * 16);
+      lamf[j] = *(const float4*)(slot + L::off_lam + (16 * kt + 4 * kg) * 4);
+    }
+    {
+      bf16x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = to_bf16(dl[r]);
+      // delta B fragment t packs row tiles 2t (low half) and 2t + 1 (high half)
+      *(bf16x4*)(st + L::st_dl + ((cw / 2) * 64 + lane) * 16 + (cw % 2) * 8) = x;
+    }
+    f32x4 acc[KPW];
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      acc[j][0] = lamf[j].x * S[j][0];
+      acc[j][1] = lamf[j].y * S[j][1];
+      acc[j][2] = lamf[j].z * S[j][2];
+      acc[j][3] = lamf[j].w * S[j][3];
+    }
+    wait_lgkm0();
+    ring_barrier();  // B2(ci): every delta tile staged
+    const bf16x8 D0 = *(const bf16x8*)(st + L::st_dl + lane * 16);
+    const bf16x8 D1 = *(const bf16x8*)(st + L::st_dl + (64 + lane) * 16);
     // S = lam S + Kd^T delta
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      f32x4 acc;
-      acc[0] = lamf[kt].x * S[kt][0];
-      acc[1] = lamf[kt].y * S[kt][1];
-      acc[2] = lamf[kt].z * S[kt][2];
-      acc[3] = lamf[kt].w * S[kt][3];
-      S[kt] = mfma16(kf[kt][0], D0, acc);
-    }
+    for (int j = 0; j < KPW; ++j) S[j] = mfma16(kf[j][0], D0, acc[j]);
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) S[kt] = mfma16(kf[kt][1], D1, S[kt]);
-    // the slot and the staging buffer are handed over at the next barrier
+    for (int j = 0; j < KPW; ++j) S[j] = mfma16(kf[j][1], D1, S[j]);
+    put_state(smem + L::off_stage + ((ci + 1) & 1) * L::stage);
     wait_lgkm0();
   }
-  ring_barrier();
+  ring_barrier();  // B1(n)
   if (a.sfin) {
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      const int k0 = 16 * kt + 4 * kg;
+    for (int j = 0; j < KPW; ++j) {
+      const int k0 = 16 * (cw * KPW + j) + 4 * kg;
       *(float4*)(a.sfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
-          make_float4(S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+          make_float4(S[j][0], S[j][1], S[j][2], S[j][3]);
     }
   }
 }
