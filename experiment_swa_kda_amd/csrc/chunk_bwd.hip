@@ -63,7 +63,7 @@ struct BwdArgs {
 // Same structure as the forward scan, walking the chunks backwards: all global operands
 // of a chunk sit in a register ring kBwdRing chunks ahead, the dO strip is
 // double-buffered in LDS, and each per-step global access is one vector instruction.
-constexpr int kBwdRing = 3;
+constexpr int kBwdRing = 2;
 
 template <int K>
 struct BwdScanFrag {
@@ -84,7 +84,8 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
   constexpr int FP = 16 + 4;
   __shared__ __attribute__((aligned(16))) bf16 sDS[16 * SP];     // dS' as [v][k]
   __shared__ __attribute__((aligned(16))) float sDSf[K * FP];    // f32 dS' as [k][v]
-  __shared__ __attribute__((aligned(16))) bf16 sDO[2][16 * DP];  // dO strip as [v][t]
+  constexpr int OP = 16 + 4;
+  __shared__ __attribute__((aligned(16))) bf16 sDO[2][64 * OP];  // dO strip as [t][v]
   __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];     // dDelta strip as [v][t]
   const int H = a.H;
   int rec, strip;
@@ -169,8 +170,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
       }
       *(bf16x4*)(sDS + lr * SP + k0) = x;
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) sO[(dvq + q) * DP + dt] = dt < f.dlen ? f.dout[q] : to_bf16(0.f);
+    *(bf16x4*)(sO + dt * OP + dvq) = dt < f.dlen ? f.dout : bf16x4{};
     __syncthreads();
     // (2) f32 dS' history [K][V] (fixed-count vector stores)
     {
@@ -182,11 +182,17 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
         *(float4*)(DSH + (size_t)kk * V + v0 + q4) = *(const float4*)(sDSf + kk * FP + q4);
       }
     }
-    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS'
+    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS', and the dDelta-independent part of
+    // (4), Qg^T dO, while the other waves finish theirs
+    // dO as B operand (tokens down the contraction): transposing reads of the [t][v] strip
+    const bf16x8 oB0 = lds_col_frag(sO, OP, 0, 0, lane), oB1 = lds_col_frag(sO, OP, 32, 0, lane);
+    f32x4 pq[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) pq[kt] = mfma16(f.qgt[kt][1], oB1, mfma16(f.qgt[kt][0], oB0, zero4()));
     {
       f32x4 acc0 = zero4(), acc1 = zero4();
-      acc0 = mfma16(f.at[0], *(const bf16x8*)(sO + lr * DP + 8 * kg), acc0);
-      acc1 = mfma16(f.at[1], *(const bf16x8*)(sO + lr * DP + 32 + 8 * kg), acc1);
+      acc0 = mfma16(f.at[0], oB0, acc0);
+      acc1 = mfma16(f.at[1], oB1, acc1);
 #pragma unroll
       for (int s = 0; s < K / 32; s += 2) {
         acc0 = mfma16(f.kd[s], *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg), acc0);
@@ -204,16 +210,13 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
     // (4) dS = lam dS' + Qg^T dO - W^T dDelta
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      f32x4 pq = zero4(), pw = zero4();
+      f32x4 pw = zero4();
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        pq = mfma16(f.qgt[kt][s], *(const bf16x8*)(sO + lr * DP + 32 * s + 8 * kg), pq);
-        pw = mfma16(f.wt[kt][s], *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
-      }
-      dS[kt][0] = fmaf(f.lam[kt].x, dS[kt][0], pq[0] - pw[0]);
-      dS[kt][1] = fmaf(f.lam[kt].y, dS[kt][1], pq[1] - pw[1]);
-      dS[kt][2] = fmaf(f.lam[kt].z, dS[kt][2], pq[2] - pw[2]);
-      dS[kt][3] = fmaf(f.lam[kt].w, dS[kt][3], pq[3] - pw[3]);
+      for (int s = 0; s < 2; ++s) pw = mfma16(f.wt[kt][s], *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
+      dS[kt][0] = fmaf(f.lam[kt].x, dS[kt][0], pq[kt][0] - pw[0]);
+      dS[kt][1] = fmaf(f.lam[kt].y, dS[kt][1], pq[kt][1] - pw[1]);
+      dS[kt][2] = fmaf(f.lam[kt].z, dS[kt][2], pq[kt][2] - pw[2]);
+      dS[kt][3] = fmaf(f.lam[kt].w, dS[kt][3], pq[kt][3] - pw[3]);
     }
   };
 
@@ -242,11 +245,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
 constexpr int kVjpThreads = 1024;  // 16 waves per (chunk, head): hides global-load latency
 constexpr int kVjpWaves = kVjpThreads / kWave;
 
-// 512 threads and under 80 KB of LDS, so two tiles share a CU and one tile's global-load
-// latency overlaps the other's work.  T, dT, T^T dT and dW only ever feed bf16 MFMA
-// operands and are stored as bf16; T, dT and T^T dT reuse the (dU lo, delta) region once the
-// dQg / dKd / dW / dA phase is done.
-constexpr int kDenseThreads = 512;
+// 1024 threads per tile.  Every global operand of the tile is requested in one batch at the
+// start (dO, v and beta kh e^G rows staged in LDS, the state rows in registers), so a tile
+// waits on one global round trip instead of one per row tile and item.  T, dT, T^T dT and dW
+// only ever feed bf16 MFMA operands and are stored as bf16; T, dT and T^T dT reuse the
+// (dU lo, delta) region once the dQg / dKd / dW / dA phase is done.
+constexpr int kDenseThreads = 1024;
 constexpr int kDenseWaves = kDenseThreads / kWave;
 
 template <int K, int V>
@@ -263,7 +267,10 @@ struct DenseSmem {
   static constexpr size_t off_b = off_dw + 64 * KP * 2;         // f32 [64] beta
   static constexpr size_t off_pv = off_b + 64 * 4;              // f32 [V/16][64] dbeta partials
   static constexpr size_t off_pm = off_pv + (V / 16) * 64 * 4;  // f32 [4][64]
-  static constexpr size_t end = off_pm + 4 * 64 * 4;
+  static constexpr size_t off_do = off_pm + 4 * 64 * 4;        // bf16 [64][VP] dO (rows >= len zero)
+  static constexpr size_t off_v = off_do + 64 * VP * 2;          // bf16 [64][VP] v (rows >= len zero)
+  static constexpr size_t off_kb = off_v + 64 * VP * 2;          // bf16 [64][KP] beta kh e^G
+  static constexpr size_t end = off_kb + 64 * KP * 2;
   // T, dT, T^T dT (bf16 [64][TP] each, after dA): in the dU-lo / delta region when it is
   // large enough (V = 128), else behind everything
   static constexpr bool kAlias = 3 * 64 * TP * 2 <= 2 * 64 * VP * 2;
@@ -274,7 +281,7 @@ struct DenseSmem {
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs a) {
   using L = DenseSmem<K, V>;
   constexpr int MP = L::TP, KP = L::KP, VP = L::VP;
   constexpr int kVjpThreads = kDenseThreads, kVjpWaves = kDenseWaves;
@@ -289,6 +296,9 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
   float* sB = (float*)(smem + L::off_b);
   float* sPV = (float*)(smem + L::off_pv);
   float* sPM = (float*)(smem + L::off_pm);
+  bf16* sDO = (bf16*)(smem + L::off_do);
+  bf16* sV = (bf16*)(smem + L::off_v);
+  bf16* sKB = (bf16*)(smem + L::off_kb);
 
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
   const int len = ch.y;
@@ -313,8 +323,52 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
   float* DA = (float*)a.sc.p[S_DA] + tile * 64 * 64;
   float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
 
-  // ---- P0: stage dU, delta, beta; clear partials; T waits in registers until after dA ----
+  // PA's state rows: wave w owns key tile w / (4 / RPW) and RPW row tiles; its f32 S and
+  // dS' rows are requested first, with everything P0 loads
+  constexpr int NKT = 4 * (K / 16);
+  constexpr int RPW = NKT / kVjpWaves;  // row tiles per wave (2 for K = 128, 1 for K = 64)
+  constexpr int NVS = V / 32;
+  static_assert(RPW >= 1 && 4 % RPW == 0, "row tiles per wave");
+  const int pa_ct = wave / (4 / RPW), pa_rt0 = (wave % (4 / RPW)) * RPW;
+  float xs[NVS][8], xd[NVS][8];
+  {
+    const int c = 16 * pa_ct + lr;
+#pragma unroll
+    for (int sv = 0; sv < NVS; ++sv) {
+      load8f(SH + (size_t)c * V + 32 * sv + 8 * kg, xs[sv]);
+      load8f(DSH + (size_t)c * V + 32 * sv + 8 * kg, xd[sv]);
+    }
+  }
+
+  // ---- P0: stage dU, delta, beta, dO, v, beta kh e^G; clear partials; T waits in
+  // registers until after dA ----
   static_assert(64 * 64 % (4 * kDenseThreads) == 0, "T staging");
+  {
+    // rows of dO, v (8 values per thread and matrix) and k, G: clamped rows, zeroed after
+    static_assert(64 * V / 8 <= kDenseThreads && 64 * K / 8 <= kDenseThreads, "one row chunk per thread");
+    const int t = tid / (V / 8), c0 = (tid % (V / 8)) * 8;
+    const int tk = tid / (K / 8), ck = (tid % (K / 8)) * 8, tkc = tk < 64 ? tk : 63;
+    const size_t rv = (size_t)(row0 + (t < len ? t : len - 1)) * H + h;
+    const size_t rk = (size_t)(row0 + (tk < len ? tk : len - 1)) * H + h;
+    bf16x8 xo = *(const bf16x8*)(a.dout + rv * V + c0);
+    bf16x8 xv = *(const bf16x8*)(a.v + rv * V + c0);
+    const bf16x8 xk = *(const bf16x8*)(a.k + rk * K + ck);
+    float gk[8];
+    load8f(Gg + tkc * K + ck, gk);
+    const float bk = tk < len ? ((const float*)a.ws.p[R_BETA])[tile * 64 + tkc] * RK[tkc] : 0.f;
+    bf16x8 xb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xo[e] = t < len ? xo[e] : to_bf16(0.f);
+      xv[e] = t < len ? xv[e] : to_bf16(0.f);
+      xb[e] = to_bf16(bk * to_f32(xk[e]) * __expf(gk[e]));
+    }
+    if (t < 64) {
+      *(bf16x8*)(sDO + t * VP + c0) = xo;
+      *(bf16x8*)(sV + t * VP + c0) = xv;
+    }
+    if (tk < 64) *(bf16x8*)(sKB + tk * KP + ck) = xb;
+  }
   float4 treg[64 * 64 / (4 * kDenseThreads)];
 #pragma unroll
   for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
@@ -343,16 +397,6 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
   __syncthreads();
 
-  // branch-free: the row is clamped for the load and zeroed after it, so loads issued
-  // together stay in flight together
-  auto load_dout8 = [&](int i, int c0) -> bf16x8 {
-    const int ic = i < len ? i : len - 1;
-    bf16x8 x = *(const bf16x8*)(a.dout + ((size_t)(row0 + ic) * H + h) * V + c0);
-    const bf16 z = to_bf16(0.f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = i < len ? x[e] : z;
-    return x;
-  };
   auto f2b8 = [&](const float* p) -> bf16x8 {
     bf16x8 x;
 #pragma unroll
@@ -362,21 +406,11 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
 
   // ---- PA: dQg, dKd, dW over the 64 x K grid ----
   // Wave w owns key tile ct and RPW row tiles: the f32 state rows S[c][.] and dS'[c][.] of
-  // its 16 keys are loaded once (loads issued together), split into hi + lo bf16 once, and
-  // reused for every row tile.  The same rows give dlam = lam * sum_v S dS'.
-  constexpr int NKT = 4 * (K / 16);
+  // its 16 keys (requested at the start) are split into hi + lo bf16 once and reused for
+  // every row tile.  The same rows give dlam = lam * sum_v S dS'.
   {
-    constexpr int RPW = NKT / kVjpWaves;  // row tiles per wave (2 for K = 128, 1 for K = 64)
-    constexpr int NVS = V / 32;
-    static_assert(RPW >= 1 && 4 % RPW == 0, "row tiles per wave");
-    const int ct = wave / (4 / RPW), rt0 = (wave % (4 / RPW)) * RPW;
+    const int ct = pa_ct, rt0 = pa_rt0;
     const int c = 16 * ct + lr;
-    float xs[NVS][8], xd[NVS][8];
-#pragma unroll
-    for (int sv = 0; sv < NVS; ++sv) {
-      load8f(SH + (size_t)c * V + 32 * sv + 8 * kg, xs[sv]);
-      load8f(DSH + (size_t)c * V + 32 * sv + 8 * kg, xd[sv]);
-    }
     const float lamc = ((const float*)a.ws.p[R_LAM])[tile * K + c];
     bf16x8 sHi[NVS], sLo[NVS], dHi[NVS], dLo[NVS];
     float dl = 0.f;
@@ -395,7 +429,7 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
       const int p = rt + 4 * ct;
       bf16x8 aO[NVS];
 #pragma unroll
-      for (int sv = 0; sv < NVS; ++sv) aO[sv] = load_dout8(i, 32 * sv + 8 * kg);
+      for (int sv = 0; sv < NVS; ++sv) aO[sv] = *(const bf16x8*)(sDO + i * VP + 32 * sv + 8 * kg);
       f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
 #pragma unroll
       for (int sv = 0; sv < NVS; ++sv) {
@@ -431,7 +465,7 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
       const int vv = 32 * s + 8 * kg;
-      acc = mfma16(load_dout8(i, vv), *(const bf16x8*)(sDL + j * VP + vv), acc);
+      acc = mfma16(*(const bf16x8*)(sDO + i * VP + vv), *(const bf16x8*)(sDL + j * VP + vv), acc);
     }
     const int jj = 16 * bb + lr;
 #pragma unroll
@@ -457,35 +491,19 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
-    const bool jv = j < len;
-    // all global operands of the pair first (row clamped, zeroed by the select below)
-    const size_t rj = (size_t)(row0 + (jv ? j : len - 1)) * H + h;
-    bf16x8 vrow[V / 32], krow[K / 32];
-    float grow[K / 32][8];
-#pragma unroll
-    for (int s = 0; s < V / 32; ++s) vrow[s] = *(const bf16x8*)(a.v + rj * V + 32 * s + 8 * kg);
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
-      krow[s] = *(const bf16x8*)(a.k + rj * K + 32 * s + 8 * kg);
-      load8f(Gg + j * K + 32 * s + 8 * kg, grow[s]);
-    }
-    const float bj = jv ? sB[j] : 0.f;
-    const float bk = bj * RK[j];
+    const float bj = j < len ? sB[j] : 0.f;
     f32x4 acc = zero4();
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
+      const bf16x8 vr = *(const bf16x8*)(sV + j * VP + 32 * s + 8 * kg);
       bf16x8 fb;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * to_f32(vrow[s][e]));
+      for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bj * to_f32(vr[e]));
       acc = mfma16(*(const bf16x8*)(sDU + i * VP + 32 * s + 8 * kg), fb, acc);
     }
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
-      bf16x8 fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fb[e] = to_bf16(bk * to_f32(krow[s][e]) * __expf(grow[s][e]));
-      acc = mfma16(*(const bf16x8*)(sDW + i * KP + 32 * s + 8 * kg), fb, acc);
-    }
+    for (int s = 0; s < K / 32; ++s)
+      acc = mfma16(*(const bf16x8*)(sDW + i * KP + 32 * s + 8 * kg), *(const bf16x8*)(sKB + j * KP + 32 * s + 8 * kg), acc);
     const int jj = 16 * bb + lr;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) sDT[(16 * ba + 4 * kg + rr) * MP + jj] = to_bf16(acc[rr]);
@@ -504,7 +522,7 @@ __global__ __launch_bounds__(kDenseThreads, 4) void chunk_bwd_dense_kernel(BwdAr
       if (jj < len) {
         const size_t off = ((size_t)(row0 + jj) * H + h) * V + col;
         a.dv[off] = to_bf16(sB[jj] * acc[rr]);
-        part = acc[rr] * to_f32(a.v[off]);
+        part = acc[rr] * to_f32(sV[jj * VP + col]);
       }
       part = group_sum<16>(part);
       if (lr == 0) sPV[ct * 64 + jj] = part;
