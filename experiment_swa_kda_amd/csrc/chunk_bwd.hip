@@ -342,20 +342,37 @@ __global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs 
 
   // ---- P0: stage dU, delta, beta, dO, v, beta kh e^G; clear partials; T waits in
   // registers until after dA ----
+  // Every load of P0 is issued before the first LDS write (fixed per-thread counts), so the
+  // stage costs one global round trip.
   static_assert(64 * 64 % (4 * kDenseThreads) == 0, "T staging");
+  static_assert(64 * V / 8 <= kDenseThreads && 64 * K / 8 <= kDenseThreads, "one row chunk per thread");
+  constexpr int NDU = (V * 16 + kDenseThreads - 1) / kDenseThreads;
+  constexpr int NDL = (64 * V / 8 + kDenseThreads - 1) / kDenseThreads;
+  // rows of dO, v (8 values per thread and matrix) and k, G: clamped rows, zeroed after
+  const int t = tid / (V / 8), c0 = (tid % (V / 8)) * 8;
+  const int tk = tid / (K / 8), ck = (tid % (K / 8)) * 8, tkc = tk < 64 ? tk : 63;
+  const size_t rv = (size_t)(row0 + (t < len ? t : len - 1)) * H + h;
+  const size_t rk = (size_t)(row0 + (tk < len ? tk : len - 1)) * H + h;
+  bf16x8 xo = *(const bf16x8*)(a.dout + rv * V + c0);
+  bf16x8 xv = *(const bf16x8*)(a.v + rv * V + c0);
+  const bf16x8 xk = *(const bf16x8*)(a.k + rk * K + ck);
+  float gk[8];
+  load8f(Gg + tkc * K + ck, gk);
+  const float bt = ((const float*)a.ws.p[R_BETA])[tile * 64 + tkc], rkt = RK[tkc];
+  float4 treg[64 * 64 / (4 * kDenseThreads)];
+#pragma unroll
+  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
+  float4 ddl[NDU];
+#pragma unroll
+  for (int q = 0; q < NDU; ++q) {
+    const int idx = min(q * kDenseThreads + tid, V * 16 - 1);
+    ddl[q] = *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
+  }
+  bf16x8 dlf[NDL];
+#pragma unroll
+  for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
   {
-    // rows of dO, v (8 values per thread and matrix) and k, G: clamped rows, zeroed after
-    static_assert(64 * V / 8 <= kDenseThreads && 64 * K / 8 <= kDenseThreads, "one row chunk per thread");
-    const int t = tid / (V / 8), c0 = (tid % (V / 8)) * 8;
-    const int tk = tid / (K / 8), ck = (tid % (K / 8)) * 8, tkc = tk < 64 ? tk : 63;
-    const size_t rv = (size_t)(row0 + (t < len ? t : len - 1)) * H + h;
-    const size_t rk = (size_t)(row0 + (tk < len ? tk : len - 1)) * H + h;
-    bf16x8 xo = *(const bf16x8*)(a.dout + rv * V + c0);
-    bf16x8 xv = *(const bf16x8*)(a.v + rv * V + c0);
-    const bf16x8 xk = *(const bf16x8*)(a.k + rk * K + ck);
-    float gk[8];
-    load8f(Gg + tkc * K + ck, gk);
-    const float bk = tk < len ? ((const float*)a.ws.p[R_BETA])[tile * 64 + tkc] * RK[tkc] : 0.f;
+    const float bk = tk < len ? bt * rkt : 0.f;
     bf16x8 xb;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -369,14 +386,12 @@ __global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs 
     }
     if (tk < 64) *(bf16x8*)(sKB + tk * KP + ck) = xb;
   }
-  float4 treg[64 * 64 / (4 * kDenseThreads)];
-#pragma unroll
-  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
   // dU = dDelta (hi/lo bf16 split) and delta, transposed from their [V][64] histories
-  for (int idx = tid; idx < V * 16; idx += kVjpThreads) {
-    const int vv = idx / 16, t4 = (idx % 16) * 4;
-    const float4 d = *(const float4*)(DDLT + (size_t)vv * 64 + t4);
-    const float dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+  for (int q = 0; q < NDU; ++q) {
+    const int idx = q * kDenseThreads + tid, vv = idx / 16, t4 = (idx % 16) * 4;
+    if (idx >= V * 16) break;
+    const float dv[4] = {ddl[q].x, ddl[q].y, ddl[q].z, ddl[q].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bf16 hi = to_bf16(dv[e]);
@@ -386,12 +401,14 @@ __global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs 
   }
   // delta from its B-operand fragments [strip][2][64 lanes][8] in the scan's permuted
   // token order: element e of lane l is t = 32 s + 16 (e/4) + 4 (l/16) + e%4
-  for (int idx = tid; idx < 64 * V / 8; idx += kVjpThreads) {
+#pragma unroll
+  for (int q = 0; q < NDL; ++q) {
+    const int idx = q * kDenseThreads + tid;
+    if (idx >= 64 * V / 8) break;
     const int lane_ = idx % 64, sl = (idx / 64) % 2, strip = idx / 128;
-    const bf16x8 x = *(const bf16x8*)(DLF + (size_t)idx * 8);
     const int vv = 16 * strip + lane_ % 16, t0 = 32 * sl + 4 * (lane_ / 16);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sDL[(t0 + 16 * (e / 4) + e % 4) * VP + vv] = x[e];
+    for (int e = 0; e < 8; ++e) sDL[(t0 + 16 * (e / 4) + e % 4) * VP + vv] = dlf[q][e];
   }
   if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
@@ -596,26 +613,31 @@ __global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs 
 // ---------------------------------------------------------------------------
 template <int K>
 struct DecaySmem {
-  static constexpr int KP = K + 4;
-  static constexpr int MP = 65;
+  static constexpr int QP = K + 8;                               // bf16 row stride of q, k
+  static constexpr int GP = K + 4;                               // f32 row stride of G
+  static constexpr int AP = 64 + 8;                              // bf16 row stride of dA, dM'
+  static constexpr int HALF = K / 2;                             // key columns per pass
+  static constexpr int OP = HALF + 8;                            // bf16 row stride of the operands
   static constexpr int NSEG = kVjpThreads / K;                   // cumsum segments per column
-  static constexpr size_t off_q = 0;                             // f32 [64][KP] qh, later dq
-  static constexpr size_t off_k = off_q + 64 * KP * 4;           // f32 [64][KP] kh, later dk
-  static constexpr size_t off_g = off_k + 64 * KP * 4;           // f32 [64][KP] G, later dG
-  static constexpr size_t off_da = off_g + 64 * KP * 4;          // f32 [64][65] dA
-  static constexpr size_t off_dm = off_da + 64 * MP * 4;         // f32 [64][65] dM'
-  static constexpr size_t off_pb = off_dm + 64 * MP * 4;         // f32 [K/16][64] dbeta partials
+  static constexpr size_t off_q = 0;                             // bf16 [64][QP] q, later dq
+  static constexpr size_t off_k = off_q + 64 * QP * 2;           // bf16 [64][QP] k, later dk
+  static constexpr size_t off_g = off_k + 64 * QP * 2;           // f32 [64][GP] G, later dG
+  static constexpr size_t off_da = off_g + 64 * GP * 4;          // bf16 [64][AP] dA
+  static constexpr size_t off_dm = off_da + 64 * AP * 2;         // bf16 [64][AP] dM'
+  static constexpr size_t off_op = off_dm + 64 * AP * 2;         // bf16 6 x [64][OP] operands
+  static constexpr size_t off_pb = off_op + 6 * 64 * OP * 2;     // f32 [K/16][64] dbeta partials
   static constexpr size_t off_pq = off_pb + (K / 16) * 64 * 4;   // f32 [K/16][64] qh . dqh
   static constexpr size_t off_pk = off_pq + (K / 16) * 64 * 4;   // f32 [K/16][64] kh . dkh
   static constexpr size_t off_gl = off_pk + (K / 16) * 64 * 4;   // f32 [4][K] dG_last partials
   static constexpr size_t off_row = off_gl + 4 * K * 4;          // f32 [5][64] beta, rq, rk, fq, fk
   static constexpr size_t off_f = off_row + 5 * 64 * 4;          // int [4] unsafe-block flags
   static constexpr size_t bytes = off_f + 16;
-  // after the item phase the dA/dM' region holds the cumsum segments and parameter partials
-  static constexpr size_t off_seg = off_da;                      // f32 [NSEG][K]
+  // after the item phase the operand region holds the cumsum segments and parameter partials
+  static constexpr size_t off_seg = off_op;                      // f32 [NSEG][K]
   static constexpr size_t off_p0 = off_seg + NSEG * K * 4;       // f32 [NSEG][K]
   static constexpr size_t off_p1 = off_p0 + NSEG * K * 4;        // f32 [NSEG][K]
-  static_assert(off_p1 + NSEG * K * 4 <= off_pb, "cumsum scratch must fit in the dA/dM' region");
+  static_assert(off_p1 + NSEG * K * 4 <= off_pb, "cumsum scratch must fit in the operand region");
+  static_assert(QP % 8 == 0 && AP % 4 == 0 && OP % 4 == 0, "vector rows and transposing reads");
 };
 
 // Decay-structured VJP: gathers every dependence of the loss on qh, kh and G for one
@@ -625,20 +647,38 @@ struct DecaySmem {
 //   dG  = dQg Qg - dKd Kd + dKb Kb + qh Rq + kh Rk - kh (Cq + Ck),   dGL += sum_i dKd Kd
 // with Rq = sum_j dA_ij kh_j e^{G_i-G_j}, Rk = sum_j dM'_ij kh_j e^{G_i-G_j} (row side) and
 // Cq = sum_i dA_ij qh_i e^{G_i-G_j}, Ck = sum_i dM'_ij kh_i e^{G_i-G_j} (column side).
-// Each 16 x 16 (row tile, key tile) item is owned by one wave in MFMA C layout, the layout in
-// which the dense kernel stored dQg, dKd and dKb, so every per-element term stays in registers.
+// The sums run over 16-token blocks b, each factor split around a reference row of b:
+//   row side:    e^{G_i-G_j} = e^{G_i-G_f(b)} e^{G_f(b)-G_j},  f(b) = 16b, the first row
+//   column side: e^{G_i-G_j} = e^{G_i-G_l(b)} e^{G_l(b)-G_j},  l(b) = 16b + 15, the last row
+// so the decay-scaled operands KR = kh e^{G_f-G}, QC = qh e^{G-G_l}, KC = kh e^{G-G_l} are
+// built once per tile (every factor within a block is at most e^span <= e^80) and each
+// (row tile, key tile) item is a sum over blocks of 16-deep MFMAs scaled by one factor per
+// row (at most 1).  The operands are split hi + lo bf16: their rounding is systematic across
+// the row and column terms of dG, which nearly cancel.  A tile with a block whose decay spans
+// more than 80 nats runs an exact per-pair f32 loop instead.  Items are owned in MFMA C
+// layout, the layout in which the dense kernel stored dQg, dKd and dKb, so every
+// per-element term stays in registers.  The key columns go in two passes of K/2 (the
+// operands of one pass fit in LDS beside q, k and G).
 template <int K>
 __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a) {
   using L = DecaySmem<K>;
-  constexpr int KP = L::KP, MP = L::MP, NSEG = L::NSEG;
+  constexpr int QP = L::QP, GP = L::GP, AP = L::AP, HALF = L::HALF, OP = L::OP, NSEG = L::NSEG;
   constexpr int NKT = 4 * (K / 16);
   constexpr int IPW = (NKT + kVjpWaves - 1) / kVjpWaves;  // items per wave
+  constexpr int NIH = 4 * (HALF / 16);                    // items per pass
+  static_assert(NIH <= kVjpWaves && 64 * HALF / 4 <= kVjpThreads, "one item and one operand group per thread and pass");
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  float* sQ = (float*)(smem + L::off_q);
-  float* sK = (float*)(smem + L::off_k);
+  bf16* sQ = (bf16*)(smem + L::off_q);
+  bf16* sK = (bf16*)(smem + L::off_k);
   float* sG = (float*)(smem + L::off_g);
-  float* sDA = (float*)(smem + L::off_da);
-  float* sDM = (float*)(smem + L::off_dm);
+  bf16* sDA = (bf16*)(smem + L::off_da);
+  bf16* sDM = (bf16*)(smem + L::off_dm);
+  bf16* sKRh = (bf16*)(smem + L::off_op);
+  bf16* sKRl = sKRh + 64 * OP;
+  bf16* sQCh = sKRl + 64 * OP;
+  bf16* sQCl = sQCh + 64 * OP;
+  bf16* sKCh = sQCl + 64 * OP;
+  bf16* sKCl = sKCh + 64 * OP;
   float* sPB = (float*)(smem + L::off_pb);
   float* sPQ = (float*)(smem + L::off_pq);
   float* sPK = (float*)(smem + L::off_pk);
@@ -660,61 +700,71 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   const int lr = lane % 16, kg = lane / 16;
 
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
+  const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
+  const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
   // dQg/dKd/dKb of this tile; they are overwritten with dqh, dkh and dG (same lane, same
   // address) to carry them across the barrier that completes the per-row dot products
   float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
   float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
   float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
 
-  // ---- P0: stage qh, kh, G, dA, dM', beta and the per-row norm factors ----
+  // ---- P0: stage q, k (bf16), G, dA, dM' (bf16), beta and the per-row norm factors ----
   if (tid < 4) sF[tid] = 0;
-  if (tid < 64 * (K / 8)) {
-    constexpr int LPR = K / 8;
-    const int t = tid / LPR, c0 = (tid % LPR) * 8;
-    // every load of the row first (clamped row, zeroed after), so they are in flight together
-    const size_t base = ((size_t)(row0 + (t < len ? t : len - 1)) * H + h) * K + c0;
-    const bf16x8 qr = *(const bf16x8*)(a.q + base), kr = *(const bf16x8*)(a.k + base);
-    const float rq = ((const float*)a.ws.p[R_RQ])[tile * 64 + t];
-    const float rk = ((const float*)a.ws.p[R_RK])[tile * 64 + t];
-    float gv[8];
-    load8f(Gg + t * K + c0, gv);
-    float qv[8], kv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qv[e] = t < len ? (float)qr[e] : 0.f;
-      kv[e] = t < len ? (float)kr[e] : 0.f;
-    }
-    float sq = 0.f, sk = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sq += qv[e] * qv[e];
-      sk += kv[e] * kv[e];
-      sQ[t * KP + c0 + e] = qv[e] * rq;
-      sK[t * KP + c0 + e] = kv[e] * rk;
-      sG[t * KP + c0 + e] = gv[e];
-    }
-    sq = group_sum<LPR>(sq);
-    sk = group_sum<LPR>(sk);
-    if (c0 == 0) {
-      // dx = r (g - xhat (xhat . g)) with xhat = x/||x||; expressed through qh = r x:
-      // dx = r g - qh (qh . g) / (||x||^2 r); clamped norms pass r g through
-      sRq[t] = rq;
-      sRk[t] = rk;
-      sFq[t] = sqrtf(sq) > 1e-12f ? 1.f / (sq * rq) : 0.f;
-      sFk[t] = sqrtf(sk) > 1e-12f ? 1.f / (sk * rk) : 0.f;
-      sBeta[t] = ((const float*)a.ws.p[R_BETA])[tile * 64 + t];
-    }
-  }
   {
-    const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
-    const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
-    for (int idx = tid * 4; idx < 64 * 64; idx += kVjpThreads * 4) {
-      const float4 x = *(const float4*)(DA + idx);
-      const float4 y = *(const float4*)(DMP + idx);
-      float* da = sDA + (idx / 64) * MP + idx % 64;
-      float* dm = sDM + (idx / 64) * MP + idx % 64;
-      da[0] = x.x; da[1] = x.y; da[2] = x.z; da[3] = x.w;
-      dm[0] = y.x; dm[1] = y.y; dm[2] = y.z; dm[3] = y.w;
+    // every load first (clamped rows, zeroed after), so they are in flight together
+    constexpr int LPR = K / 8;
+    static_assert(64 * LPR <= kVjpThreads, "one row chunk per thread");
+    const int t = tid / LPR, c0 = (tid % LPR) * 8;
+    const bool act = tid < 64 * LPR;
+    const int tc = act ? t : 0;
+    const size_t base = ((size_t)(row0 + (tc < len ? tc : len - 1)) * H + h) * K + c0;
+    bf16x8 qr = *(const bf16x8*)(a.q + base), kr = *(const bf16x8*)(a.k + base);
+    const float rq = ((const float*)a.ws.p[R_RQ])[tile * 64 + tc];
+    const float rk = ((const float*)a.ws.p[R_RK])[tile * 64 + tc];
+    const float bt = ((const float*)a.ws.p[R_BETA])[tile * 64 + tc];
+    float gv[8];
+    load8f(Gg + tc * K + c0, gv);
+    // dA, dM': 64 x 64 f32 each, 4 consecutive per thread
+    const int ai = tid * 4;
+    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xm = xa;
+    if (ai < 64 * 64) {
+      xa = *(const float4*)(DA + ai);
+      xm = *(const float4*)(DMP + ai);
+    }
+    if (act) {
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (!(tc < len)) {
+          qr[e] = to_bf16(0.f);
+          kr[e] = to_bf16(0.f);
+        }
+        const float qv = to_f32(qr[e]), kv = to_f32(kr[e]);
+        sq += qv * qv;
+        sk += kv * kv;
+      }
+      *(bf16x8*)(sQ + t * QP + c0) = qr;
+      *(bf16x8*)(sK + t * QP + c0) = kr;
+      *(float4*)(sG + t * GP + c0) = make_float4(gv[0], gv[1], gv[2], gv[3]);
+      *(float4*)(sG + t * GP + c0 + 4) = make_float4(gv[4], gv[5], gv[6], gv[7]);
+      sq = group_sum<LPR>(sq);
+      sk = group_sum<LPR>(sk);
+      if (c0 == 0) {
+        // dx = r (g - xhat (xhat . g)) with xhat = x/||x||; expressed through qh = r x:
+        // dx = r g - qh (qh . g) / (||x||^2 r); clamped norms pass r g through
+        sRq[t] = rq;
+        sRk[t] = rk;
+        sFq[t] = sqrtf(sq) > 1e-12f ? 1.f / (sq * rq) : 0.f;
+        sFk[t] = sqrtf(sk) > 1e-12f ? 1.f / (sk * rk) : 0.f;
+        sBeta[t] = bt;
+      }
+    }
+    if (ai < 64 * 64) {
+      bf16x4 ya, ym;
+      ya[0] = to_bf16(xa.x); ya[1] = to_bf16(xa.y); ya[2] = to_bf16(xa.z); ya[3] = to_bf16(xa.w);
+      ym[0] = to_bf16(xm.x); ym[1] = to_bf16(xm.y); ym[2] = to_bf16(xm.z); ym[3] = to_bf16(xm.w);
+      *(bf16x4*)(sDA + (ai / 64) * AP + ai % 64) = ya;
+      *(bf16x4*)(sDM + (ai / 64) * AP + ai % 64) = ym;
     }
   }
   __syncthreads();
@@ -722,164 +772,161 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
     const int c = tid;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      if (sG[(16 * b) * KP + c] - sG[(16 * b + 15) * KP + c] > 80.f) atomicOr(&sF[b], 1);
+      if (sG[(16 * b) * GP + c] - sG[(16 * b + 15) * GP + c] > 80.f) atomicOr(&sF[b], 1);
   }
   __syncthreads();
+  const bool unsafe = (sF[0] | sF[1] | sF[2] | sF[3]) != 0;
 
-  // ---- P1: per item, row side + column side + all per-element terms ----
+  // ---- P1: per pass (K/2 key columns) build the decay-scaled operands, then one item per
+  // wave: row side + column side + all per-element terms ----
 #pragma unroll 1
-  for (int n = 0; n < IPW; ++n) {
-    const int p = wave + n * kVjpWaves;
-    if (p >= NKT) break;
-    const int rt = p % 4, ct = p / 4;
-    // lane coordinates made opaque per item: keeps the compiler from hoisting dozens of
-    // lane-dependent LDS addresses out of the item loop (they would be spilled)
-    int lr = lane % 16, kg = lane / 16;
-    asm volatile("" : "+v"(lr), "+v"(kg));
-    const int c = 16 * ct + lr;
-    const bool unsafe = sF[rt] != 0;
-    // the raw dQg/dKd/dKb items are not needed before the per-element terms: their loads
-    // overlap the MFMA work below
-    const f32x4 rdQ = *(const f32x4*)(DQG + ((size_t)p * 64 + lane) * 4);
-    const f32x4 rdK = *(const f32x4*)(DKD + ((size_t)p * 64 + lane) * 4);
-    const f32x4 rdB = *(const f32x4*)(DKB + ((size_t)p * 64 + lane) * 4);
-    // row side  Rq = sum_j dA_ij kh_j e^{G_i-G_j},  Rk = sum_j dM'_ij kh_j e^{G_i-G_j}
-    f32x4 rq = zero4(), rk = zero4();
-    // column side  Cq + Ck = sum_i (dA_ij qh_i + dM'_ij kh_i) e^{G_i-G_j}
-    f32x4 cq = zero4(), ck = zero4();
+  for (int pass = 0; pass < 2; ++pass) {
+    const int cb = pass * HALF;  // first key column of the pass
+    // lane coordinates made opaque per pass: keeps the compiler from hoisting dozens of
+    // lane-dependent LDS addresses out of the pass loop (they would be spilled)
+    int ptid = tid, plane = lane, lr = lane % 16, kg = lane / 16;
+    asm volatile("" : "+v"(ptid), "+v"(plane), "+v"(lr), "+v"(kg));
     if (!unsafe) {
-      const int r = 16 * rt;
-      const int i = 16 * rt + lr;
-      const int jmax = 16 * rt + 15;
-      const float gr = sG[r * KP + c];
-      for (int s = 0; s <= jmax / 32; ++s) {
-        const int j0 = 32 * s + 8 * kg;
-        bf16x8 fa, fm, fbh, fbl;
-        float xb[8];
-        // every operand is read unconditionally (all rows are in bounds) and the causal
-        // mask is a select: a masked read would become a branch that waits on each load
-        float kj[8], gj[8];
+      // operand group: row t, 4 consecutive columns
+      const int t = ptid / (HALF / 4), c4 = (ptid % (HALF / 4)) * 4;
+      if (t < 64) {
+        const int c = cb + c4, bf = t & ~15, bl = bf + 15;
+        const float4 g = *(const float4*)(sG + t * GP + c);
+        const float4 gf = *(const float4*)(sG + bf * GP + c);
+        const float4 gl = *(const float4*)(sG + bl * GP + c);
+        const bf16x4 qq = *(const bf16x4*)(sQ + t * QP + c), kk = *(const bf16x4*)(sK + t * QP + c);
+        const float rq = sRq[t], rk = sRk[t];
+        const float gt[4] = {g.x, g.y, g.z, g.w}, gft[4] = {gf.x, gf.y, gf.z, gf.w}, glt[4] = {gl.x, gl.y, gl.z, gl.w};
+        bf16x4 krh, krl, qch, qcl, kch, kcl;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = j0 + e;
-          fa[e] = to_bf16(sDA[i * MP + j]);
-          fm[e] = to_bf16(sDM[i * MP + j]);
-          kj[e] = sK[j * KP + c];
-          gj[e] = sG[j * KP + c];
+        for (int e = 0; e < 4; ++e) {
+          const float qh = to_f32(qq[e]) * rq, kh = to_f32(kk[e]) * rk;
+          const float e1 = __expf(gft[e] - gt[e]), e2 = __expf(gt[e] - glt[e]);
+          const float kr = kh * e1, qc = qh * e2, kc = kh * e2;
+          krh[e] = to_bf16(kr);
+          krl[e] = to_bf16(kr - to_f32(krh[e]));
+          qch[e] = to_bf16(qc);
+          qcl[e] = to_bf16(qc - to_f32(qch[e]));
+          kch[e] = to_bf16(kc);
+          kcl[e] = to_bf16(kc - to_f32(kch[e]));
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = kj[e] * __expf(gr - gj[e]);
-          xb[e] = j0 + e <= jmax ? x : 0.f;
-        }
-        // the decay-scaled operands are split (hi + lo): their rounding is systematic
-        // across the row/column terms of dG, which nearly cancel
-        split8(xb, fbh, fbl);
-        rq = mfma16(fa, fbh, rq);
-        rq = mfma16(fa, fbl, rq);
-        rk = mfma16(fm, fbh, rk);
-        rk = mfma16(fm, fbl, rk);
+        const int o = t * OP + c4;
+        *(bf16x4*)(sKRh + o) = krh;
+        *(bf16x4*)(sKRl + o) = krl;
+        *(bf16x4*)(sQCh + o) = qch;
+        *(bf16x4*)(sQCl + o) = qcl;
+        *(bf16x4*)(sKCh + o) = kch;
+        *(bf16x4*)(sKCl + o) = kcl;
       }
-      const int rp = 16 * rt + 15;
-      const int j = 16 * rt + lr;
-      const float gp = sG[rp * KP + c];
-      for (int s = (16 * rt) / 32; s < 2; ++s) {
-        const int i0 = 32 * s + 8 * kg;
-        bf16x8 fa, fm, bqh, bql, bkh, bkl;
-        float xq[8], xk[8];
-        float gi[8];
+    }
+    __syncthreads();
+    if (wave < NIH) {
+      const int rt = wave % 4, ctl = wave / 4, ct = cb / 16 + ctl;
+      const int p = rt + 4 * ct;
+      const int c = 16 * ct + lr;
+      // the raw dQg/dKd/dKb items are not needed before the per-element terms: their loads
+      // overlap the MFMA work below
+      const f32x4 rdQ = *(const f32x4*)(DQG + ((size_t)p * 64 + plane) * 4);
+      const f32x4 rdK = *(const f32x4*)(DKD + ((size_t)p * 64 + plane) * 4);
+      const f32x4 rdB = *(const f32x4*)(DKB + ((size_t)p * 64 + plane) * 4);
+      f32x4 rq = zero4(), rk = zero4(), cq = zero4(), ck = zero4();
+      if (!unsafe) {
+        // row side: blocks b <= rt, A = dA / dM' rows of tile rt, B = KR rows of block b
+        for (int b = 0; b <= rt; ++b) {
+          const bf16x4 fa = *(const bf16x4*)(sDA + (16 * rt + lr) * AP + 16 * b + 4 * kg);
+          const bf16x4 fm = *(const bf16x4*)(sDM + (16 * rt + lr) * AP + 16 * b + 4 * kg);
+          const bf16x4 bh = lds_col_frag4(sKRh, OP, 16 * b, 16 * ctl, plane);
+          const bf16x4 bl = lds_col_frag4(sKRl, OP, 16 * b, 16 * ctl, plane);
+          const f32x4 pq = mfma16k16(fa, bl, mfma16k16(fa, bh, zero4()));
+          const f32x4 pk = mfma16k16(fm, bl, mfma16k16(fm, bh, zero4()));
+          const float gref = sG[(16 * b) * GP + c];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int ii = i0 + e;
-          fa[e] = to_bf16(sDA[ii * MP + j]);
-          fm[e] = to_bf16(sDM[ii * MP + j]);
-          xq[e] = sQ[ii * KP + c];
-          xk[e] = sK[ii * KP + c];
-          gi[e] = sG[ii * KP + c];
+          for (int r = 0; r < 4; ++r) {
+            const float f = __expf(sG[(16 * rt + 4 * kg + r) * GP + c] - gref);
+            rq[r] = fmaf(pq[r], f, rq[r]);
+            rk[r] = fmaf(pk[r], f, rk[r]);
+          }
         }
+        // column side: blocks b >= rt, A = dA^T / dM'^T (columns of tile rt), B = QC / KC
+        for (int b = rt; b < 4; ++b) {
+          const bf16x4 fa = lds_col_frag4(sDA, AP, 16 * b, 16 * rt, plane);
+          const bf16x4 fm = lds_col_frag4(sDM, AP, 16 * b, 16 * rt, plane);
+          const bf16x4 qh = lds_col_frag4(sQCh, OP, 16 * b, 16 * ctl, plane);
+          const bf16x4 ql = lds_col_frag4(sQCl, OP, 16 * b, 16 * ctl, plane);
+          const bf16x4 kh = lds_col_frag4(sKCh, OP, 16 * b, 16 * ctl, plane);
+          const bf16x4 kl = lds_col_frag4(sKCl, OP, 16 * b, 16 * ctl, plane);
+          const f32x4 pq = mfma16k16(fa, ql, mfma16k16(fa, qh, zero4()));
+          const f32x4 pk = mfma16k16(fm, kl, mfma16k16(fm, kh, zero4()));
+          const float gref = sG[(16 * b + 15) * GP + c];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = __expf(gi[e] - gp);
-          const float f = i0 + e >= 16 * rt ? x : 0.f;
-          xq[e] *= f;
-          xk[e] *= f;
+          for (int r = 0; r < 4; ++r) {
+            const float f = __expf(gref - sG[(16 * rt + 4 * kg + r) * GP + c]);
+            cq[r] = fmaf(pq[r], f, cq[r]);
+            ck[r] = fmaf(pk[r], f, ck[r]);
+          }
         }
-        split8(xq, bqh, bql);
-        split8(xk, bkh, bkl);
-        cq = mfma16(fa, bqh, cq);
-        cq = mfma16(fa, bql, cq);
-        ck = mfma16(fm, bkh, ck);
-        ck = mfma16(fm, bkl, ck);
+      } else {
+        // a block whose decay spans more than 80 nats: exact per-pair factors (f32 dA, dM'
+        // from the dense kernel's output)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int ii = 16 * rt + 4 * kg + rr;
+          const float gi = sG[ii * GP + c];
+          float sq = 0.f, sk = 0.f;
+          for (int j = 0; j <= ii; ++j) {
+            const float kj = to_f32(sK[j * QP + c]) * sRk[j] * expf(gi - sG[j * GP + c]);
+            sq = fmaf(DA[ii * 64 + j], kj, sq);
+            sk = fmaf(DMP[ii * 64 + j], kj, sk);
+          }
+          float tq = 0.f, tk = 0.f;
+          for (int i = ii; i < 64; ++i) {
+            const float e = expf(sG[i * GP + c] - gi);
+            tq = fmaf(DA[i * 64 + ii], to_f32(sQ[i * QP + c]) * sRq[i] * e, tq);
+            tk = fmaf(DMP[i * 64 + ii], to_f32(sK[i * QP + c]) * sRk[i] * e, tk);
+          }
+          rq[rr] = sq;
+          rk[rr] = sk;
+          cq[rr] = tq;
+          ck[rr] = tk;
+        }
       }
+      const float GL = sG[63 * GP + c];
+      float glp = 0.f;
+      f32x4 dqs, dks, dgs;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int ii = 16 * rt + 4 * kg + rr;
-        const float gi = sG[ii * KP + c];
-        const float fr = __expf(gi - gr), fc = __expf(gp - gi);
-        rq[rr] *= fr;
-        rk[rr] *= fr;
-        cq[rr] *= fc;
-        ck[rr] *= fc;
-      }
-    } else {
-      // a block whose decay spans more than 80 nats: exact per-pair factors
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = 16 * rt + 4 * kg + rr;
-        const float gi = sG[ii * KP + c];
-        float sq = 0.f, sk = 0.f;
-        for (int j = 0; j <= ii; ++j) {
-          const float kj = sK[j * KP + c] * expf(gi - sG[j * KP + c]);
-          sq = fmaf(sDA[ii * MP + j], kj, sq);
-          sk = fmaf(sDM[ii * MP + j], kj, sk);
+        const float qh = to_f32(sQ[ii * QP + c]) * sRq[ii], kh = to_f32(sK[ii * QP + c]) * sRk[ii];
+        const float G = sG[ii * GP + c];
+        const float bt = sBeta[ii];
+        const float eG = expf(G), eKd = expf(GL - G);
+        const float dQg = rdQ[rr], dKd = rdK[rr], dKb = rdB[rr];
+        const float cc = cq[rr] + ck[rr];
+        const float dqh = fmaf(dQg, eG, rq[rr]);
+        const float dkh = dKd * eKd + bt * eG * dKb + rk[rr] + cc;
+        const float kdd = dKd * kh * eKd;
+        const float kbb = dKb * kh * eG;  // dbeta partial (the beta factor of Kb removed)
+        dgs[rr] = dQg * qh * eG - kdd + bt * kbb + qh * rq[rr] + kh * rk[rr] - kh * cc;
+        dqs[rr] = dqh;
+        dks[rr] = dkh;
+        glp += kdd;
+        const float pb = group_sum<16>(kbb);
+        const float pq = group_sum<16>(qh * dqh);
+        const float pk = group_sum<16>(kh * dkh);
+        if (lr == 0) {
+          sPB[ct * 64 + ii] = pb;
+          sPQ[ct * 64 + ii] = pq;
+          sPK[ct * 64 + ii] = pk;
         }
-        float tq = 0.f, tk = 0.f;
-        for (int i = ii; i < 64; ++i) {
-          const float e = expf(sG[i * KP + c] - gi);
-          tq = fmaf(sDA[i * MP + ii], sQ[i * KP + c] * e, tq);
-          tk = fmaf(sDM[i * MP + ii], sK[i * KP + c] * e, tk);
-        }
-        rq[rr] = sq;
-        rk[rr] = sk;
-        cq[rr] = tq;
-        ck[rr] = tk;
       }
+      *(f32x4*)(DQG + ((size_t)p * 64 + plane) * 4) = dqs;
+      *(f32x4*)(DKD + ((size_t)p * 64 + plane) * 4) = dks;
+      *(f32x4*)(DKB + ((size_t)p * 64 + plane) * 4) = dgs;
+      glp = lane_stride_sum<16>(glp);
+      if (kg == 0) sGL[rt * K + c] = glp;
     }
-    const float GL = sG[63 * KP + c];
-    float glp = 0.f;
-    f32x4 dqs, dks, dgs;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int ii = 16 * rt + 4 * kg + rr;
-      const float qh = sQ[ii * KP + c], kh = sK[ii * KP + c], G = sG[ii * KP + c];
-      const float bt = sBeta[ii];
-      const float eG = expf(G), eKd = expf(GL - G);
-      const float dQg = rdQ[rr], dKd = rdK[rr], dKb = rdB[rr];
-      const float cc = cq[rr] + ck[rr];
-      const float dqh = fmaf(dQg, eG, rq[rr]);
-      const float dkh = dKd * eKd + bt * eG * dKb + rk[rr] + cc;
-      const float kdd = dKd * kh * eKd;
-      const float kbb = dKb * kh * eG;  // dbeta partial (the beta factor of Kb removed)
-      dgs[rr] = dQg * qh * eG - kdd + bt * kbb + qh * rq[rr] + kh * rk[rr] - kh * cc;
-      dqs[rr] = dqh;
-      dks[rr] = dkh;
-      glp += kdd;
-      const float pb = group_sum<16>(kbb);
-      const float pq = group_sum<16>(qh * dqh);
-      const float pk = group_sum<16>(kh * dkh);
-      if (lr == 0) {
-        sPB[ct * 64 + ii] = pb;
-        sPQ[ct * 64 + ii] = pq;
-        sPK[ct * 64 + ii] = pk;
-      }
-    }
-    *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = dqs;
-    *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = dks;
-    *(f32x4*)(DKB + ((size_t)p * 64 + lane) * 4) = dgs;
-    glp = lane_stride_sum<16>(glp);
-    if (kg == 0) sGL[rt * K + c] = glp;
+    __syncthreads();  // the next pass rebuilds the operands
   }
-  __syncthreads();
 
   // per-row dot products (fixed order) and dbeta
   if (tid < 64) {
@@ -900,7 +947,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   }
   __syncthreads();
 
-  // ---- P2: L2-norm chains; dq, dk, dG into LDS (qh/kh/G are consumed) ----
+  // ---- P2: L2-norm chains; dq, dk (bf16) and dG into LDS (q, k, G are consumed) ----
 #pragma unroll
   for (int n = 0; n < IPW; ++n) {
     const int p = wave + n * kVjpWaves;
@@ -914,16 +961,16 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int ii = 16 * rt + 4 * kg + rr;
-      dqv[rr] = sRq[ii] * dqs[rr] - sQ[ii * KP + c] * sPQ[ii];
-      dkv[rr] = sRk[ii] * dks[rr] - sK[ii * KP + c] * sPK[ii];
+      dqv[rr] = sRq[ii] * dqs[rr] - to_f32(sQ[ii * QP + c]) * sRq[ii] * sPQ[ii];
+      dkv[rr] = sRk[ii] * dks[rr] - to_f32(sK[ii * QP + c]) * sRk[ii] * sPK[ii];
     }
-    // every read of this element's qh/kh happened in this lane; write back in place
+    // every read of this element's q / k happened in this lane; write back in place
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int ii = 16 * rt + 4 * kg + rr;
-      sQ[ii * KP + c] = dqv[rr];
-      sK[ii * KP + c] = dkv[rr];
-      sG[ii * KP + c] = ii < len ? dgs[rr] : 0.f;
+      sQ[ii * QP + c] = to_bf16(dqv[rr]);
+      sK[ii * QP + c] = to_bf16(dkv[rr]);
+      sG[ii * GP + c] = ii < len ? dgs[rr] : 0.f;
     }
   }
   __syncthreads();
@@ -935,8 +982,8 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
       const int t = idx / LPR, c0 = (idx % LPR) * 8;
       if (t >= len) continue;
       const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
-      store8(a.dq + base, sQ + t * KP + c0);
-      store8(a.dk + base, sK + t * KP + c0);
+      *(bf16x8*)(a.dq + base) = *(const bf16x8*)(sQ + t * QP + c0);
+      *(bf16x8*)(a.dk + base) = *(const bf16x8*)(sK + t * QP + c0);
     }
   }
 
@@ -949,7 +996,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   {
     float sum = 0.f;
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) sum += sG[(seg * RPS + r) * KP + c];
+    for (int r = 0; r < RPS; ++r) sum += sG[(seg * RPS + r) * GP + c];
     sSeg[seg * K + c] = sum;
   }
   __syncthreads();
@@ -965,7 +1012,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
 #pragma unroll
     for (int r = RPS - 1; r >= 0; --r) {
       const int t = seg * RPS + r;
-      acc += sG[t * KP + c];
+      acc += sG[t * GP + c];
       if (t < len) {
         const size_t off = ((size_t)(row0 + t) * H + h) * K + c;
         if (k3) {

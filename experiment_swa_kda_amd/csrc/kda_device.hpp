@@ -145,6 +145,20 @@ __device__ __forceinline__ bf16x8 lds_col_frag(const bf16* m, int pitch, int r0,
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Four-row column fragment (the B operand of a 16-deep MFMA, or an A operand read down a
+// column): lane (l % 16, l / 16) gets m[r0 + 4 (l / 16) + e][c0 + l % 16], e = 0..3, from one
+// transposing read (same lane mapping as lds_col_frag, four rows per lane group).
+__device__ __forceinline__ bf16x4 lds_col_frag4(const bf16* m, int pitch, int r0, int c0, int lane) {
+  const int lr = lane % 16, kg = lane / 16;
+  const bf16* p = m + (r0 + 4 * kg + lr / 4) * pitch + c0 + 4 * (lr % 4);
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p));
+}
+
+// v_mfma_f32_16x16x16_bf16: A[l % 16][4 (l / 16) + e], B[4 (l / 16) + e][l % 16], C as above.
+__device__ __forceinline__ f32x4 mfma16k16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, a), __builtin_bit_cast(short4_t, b), c, 0, 0, 0);
+}
+
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): two MFMAs with (hi, lo) recover
 // ~16 mantissa bits of an f32 operand.
 __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
