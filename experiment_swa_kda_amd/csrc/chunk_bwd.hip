@@ -786,15 +786,24 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
     // lane-dependent LDS addresses out of the pass loop (they would be spilled)
     int ptid = tid, plane = lane, lr = lane % 16, kg = lane / 16;
     asm volatile("" : "+v"(ptid), "+v"(plane), "+v"(lr), "+v"(kg));
+    // this wave's item of the pass; its raw dQg/dKd/dKb are not needed before the
+    // per-element terms, so their loads are issued first and overlap the operand build
+    const int rt = wave % 4, ctl = wave / 4, ct = cb / 16 + ctl;
+    const int p = rt + 4 * ct;
+    const int c = 16 * ct + lr;
+    const int pi = wave < NIH ? p : 0;
+    const f32x4 rdQ = *(const f32x4*)(DQG + ((size_t)pi * 64 + plane) * 4);
+    const f32x4 rdK = *(const f32x4*)(DKD + ((size_t)pi * 64 + plane) * 4);
+    const f32x4 rdB = *(const f32x4*)(DKB + ((size_t)pi * 64 + plane) * 4);
     if (!unsafe) {
       // operand group: row t, 4 consecutive columns
       const int t = ptid / (HALF / 4), c4 = (ptid % (HALF / 4)) * 4;
       if (t < 64) {
-        const int c = cb + c4, bf = t & ~15, bl = bf + 15;
-        const float4 g = *(const float4*)(sG + t * GP + c);
-        const float4 gf = *(const float4*)(sG + bf * GP + c);
-        const float4 gl = *(const float4*)(sG + bl * GP + c);
-        const bf16x4 qq = *(const bf16x4*)(sQ + t * QP + c), kk = *(const bf16x4*)(sK + t * QP + c);
+        const int cc = cb + c4, bf = t & ~15, bl = bf + 15;
+        const float4 g = *(const float4*)(sG + t * GP + cc);
+        const float4 gf = *(const float4*)(sG + bf * GP + cc);
+        const float4 gl = *(const float4*)(sG + bl * GP + cc);
+        const bf16x4 qq = *(const bf16x4*)(sQ + t * QP + cc), kk = *(const bf16x4*)(sK + t * QP + cc);
         const float rq = sRq[t], rk = sRk[t];
         const float gt[4] = {g.x, g.y, g.z, g.w}, gft[4] = {gf.x, gf.y, gf.z, gf.w}, glt[4] = {gl.x, gl.y, gl.z, gl.w};
         bf16x4 krh, krl, qch, qcl, kch, kcl;
@@ -821,16 +830,9 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
     }
     __syncthreads();
     if (wave < NIH) {
-      const int rt = wave % 4, ctl = wave / 4, ct = cb / 16 + ctl;
-      const int p = rt + 4 * ct;
-      const int c = 16 * ct + lr;
-      // the raw dQg/dKd/dKb items are not needed before the per-element terms: their loads
-      // overlap the MFMA work below
-      const f32x4 rdQ = *(const f32x4*)(DQG + ((size_t)p * 64 + plane) * 4);
-      const f32x4 rdK = *(const f32x4*)(DKD + ((size_t)p * 64 + plane) * 4);
-      const f32x4 rdB = *(const f32x4*)(DKB + ((size_t)p * 64 + plane) * 4);
       f32x4 rq = zero4(), rk = zero4(), cq = zero4(), ck = zero4();
       if (!unsafe) {
+        const float gf_rt = sG[(16 * rt) * GP + c], gl_rt = sG[(16 * rt + 15) * GP + c];
         // row side: blocks b <= rt, A = dA / dM' rows of tile rt, B = KR rows of block b
         for (int b = 0; b <= rt; ++b) {
           const bf16x4 fa = *(const bf16x4*)(sDA + (16 * rt + lr) * AP + 16 * b + 4 * kg);
@@ -839,13 +841,20 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
           const bf16x4 bl = lds_col_frag4(sKRl, OP, 16 * b, 16 * ctl, plane);
           const f32x4 pq = mfma16k16(fa, bl, mfma16k16(fa, bh, zero4()));
           const f32x4 pk = mfma16k16(fm, bl, mfma16k16(fm, bh, zero4()));
-          const float gref = sG[(16 * b) * GP + c];
+          // e^{G_i - G_f(b)} = e^{G_i - G_f(rt)} e^{G_f(rt) - G_f(b)}: the block factor is
+          // one per lane (<= 1), the row factor is applied once after the block sum
+          const float f = __expf(gf_rt - sG[(16 * b) * GP + c]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float f = __expf(sG[(16 * rt + 4 * kg + r) * GP + c] - gref);
             rq[r] = fmaf(pq[r], f, rq[r]);
             rk[r] = fmaf(pk[r], f, rk[r]);
           }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float f = __expf(sG[(16 * rt + 4 * kg + r) * GP + c] - gf_rt);
+          rq[r] *= f;
+          rk[r] *= f;
         }
         // column side: blocks b >= rt, A = dA^T / dM'^T (columns of tile rt), B = QC / KC
         for (int b = rt; b < 4; ++b) {
@@ -857,13 +866,19 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
           const bf16x4 kl = lds_col_frag4(sKCl, OP, 16 * b, 16 * ctl, plane);
           const f32x4 pq = mfma16k16(fa, ql, mfma16k16(fa, qh, zero4()));
           const f32x4 pk = mfma16k16(fm, kl, mfma16k16(fm, kh, zero4()));
-          const float gref = sG[(16 * b + 15) * GP + c];
+          // e^{G_l(b) - G_j} = e^{G_l(b) - G_l(rt)} e^{G_l(rt) - G_j}, both <= 1
+          const float f = __expf(sG[(16 * b + 15) * GP + c] - gl_rt);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float f = __expf(gref - sG[(16 * rt + 4 * kg + r) * GP + c]);
             cq[r] = fmaf(pq[r], f, cq[r]);
             ck[r] = fmaf(pk[r], f, ck[r]);
           }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float f = __expf(gl_rt - sG[(16 * rt + 4 * kg + r) * GP + c]);
+          cq[r] *= f;
+          ck[r] *= f;
         }
       } else {
         // a block whose decay spans more than 80 nats: exact per-pair factors (f32 dA, dM'
@@ -899,7 +914,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
         const float qh = to_f32(sQ[ii * QP + c]) * sRq[ii], kh = to_f32(sK[ii * QP + c]) * sRk[ii];
         const float G = sG[ii * GP + c];
         const float bt = sBeta[ii];
-        const float eG = expf(G), eKd = expf(GL - G);
+        const float eG = __expf(G), eKd = __expf(GL - G);
         const float dQg = rdQ[rr], dKd = rdK[rr], dKb = rdB[rr];
         const float cc = cq[rr] + ck[rr];
         const float dqh = fmaf(dQg, eG, rq[rr]);
