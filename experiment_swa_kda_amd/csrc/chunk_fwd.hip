@@ -50,6 +50,12 @@ struct FwdArgs {
   bf16* out;
   float* sfin;
   Regions ws;
+  // optional output RMSNorm * weight * sigmoid(gate) epilogue (all null / unused if ng_out is null)
+  const bf16* ng_gate;
+  const float* ng_weight;
+  float ng_eps;
+  bf16* ng_out;
+  float* ng_inv_rms;
 };
 
 // ---------------------------------------------------------------------------
@@ -851,7 +857,9 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   for (int s = 0; s < K / 32; ++s) fq[s] = *(const bf16x8*)(QGF + frag_off(K, wave, s, lane));
 #pragma unroll
   for (int s = 0; s < 2; ++s) fa[s] = *(const bf16x8*)(AF + frag_off(64, wave, s, lane));
-#pragma unroll 2
+  // o of this lane's 4 rows x V/16 columns, kept for the optional norm epilogue
+  float ov[V / 16][4];
+#pragma unroll
   for (int ct = 0; ct < V / 16; ++ct) {
     const int vcol = 16 * ct + lr;
     const bf16* sb = SHBF + (size_t)ct * 16 * K;
@@ -867,8 +875,39 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * kg + r;
-      if (t < len) a.out[((size_t)(ch.x + t) * H + h) * V + vcol] = to_bf16(o0[r] + o1[r]);
+      const bf16 ob = to_bf16(o0[r] + o1[r]);
+      ov[ct][r] = to_f32(ob);
+      if (t < len) a.out[((size_t)(ch.x + t) * H + h) * V + vcol] = ob;
     }
+  }
+  if (a.ng_out == nullptr) return;
+  // fused RMSNorm * weight * sigmoid(gate) over each token's V values of this head, from the
+  // bf16-rounded o exactly as the standalone norm kernel reads it: a row's V values live in
+  // the 16 lanes of one lane group (V/16 columns each)
+  float gv[V / 16][4], w[V / 16];
+#pragma unroll
+  for (int ct = 0; ct < V / 16; ++ct) {
+    w[ct] = a.ng_weight[16 * ct + lr];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = min(16 * wave + 4 * kg + r, len - 1);
+      gv[ct][r] = to_f32(a.ng_gate[((size_t)(ch.x + t) * H + h) * V + 16 * ct + lr]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float ss = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < V / 16; ++ct) ss = fmaf(ov[ct][r], ov[ct][r], ss);
+    ss = group_sum<16>(ss);
+    const float inv = rsqrtf(ss / V + a.ng_eps);
+    const int t = 16 * wave + 4 * kg + r;
+    if (t >= len) continue;
+    const size_t row = (size_t)(ch.x + t) * H + h;
+#pragma unroll
+    for (int ct = 0; ct < V / 16; ++ct)
+      a.ng_out[row * V + 16 * ct + lr] = to_bf16(ov[ct][r] * inv * w[ct] * sigmoid_fast(gv[ct][r]));
+    if (lr == 0) a.ng_inv_rms[row] = inv;
   }
 }
 
@@ -970,7 +1009,10 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
                                  const void* v, const void* gate, const void* beta_logits,
                                  const float* A_log, const float* dt_bias,
                                  const float* initial_state, void* output, float* final_state,
-                                 void* workspace, hipStream_t stream) {
+                                 void* workspace, hipStream_t stream,
+                                 const void* norm_gate = nullptr, const float* norm_weight = nullptr,
+                                 float norm_eps = 0.f, void* norm_output = nullptr,
+                                 float* norm_inv_rms = nullptr) {
   using namespace kda;
   int rc = validate_problem(p, "chunk_forward");
   if (rc != KDA_OK) return rc;
@@ -1001,6 +1043,11 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   a.out = (bf16*)output;
   a.sfin = final_state;
   a.ws = ws_regions(g, workspace);
+  a.ng_gate = (const bf16*)norm_gate;
+  a.ng_weight = norm_weight;
+  a.ng_eps = norm_eps;
+  a.ng_out = (bf16*)norm_output;
+  a.ng_inv_rms = norm_inv_rms;
   // fixed-length problems with at least one chunk get their tables from the intra kernel
   a.fixed_T = (p->cu_seqlens == nullptr && g.max_chunks > 0) ? p->seq_len : 0;
   if ((stages & (1 << KDA_STAGE_PREP)) && a.fixed_T == 0) {
@@ -1020,6 +1067,27 @@ extern "C" int kda_chunk_forward(const kda_chunk_problem* p, const void* q, cons
                                  void* workspace, hipStream_t stream) {
   return chunk_forward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
                             output, final_state, workspace, stream);
+}
+
+extern "C" int kda_chunk_forward_norm_gate(const kda_chunk_problem* p, const void* q, const void* k,
+                                           const void* v, const void* gate, const void* beta_logits,
+                                           const float* A_log, const float* dt_bias,
+                                           const float* initial_state, void* output,
+                                           float* final_state, void* workspace,
+                                           const void* norm_gate, const float* norm_weight,
+                                           float epsilon, void* norm_output, float* inverse_rms,
+                                           hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(p != nullptr, "chunk_forward_norm_gate: null problem");
+  const bool empty = (size_t)p->batch * p->seq_len == 0;
+  KDA_REQUIRE(p->value_dim == 64 || p->value_dim == 128,
+              "chunk_forward_norm_gate: value_dim must be 64 or 128");
+  KDA_REQUIRE(empty || (norm_gate && norm_weight && norm_output && inverse_rms),
+              "chunk_forward_norm_gate: null norm pointer");
+  KDA_REQUIRE(epsilon >= 0.f, "chunk_forward_norm_gate: epsilon must be non-negative");
+  return chunk_forward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
+                            output, final_state, workspace, stream, norm_gate, norm_weight, epsilon,
+                            norm_output, inverse_rms);
 }
 
 extern "C" int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,

@@ -145,6 +145,7 @@ def _record_backward(output: torch.Tensor, component: str) -> torch.Tensor:
 _COMPONENTS = {
     "chunk_forward": ("kda_chunk_forward", "chunk_fwd.hip"),
     "chunk_backward": ("kda_chunk_backward", "chunk_bwd.hip"),
+    "chunk_forward_norm_gate": ("kda_chunk_forward_norm_gate", "chunk_fwd.hip"),
     "recurrent_decode": ("kda_recurrent_decode", "decode.hip"),
     "causal_convolution_forward": ("kda_causal_conv_forward", "conv.hip"),
     "causal_convolution_backward": ("kda_causal_conv_backward", "conv.hip"),
@@ -334,6 +335,61 @@ class _ProjectRMSNormGateAutograd(torch.autograd.Function):
         dx, dgate, dweight = ops.rmsnorm_gate_backward(x, gate, weight, inverse_rms,
                                                        grad_output, ctx.epsilon)
         return dx, dgate, dweight, None
+
+
+class _ProjectKDANormGateAutograd(torch.autograd.Function):
+    """Chunked KDA with the output RMSNorm * sigmoid(gate) fused into its last kernel
+    (producer/consumer fusion of reference kda.py:761-770).  The forward keeps o and the
+    inverse RMS; the backward runs the norm VJP and then the chunk VJP on its dx."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, raw_gate, beta_logits, A_log, dt_bias, output_gate, norm_weight,
+                epsilon, lower_bound, scale, gate="k3"):
+        o, normed, inverse_rms, _, workspace = ops.chunk_forward_norm_gate(
+            q, k, v, raw_gate, beta_logits, A_log, dt_bias, None, False, lower_bound, scale,
+            output_gate, norm_weight, epsilon, gate=gate)
+        ctx.epsilon, ctx.lower_bound, ctx.scale, ctx.gate = epsilon, lower_bound, scale, gate
+        ctx.save_for_backward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, output_gate,
+                              norm_weight, o, inverse_rms, workspace)
+        return normed
+
+    @staticmethod
+    def backward(ctx, grad_normed):
+        (q, k, v, raw_gate, beta_logits, A_log, dt_bias, output_gate, norm_weight, o,
+         inverse_rms, workspace) = ctx.saved_tensors
+        do, dgate_out, dweight = ops.rmsnorm_gate_backward(o, output_gate, norm_weight, inverse_rms,
+                                                           grad_normed, ctx.epsilon)
+        dq, dk, dv, draw_gate, dbeta, dA, ddt, _ = ops.chunk_backward(
+            q, k, v, raw_gate, beta_logits, A_log, dt_bias, None, workspace, do, None,
+            ctx.lower_bound, ctx.scale, gate=ctx.gate)
+        if ddt is not None:
+            ddt = ddt.reshape(dt_bias.shape)
+        return (dq, dk, dv, draw_gate, dbeta, dA, ddt, dgate_out, dweight, None, None, None, None)
+
+
+def kda_norm_gate(q, k, v, raw_gate, beta_logits, A_log, dt_bias, output_gate, norm_weight, *,
+                  eps=1e-5, lower_bound=-5.0, scale=None, gate="k3"):
+    """``rms_norm(kda(...), norm_weight, eps) * sigmoid(output_gate)`` for the chunked HIP
+    path with the norm fused into the chunk forward's output kernel (no initial or final
+    state, as in training).  Same validation and result as ``kda(mode="project_chunk")``
+    followed by ``RMSNormGated``."""
+    if gate not in ("k3", "precomputed"):
+        raise ValueError(f"unknown gate parameterisation: {gate}")
+    _validate_operator_inputs(q, k, v, raw_gate, beta_logits, None, None)
+    if gate == "k3":
+        _gate_shapes(raw_gate, A_log, dt_bias)
+    reason = _backend_reason(q, k, v, raw_gate, beta_logits, A_log, dt_bias, None,
+                             lower_bound=lower_bound, gate=gate)
+    if reason is None and v.shape[-1] not in (64, 128):
+        reason = "the fused norm needs head_dim 64 or 128"
+    if reason is not None:
+        raise RuntimeError(f"project CUDA KDA backend unavailable: {reason}")
+    resolved_scale = float(scale if scale is not None else q.shape[-1] ** -0.5)
+    out = _ProjectKDANormGateAutograd.apply(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
+                                            output_gate, norm_weight, float(eps),
+                                            float(lower_bound), resolved_scale, gate)
+    _record("chunk_forward_norm_gate")
+    return _record_backward(out, "chunk_backward")
 
 
 class _ProjectConvolutionAutograd(torch.autograd.Function):
@@ -588,10 +644,15 @@ class KimiDeltaAttention(nn.Module):
         qkv = _record_backward(qkv, "causal_convolution_backward")
         q, k, v = (t.view(batch, length, H, D) for t in _SplitColumns.apply(qkv, (C, C, C)))
         raw_gate = self.f_b_proj(fa).view(batch, length, H, D)
+        output_gate = gate_lin.view(batch, length, H, D)
+        if D in (64, 128) and self.o_norm.weight.dtype == torch.float32:
+            # the output norm fused into the chunk forward's last kernel
+            mixed = kda_norm_gate(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias, output_gate,
+                                  self.o_norm.weight, eps=self.o_norm.eps, lower_bound=self.lower_bound)
+            return self.o_proj(mixed.reshape(batch, length, C))
         mixed, _ = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias, initial_state=None,
                        output_final_state=False, mode=mode, lower_bound=self.lower_bound,
                        allow_fallback=allow_fallback)
-        output_gate = gate_lin.view(batch, length, H, D)
         if D in (64, 128) and self.o_norm.weight.dtype == torch.float32:
             mixed = _ProjectRMSNormGateAutograd.apply(mixed, output_gate, self.o_norm.weight, self.o_norm.eps)
             _record("rmsnorm_gate_forward")
@@ -601,6 +662,6 @@ class KimiDeltaAttention(nn.Module):
         return self.o_proj(mixed.reshape(batch, length, C))
 
 
-__all__ = ["KDAState", "KimiDeltaAttention", "k3_decay_gate", "kda", "prepare_kda_backend",
+__all__ = ["KDAState", "KimiDeltaAttention", "k3_decay_gate", "kda", "kda_norm_gate", "prepare_kda_backend",
            "ShortConvolution", "RMSNormGated", "Linear", "kda_backend_provenance",
            "project_runtime_events", "reset_project_runtime_events"]

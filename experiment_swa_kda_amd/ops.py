@@ -144,6 +144,45 @@ def chunk_forward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_sta
     return output, final_state, workspace
 
 
+def chunk_forward_norm_gate(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state,
+                            output_final_state, lower_bound, scale, norm_gate, norm_weight, eps, *,
+                            cu_seqlens=None, gate="k3"):
+    """Chunked forward with the output RMSNorm * weight * sigmoid(norm_gate) fused into its
+    last kernel.  Returns (output o, normed output, inverse_rms, final_state or None,
+    workspace): o and inverse_rms are what :func:`rmsnorm_gate_backward` needs."""
+    gm = GATE_MODES[gate]
+    dev = _check_chunk_inputs("chunk_forward_norm_gate", q, k, v, gate_values, beta_logits, A_log,
+                              dt_bias, initial_state, cu_seqlens, gm)
+    _check_dtype("chunk_forward_norm_gate", norm_gate, torch.bfloat16, "norm_gate")
+    _check_dtype("chunk_forward_norm_gate", norm_weight, torch.float32, "norm_weight")
+    if norm_gate.shape != v.shape or norm_weight.shape != (v.shape[-1],):
+        raise RuntimeError("chunk_forward_norm_gate: norm_gate must be shaped like v and norm_weight [V]")
+    q, k, v, gate_values, beta_logits = (_c(t) for t in (q, k, v, gate_values, beta_logits))
+    A_log, dt_bias, initial_state = _c(A_log), _c(dt_bias), _c(initial_state)
+    norm_gate, norm_weight = _c(norm_gate), _c(norm_weight)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    n = B if cu_seqlens is None else cu_seqlens.numel() - 1
+    p = _problem(q, v, cu_seqlens, gm, lower_bound, scale)
+    lib = _lib.load()
+    ws_bytes = lib.kda_chunk_workspace_bytes(ctypes.byref(p))
+    if ws_bytes == 0 and (B * T > 0 or n > 0):
+        check(1, "chunk_workspace_bytes")
+    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    output = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    normed = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    inv = torch.empty(B * T * H, dtype=torch.float32, device=dev)
+    final_state = torch.empty(n, H, V, K, dtype=torch.float32, device=dev) if output_final_state else None
+    with torch.cuda.device(dev):
+        rc = lib.kda_chunk_forward_norm_gate(
+            ctypes.byref(p), ptr(q), ptr(k), ptr(v), ptr(gate_values), ptr(beta_logits),
+            ptr(A_log), ptr(dt_bias), ptr(initial_state), ptr(output), ptr(final_state),
+            ptr(workspace), ptr(norm_gate), ptr(norm_weight), float(eps), ptr(normed), ptr(inv),
+            _stream(dev))
+    check(rc, "kda_chunk_forward_norm_gate")
+    return output, normed, inv, final_state, workspace
+
+
 def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace,
                    grad_output, grad_final_state, lower_bound, scale, *, cu_seqlens=None,
                    gate="k3"):

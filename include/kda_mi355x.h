@@ -81,6 +81,26 @@ int kda_chunk_forward(const kda_chunk_problem* p,
                       void* workspace, hipStream_t stream);
 
 /*
+ * kda_chunk_forward with the mixer's output RMSNorm * weight * sigmoid(gate) fused into the
+ * output kernel's epilogue (SURVEY-ranked producer/consumer fusion).  No single counterpart in
+ * the reference: it replaces the pair chunk_forward (chunk.cu:1380-1757) followed by
+ * torch.ops.nanochat_kda.rmsnorm_gate_forward (rmsnorm_gate.cu:31-71) on its output, as
+ * composed in kda.py:761-770.  All arguments of kda_chunk_forward keep their meaning (output
+ * still receives o, which the norm backward reads), plus
+ *   norm_gate bf16 [B,T,H,V], norm_weight f32 [V], epsilon >= 0,
+ *   norm_output bf16 [B,T,H,V] = rms_norm(bf16(o), weight, eps) * sigmoid(norm_gate),
+ *   inverse_rms f32 [B*T*H] (what kda_rmsnorm_gate_backward takes).
+ * value_dim must be 64 or 128.
+ */
+int kda_chunk_forward_norm_gate(const kda_chunk_problem* p,
+                                const void* q, const void* k, const void* v, const void* gate,
+                                const void* beta_logits, const float* A_log, const float* dt_bias,
+                                const float* initial_state, void* output, float* final_state,
+                                void* workspace, const void* norm_gate, const float* norm_weight,
+                                float epsilon, void* norm_output, float* inverse_rms,
+                                hipStream_t stream);
+
+/*
  * Exact chunked backward.  Replaces torch.ops.nanochat_kda.chunk_backward
  * (nanochat/mixers/cuda_kda/chunk.cu:1758-2113, schema chunk.cu:2122-2129).
  *   workspace: as filled by kda_chunk_forward on the same inputs

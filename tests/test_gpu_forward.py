@@ -162,3 +162,59 @@ def test_unaligned_views_are_copied_before_the_kernels():
     y, _ = ops.causal_conv_forward(x, w, None, False)
     y2, _ = ops.causal_conv_forward(x.clone(), w, None, False)
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("gate,K,V,T", [("k3", 128, 128, 200), ("precomputed", 64, 64, 130),
+                                         ("k3", 128, 64, 65), ("k3", 64, 128, 1)])
+def test_chunk_forward_norm_gate_fused_matches_separate(gate, K, V, T):
+    """The fused epilogue equals the separate norm kernel on the same o (up to the order of
+    the f32 row sum), o is unchanged, and the norm output matches the oracle chain."""
+    d = make_kda_inputs(2, T, 3, K, V, seed=T + K, gate=gate, state=False)
+    g = torch.Generator().manual_seed(T)
+    og = torch.randn(2, T, 3, V, generator=g).bfloat16().cuda()
+    w = (1 + 0.3 * torch.randn(V, generator=g)).float().cuda()
+    scale = K ** -0.5
+    o, normed, inv, fin, _ = ops.chunk_forward_norm_gate(
+        d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None, True, -5.0,
+        scale, og, w, 1e-5, gate=gate)
+    o_ref, fin_ref, _ = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"],
+                                          d["dt_bias"], None, True, -5.0, scale, gate=gate)
+    assert torch.equal(o, o_ref) and torch.equal(fin, fin_ref)
+    y_ref, inv_ref = ops.rmsnorm_gate_forward(o_ref, og, w, 1e-5)
+    torch.testing.assert_close(inv, inv_ref, rtol=1e-6, atol=0)
+    # one bf16 ulp where the f32 row sums round differently
+    torch.testing.assert_close(normed.float(), y_ref.float(), rtol=8e-3, atol=1e-6)
+    eo, _ = oracle_fwd(d, gate)
+    ey, _ = O.rmsnorm_gate_forward(eo, np64(og), np64(w), 1e-5)
+    assert rel_err(normed, ey) < 2e-2
+
+
+def test_chunk_forward_norm_gate_autograd_matches_unfused():
+    from experiment_swa_kda_amd.kda import _ProjectRMSNormGateAutograd, kda, kda_norm_gate
+    d = make_kda_inputs(1, 150, 2, 128, 128, seed=5, state=False)
+    g = torch.Generator().manual_seed(5)
+    og = torch.randn(1, 150, 2, 128, generator=g).bfloat16().cuda()
+    dy = torch.randn(1, 150, 2, 128, generator=g).bfloat16().cuda()
+    names = ["q", "k", "v", "g", "beta"]
+
+    def run(fused):
+        leaves = {n: d[n].detach().clone().requires_grad_() for n in names}
+        A = d["A_log"].detach().clone().requires_grad_()
+        dt = d["dt_bias"].detach().clone().requires_grad_()
+        gt = og.clone().requires_grad_()
+        w = (1 + 0.3 * torch.randn(128, generator=torch.Generator().manual_seed(6))).cuda().requires_grad_()
+        if fused:
+            y = kda_norm_gate(leaves["q"], leaves["k"], leaves["v"], leaves["g"], leaves["beta"], A, dt,
+                              gt, w, eps=1e-5)
+        else:
+            o, _ = kda(leaves["q"], leaves["k"], leaves["v"], leaves["g"], leaves["beta"], A, dt,
+                       mode="project_chunk")
+            y = _ProjectRMSNormGateAutograd.apply(o, gt, w, 1e-5)
+        y.backward(dy)
+        return [y] + [leaves[n].grad for n in names] + [A.grad, dt.grad, gt.grad, w.grad]
+
+    a, b = run(True), run(False)
+    for x, e in zip(a, b):
+        assert x is not None and e is not None
+        cos = torch.nn.functional.cosine_similarity(x.double().flatten(), e.double().flatten(), dim=0)
+        assert cos > 0.9999, float(cos)
