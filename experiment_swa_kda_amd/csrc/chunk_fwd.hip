@@ -840,6 +840,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a)
 // walks the V/16 column tiles, so its Qg and A operands are loaded once.
 template <int K, int V>
 __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
+  constexpr int OP = V + 8;  // bf16 row stride of a wave's 16-row staging tile
+  __shared__ __attribute__((aligned(16))) bf16 sOut[4][16 * OP];
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
   const int len = ch.y;
   if (len <= 0) return;
@@ -874,12 +876,23 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
     o1 = mfma16(fa[1], *(const bf16x8*)(db + (size_t)(64 + lane) * 8), o1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = 16 * wave + 4 * kg + r;
       const bf16 ob = to_bf16(o0[r] + o1[r]);
       ov[ct][r] = to_f32(ob);
-      if (t < len) a.out[((size_t)(ch.x + t) * H + h) * V + vcol] = ob;
+      sOut[wave][(4 * kg + r) * OP + vcol] = ob;
     }
   }
+  // the wave's 16 x V tile leaves through LDS as 16-byte row pieces
+  bf16* so = sOut[wave];
+  auto store_tile = [&](bf16* dst) {
+#pragma unroll
+    for (int it = 0; it < 16 * V / 8 / kWave; ++it) {
+      const int idx = it * kWave + lane, rr = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
+      const int t = 16 * wave + rr;
+      if (t < len) *(bf16x8*)(dst + ((size_t)(ch.x + t) * H + h) * V + c8) = *(const bf16x8*)(so + rr * OP + c8);
+    }
+  };
+  __builtin_amdgcn_wave_barrier();
+  store_tile(a.out);
   if (a.ng_out == nullptr) return;
   // fused RMSNorm * weight * sigmoid(gate) over each token's V values of this head, from the
   // bf16-rounded o exactly as the standalone norm kernel reads it: a row's V values live in
@@ -902,13 +915,13 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
     ss = group_sum<16>(ss);
     const float inv = rsqrtf(ss / V + a.ng_eps);
     const int t = 16 * wave + 4 * kg + r;
-    if (t >= len) continue;
-    const size_t row = (size_t)(ch.x + t) * H + h;
 #pragma unroll
     for (int ct = 0; ct < V / 16; ++ct)
-      a.ng_out[row * V + 16 * ct + lr] = to_bf16(ov[ct][r] * inv * w[ct] * sigmoid_fast(gv[ct][r]));
-    if (lr == 0) a.ng_inv_rms[row] = inv;
+      so[(4 * kg + r) * OP + 16 * ct + lr] = to_bf16(ov[ct][r] * inv * w[ct] * sigmoid_fast(gv[ct][r]));
+    if (lr == 0 && t < len) a.ng_inv_rms[(size_t)(ch.x + t) * H + h] = inv;
   }
+  __builtin_amdgcn_wave_barrier();
+  store_tile(a.ng_out);
 }
 
 // ---------------------------------------------------------------------------
