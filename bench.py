@@ -35,7 +35,8 @@ KERNEL_FLOP_PER_TILE = {
     "bwd_dense": 3 * 2_097_152 + 5 * 1_048_576 + 4 * 262_144,  # dQg dKd dW; dA dT(2) dVb dKb; Y dM
     "bwd_decay": 4 * 1_048_576,                        # row/column terms of A and M'
 }
-STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12}
+STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12,
+          "bwd_dense_decay": 14}
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 
@@ -381,7 +382,7 @@ def main():
     ms, ms_fwd, t, do = results["precomputed"]
     kt = kernel_times(torch, t, do, "precomputed")
     traffic = load_traffic()
-    dom = max(kt, key=kt.get)
+    dom = max((n for n in kt if n in KERNEL_FLOP_PER_TILE), key=kt.get)
     achieved = tiles * KERNEL_FLOP_PER_TILE[dom] / (kt[dom] * 1e-3) / 1e12
     line = {
         "metric": "KDA fwd+bwd TFLOP/s (B2 T4096 H3 D128 bf16)",

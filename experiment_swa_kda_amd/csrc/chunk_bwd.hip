@@ -281,7 +281,7 @@ struct DenseSmem {
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs a) {
+__device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx) {
   using L = DenseSmem<K, V>;
   constexpr int MP = L::TP, KP = L::KP, VP = L::VP;
   constexpr int kVjpThreads = kDenseThreads, kVjpWaves = kDenseWaves;
@@ -300,11 +300,11 @@ __global__ __launch_bounds__(kDenseThreads) void chunk_bwd_dense_kernel(BwdArgs 
   bf16* sV = (bf16*)(smem + L::off_v);
   bf16* sKB = (bf16*)(smem + L::off_kb);
 
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
   const int len = ch.y;
   if (len <= 0) return;
-  const int H = a.H, h = blockIdx.y;
-  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int H = a.H, h = hidx;
+  const size_t tile = (size_t)cidx * H + h;
   const int row0 = ch.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
@@ -660,7 +660,7 @@ struct DecaySmem {
 // per-element term stays in registers.  The key columns go in two passes of K/2 (the
 // operands of one pass fit in LDS beside q, k and G).
 template <int K>
-__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a) {
+__device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx) {
   using L = DecaySmem<K>;
   constexpr int QP = L::QP, GP = L::GP, AP = L::AP, HALF = L::HALF, OP = L::OP, NSEG = L::NSEG;
   constexpr int NKT = 4 * (K / 16);
@@ -690,11 +690,11 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
   float* sFk = sBeta + 256;
   int* sF = (int*)(smem + L::off_f);
 
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
   const int len = ch.y;
   if (len <= 0) return;
-  const int H = a.H, h = blockIdx.y;
-  const size_t tile = (size_t)blockIdx.x * H + h;
+  const int H = a.H, h = hidx;
+  const size_t tile = (size_t)cidx * H + h;
   const int row0 = ch.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
@@ -1063,6 +1063,28 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_decay_kernel(BwdArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// dense and decay tiles in one launch
+// ---------------------------------------------------------------------------
+// Workgroup i < dense_count runs the dense VJP of tile dense_begin + i; the others run the
+// decay VJP of tile decay_begin + (i - dense_count).  The backward cuts the sequence "all
+// dense tiles, then all decay tiles" into launches of one workgroup per CU, so a launch that
+// finishes the dense tiles also starts the decay tiles whose dense tiles an earlier launch
+// completed: no round runs half empty, and no workgroup waits on another.
+static_assert(kDenseThreads == kVjpThreads, "dense and decay tiles share the block size");
+template <int K, int V>
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, int dense_begin, int dense_count,
+                                                                    int decay_begin) {
+  const int item = blockIdx.x;
+  if (item < dense_count) {
+    const int t = dense_begin + item;
+    dense_tile<K, V>(a, t / a.H, t % a.H);
+  } else {
+    const int t = decay_begin + item - dense_count;
+    decay_tile<K>(a, t / a.H, t % a.H);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // gate parameter reduction (fixed order)
 // ---------------------------------------------------------------------------
 constexpr int kParamThreads = 1024;
@@ -1103,6 +1125,19 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
   if (threadIdx.x == 0) a.dA_log[h] = s1[0][0];
 }
 
+// Compute units of the current device (the launch granularity of the dense/decay rounds);
+// 0 if it cannot be queried.
+static int device_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int K, int V>
 static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdArgs& a,
                            hipStream_t stream, int stages) {
@@ -1114,27 +1149,40 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     KDA_LAUNCH_CHECK("chunk_backward scan");
   }
   if (g.max_chunks > 0) {
-    constexpr size_t smem_d = DenseSmem<K, V>::bytes;
-    constexpr size_t smem_e = DecaySmem<K>::bytes;
+    constexpr size_t smem = DenseSmem<K, V>::bytes > DecaySmem<K>::bytes ? DenseSmem<K, V>::bytes
+                                                                          : DecaySmem<K>::bytes;
+    auto vjp = chunk_bwd_vjp_kernel<K, V>;
     static bool attr = false;
     if (!attr) {
-      hipError_t e1 = hipFuncSetAttribute((const void*)chunk_bwd_dense_kernel<K, V>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_d);
-      hipError_t e2 = hipFuncSetAttribute((const void*)chunk_bwd_decay_kernel<K>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_e);
-      if (e1 != hipSuccess || e2 != hipSuccess)
+      if (hipFuncSetAttribute((const void*)vjp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
         return set_error(KDA_ERR_LAUNCH, "chunk_backward: LDS attribute failed");
       attr = true;
     }
-    if (stages & (1 << (KDA_STAGE_BWD_DENSE - 10))) {
-      auto dense = chunk_bwd_dense_kernel<K, V>;
-      hipLaunchKernelGGL(dense, dim3(g.max_chunks, p->heads), dim3(kDenseThreads), smem_d, stream, a);
-      KDA_LAUNCH_CHECK("chunk_backward dense");
-    }
-    if (stages & (1 << (KDA_STAGE_BWD_DECAY - 10))) {
-      auto decay = chunk_bwd_decay_kernel<K>;
-      hipLaunchKernelGGL(decay, dim3(g.max_chunks, p->heads), dim3(kVjpThreads), smem_e, stream, a);
-      KDA_LAUNCH_CHECK("chunk_backward decay");
+    const bool dense = stages & (1 << (KDA_STAGE_BWD_DENSE - 10));
+    const bool decay = stages & (1 << (KDA_STAGE_BWD_DECAY - 10));
+    const int N = g.max_chunks * p->heads;
+    const int R = device_cu_count();
+    auto launch = [&](int dense_begin, int dense_count, int decay_begin, int items) {
+      hipLaunchKernelGGL(vjp, dim3(items), dim3(kVjpThreads), smem, stream, a, dense_begin, dense_count, decay_begin);
+    };
+    if (dense && decay && R > 0 && N >= R) {
+      // items 0..N-1 dense, N..2N-1 decay, in launches of R: decay tile j (item N + j) is
+      // always in a later launch than dense tile j (item j) because N >= R
+      for (int start = 0; start < 2 * N; start += R) {
+        const int end = start + R < 2 * N ? start + R : 2 * N;
+        const int dcount = start < N ? (end < N ? end : N) - start : 0;
+        launch(start < N ? start : 0, dcount, (start > N ? start : N) - N, end - start);
+        KDA_LAUNCH_CHECK("chunk_backward dense/decay");
+      }
+    } else {
+      if (dense) {
+        launch(0, N, 0, N);
+        KDA_LAUNCH_CHECK("chunk_backward dense");
+      }
+      if (decay) {
+        launch(0, 0, 0, N);
+        KDA_LAUNCH_CHECK("chunk_backward decay");
+      }
     }
   }
   if (p->gate_mode == KDA_GATE_K3 && (stages & (1 << (KDA_STAGE_BWD_PARAMS - 10)))) {
@@ -1225,9 +1273,11 @@ extern "C" int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* 
                                         void* dv, void* dgate, void* dbeta_logits,
                                         float* dA_log, float* ddt_bias, float* dinitial_state,
                                         void* scratch, hipStream_t stream) {
-  if (stage < KDA_STAGE_BWD_SCAN || stage > KDA_STAGE_BWD_PARAMS)
+  if ((stage < KDA_STAGE_BWD_SCAN || stage > KDA_STAGE_BWD_PARAMS) && stage != KDA_STAGE_BWD_VJP)
     return kda::set_error(KDA_ERR_INVALID, "chunk_backward_stage: unknown stage %d", stage);
-  return chunk_backward_impl(1 << (stage - 10), p, q, k, v, gate, beta_logits, A_log, dt_bias,
+  const int mask = stage == KDA_STAGE_BWD_VJP ? (1 << (KDA_STAGE_BWD_DENSE - 10)) | (1 << (KDA_STAGE_BWD_DECAY - 10))
+                                              : 1 << (stage - 10);
+  return chunk_backward_impl(mask, p, q, k, v, gate, beta_logits, A_log, dt_bias,
                              initial_state, workspace, grad_output, grad_final_state, dq, dk, dv,
                              dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch,
                              stream);

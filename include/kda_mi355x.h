@@ -138,6 +138,7 @@ int kda_chunk_backward(const kda_chunk_problem* p,
 #define KDA_STAGE_BWD_DENSE 11
 #define KDA_STAGE_BWD_DECAY 12
 #define KDA_STAGE_BWD_PARAMS 13
+#define KDA_STAGE_BWD_VJP 14 /* dense and decay tiles together, as the full backward launches them */
 int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,
                             const void* k, const void* v, const void* gate,
                             const void* beta_logits, const float* A_log, const float* dt_bias,
