@@ -60,33 +60,47 @@ struct BwdArgs {
 // ---------------------------------------------------------------------------
 // reverse state-gradient scan
 // ---------------------------------------------------------------------------
-// Same structure as the forward scan, walking the chunks backwards: all global operands
-// of a chunk sit in a register ring kBwdRing chunks ahead, the dO strip is
-// double-buffered in LDS, and each per-step global access is one vector instruction.
+// One workgroup per (sequence, head, 16-wide V strip) walks the chunks backwards: four
+// compute waves (wave w owns the dDelta row tile w and the dS tiles w K/64 .., as MFMA
+// accumulators) and two loader waves.  The loaders stream each chunk's A^T, Kd, Qg^T and W^T
+// fragments, lam and the dO strip into a kBwdRing-deep LDS ring with direct global->LDS
+// loads, so the compute waves' instruction streams hold no global loads (issuing ~70 KB of
+// loads per chunk from the compute waves themselves serialised with the chain).  Per chunk
+// the six waves meet at two barriers: S1 (dS' published, slot complete) and S2 (dDelta
+// published).  A slot's A^T, Kd, Qg^T and dO are last read before S2 and are refilled (for
+// the chunk two steps on) right after it; its W^T and lam are last read before the next S1
+// and are refilled after that.
 constexpr int kBwdRing = 2;
+constexpr int kBwdThreads = 6 * kWave;
 
-template <int K>
-struct BwdScanFrag {
-  bf16x8 at[2];            // A^T rows of this wave's dDelta tile
-  bf16x8 kd[K / 32];       // Kd rows of this wave's dDelta tile
-  bf16x8 qgt[K / 64][2];   // Qg^T rows of this wave's dS tiles
-  bf16x8 wt[K / 64][2];    // W^T rows of this wave's dS tiles
-  float4 lam[K / 64];
-  bf16x4 dout;             // this thread's 4 values of the dO strip
-  int dlen;                // chunk length (rows >= dlen of the strip are zero)
+template <int K, int V>
+struct BwdScanLds {
+  static constexpr int off_at = 0;                        // A^T fragments, 64 x 64 bf16
+  static constexpr int off_kd = off_at + 64 * 64 * 2;     // Kd fragments, 64 x K bf16
+  static constexpr int off_qgt = off_kd + 64 * K * 2;     // Qg^T fragments, K x 64 bf16
+  static constexpr int off_wt = off_qgt + K * 64 * 2;     // W^T fragments, K x 64 bf16
+  static constexpr int off_lam = off_wt + K * 64 * 2;     // lam, K f32
+  static constexpr int off_do = off_lam + K * 4;          // dO strip [64 t][16 v] bf16 (rows >= len undefined)
+  static constexpr int slot = off_do + 64 * 16 * 2;
+  static constexpr int n_load0 = (64 * 64 * 2 + 2 * 64 * K * 2) / 1024 + 2;  // A^T, Kd, Qg^T, dO
+  static constexpr int n_load1 = (K * 64 * 2) / 1024 + 1;                    // W^T, lam
+  static constexpr int SP = K + 8, DP = 64 + 8;
+  static constexpr int off_ds = kBwdRing * slot;           // dS' as [v][k] bf16
+  static constexpr int off_dsf = off_ds + 16 * SP * 2;     // f32 dS' in accumulator order [K/16][64][4]
+  static constexpr int off_dd = off_dsf + K * 16 * 4;      // dDelta strip as [v][t] bf16
+  static constexpr int bytes = off_dd + 16 * DP * 2;
+  static_assert(n_load0 < 64 && n_load1 < 64, "vmcnt range");
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a) {
+  using L = BwdScanLds<K, V>;
   constexpr int KT = K / 16 / 4;
-  constexpr int SP = K + 8;
-  constexpr int DP = 64 + 8;
-  constexpr int FP = 16 + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sDS[16 * SP];     // dS' as [v][k]
-  __shared__ __attribute__((aligned(16))) float sDSf[K * FP];    // f32 dS' as [k][v]
-  constexpr int OP = 16 + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sDO[2][64 * OP];  // dO strip as [t][v]
-  __shared__ __attribute__((aligned(16))) bf16 sDD[16 * DP];     // dDelta strip as [v][t]
+  constexpr int SP = L::SP, DP = L::DP, OP = 16;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* sDS = (bf16*)(smem + L::off_ds);
+  float* sDSf = (float*)(smem + L::off_dsf);
+  bf16* sDD = (bf16*)(smem + L::off_dd);
   const int H = a.H;
   int rec, strip;
   if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
@@ -95,8 +109,6 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
-  const int j = 16 * wave + lr;
-  const int dt = tid / 4, dvq = (tid % 4) * 4;  // dO staging: token, 4-wide v group
 
   // Chunks of one sequence are consecutive 64-token blocks: chunk ci starts at
   // seq_row0 + 64 ci, so no per-chunk table read sits in front of the dO load.
@@ -107,35 +119,81 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
     seq_row0 = c_first.x;
     seq_end = c_last.x + c_last.y;
   }
-  auto load = [&](int chunk, BwdScanFrag<K>& f) {
-    const int row0 = seq_row0 + (chunk - sq.x) * 64;
-    const int len = min(64, seq_end - row0);
-    const size_t tile = (size_t)chunk * H + h;
-    const bf16* ATF = (const bf16*)a.ws.p[R_ATF] + tile * 64 * 64;
-    const bf16* KDF = (const bf16*)a.ws.p[R_KDF] + tile * 64 * K;
-    const bf16* QGTF = (const bf16*)a.ws.p[R_QGTF] + tile * K * 64;
-    const bf16* WTF = (const bf16*)a.ws.p[R_WTF] + tile * K * 64;
-    const float* lam = (const float*)a.ws.p[R_LAM] + tile * K;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) f.at[s] = *(const bf16x8*)(ATF + frag_off(64, wave, s, lane));
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) f.kd[s] = *(const bf16x8*)(KDF + frag_off(K, wave, s, lane));
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      const int kb = 16 * (wave * KT + kt);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        f.qgt[kt][s] = *(const bf16x8*)(QGTF + frag_off(64, wave * KT + kt, s, lane));
-        f.wt[kt][s] = *(const bf16x8*)(WTF + frag_off(64, wave * KT + kt, s, lane));
-      }
-      f.lam[kt] = *(const float4*)(lam + kb + 4 * kg);
-    }
-    // rows past the chunk end read row 0 of the chunk and are zeroed when staged
-    const int tr = dt < len ? dt : 0;
-    f.dout = *(const bf16x4*)(a.dout + ((size_t)(row0 + tr) * H + h) * V + v0 + dvq);
-    f.dlen = len;
-  };
 
+  if (wave >= 4) {
+    // ---- loader waves: step r's slot holds chunk sq.x + n - 1 - r ----
+    const int lw = wave - 4;
+    auto issue = [&](int r) {
+      const int chunk = sq.x + max(n - 1 - r, 0);  // clamped: fixed load count
+      const size_t tile = (size_t)chunk * H + h;
+      char* slot = smem + (r % kBwdRing) * L::slot;
+      if (lw == 0) {
+        const char* at = (const char*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (64 * 64 * 2) / 1024; ++b) dma16(at + b * 1024, slot + L::off_at + b * 1024);
+        const char* kd = (const char*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (64 * K * 2) / 1024; ++b) dma16(kd + b * 1024, slot + L::off_kd + b * 1024);
+        const char* qg = (const char*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(qg + b * 1024, slot + L::off_qgt + b * 1024);
+        // dO strip: lane -> token (lane / 2 + 32 i), half lane % 2 of its 16 values; rows past
+        // the chunk end read row 0 of the chunk (masked by the compute waves)
+        const int row0 = seq_row0 + (chunk - sq.x) * 64;
+        const int len = min(64, seq_end - row0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int t = lane / 2 + 32 * i, tr = t < len ? t : 0;
+          dma16(a.dout + ((size_t)(row0 + tr) * H + h) * V + v0 + 8 * (lane % 2), slot + L::off_do + i * 1024);
+        }
+      } else {
+        const char* wt = (const char*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64) + lane * 16;
+#pragma unroll
+        for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(wt + b * 1024, slot + L::off_wt + b * 1024);
+        if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
+      }
+    };
+    if (lw == 0) {
+      issue(0);
+      issue(1);
+      for (int r = 0; r < n; ++r) {
+        wait_vmcnt<L::n_load0>();  // part of slot r complete (step r + 1's loads may be in flight)
+        ring_barrier();            // S1(r)
+        ring_barrier();            // S2(r): slot r's A^T, Kd, Qg^T, dO are consumed
+        issue(r + 2);
+      }
+    } else {
+      issue(0);
+      for (int r = 0; r < n; ++r) {
+        wait_vmcnt<0>();  // W^T, lam of slot r complete (and last step's history stores)
+        ring_barrier();   // S1(r): slot r - 1's W^T, lam are consumed
+        issue(r + 1);
+        // f32 dS' history [K][V] of this step: element (k, v) sits in accumulator order at
+        // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4; read before S2 (the compute
+        // waves republish after it), stored after
+        const size_t tile = (size_t)(sq.x + n - 1 - r) * H + h;
+        float4 hv[K / 16];
+#pragma unroll
+        for (int it = 0; it < K / 16; ++it) {
+          const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
+          const float* f = sDSf + ((kk / 16) * 64 + 16 * ((kk % 16) / 4) + c4) * 4 + kk % 4;
+          hv[it] = make_float4(f[0], f[4], f[8], f[12]);
+        }
+        wait_lgkm0();
+        ring_barrier();   // S2(r)
+        float* DSH = (float*)a.sc.p[S_DSH] + tile * K * V + v0;
+#pragma unroll
+        for (int it = 0; it < K / 16; ++it) {
+          const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
+          *(float4*)(DSH + (size_t)kk * V + c4) = hv[it];
+        }
+      }
+    }
+    wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
+    return;
+  }
+
+  // ---- compute waves ----
   f32x4 dS[KT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
@@ -147,56 +205,52 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
       dS[kt] = zero4();
     }
   }
-  BwdScanFrag<K> ring[kBwdRing];
-  if (n > 0) {
-#pragma unroll
-    for (int d = 0; d < kBwdRing; ++d) load(sq.x + max(n - 1 - d, 0), ring[d]);
-  }
-
-  // step r processes chunk index ci = n - 1 - r
-  auto step = [&](int r, BwdScanFrag<K>& f) {
+  for (int r = 0; r < n; ++r) {
     const int chunk = sq.x + n - 1 - r;
     const size_t tile = (size_t)chunk * H + h;
-    bf16* sO = sDO[r & 1];
-    // (1) publish dS' (bf16 [v][k] operand, f32 [k][v] staging) and the dO strip
+    const int len = min(64, seq_end - (seq_row0 + (chunk - sq.x) * 64));
+    const char* slot = smem + (r % kBwdRing) * L::slot;
+    const bf16* sO = (const bf16*)(slot + L::off_do);
+    // (1) publish dS' (bf16 [v][k] operand, f32 [k][v] staging)
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       bf16x4 x;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        x[q] = to_bf16(dS[kt][q]);
-        sDSf[(k0 + q) * FP + lr] = dS[kt][q];
-      }
+      for (int q = 0; q < 4; ++q) x[q] = to_bf16(dS[kt][q]);
       *(bf16x4*)(sDS + lr * SP + k0) = x;
+      *(f32x4*)(sDSf + ((wave * KT + kt) * 64 + lane) * 4) = dS[kt];
     }
-    *(bf16x4*)(sO + dt * OP + dvq) = dt < f.dlen ? f.dout : bf16x4{};
-    __syncthreads();
-    // (2) f32 dS' history [K][V] (fixed-count vector stores)
-    {
-      float* DSH = (float*)a.sc.p[S_DSH] + tile * K * V;
+    wait_lgkm0();
+    ring_barrier();  // S1(r)
+    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS', and the dDelta-independent part of
+    // (4), Qg^T dO, while the other waves finish theirs.  dO as B operand (tokens down the
+    // contraction): transposing reads of the [t][v] strip, tokens past the chunk end zeroed
+    bf16x8 oB0 = lds_col_frag(sO, OP, 0, 0, lane), oB1 = lds_col_frag(sO, OP, 32, 0, lane);
+    if (len < 64) {  // uniform: only a sequence's last chunk can be partial
 #pragma unroll
-      for (int it = 0; it < K / 64; ++it) {
-        const int idx = tid + 256 * it;
-        const int kk = idx / 4, q4 = (idx % 4) * 4;
-        *(float4*)(DSH + (size_t)kk * V + v0 + q4) = *(const float4*)(sDSf + kk * FP + q4);
+      for (int e = 0; e < 8; ++e) {
+        if (8 * kg + e >= len) oB0[e] = to_bf16(0.f);
+        if (32 + 8 * kg + e >= len) oB1[e] = to_bf16(0.f);
       }
     }
-    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS', and the dDelta-independent part of
-    // (4), Qg^T dO, while the other waves finish theirs
-    // dO as B operand (tokens down the contraction): transposing reads of the [t][v] strip
-    const bf16x8 oB0 = lds_col_frag(sO, OP, 0, 0, lane), oB1 = lds_col_frag(sO, OP, 32, 0, lane);
     f32x4 pq[KT];
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) pq[kt] = mfma16(f.qgt[kt][1], oB1, mfma16(f.qgt[kt][0], oB0, zero4()));
+    for (int kt = 0; kt < KT; ++kt) {
+      const bf16x8 q0 = *(const bf16x8*)(slot + L::off_qgt + frag_off(64, wave * KT + kt, 0, lane) * 2);
+      const bf16x8 q1 = *(const bf16x8*)(slot + L::off_qgt + frag_off(64, wave * KT + kt, 1, lane) * 2);
+      pq[kt] = mfma16(q1, oB1, mfma16(q0, oB0, zero4()));
+    }
     {
       f32x4 acc0 = zero4(), acc1 = zero4();
-      acc0 = mfma16(f.at[0], oB0, acc0);
-      acc1 = mfma16(f.at[1], oB1, acc1);
+      acc0 = mfma16(*(const bf16x8*)(slot + L::off_at + frag_off(64, wave, 0, lane) * 2), oB0, acc0);
+      acc1 = mfma16(*(const bf16x8*)(slot + L::off_at + frag_off(64, wave, 1, lane) * 2), oB1, acc1);
 #pragma unroll
       for (int s = 0; s < K / 32; s += 2) {
-        acc0 = mfma16(f.kd[s], *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg), acc0);
-        acc1 = mfma16(f.kd[s + 1], *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
+        acc0 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s, lane) * 2),
+                      *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg), acc0);
+        acc1 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s + 1, lane) * 2),
+                      *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
       }
       float* DDLT = (float*)a.sc.p[S_DDLT] + tile * V * 64;
       const f32x4 d = acc0 + acc1;
@@ -206,28 +260,23 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(BwdArgs a) {
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
       *(bf16x4*)(sDD + lr * DP + 16 * wave + 4 * kg) = x;
     }
-    __syncthreads();
+    wait_lgkm0();
+    ring_barrier();  // S2(r)
     // (4) dS = lam dS' + Qg^T dO - W^T dDelta
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       f32x4 pw = zero4();
 #pragma unroll
-      for (int s = 0; s < 2; ++s) pw = mfma16(f.wt[kt][s], *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
-      dS[kt][0] = fmaf(f.lam[kt].x, dS[kt][0], pq[kt][0] - pw[0]);
-      dS[kt][1] = fmaf(f.lam[kt].y, dS[kt][1], pq[kt][1] - pw[1]);
-      dS[kt][2] = fmaf(f.lam[kt].z, dS[kt][2], pq[kt][2] - pw[2]);
-      dS[kt][3] = fmaf(f.lam[kt].w, dS[kt][3], pq[kt][3] - pw[3]);
+      for (int s = 0; s < 2; ++s)
+        pw = mfma16(*(const bf16x8*)(slot + L::off_wt + frag_off(64, wave * KT + kt, s, lane) * 2),
+                    *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
+      const float4 lam = *(const float4*)(slot + L::off_lam + (16 * (wave * KT + kt) + 4 * kg) * 4);
+      dS[kt][0] = fmaf(lam.x, dS[kt][0], pq[kt][0] - pw[0]);
+      dS[kt][1] = fmaf(lam.y, dS[kt][1], pq[kt][1] - pw[1]);
+      dS[kt][2] = fmaf(lam.z, dS[kt][2], pq[kt][2] - pw[2]);
+      dS[kt][3] = fmaf(lam.w, dS[kt][3], pq[kt][3] - pw[3]);
     }
-  };
-
-  // unconditional ring loads (index clamped to the first chunk), see the forward scan
-  for (int r0 = 0; r0 < n; r0 += kBwdRing) {
-#pragma unroll
-    for (int d = 0; d < kBwdRing; ++d) {
-      const int r = r0 + d;
-      if (r < n) step(r, ring[d]);
-      load(sq.x + max(n - 1 - (r + kBwdRing), 0), ring[d]);
-    }
+    wait_lgkm0();  // the slot is released at the next S1
   }
   if (a.ds0) {
 #pragma unroll
@@ -1143,9 +1192,16 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
                            hipStream_t stream, int stages) {
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     auto scan = chunk_bwd_scan_kernel<K, V>;
+    constexpr size_t smem_s = BwdScanLds<K, V>::bytes;
+    static bool attr_s = false;
+    if (!attr_s) {
+      if (hipFuncSetAttribute((const void*)scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_s) != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_backward: scan LDS attribute failed");
+      attr_s = true;
+    }
     const int nrec = p->num_seqs * p->heads;
     const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
-    hipLaunchKernelGGL(scan, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(scan, dim3(grid), dim3(kBwdThreads), smem_s, stream, a);
     KDA_LAUNCH_CHECK("chunk_backward scan");
   }
   if (g.max_chunks > 0) {

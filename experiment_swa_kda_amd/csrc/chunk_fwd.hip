@@ -616,27 +616,6 @@ struct ScanLds {
   static constexpr int bytes = off_stage + 2 * stage;
 };
 
-// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane.
-__device__ __forceinline__ void dma16(const void* src, char* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt, lgkmcnt left open)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// Workgroup barrier that orders the surrounding memory accesses for the compiler only; the
-// hardware waits the ring protocol needs (vmcnt / lgkmcnt) are issued explicitly.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 __device__ __forceinline__ bf16x8 pack_tiles(const f32x4& lo, const f32x4& hi) {
   bf16x8 x;
 #pragma unroll
