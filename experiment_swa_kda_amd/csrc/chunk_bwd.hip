@@ -92,8 +92,40 @@ struct BwdScanLds {
   static_assert(n_load0 < 64 && n_load1 < 64, "vmcnt range");
 };
 
+// Memory regions the backward reads next (the scan's per-chunk operands, then the dense and
+// decay kernels' inputs).  Workgroups of the scan launch past the scan's own touch one word
+// of every 128-byte line of them while the scan runs on its few CUs, so the scan's
+// latency-bound loads and the next kernel's loads find their lines in the caches (the
+// forward wrote them long before the backward in training).  Loads only: the results are
+// folded into a value that is never stored.
+constexpr int kMaxPrefetch = 20;
+struct PrefetchList {
+  const char* p[kMaxPrefetch];
+  unsigned long long lines[kMaxPrefetch];
+  int n;
+};
+
+__device__ __forceinline__ void prefetch_lines(const PrefetchList& pf, int w, int nw, char* sink) {
+  const unsigned long long stride = (unsigned long long)nw * kBwdThreads;
+  unsigned acc = 0;
+  for (int r = 0; r < pf.n; ++r) {
+    const char* base = pf.p[r];
+    const unsigned long long n = pf.lines[r];
+    unsigned long long l = (unsigned long long)w * kBwdThreads + threadIdx.x;
+    for (; l + 7 * stride < n; l += 8 * stride) {
+      unsigned x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *(const unsigned*)(base + (l + u * stride) * 128);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= x[u];
+    }
+    for (; l < n; l += stride) acc ^= *(const unsigned*)(base + l * 128);
+  }
+  if (acc == 0x9e3779b9u) *(unsigned*)sink = acc;  // keeps the loads; the value is irrelevant
+}
+
 template <int K, int V>
-__global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, PrefetchList pf, int scan_blocks) {
   using L = BwdScanLds<K, V>;
   constexpr int KT = K / 16 / 4;
   constexpr int SP = L::SP, DP = L::DP, OP = 16;
@@ -101,6 +133,10 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a) 
   bf16* sDS = (bf16*)(smem + L::off_ds);
   float* sDSf = (float*)(smem + L::off_dsf);
   bf16* sDD = (bf16*)(smem + L::off_dd);
+  if ((int)blockIdx.x >= scan_blocks) {
+    prefetch_lines(pf, blockIdx.x - scan_blocks, gridDim.x - scan_blocks, smem);
+    return;
+  }
   const int H = a.H;
   int rec, strip;
   if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
@@ -1201,7 +1237,25 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     }
     const int nrec = p->num_seqs * p->heads;
     const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
-    hipLaunchKernelGGL(scan, dim3(grid), dim3(kBwdThreads), smem_s, stream, a);
+    PrefetchList pf = {};
+    const size_t rows = (size_t)p->batch * p->seq_len * p->heads;
+    auto add = [&](const void* ptr, size_t bytes) {
+      if (ptr && bytes >= 128 && pf.n < kMaxPrefetch) {
+        pf.p[pf.n] = (const char*)ptr;
+        pf.lines[pf.n++] = bytes / 128;
+      }
+    };
+    for (int r : {R_ATF, R_KDF, R_QGTF, R_WTF, R_LAM}) add(a.ws.p[r], ws_region_bytes(g, r));
+    add(a.dout, rows * V * 2);
+    if (stages & ((1 << (KDA_STAGE_BWD_DENSE - 10)) | (1 << (KDA_STAGE_BWD_DECAY - 10)))) {
+      for (int r : {R_T, R_SH, R_MP, R_G, R_DLF, R_RQ, R_RK, R_BETA}) add(a.ws.p[r], ws_region_bytes(g, r));
+      add(a.q, rows * K * 2);
+      add(a.k, rows * K * 2);
+      add(a.v, rows * V * 2);
+    }
+    const int cus = device_cu_count();
+    const int extra = cus > grid ? cus - grid : 0;
+    hipLaunchKernelGGL(scan, dim3(grid + extra), dim3(kBwdThreads), smem_s, stream, a, pf, grid);
     KDA_LAUNCH_CHECK("chunk_backward scan");
   }
   if (g.max_chunks > 0) {
