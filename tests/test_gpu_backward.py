@@ -143,3 +143,33 @@ def test_varlen_mixed_lengths():
     d["s0"] = torch.randn(len(lens), 2, 64, 64, generator=torch.Generator().manual_seed(3)).cuda() * 0.05
     do, dsT = cotangents(d, 11, n_states=len(lens))
     check(gpu_grads(d, "k3", do, dsT, cu), oracle_grads(d, "k3", do, dsT, cu))
+
+
+def test_dense_decay_rounds_equal_separate_stages():
+    """With at least one tile per CU the backward runs the dense and decay tiles as full
+    rounds of one kernel (the launch that finishes the dense tiles starts the first decay
+    tiles).  Its gradients must equal, bit for bit, the stage-by-stage run (scan, all dense
+    tiles, all decay tiles, parameter reduction) on the same workspace."""
+    import ctypes
+    from experiment_swa_kda_amd import _lib
+    from experiment_swa_kda_amd._lib import ptr
+    d = make_kda_inputs(2, 4096, 3, 128, 128, seed=21, dist="baseline")  # 384 tiles
+    do, _ = cotangents(d, 22)
+    K = 128
+    full = gpu_grads(d, "k3", do, None)
+    _, _, ws = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None,
+                                 False, -5.0, K ** -0.5, gate="k3")
+    p = ops._problem(d["q"], d["v"], None, ops.GATE_MODES["k3"], -5.0, K ** -0.5)
+    lib = _lib.load()
+    scratch = torch.empty(lib.kda_chunk_backward_scratch_bytes(ctypes.byref(p)), dtype=torch.uint8, device="cuda")
+    outs = [torch.empty_like(d[n]) for n in ("q", "k", "v", "g", "beta")]
+    dA, ddt = torch.empty_like(d["A_log"]), torch.empty_like(d["dt_bias"])
+    args = (ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(d["g"]), ptr(d["beta"]), ptr(d["A_log"]), ptr(d["dt_bias"]),
+            None, ptr(ws), ptr(do), None, *[ptr(x) for x in outs], ptr(dA), ptr(ddt), None, ptr(scratch),
+            torch.cuda.current_stream().cuda_stream)
+    for stage in (10, 11, 12, 13):
+        _lib.check(lib.kda_chunk_backward_stage(stage, ctypes.byref(p), *args), f"stage {stage}")
+    torch.cuda.synchronize()
+    staged = outs + [dA, ddt.reshape(full[6].shape)]
+    for a, b in zip(full[:7], staged):
+        assert torch.equal(a, b)
