@@ -1093,6 +1093,17 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
   float* sP0 = (float*)(smem + L::off_p0);
   float* sP1 = (float*)(smem + L::off_p1);
   const int c = tid % K, seg = tid / K;
+  const bool k3 = a.gate_mode == KDA_GATE_K3;
+  // K3: this thread's raw gate values, requested together before the segment sums (rows
+  // past the chunk end read the last row and are not used)
+  float graw[RPS];
+  if (k3) {
+#pragma unroll
+    for (int r = 0; r < RPS; ++r) {
+      const int t = min(seg * RPS + r, len - 1);
+      graw[r] = to_f32(((const bf16*)a.gate)[((size_t)(row0 + t) * H + h) * K + c]);
+    }
+  }
   {
     float sum = 0.f;
 #pragma unroll
@@ -1106,7 +1117,6 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
     for (int q = 0; q < 4; ++q) acc += sGL[q * K + c];
     for (int s = NSEG - 1; s > seg; --s) acc += sSeg[s * K + c];
     float p0 = 0.f, p1 = 0.f;
-    const bool k3 = a.gate_mode == KDA_GATE_K3;
     const float ea = k3 ? expf(a.A_log[h]) : 0.f;
     const float bias = k3 ? a.dt_bias[h * K + c] : 0.f;
 #pragma unroll
@@ -1116,8 +1126,8 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
       if (t < len) {
         const size_t off = ((size_t)(row0 + t) * H + h) * K + c;
         if (k3) {
-          const float pre = to_f32(((const bf16*)a.gate)[off]) + bias;
-          const float s = sigmoid_acc(ea * pre);
+          const float pre = graw[r] + bias;
+          const float s = sigmoid_fast(ea * pre);  // the forward gate uses the same form
           const float dz = acc * a.lb * s * (1.f - s) * ea;
           ((bf16*)a.dgate)[off] = to_bf16(dz);
           p0 += dz;
@@ -1184,11 +1194,25 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
   const float* PP = (const float*)a.sc.p[S_PP];
   float p0 = 0.f, p1 = 0.f;
-  for (int chn = part; chn < max_chunks; chn += P) {
-    if (chunks[chn].y <= 0) continue;
-    const size_t tile = (size_t)chn * a.H + h;
-    p0 += PP[tile * 2 * K + c];
-    p1 += PP[tile * 2 * K + K + c];
+  // batches of 8 chunks: every load of a batch is issued before any is used (empty chunks'
+  // partials were never written and are selected away, not multiplied)
+  constexpr int U = 8;
+  for (int chn0 = part; chn0 < max_chunks; chn0 += U * P) {
+    float x0[U], x1[U];
+    bool live[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int chn = min(chn0 + u * P, max_chunks - 1);
+      const size_t tile = (size_t)chn * a.H + h;
+      live[u] = chn0 + u * P < max_chunks && chunks[chn].y > 0;
+      x0[u] = PP[tile * 2 * K + c];
+      x1[u] = PP[tile * 2 * K + K + c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      p0 += live[u] ? x0[u] : 0.f;
+      p1 += live[u] ? x1[u] : 0.f;
+    }
   }
   s0[part][c] = p0;
   s1[part][c] = p1;
