@@ -18,13 +18,16 @@
 //
 // MI355X mapping:
 //  * scan kernel: one workgroup per (sequence, head, 16-wide V strip); dS columns are
-//    independent, so the 128x16 f32 slice of dS lives in VGPRs as MFMA accumulators.
-//  * dense kernel: one workgroup per (chunk, head); all products are 16x16x32 bf16
-//    MFMA tiles with f32 accumulation; T, dT and T^T dT stay in f32 LDS.
-//  * decay kernel: one workgroup per (chunk, head); exp(G_i - G_j) is split around the
-//    first row of the row block (row side) or the last row of the column block (column
-//    side) so that every off-diagonal factor is <= 1, exactly as in the forward; a block
-//    whose decay span exceeds 80 nats runs an exact per-pair f32 loop instead.
+//    independent, so the 128x16 f32 slice of dS lives in VGPRs as MFMA accumulators of four
+//    compute waves, fed by two loader waves through an LDS ring of direct global->LDS loads.
+//    The launch also carries cache-warming workgroups for the CUs the scan leaves idle.
+//  * dense and decay VJPs: one workgroup per (chunk, head) tile, both bodies in one kernel
+//    (role by workgroup index) launched as full rounds over "all dense tiles, then all
+//    decay tiles".  Dense: 16x16x32 bf16 MFMA tiles with f32 accumulation, every global
+//    operand requested in one batch.  Decay: the decay-scaled operands are built once per
+//    tile around the first (row side) or last (column side) row of each 16-row block, so
+//    every factor is <= 1 or bounded by the block's span; a tile with a block whose decay
+//    span exceeds 80 nats runs an exact per-pair f32 loop instead.
 #include "chunk_host.hpp"
 #include "kda_device.hpp"
 

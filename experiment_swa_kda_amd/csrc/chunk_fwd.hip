@@ -11,8 +11,8 @@
 //
 // MI355X design:
 //  * kda_chunk_prep: builds the chunk / sequence tables (B x T or packed cu_seqlens).
-//  * intra kernel: one 1024-thread workgroup per (chunk, head) tile, everything staged in
-//    LDS (f32 qh/kh/G).  The 64x64 A and M' are built as 16x16 MFMA tiles
+//  * intra kernel: one workgroup per (chunk, head) tile, everything staged in LDS (f32
+//    qh/kh/G).  The 64x64 A and M' are built as 16x16 MFMA tiles
 //    (v_mfma_f32_16x16x32_bf16).  Pairwise decays exp(G_i - G_j) are factorised around
 //    the first row r of the row block: exp(G_i - G_r) <= 1 and, for j < r,
 //    exp(G_r - G_j) <= 1, so no factor can overflow; only the diagonal block can, and a
@@ -21,10 +21,12 @@
 //    U and W by MFMA.  Factors are written once to the workspace in both row- and
 //    column-major form so every later MFMA operand is a contiguous 16-byte load.
 //  * scan kernel: one workgroup per (sequence, head, 16-wide V strip) walks the chunks
-//    in order; one wave holds the K x 16 f32 state slice in MFMA accumulators and runs
-//    delta = U - W S and S <- lam S + Kd^T delta from registers, fed by two loader waves
-//    (direct global->LDS ring) and drained by a store wave (state / delta histories).
-//  * output kernel: O = Qg S + A delta, chunk-parallel after the scan.
+//    in order; four compute waves hold the K x 16 f32 state slice in MFMA accumulators and
+//    run delta = U - W S and S <- lam S + Kd^T delta, exchanging the packed state and the
+//    delta tiles through LDS; two loader waves feed them through a direct global->LDS ring
+//    and a store wave drains the bf16 state / delta histories.
+//  * output kernel: O = Qg S + A delta, chunk-parallel after the scan; optionally the
+//    mixer's output RMSNorm * sigmoid(gate) in its epilogue.
 // Every reduction has a fixed order, so the forward is bitwise deterministic.
 #include "chunk_host.hpp"
 #include "kda_device.hpp"
