@@ -95,12 +95,12 @@ struct BwdScanLds {
   static_assert(n_load0 < 64 && n_load1 < 64, "vmcnt range");
 };
 
-// Memory regions the backward reads next (the scan's per-chunk operands, then the dense and
-// decay kernels' inputs).  Workgroups of the scan launch past the scan's own touch one word
-// of every 128-byte line of them while the scan runs on its few CUs, so the scan's
-// latency-bound loads and the next kernel's loads find their lines in the caches (the
-// forward wrote them long before the backward in training).  Loads only: the results are
-// folded into a value that is never stored.
+// The scan's per-chunk operands.  Workgroups of the scan launch past the scan's own touch
+// one word of every 128-byte line of them while the scan runs on its few CUs, so the scan's
+// latency-bound loads find their lines in the caches (the forward wrote them long before
+// the backward in training).  Loads only: the results are folded into a value that is never
+// stored.  (Warming the dense/decay inputs as well measured slower, cold and warm: the extra
+// requests delay the scan's own.)
 constexpr int kMaxPrefetch = 20;
 struct PrefetchList {
   const char* p[kMaxPrefetch];
@@ -1274,12 +1274,6 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     };
     for (int r : {R_ATF, R_KDF, R_QGTF, R_WTF, R_LAM}) add(a.ws.p[r], ws_region_bytes(g, r));
     add(a.dout, rows * V * 2);
-    if (stages & ((1 << (KDA_STAGE_BWD_DENSE - 10)) | (1 << (KDA_STAGE_BWD_DECAY - 10)))) {
-      for (int r : {R_T, R_SH, R_MP, R_G, R_DLF, R_RQ, R_RK, R_BETA}) add(a.ws.p[r], ws_region_bytes(g, r));
-      add(a.q, rows * K * 2);
-      add(a.k, rows * K * 2);
-      add(a.v, rows * V * 2);
-    }
     const int cus = device_cu_count();
     const int extra = cus > grid ? cus - grid : 0;
     hipLaunchKernelGGL(scan, dim3(grid + extra), dim3(kBwdThreads), smem_s, stream, a, pf, grid);
