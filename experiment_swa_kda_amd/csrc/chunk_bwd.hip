@@ -192,6 +192,7 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
         if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
       }
     };
+    if (n <= 0) return;  // an empty sequence: no steps, no barriers, nothing to load
     if (lw == 0) {
       issue(0);
       issue(1);

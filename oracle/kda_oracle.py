@@ -328,6 +328,14 @@ def kda_varlen_backward(q, k, v, gate, beta_logits, A_log, dt_bias, cu_seqlens, 
         a, b = cu[i], cu[i + 1]
         s0 = None if initial_state is None else np.asarray(initial_state)[i:i + 1]
         gS = None if grad_final_state is None else np.asarray(grad_final_state)[i:i + 1]
+        if b == a:
+            # an empty sequence: final state = initial state, so its gradient passes through
+            H, K, V = q.shape[2], q.shape[3], v.shape[3]
+            z = lambda x: np.zeros((1, 0) + x.shape[2:])  # noqa: E731
+            dS0 = np.zeros((1, H, V, K)) if gS is None else np.array(gS, dtype=np.float64)
+            parts.append((z(q), z(k), z(v), z(gate), z(beta_logits), np.zeros_like(np.asarray(A_log, dtype=np.float64)),
+                          np.zeros_like(np.asarray(dt_bias, dtype=np.float64)), dS0))
+            continue
         parts.append(kda_backward(q[:, a:b], k[:, a:b], v[:, a:b], gate[:, a:b],
                                   beta_logits[:, a:b], A_log, dt_bias, initial_state=s0,
                                   grad_output=grad_output[:, a:b], grad_final_state=gS,

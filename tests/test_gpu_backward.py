@@ -173,3 +173,23 @@ def test_dense_decay_rounds_equal_separate_stages():
     staged = outs + [dA, ddt.reshape(full[6].shape)]
     for a, b in zip(full[:7], staged):
         assert torch.equal(a, b)
+
+
+def test_varlen_with_empty_sequences():
+    """Zero-length sequences in cu_seqlens (non-decreasing offsets, as the reference allows):
+    their final state is the initial state and their state gradient passes straight through."""
+    d = make_kda_inputs(1, 300, 2, 64, 64, seed=41, state=True)
+    cu = torch.tensor([0, 70, 70, 200, 200, 300], dtype=torch.int32, device="cuda")
+    d["s0"] = torch.randn(5, 2, 64, 64, generator=torch.Generator().manual_seed(5)).cuda() * 0.05
+    do, dsT = cotangents(d, 6, n_states=5)
+    K = d["q"].shape[-1]
+    out, fin, _ = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], d["s0"],
+                                    True, -5.0, K ** -0.5, cu_seqlens=cu, gate="k3")
+    assert torch.equal(fin[1], d["s0"][1]) and torch.equal(fin[3], d["s0"][3])
+    eo, ef = O.kda_varlen_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
+                                  np64(d["A_log"]), np64(d["dt_bias"]), cu.cpu().numpy(),
+                                  initial_state=np64(d["s0"]), gate_mode="k3")
+    assert rel_err(out, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+    grads = gpu_grads(d, "k3", do, dsT, cu)
+    assert torch.equal(grads[7][1], dsT[1]) and torch.equal(grads[7][3], dsT[3])
+    check(grads, oracle_grads(d, "k3", do, dsT, cu))

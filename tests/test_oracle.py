@@ -285,3 +285,29 @@ def test_softcap_cross_entropy_uniform_closed_form():
     exp = np.full((rows, vocab), 1.0 / vocab)
     exp[np.arange(rows), t] -= 1.0
     np.testing.assert_allclose(d, exp / rows * sech2, atol=1e-15)
+
+
+def test_varlen_empty_sequence_passes_state_and_gradient_through():
+    """An empty packed sequence leaves the others unchanged; its final state is its initial
+    state and its state gradient is the final-state gradient (closed form)."""
+    r = np.random.default_rng(11)
+    T, H, K, V = 12, 1, 8, 8
+    q, k, g = (r.standard_normal((1, T, H, K)) for _ in range(3))
+    v = r.standard_normal((1, T, H, V))
+    b = r.standard_normal((1, T, H))
+    A, dt = np.zeros(H), np.zeros(H * K)
+    s0, gS = r.standard_normal((3, H, V, K)), r.standard_normal((3, H, V, K))
+    do = r.standard_normal((1, T, H, V))
+    o3, f3 = O.kda_varlen_forward(q, k, v, g, b, A, dt, [0, 5, 5, 12], initial_state=s0)
+    o2, f2 = O.kda_varlen_forward(q, k, v, g, b, A, dt, [0, 5, 12], initial_state=s0[[0, 2]])
+    np.testing.assert_array_equal(o3, o2)
+    np.testing.assert_array_equal(f3[1], s0[1])
+    np.testing.assert_array_equal(f3[[0, 2]], f2)
+    g3 = O.kda_varlen_backward(q, k, v, g, b, A, dt, [0, 5, 5, 12], grad_output=do, grad_final_state=gS,
+                               initial_state=s0)
+    g2 = O.kda_varlen_backward(q, k, v, g, b, A, dt, [0, 5, 12], grad_output=do, grad_final_state=gS[[0, 2]],
+                               initial_state=s0[[0, 2]])
+    for a3, a2 in zip(g3[:7], g2[:7]):
+        np.testing.assert_allclose(a3, a2, rtol=0, atol=1e-12)
+    np.testing.assert_array_equal(g3[7][1], gS[1])
+    np.testing.assert_allclose(g3[7][[0, 2]], g2[7], rtol=0, atol=1e-12)
