@@ -5,7 +5,9 @@ Default workload: one KDA layer forward+backward in bf16 wit
 state and gates, B=2, T=4096, H=3, K=V=128, chunk 64, seed 42; q,k L2-normalised from
 N(0,1), v ~ N(0,1), beta logits ~ N(0,1), g = -exp(A_log) softplus(N(0,1) + dt_bias) with
 A_log ~ U(-1,1), dt_bias = 0, upstream gradient ~ N(0,1) bf16.  All inputs are resident
-in HBM before the timed region.  A "step" is one forward+backward of the operator.
+in HBM before the timed region.  A "step" is one forward+backward of the operator,
+captured once as a HIP graph and replayed (ms_per_step_eager: the same step issued from
+Python autograd, which depends on the host's speed).
 
 Prints ONE JSON line: value = algorithmic TFLOP/s of the KDA core (13.388 GFLOP per layer
 forward+backward), ms_per_step = ms per layer forward+backward, plus the forward-only
@@ -90,6 +92,22 @@ def time_steps(torch, fn, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def time_graph_steps(torch, fn, steps, warmup):
+    """Per-step time (ms) of fn captured once in a HIP graph and replayed: the same kernels
+    as the eager step, issued by one host call per step, so the figure does not depend on
+    the box's host speed.  Warm-up runs on a side stream before capture, as capture needs."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return time_steps(torch, graph.replay, steps, warmup)
 
 
 def kernel_times(torch, t, do, gate, reps=20):
@@ -375,11 +393,12 @@ def main():
                     mode="project_chunk", gate=gate, allow_fallback=False)
 
         torch.cuda.synchronize()
-        ms = time_steps(torch, step, args.steps, args.warmup)
-        ms_fwd = time_steps(torch, fwd, args.steps, args.warmup)
-        results[gate] = (ms, ms_fwd, t, do)
+        ms_eager = time_steps(torch, step, args.steps, args.warmup)
+        ms = time_graph_steps(torch, step, args.steps, args.warmup)
+        ms_fwd = time_graph_steps(torch, fwd, args.steps, args.warmup)
+        results[gate] = (ms, ms_fwd, t, do, ms_eager)
 
-    ms, ms_fwd, t, do = results["precomputed"]
+    ms, ms_fwd, t, do, ms_eager = results["precomputed"]
     kt = kernel_times(torch, t, do, "precomputed")
     traffic = load_traffic()
     dom = max((n for n in kt if n in KERNEL_FLOP_PER_TILE), key=kt.get)
@@ -400,10 +419,12 @@ def main():
         "config": {"workload": "config2: single KDA layer fwd+bwd, precomputed gate g=-exp(A_log)softplus(.)",
                    "batch": B, "seq_len": T, "heads": H, "key_dim": K, "value_dim": V, "chunk": 64,
                    "parallelism": "single GPU"},
+        "ms_per_step_eager": round(ms_eager, 4),
         "ms_fwd": round(ms_fwd, 4),
         "tflops_fwd": round(flop / 3 / (ms_fwd * 1e-3) / 1e12, 3),
         "tokens_per_s_fwd_bwd": round(B * T / (ms * 1e-3), 1),
-        "k3_gate": {"ms_per_step": round(results["k3"][0], 4), "ms_fwd": round(results["k3"][1], 4)},
+        "k3_gate": {"ms_per_step": round(results["k3"][0], 4), "ms_fwd": round(results["k3"][1], 4),
+                    "ms_per_step_eager": round(results["k3"][4], 4)},
         "kernel_ms": {n: round(v, 4) for n, v in kt.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
