@@ -1198,9 +1198,10 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
   const float* PP = (const float*)a.sc.p[S_PP];
   float p0 = 0.f, p1 = 0.f;
-  // batches of 8 chunks: every load of a batch is issued before any is used (empty chunks'
-  // partials were never written and are selected away, not multiplied)
-  constexpr int U = 8;
+  // batches of 16 chunks (one batch per part at 128 chunks): every load of a batch is issued
+  // before any is used (empty chunks' partials were never written and are selected away,
+  // not multiplied)
+  constexpr int U = 16;
   for (int chn0 = part; chn0 < max_chunks; chn0 += U * P) {
     float x0[U], x1[U];
     bool live[U];
@@ -1221,6 +1222,7 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
   s0[part][c] = p0;
   s1[part][c] = p1;
   __syncthreads();
+  __shared__ float s_wave[K / 64];
   if (part == 0) {
     float t0 = 0.f, t1 = 0.f;
     for (int q = 0; q < P; ++q) {
@@ -1228,14 +1230,15 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
       t1 += s1[q][c];
     }
     a.ddt_bias[h * K + c] = t0;
-    s1[0][c] = t1;
+    t1 = wave_sum(t1);  // fixed butterfly order within the wave
+    if (c % 64 == 0) s_wave[c / 64] = t1;
   }
   __syncthreads();
-  for (int w = K / 2; w >= 1; w >>= 1) {
-    if (part == 0 && c < w) s1[0][c] += s1[0][c + w];
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int q = 0; q < K / 64; ++q) t += s_wave[q];
+    a.dA_log[h] = t;
   }
-  if (threadIdx.x == 0) a.dA_log[h] = s1[0][0];
 }
 
 // Compute units of the current device (the launch granularity of the dense/decay rounds);
