@@ -82,7 +82,8 @@ int kda_chunk_forward(const kda_chunk_problem* p,
 
 /*
  * kda_chunk_forward with the mixer's output RMSNorm * weight * sigmoid(gate) fused into the
- * output kernel's epilogue (SURVEY-ranked producer/consumer fusion).  No single counterpart in
+ * output kernel's epilogue (a producer/consumer fusion: the norm takes o from registers instead
+ * of a second kernel reading it back from HBM).  No single counterpart in
  * the reference: it replaces the pair chunk_forward (chunk.cu:1380-1757) followed by
  * torch.ops.nanochat_kda.rmsnorm_gate_forward (rmsnorm_gate.cu:31-71) on its output, as
  * composed in kda.py:761-770.  All arguments of kda_chunk_forward keep their meaning (output
