@@ -4,7 +4,8 @@
 // Reference: the weight-gradient GEMM that autograd runs for nanochat's Linear
 // (nanochat/gpt.py:52-57: F.linear on the bf16 cast of an f32 master weight).  Library
 // GEMMs tile this shape (a long contraction, a small output) into a few dozen workgroups;
-// here the contraction is split into 512-row ranges, one workgroup per (output tile, range),
+// here the contraction is split into ranges of 512-row blocks, one workgroup per (output tile,
+// range), as many ranges as it takes to fill the chip,
 // and the f32 partials are summed in a fixed order by a second kernel (deterministic, no
 // atomics).
 //
@@ -99,15 +100,17 @@ __global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(
     int M, int N, int K, const bf16* __restrict__ dy, long ldd, const bf16* __restrict__ x, long ldx,
     int rows_per_split, float* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) WgLds s;
-  // 1-D grid of kXcds * tiles * ceil(splits / kXcds): workgroups are dispatched round-robin
-  // over the XCDs (linear id mod 8), so all tiles of one split (the same dy / x rows) share
-  // an XCD and its L2, and every row range is fetched from HBM about once.
+  // 1-D grid of kXcds * per_xcd: workgroups are dispatched round-robin over the XCDs
+  // (linear id mod 8), and XCD x takes the items x * per_xcd .. of the (split, tile) order,
+  // so the tiles of one split (the same dy / x rows) share an XCD and its L2, and every row
+  // range is fetched from HBM about once.
   const int tiles_k = (K + kWgTile - 1) / kWgTile;
   const int tiles = tiles_k * ((N + kWgTile - 1) / kWgTile);
-  const int L = blockIdx.x, rest = L / kXcds;
-  const int tile = rest % tiles;
-  const int split = (rest / tiles) * kXcds + L % kXcds;
-  if (split * rows_per_split >= max(M, 1)) return;  // past the last split (grid rounding)
+  const int splits = (max(M, 1) + rows_per_split - 1) / rows_per_split;
+  const int per_xcd = (tiles * splits + kXcds - 1) / kXcds;
+  const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (item >= tiles * splits) return;  // grid rounding
+  const int tile = item % tiles, split = item / tiles;
   const int n0 = (tile / tiles_k) * kWgTile, k0 = (tile % tiles_k) * kWgTile;
   const int m_begin = split * rows_per_split;
   const int m_end = min(M, m_begin + rows_per_split);
@@ -144,12 +147,16 @@ __global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(
       }
     return;
   }
-  // A workgroup runs exactly kWgDepth 128-row steps (rows past m_end are zero), and all of
-  // their global loads are issued before the first step.
+  // The range is a whole number of blocks of kWgDepth 128-row steps (rows past m_end are
+  // zero); all global loads of a block are issued before its first step.  The LDS buffer
+  // parity continues across blocks (kWgDepth is even), so one barrier per step still
+  // separates a buffer's reuse from its last reads.
+  static_assert(kWgDepth % 2 == 0, "buffer parity across blocks");
+  for (int blk = m_begin; blk < m_end; blk += kWgDepth * kWgRows) {
   bf16x8 v[kWgDepth][8];
 #pragma unroll
   for (int d = 0; d < kWgDepth; ++d)
-    load_block<VEC>(src, ld, ncols, m_begin + d * kWgRows + 8 * mb, m_end, col, v[d]);
+    load_block<VEC>(src, ld, ncols, blk + d * kWgRows + 8 * mb, m_end, col, v[d]);
 #pragma unroll
   for (int st = 0; st < kWgDepth; ++st) {
     const int buf = st & 1;
@@ -175,6 +182,7 @@ __global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma16(a[i], bb[j], acc[i][j]);
     }
+  }
   }
   float* o = out + (size_t)split * N * K;
 #pragma unroll
@@ -227,11 +235,20 @@ struct WgPlan {
   int tiles, splits, rows_per_split;
 };
 
+// Enough (tile, range) workgroups to fill the chip about twice over (kWgTarget), with as few
+// ranges as that allows: every extra range adds an f32 partial of the whole output that the
+// reduction writes and reads back.  A range is a whole number of 512-row blocks.
+constexpr int kWgTarget = 1024;
+
 static WgPlan plan_weight_grad(int M, int N, int K) {
   WgPlan p;
   p.tiles = ((N + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
-  p.rows_per_split = kWgDepth * kWgRows;
-  p.splits = max(1, (M + p.rows_per_split - 1) / p.rows_per_split);
+  const int block = kWgDepth * kWgRows;
+  const int blocks = max(1, (M + block - 1) / block);
+  const int want = max(1, min(blocks, (kWgTarget + p.tiles - 1) / p.tiles));
+  const int per_split = (blocks + want - 1) / want;
+  p.rows_per_split = per_split * block;
+  p.splits = (blocks + per_split - 1) / per_split;
   return p;
 }
 
@@ -258,7 +275,7 @@ extern "C" int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, 
   KDA_REQUIRE(aligned16(scratch, dweight), "weight_grad: dweight and scratch must be 16-byte aligned");
   const bool vec = aligned16(dy, x) && ldd % 8 == 0 && ldx % 8 == 0 && N % 8 == 0 && K % 8 == 0;
   float* part = p.splits > 1 ? (float*)scratch : dweight;
-  dim3 grid(kXcds * p.tiles * ((p.splits + kXcds - 1) / kXcds));
+  dim3 grid(kXcds * ((p.tiles * p.splits + kXcds - 1) / kXcds));
   if (vec)
     hipLaunchKernelGGL(weight_grad_kernel<true>, grid, dim3(kWgThreads), 0, stream, (int)M, N, K,
                        (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);

@@ -73,6 +73,8 @@ def test_softcap_ce_rejects_bad_arguments():
 @pytest.mark.parametrize("M,N,K", [
     (8192, 384, 384),   # the trainer's projections
     (8192, 1536, 384),  # MLP
+    (8192, 2312, 384),  # the six fused input projections: 4 ranges of 4 blocks each
+    (9000, 1536, 384),  # several blocks per range, the last range ragged
     (4097, 128, 384),   # ragged contraction
     (1000, 3, 384),     # unaligned output rows (element path)
     (777, 130, 24),     # ragged tile edges
