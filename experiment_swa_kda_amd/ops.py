@@ -111,13 +111,22 @@ def _check_chunk_inputs(what, q, k, v, gate, beta_logits, A_log, dt_bias, initia
     return dev
 
 
+def _output_bytes(B, T, H, V):
+    """Byte offset of the residual workspace when it lives behind the output tensor."""
+    return (B * T * H * V * 2 + 255) // 256 * 256
+
+
 def chunk_forward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state,
-                  output_final_state, lower_bound, scale, *, cu_seqlens=None, gate="k3"):
+                  output_final_state, lower_bound, scale, *, cu_seqlens=None, gate="k3",
+                  residuals_behind_output=False):
     """Chunked forward.  Returns (output, final_state or None, workspace).
 
     ``gate_values`` is the bf16 raw gate (``gate="k3"``) or the f32 log decay
     (``gate="precomputed"``).  The workspace holds the residuals that
-    :func:`chunk_backward` consumes.
+    :func:`chunk_backward` consumes.  With ``residuals_behind_output`` the output and
+    the workspace share one allocation (output first, the workspace at the next 256-byte
+    boundary), so a caller that keeps only the output keeps the residuals too: the
+    ``torch.ops.nanochat_kda`` schemas pass no workspace between forward and backward.
     """
     gm = GATE_MODES[gate]
     dev = _check_chunk_inputs("chunk_forward", q, k, v, gate_values, beta_logits, A_log, dt_bias,
@@ -132,8 +141,14 @@ def chunk_forward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_sta
     ws_bytes = lib.kda_chunk_workspace_bytes(ctypes.byref(p))
     if ws_bytes == 0 and (B * T > 0 or n > 0):
         check(1, "chunk_workspace_bytes")
-    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
-    output = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    if residuals_behind_output:
+        off = _output_bytes(B, T, H, V)
+        buf = torch.empty(off + max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        output = buf[:B * T * H * V * 2].view(torch.bfloat16).view(B, T, H, V)
+        workspace = buf[off:]
+    else:
+        workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        output = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
     final_state = torch.empty(n, H, V, K, dtype=torch.float32, device=dev) if output_final_state else None
     with torch.cuda.device(dev):
         rc = lib.kda_chunk_forward(
@@ -501,18 +516,36 @@ def rms_norm_backward(x, rinv, grad):
 
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):
+    # the schema has no workspace output: the residuals ride in the output's allocation
     out, fin, _ = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
-                                output_final_state, lower_bound, scale)
+                                output_final_state, lower_bound, scale, residuals_behind_output=True)
     return out, fin
+
+
+def _residuals_of(output, q, v, gate_mode, lower_bound, scale):
+    """The workspace stored behind ``output`` by the schema forward, or None when ``output``
+    was not made by it (wrong allocation size or a view into another tensor)."""
+    B, T, H, _ = q.shape
+    V = v.shape[-1]
+    p = _problem(q, v, None, gate_mode, lower_bound, scale)
+    ws_bytes = max(_lib.load().kda_chunk_workspace_bytes(ctypes.byref(p)), 256)
+    off = _output_bytes(B, T, H, V)
+    storage = output.untyped_storage()
+    if (output.storage_offset() != 0 or not output.is_contiguous() or output.dtype != torch.bfloat16
+            or tuple(output.shape) != (B, T, H, V) or storage.nbytes() != off + ws_bytes):
+        return None
+    return torch.empty(0, dtype=torch.uint8, device=output.device).set_(storage, off, (ws_bytes,))
 
 
 def _op_chunk_backward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, output,
                        final_state, grad_output, grad_final_state, lower_bound, scale):
-    # The reference keeps its residuals behind `output`'s storage; this schema has no
-    # workspace argument, so the forward residuals are recomputed here.
-    del output, final_state
-    _, _, ws = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, False,
-                             lower_bound, scale)
+    # Residuals come from behind `output` (as the reference stores them); an output that
+    # does not carry them (made elsewhere) costs one recomputation of the forward.
+    del final_state
+    ws = _residuals_of(output, q, v, KDA_GATE_K3, lower_bound, scale)
+    if ws is None:
+        _, _, ws = chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
+                                 False, lower_bound, scale)
     return chunk_backward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state, ws,
                           grad_output, grad_final_state, lower_bound, scale)
 

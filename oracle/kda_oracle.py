@@ -492,3 +492,64 @@ def full_layer(x, *, q_weight, k_weight, v_weight, q_conv_weight, k_conv_weight,
     gate = (x @ f(output_gate_weight).T).reshape(B, T, num_heads, Vd)
     y, _ = rmsnorm_gate_forward(o, gate, norm_weight, norm_eps)
     return y.reshape(B, T, -1) @ f(output_weight).T, (mem, qf, kf, vf)
+
+
+def full_layer_backward(x, grad_output, *, q_weight, k_weight, v_weight, q_conv_weight,
+                        k_conv_weight, v_conv_weight, forget_a_weight, forget_b_weight,
+                        beta_weight, A_log, dt_bias, output_gate_weight, norm_weight,
+                        output_weight, num_heads, norm_eps, lower_bound=-5.0):
+    """Reverse mode of ``full_layer`` (no initial state) by the chain rule through the
+    pinned backward functions above and the projections' transposes
+    (nanochat/mixers/kda.py:729-798 is the forward being differentiated).
+
+    Returns a dict of gradients keyed like the mixer's parameters (``q_proj``,
+    ``q_conv1d``, ``f_a_proj``, ``A_log``, ``o_norm``, ...) plus ``x``; weight gradients
+    have the parameters' shapes ([out, in] for projections, [D, W] for convolutions).
+    """
+    f = lambda a: np.asarray(a, np.float64)  # noqa: E731
+    x = f(x)
+    B, T, C = x.shape
+    x2 = x.reshape(-1, C)
+    # forward, keeping what the backward needs
+    qp, kp, vp = x @ f(q_weight).T, x @ f(k_weight).T, x @ f(v_weight).T
+    q, _ = causal_conv_forward(qp, q_conv_weight)
+    k, _ = causal_conv_forward(kp, k_conv_weight)
+    v, _ = causal_conv_forward(vp, v_conv_weight)
+    K = q.shape[-1] // num_heads
+    Vd = v.shape[-1] // num_heads
+    q4, k4, v4 = q.reshape(B, T, num_heads, K), k.reshape(B, T, num_heads, K), v.reshape(B, T, num_heads, Vd)
+    fa = x @ f(forget_a_weight).T
+    raw = (fa @ f(forget_b_weight).T).reshape(B, T, num_heads, K)
+    bl = x @ f(beta_weight).T
+    o, _ = kda_forward(q4, k4, v4, raw, bl, A_log, dt_bias, lower_bound=lower_bound)
+    gate = (x @ f(output_gate_weight).T).reshape(B, T, num_heads, Vd)
+    y, _ = rmsnorm_gate_forward(o, gate, norm_weight, norm_eps)
+    y2 = y.reshape(-1, num_heads * Vd)
+    # backward
+    dout = f(grad_output).reshape(-1, f(output_weight).shape[0])
+    g = {"o_proj": dout.T @ y2}
+    dy = (dout @ f(output_weight)).reshape(B, T, num_heads, Vd)
+    do, dgate, g["o_norm"] = rmsnorm_gate_backward(o, gate, norm_weight, norm_eps, dy)
+    dgate2 = dgate.reshape(-1, num_heads * Vd)
+    g["g_proj"] = dgate2.T @ x2
+    dx = dgate2 @ f(output_gate_weight)
+    dq, dk, dv, draw, dbl, g["A_log"], ddt, _ = kda_backward(
+        q4, k4, v4, raw, bl, A_log, dt_bias, grad_output=do, lower_bound=lower_bound)
+    g["dt_bias"] = np.asarray(ddt).reshape(np.shape(dt_bias))
+    dbl2 = dbl.reshape(-1, num_heads)
+    g["b_proj"] = dbl2.T @ x2
+    dx = dx + dbl2 @ f(beta_weight)
+    draw2 = draw.reshape(-1, num_heads * K)
+    g["f_b_proj"] = draw2.T @ fa.reshape(-1, fa.shape[-1])
+    dfa = draw2 @ f(forget_b_weight)
+    g["f_a_proj"] = dfa.T @ x2
+    dx = dx + dfa @ f(forget_a_weight)
+    for name, pre, w_proj, w_conv, d in (("q", qp, q_weight, q_conv_weight, dq),
+                                         ("k", kp, k_weight, k_conv_weight, dk),
+                                         ("v", vp, v_weight, v_conv_weight, dv)):
+        dpre, g[f"{name}_conv1d"], _ = causal_conv_backward(pre, w_conv, d.reshape(B, T, -1))
+        dpre2 = dpre.reshape(-1, dpre.shape[-1])
+        g[f"{name}_proj"] = dpre2.T @ x2
+        dx = dx + dpre2 @ f(w_proj)
+    g["x"] = dx.reshape(B, T, C)
+    return g

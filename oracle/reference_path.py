@@ -2,10 +2,10 @@
 
 TEST/BENCH INFRASTRUCTURE ONLY (imported by bench.py's cpu_baseline leg and tests).
 
-Restates nanochat/mixers/kda.py:269-327 (``_reference_kda``): an f32 token loop of
-einsums whose backward is PyTorch autograd through the loop — the path the reference
-runs with ``mode="reference"`` and falls back to on CPU.  Timed on the host cores as a
-reported baseline, never as the product.
+Restates nanochat/mixers/kda.py:269-327 (``_reference_kda``): an f32 loop over tokens
+whose backward is PyTorch autograd through the loop -- the path the reference runs with
+``mode="reference"`` and falls back to on CPU.  Timed on the host cores as a reported
+baseline, never as the product.
 """
 
 from __future__ import annotations
@@ -16,31 +16,26 @@ import torch.nn.functional as F
 
 def reference_kda_cpu(q, k, v, gate, beta_logits, A_log, dt_bias, *, initial_state=None,
                       lower_bound=-5.0, scale=None, gate_mode="k3"):
-    """f32 token loop (nanochat/mixers/kda.py:286-327); returns (o, final state V-first)."""
-    B, T, H, K = q.shape
-    V = v.shape[-1]
-    scale = K ** -0.5 if scale is None else scale
-    qf = F.normalize(q.float(), p=2, dim=-1) * scale
-    kf = F.normalize(k.float(), p=2, dim=-1)
-    vf = v.float()
+    """f32 token loop with a value-major state S [B,H,V,K]; returns (o, final state)."""
+    n_b, n_t, n_h, n_k = q.shape
+    n_v = v.shape[-1]
+    qn = F.normalize(q.float(), dim=-1) * (n_k ** -0.5 if scale is None else scale)
+    kn = F.normalize(k.float(), dim=-1)
     if gate_mode == "k3":
-        decay = lower_bound * torch.sigmoid(A_log.float().exp().reshape(H, 1)
-                                            * (gate.float() + dt_bias.float().reshape(H, K)))
+        bias = dt_bias.float().view(n_h, n_k)
+        log_decay = lower_bound * torch.sigmoid(A_log.float().exp()[:, None] * (gate.float() + bias))
     else:
-        decay = gate.float()
-    beta = beta_logits.float().sigmoid()
-    if initial_state is None:
-        state = torch.zeros(B, H, K, V, dtype=torch.float32)
-    else:
-        state = initial_state.float().transpose(-1, -2)
-    outs = []
-    for t in range(T):
-        ki = kf[:, t]
-        state = state * decay[:, t].exp().unsqueeze(-1)
-        resid = vf[:, t] - torch.einsum("bhk,bhkv->bhv", ki, state)
-        state = state + torch.einsum("bhk,bhv->bhkv", beta[:, t].unsqueeze(-1) * ki, resid)
-        outs.append(torch.einsum("bhk,bhkv->bhv", qf[:, t], state))
-    return torch.stack(outs, dim=1), state.transpose(-1, -2)
+        log_decay = gate.float()
+    decay = log_decay.exp()
+    beta = torch.sigmoid(beta_logits.float())
+    S = torch.zeros(n_b, n_h, n_v, n_k) if initial_state is None else initial_state.float()
+    rows = []
+    for t in range(n_t):
+        S = S * decay[:, t, :, None, :]
+        err = v[:, t].float() - torch.einsum("bhvk,bhk->bhv", S, kn[:, t])
+        S = S + torch.einsum("bhv,bhk->bhvk", beta[:, t, :, None] * err, kn[:, t])
+        rows.append(torch.einsum("bhvk,bhk->bhv", S, qn[:, t]))
+    return torch.stack(rows, dim=1), S
 
 
 def time_fwd_bwd(B, T, H, K, V, *, repeats=3, seed=42, threads=None):

@@ -129,21 +129,60 @@ def test_contract_errors():
         kda(d["q"], d["k"], d["v"], d["g"], d["beta"][..., :1], d["A_log"], d["dt_bias"])
 
 
-@pytest.mark.parametrize("mode", ["project_chunk", "chunk", "project_recurrent", "recurrent"])
-def test_accelerated_modes_fail_closed_on_cpu(mode, monkeypatch):
-    # no silent fallback to the eager loop, whatever allow_fallback says
+@pytest.mark.parametrize("mode", ["project_chunk", "project_recurrent"])
+def test_project_modes_fail_closed_on_cpu(mode, monkeypatch):
+    # project_* modes never fall back to the eager loop, whatever allow_fallback says
+    # (reference kda.py:588-598)
     import importlib
 
     impl = importlib.import_module("experiment_swa_kda_amd.kda")
 
     def forbidden(*args, **kwargs):
-        raise AssertionError("accelerated call reached the eager loop")
+        raise AssertionError("project call reached the eager loop")
 
     monkeypatch.setattr(impl, "_reference_kda", forbidden)
     d = make(1, 3, 2, 64, 64)
-    with pytest.raises(RuntimeError, match="unavailable"):
+    with pytest.raises(RuntimeError, match="project CUDA KDA backend unavailable"):
         kda(d["q"].bfloat16(), d["k"].bfloat16(), d["v"].bfloat16(), d["g"].bfloat16(), d["beta"].bfloat16(),
             d["A_log"], d["dt_bias"], mode=mode, allow_fallback=True)
+
+
+@pytest.mark.parametrize("mode", ["chunk", "recurrent"])
+def test_optimized_modes_fallback_contract_on_cpu(mode):
+    # reference kda.py:633-673: an unsupported chunk/recurrent call raises with
+    # allow_fallback=False and runs the eager loop with allow_fallback=True
+    d = make(1, 5, 2, 8, 8)
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"])
+    with pytest.raises(RuntimeError, match=f"optimized {mode} KDA backend unavailable"):
+        kda(*args, initial_state=d["s0"], output_final_state=True, mode=mode, allow_fallback=False)
+    got, got_state = kda(*args, initial_state=d["s0"], output_final_state=True, mode=mode)
+    want, want_state = kda(*args, initial_state=d["s0"], output_final_state=True, mode="reference")
+    assert torch.equal(got, want) and torch.equal(got_state, want_state)
+    out, none_state = kda(*args, mode=mode)
+    assert none_state is None and out.shape == d["v"].shape
+
+
+def test_layer_recurrent_mode_token_decode_matches_full_sequence():
+    # restates tests/test_kda_layer.py:148-169: mode="recurrent" on CPU falls back to the
+    # eager loop; decoding one token at a time equals the full-sequence reference forward
+    layer = KimiDeltaAttention(16, 2, 8, conv_size=4, layer_idx=0, mode="reference")
+    gen = torch.Generator().manual_seed(314159)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * 0.08)
+        layer.A_log.copy_(torch.tensor([-0.2, 0.15]))
+        layer.dt_bias.copy_(torch.linspace(-0.4, 0.3, 16))
+    layer.eval()
+    x = torch.randn(2, 11, 16, generator=torch.Generator().manual_seed(19))
+    full, full_state = layer(x, state=None, output_final_state=True, mode="reference")
+    state, pieces = None, []
+    for t in range(x.shape[1]):
+        piece, state = layer(x[:, t:t + 1], state=state, output_final_state=True, mode="recurrent")
+        pieces.append(piece)
+    torch.testing.assert_close(torch.cat(pieces, 1), full, atol=3e-5, rtol=3e-5)
+    for a, b in ((state.memory, full_state.memory), (state.q_conv, full_state.q_conv),
+                 (state.k_conv, full_state.k_conv), (state.v_conv, full_state.v_conv)):
+        torch.testing.assert_close(a, b, atol=3e-5, rtol=3e-5)
 
 
 def test_layer_structure_and_reference_forward_matches_oracle():
