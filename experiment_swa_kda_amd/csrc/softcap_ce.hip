@@ -168,3 +168,54 @@ extern "C" int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, i
   KDA_LAUNCH_CHECK("softcap_cross_entropy_backward");
   return KDA_OK;
 }
+
+namespace kda {
+
+// Mean of the row losses over the rows whose target is not ignore_index, and that count,
+// in one workgroup with a fixed summation order (thread t sums rows t, t + 1024, ...; then
+// a fixed tree).  Keeps the loss reduction inside the library: a multi-block library
+// reduction would record memory-set nodes when captured in a HIP graph.
+constexpr int kMeanThreads = 1024;
+
+__global__ __launch_bounds__(kMeanThreads) void softcap_ce_mean_kernel(
+    long rows, const float* __restrict__ loss_row, const int64_t* __restrict__ targets,
+    int64_t ignore_index, float* __restrict__ loss, float* __restrict__ count) {
+  __shared__ float red_s[kMeanThreads / kWave], red_c[kMeanThreads / kWave];
+  float s = 0.f, c = 0.f;
+  for (long r = threadIdx.x; r < rows; r += kMeanThreads) {
+    s += loss_row[r];
+    c += targets[r] != ignore_index ? 1.f : 0.f;
+  }
+  s = wave_sum(s);
+  c = wave_sum(c);
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    red_s[wave] = s;
+    red_c[wave] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ts = 0.f, tc = 0.f;
+    for (int w = 0; w < kMeanThreads / kWave; ++w) {
+      ts += red_s[w];
+      tc += red_c[w];
+    }
+    *loss = ts / tc;  // NaN when every row is ignored, as the library cross entropy
+    *count = tc;
+  }
+}
+
+}  // namespace kda
+
+extern "C" int kda_softcap_cross_entropy_mean(int64_t rows, const float* loss_rows, const int64_t* targets,
+                                              int64_t ignore_index, float* loss, float* count,
+                                              hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(rows >= 0, "softcap_cross_entropy_mean: negative row count");
+  KDA_REQUIRE(loss && count && (rows == 0 || (loss_rows && targets)),
+              "softcap_cross_entropy_mean: null pointer");
+  hipLaunchKernelGGL(softcap_ce_mean_kernel, dim3(1), dim3(kMeanThreads), 0, stream, (long)rows, loss_rows,
+                     targets, ignore_index, loss, count);
+  KDA_LAUNCH_CHECK("softcap_cross_entropy_mean");
+  return KDA_OK;
+}

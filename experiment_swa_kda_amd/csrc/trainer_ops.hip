@@ -358,3 +358,130 @@ extern "C" int kda_relu2_backward(int64_t n, const void* x, const void* grad, vo
   KDA_LAUNCH_CHECK("relu2_backward");
   return KDA_OK;
 }
+
+namespace kda {
+
+// ---------------------------------------------------------------------------------------
+// Token-embedding gradient (the backward of the decoder's wte lookup, nanochat/gpt.py:559)
+// without sorting: dW[v] = sum over tokens t with idx[t] == v of dy[t], summed in token
+// order (deterministic, no atomics, no memset).  A workgroup owns kEmbRows vocabulary rows
+// and every row of dW it owns is written exactly once (zeros for unseen rows).  It walks
+// the token ids in windows of kEmbWindow, compacts the tokens that hit its rows into an
+// LDS list in token order (per-thread counts + a fixed-order workgroup scan), then each
+// wave accumulates the dy rows of its own rows (wave w owns rows w, w+4, ...) in f32.
+// Every workgroup reads the whole id vector (8 B per token, from L2 after the first).
+// ---------------------------------------------------------------------------------------
+constexpr int kEmbRows = 32;                          // vocabulary rows per workgroup
+constexpr int kEmbThreads = 256;                      // 4 waves x 8 rows
+constexpr int kEmbPerThread = 8;                      // ids per thread per window
+constexpr int kEmbWindow = kEmbThreads * kEmbPerThread;
+constexpr int kEmbRowsPerWave = kEmbRows / (kEmbThreads / kWave);
+constexpr int kEmbMaxDim = kWave * 8;                 // one 16-byte vector per lane and row
+
+__global__ __launch_bounds__(kEmbThreads) void embedding_bwd_kernel(long n_tok, int vocab, int dim,
+                                                                    const int64_t* __restrict__ idx,
+                                                                    const bf16* __restrict__ dy,
+                                                                    bf16* __restrict__ dw) {
+  __shared__ int list[kEmbWindow];   // (token - window start) << 5 | local row
+  __shared__ int wave_total[kEmbThreads / kWave];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const long r0 = (long)blockIdx.x * kEmbRows;
+  const int nvec = dim / 8;
+  const bool active = lane < nvec;
+  float acc[kEmbRowsPerWave][8];
+#pragma unroll
+  for (int r = 0; r < kEmbRowsPerWave; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
+
+  for (long w0 = 0; w0 < n_tok; w0 += kEmbWindow) {
+    // ids of this thread's contiguous run of the window
+    int hits[kEmbPerThread];
+    int count = 0;
+#pragma unroll
+    for (int u = 0; u < kEmbPerThread; ++u) {
+      const long t = w0 + tid * kEmbPerThread + u;
+      const long v = t < n_tok ? (long)idx[t] : -1;
+      const long d = v - r0;
+      hits[u] = (d >= 0 && d < kEmbRows) ? (int)d : -1;
+      count += hits[u] >= 0;
+    }
+    // exclusive scan of the counts in thread order: wave prefix by shuffles, then the
+    // wave totals in order
+    int incl = count;
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+      const int o = __shfl_up(incl, s, kWave);
+      if (lane >= s) incl += o;
+    }
+    if (lane == kWave - 1) wave_total[wave] = incl;
+    __syncthreads();
+    int pos = incl - count, n_list = 0;
+#pragma unroll
+    for (int w = 0; w < kEmbThreads / kWave; ++w) {
+      pos += w < wave ? wave_total[w] : 0;
+      n_list += wave_total[w];
+    }
+#pragma unroll
+    for (int u = 0; u < kEmbPerThread; ++u)
+      if (hits[u] >= 0) list[pos++] = ((tid * kEmbPerThread + u) << 5) | hits[u];
+    __syncthreads();
+    // accumulate this wave's rows, four list entries' loads in flight at a time
+    for (int e0 = 0; e0 < n_list; e0 += 4) {
+      bf16x8 v[4];
+      int ent[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ent[u] = __builtin_amdgcn_readfirstlane(e0 + u < n_list ? list[e0 + u] : -1);
+        const bool mine = ent[u] >= 0 && (ent[u] & 31) % (kEmbThreads / kWave) == wave;
+        if (mine && active) {
+          v[u] = *reinterpret_cast<const bf16x8*>(dy + (w0 + (ent[u] >> 5)) * dim + lane * 8);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[u][e] = to_bf16(0.f);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (ent[u] < 0 || (ent[u] & 31) % (kEmbThreads / kWave) != wave) continue;
+        const int rl = (ent[u] & 31) / (kEmbThreads / kWave);
+#pragma unroll
+        for (int r = 0; r < kEmbRowsPerWave; ++r)
+          if (rl == r)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r][e] += (float)v[u][e];
+      }
+    }
+    __syncthreads();  // the list is rebuilt for the next window
+  }
+#pragma unroll
+  for (int r = 0; r < kEmbRowsPerWave; ++r) {
+    const long row = r0 + wave + r * (kEmbThreads / kWave);
+    if (row < vocab && active) {
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = to_bf16(acc[r][e]);
+      *reinterpret_cast<bf16x8*>(dw + row * dim + lane * 8) = o;
+    }
+  }
+}
+
+}  // namespace kda
+
+extern "C" int kda_embedding_backward(int64_t n_tokens, int32_t vocab, int32_t dim, const int64_t* idx,
+                                      const void* grad_output, void* grad_weight, hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(n_tokens >= 0 && vocab >= 0, "embedding_backward: negative size");
+  KDA_REQUIRE(dim > 0 && dim % 8 == 0 && dim <= kEmbMaxDim,
+              "embedding_backward: dim must be a positive multiple of 8, at most %d", kEmbMaxDim);
+  KDA_REQUIRE(vocab == 0 || grad_weight, "embedding_backward: null grad_weight");
+  KDA_REQUIRE(n_tokens == 0 || (idx && grad_output), "embedding_backward: null input");
+  KDA_REQUIRE(aligned16(grad_output, grad_weight), "embedding_backward: buffers must be 16-byte aligned");
+  if (vocab == 0) return KDA_OK;
+  hipLaunchKernelGGL(embedding_bwd_kernel, dim3((unsigned)((vocab + kEmbRows - 1) / kEmbRows)),
+                     dim3(kEmbThreads), 0, stream, (long)n_tokens, vocab, dim, idx,
+                     (const bf16*)grad_output, (bf16*)grad_weight);
+  KDA_LAUNCH_CHECK("embedding_backward");
+  return KDA_OK;
+}
+

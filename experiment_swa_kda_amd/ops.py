@@ -393,6 +393,39 @@ def softcap_cross_entropy_forward(logits, targets, vocab, softcap, ignore_index=
     return loss, lse
 
 
+def softcap_cross_entropy_mean(loss_rows, targets, ignore_index=-1):
+    """(mean loss over non-ignored rows, that row count): two f32 device scalars."""
+    dev = _require_cuda("softcap_cross_entropy_mean", loss_rows, targets)
+    _check_dtype("softcap_cross_entropy_mean", loss_rows, torch.float32, "loss_rows")
+    _check_dtype("softcap_cross_entropy_mean", targets, torch.int64, "targets")
+    loss_rows, targets = _c(loss_rows), _c(targets)
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_softcap_cross_entropy_mean(loss_rows.numel(), ptr(loss_rows), ptr(targets),
+                                                        int(ignore_index), ptr(out), out.data_ptr() + 4,
+                                                        _stream(dev))
+    check(rc, "kda_softcap_cross_entropy_mean")
+    return out[0], out[1]
+
+
+def embedding_backward(idx, grad_output, vocab):
+    """Gradient of an embedding lookup: idx int64 [...], grad_output bf16 [..., dim] ->
+    grad_weight bf16 [vocab, dim] (token-order f32 sums, deterministic)."""
+    dev = _require_cuda("embedding_backward", idx, grad_output)
+    _check_dtype("embedding_backward", idx, torch.int64, "idx")
+    _check_dtype("embedding_backward", grad_output, torch.bfloat16, "grad_output")
+    dim = grad_output.shape[-1]
+    if grad_output.shape[:-1] != idx.shape:
+        raise RuntimeError("embedding_backward: grad_output must be idx.shape + [dim]")
+    idx, grad_output = _c(idx), _c(grad_output)
+    dw = torch.empty(vocab, dim, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_embedding_backward(idx.numel(), int(vocab), int(dim), ptr(idx), ptr(grad_output),
+                                                ptr(dw), _stream(dev))
+    check(rc, "kda_embedding_backward")
+    return dw
+
+
 def softcap_cross_entropy_backward(logits, targets, lse, grad_scale, vocab, softcap, ignore_index=-1):
     """grad_scale: f32 device scalar (dL/dmean / non-ignored count) -> grad [rows, stride] bf16."""
     dev = _require_cuda("softcap_cross_entropy_backward", logits, targets, lse, grad_scale)

@@ -242,6 +242,16 @@ int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, int64_t stri
                                        const float* grad_scale, void* grad_logits,
                                        hipStream_t stream);
 
+/*
+ * Mean of loss_rows [rows] over the rows whose target differs from ignore_index, and that
+ * row count (both f32 scalars on the device; loss is NaN when every row is ignored).  The
+ * reduction F.cross_entropy(reduction="mean") applies in nanochat/gpt.py:600-608, in one
+ * workgroup with a fixed summation order.
+ */
+int kda_softcap_cross_entropy_mean(int64_t rows, const float* loss_rows, const int64_t* targets,
+                                   int64_t ignore_index, float* loss, float* count,
+                                   hipStream_t stream);
+
 /* Bytes of scratch kda_weight_grad needs for an (M, N, K) problem (0: none). */
 size_t kda_weight_grad_scratch_bytes(int64_t M, int32_t N, int32_t K);
 
@@ -277,6 +287,15 @@ int kda_rms_norm_forward(int64_t rows, int32_t dim, float eps, const void* x, vo
 int kda_rms_norm_backward(int64_t rows, int32_t dim, const void* x, const float* rinv,
                           const void* grad, void* dx, hipStream_t stream);
 int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx, hipStream_t stream);
+/*
+ * Gradient of the token-embedding lookup (the backward of nn.Embedding for the decoder's
+ * wte, nanochat/gpt.py:559): grad_weight [vocab, dim] bf16 = sum over tokens t with
+ * idx[t] == v of grad_output[t] (f32 sums in token order, one bf16 rounding; rows no token
+ * hits are zero).  dim a multiple of 8, at most 512; idx values outside [0, vocab) are
+ * ignored.  No sort, atomics or memory-set operations (HIP-graph safe).
+ */
+int kda_embedding_backward(int64_t n_tokens, int32_t vocab, int32_t dim, const int64_t* idx,
+                           const void* grad_output, void* grad_weight, hipStream_t stream);
 
 #ifdef __cplusplus
 }

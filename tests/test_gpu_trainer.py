@@ -159,3 +159,64 @@ def test_rms_norm_matches_torch(D):
     y64 = x64 * torch.rsqrt((x64 * x64).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)
     y64.backward(gy.double())
     assert rel_err(y, y64) < 4e-3 and rel_err(x.grad, x64.grad) < 4e-3
+
+
+@pytest.mark.parametrize("n_tok,vocab,dim", [
+    (8192, 32768, 384),   # the trainer's lookup: B2 x T4096, vocab 32768, d384
+    (3000, 100, 256),     # many repeats per row, ragged last workgroup
+    (5, 40, 8),           # fewer tokens than one window
+    (0, 64, 16),          # no tokens: all-zero gradient
+])
+def test_embedding_backward_matches_index_add(n_tok, vocab, dim):
+    g = torch.Generator().manual_seed(n_tok + vocab)
+    idx = torch.randint(0, vocab, (n_tok,), generator=g)
+    if n_tok > 10:
+        idx[: n_tok // 3] = 7  # a frequent token
+    dy = torch.randn(n_tok, dim, generator=g).bfloat16()
+    exp = torch.zeros(vocab, dim, dtype=torch.float64).index_add_(0, idx, dy.double())
+    dw = ops.embedding_backward(idx.cuda(), dy.cuda(), vocab)
+    assert dw.dtype == torch.bfloat16 and dw.shape == (vocab, dim)
+    # f32 sums, one bf16 rounding per element
+    torch.testing.assert_close(dw.cpu().double(), exp, atol=1e-2, rtol=8e-3)
+    assert torch.equal(dw, ops.embedding_backward(idx.cuda(), dy.cuda(), vocab))
+    # as the gradient of the model's lookup, through autograd
+    from experiment_swa_kda_amd.model import embed
+    table = torch.nn.Embedding(vocab, dim).cuda().to(torch.bfloat16)
+    if n_tok:
+        embed(table, idx.cuda().view(1, -1)).backward(dy.cuda().view(1, n_tok, dim))
+        assert torch.equal(table.weight.grad, dw)
+
+
+def test_embedding_backward_ignores_out_of_range_ids():
+    idx = torch.tensor([0, 5, 99, -3, 64, 5], device="cuda")
+    dy = torch.ones(6, 16, dtype=torch.bfloat16, device="cuda")
+    dw = ops.embedding_backward(idx, dy, 64)
+    assert dw[5].float().eq(2).all() and dw[0].float().eq(1).all() and dw.float().sum() == 3 * 16
+
+
+def test_softcap_ce_mean_and_count():
+    rows = torch.randn(5000, device="cuda").abs()
+    t = torch.randint(0, 10, (5000,), device="cuda")
+    t[::4] = -1
+    loss, count = ops.softcap_cross_entropy_mean(rows * (t != -1), t, -1)
+    assert count.item() == float((t != -1).sum())
+    exp = (rows.double() * (t != -1)).sum() / (t != -1).sum()
+    assert abs(loss.item() - exp.item()) < 1e-5 * exp.item()
+    loss2, _ = ops.softcap_cross_entropy_mean(rows, t, -1)
+    assert torch.equal(loss2, ops.softcap_cross_entropy_mean(rows, t, -1)[0])
+    allign, n0 = ops.softcap_cross_entropy_mean(rows[:10], torch.full((10,), -1, device="cuda"), -1)
+    assert n0.item() == 0 and torch.isnan(allign)
+
+
+def test_scalar_scale_gradient():
+    from experiment_swa_kda_amd.model import scalar_scale
+    g = torch.Generator().manual_seed(11)
+    lam = torch.tensor([0.37], device="cuda", requires_grad=True)
+    t = torch.randn(2, 4095, 1, generator=g).bfloat16().cuda().requires_grad_()
+    y = scalar_scale(lam, t)
+    gy = torch.randn(y.shape, generator=g).bfloat16().cuda()
+    y.backward(gy)
+    assert torch.equal(y, lam.detach().bfloat16() * t.detach())
+    exp = (gy.double() * t.detach().double()).sum()
+    assert abs(lam.grad.item() - exp.item()) < 1e-4 * max(1.0, abs(exp.item()))
+    assert torch.equal(t.grad, gy * lam.detach().bfloat16())
