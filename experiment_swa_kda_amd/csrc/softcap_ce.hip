@@ -183,8 +183,9 @@ __global__ __launch_bounds__(kMeanThreads) void softcap_ce_mean_kernel(
   __shared__ float red_s[kMeanThreads / kWave], red_c[kMeanThreads / kWave];
   float s = 0.f, c = 0.f;
   for (long r = threadIdx.x; r < rows; r += kMeanThreads) {
-    s += loss_row[r];
-    c += targets[r] != ignore_index ? 1.f : 0.f;
+    const bool valid = targets[r] != ignore_index;
+    s += valid ? loss_row[r] : 0.f;
+    c += valid ? 1.f : 0.f;
   }
   s = wave_sum(s);
   c = wave_sum(c);
