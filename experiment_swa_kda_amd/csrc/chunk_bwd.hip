@@ -1417,3 +1417,69 @@ extern "C" int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* 
                              dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch,
                              stream);
 }
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free backward: the scratch lives in a file-scope device array instead of a
+// caller buffer.  Each device that loads the library holds its own copy of the array for
+// the life of the process; host code reaches it only through the address
+// hipGetSymbolAddress returns on that device (the array's name is not a device address
+// in host code).  The kernels write every scratch element they read, so nothing needs
+// clearing between calls; calls that overlap on one device share the array and race.
+// ---------------------------------------------------------------------------------------
+#include <mutex>
+
+namespace kda {
+
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+// Device address of this device's scratch array, looked up once per device.
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(KDA_ERR_LAUNCH, "chunk_backward_noalloc: no current device (or device index >= %d)",
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(KDA_ERR_LAUNCH, "chunk_backward_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return KDA_OK;
+}
+
+}  // namespace kda
+
+extern "C" size_t kda_chunk_backward_noalloc_max_scratch_bytes(void) { return kda::kNoAllocScratchBytes; }
+
+extern "C" int kda_chunk_backward_noalloc(const kda_chunk_problem* p, const void* q, const void* k,
+                                          const void* v, const void* gate, const void* beta_logits,
+                                          const float* A_log, const float* dt_bias,
+                                          const float* initial_state, const void* workspace,
+                                          const void* grad_output, const float* grad_final_state,
+                                          void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
+                                          float* dA_log, float* ddt_bias, float* dinitial_state,
+                                          hipStream_t stream) {
+  using namespace kda;
+  int rc = validate_problem(p, "chunk_backward_noalloc");
+  if (rc != KDA_OK) return rc;
+  const size_t need = sc_total_bytes(make_geom(p));
+  KDA_REQUIRE(need <= kNoAllocScratchBytes,
+              "chunk_backward_noalloc: problem needs %zu bytes of scratch, more than the %zu-byte "
+              "static array (use kda_chunk_backward with a caller buffer)",
+              need, kNoAllocScratchBytes);
+  void* sc = nullptr;
+  rc = noalloc_scratch(&sc);
+  if (rc != KDA_OK) return rc;
+  return chunk_backward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
+                             workspace, grad_output, grad_final_state, dq, dk, dv, dgate,
+                             dbeta_logits, dA_log, ddt_bias, dinitial_state, sc, stream);
+}

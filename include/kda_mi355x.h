@@ -124,6 +124,26 @@ int kda_chunk_backward(const kda_chunk_problem* p,
                        void* scratch, hipStream_t stream);
 
 /*
+ * kda_chunk_backward without the scratch argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The scratch is a file-scope device array
+ * of kda_chunk_backward_noalloc_max_scratch_bytes() bytes (128 MiB), held by every device
+ * the library runs on until the process ends; a problem whose
+ * kda_chunk_backward_scratch_bytes exceeds it is rejected (KDA_ERR_INVALID).  Every call on
+ * one device shares that array: calls that overlap on one device (different streams or
+ * threads) race.  All other arguments and results are those of kda_chunk_backward.
+ */
+int kda_chunk_backward_noalloc(const kda_chunk_problem* p,
+                               const void* q, const void* k, const void* v, const void* gate,
+                               const void* beta_logits, const float* A_log, const float* dt_bias,
+                               const float* initial_state, const void* workspace,
+                               const void* grad_output, const float* grad_final_state,
+                               void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
+                               float* dA_log, float* ddt_bias, float* dinitial_state,
+                               hipStream_t stream);
+size_t kda_chunk_backward_noalloc_max_scratch_bytes(void);
+
+/*
  * Runs one kernel of the chunked forward or backward on buffers that a full
  * kda_chunk_forward / kda_chunk_backward call with the same arguments has prepared, so a
  * benchmark can time that kernel alone.  No counterpart in the reference (it exists for
