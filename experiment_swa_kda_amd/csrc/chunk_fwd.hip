@@ -815,6 +815,380 @@ __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// segmented scan: the 64-step chain of a long sequence cut into parallel segments
+// ---------------------------------------------------------------------------
+// One chunk maps the state affinely, S' = M S + Kd^T U with M = diag(lam) - Kd^T W, and the
+// columns of S evolve independently.  A segment of L chunks therefore maps its entering
+// state as S_out = P S_in + Sigma with P = M_L ... M_1 (K x K) and Sigma its end state from
+// a zero start.  Three launches replace the one sequential pass:
+//  1. local (chunk_fwd_seg_kernel<.., false>): every segment but the last of every
+//     recurrence runs its chunks from the augmented start [0 | I] (V + K columns; the
+//     identity columns see U = 0), giving [Sigma | P] -- segments run in parallel;
+//  2. combine (chunk_fwd_combine_kernel): S_in(j+1) = P_j S_in(j) + Sigma_j, sequential over
+//     the segments of one recurrence, one wave per V strip (S as hi + lo bf16 operands);
+//  3. replay (chunk_fwd_seg_kernel<.., true>): every segment reruns its chunks from its true
+//     entering state and writes the state / delta histories exactly as the one-pass scan.
+// Sequential depth: L + (segments - 1) + L steps instead of the chunk count.  In the
+// segment kernels one workgroup owns several strips and every compute wave owns whole
+// strips (its delta tiles and state tiles), so a step needs no exchange between waves:
+// a loader wave fills an LDS ring with the chunk's -W, Kd^T, U strips and lam, and the one
+// barrier per chunk only recycles ring slots.
+constexpr int kSegRing = 3;
+constexpr int kSegCompute = 4;   // compute waves, one strip each (every wave reads the
+                                 // chunk's whole -W and Kd^T from LDS)
+constexpr int kSegSPW = 1;
+constexpr int kSegThreads = (kSegCompute + 1) * kWave;
+
+template <int K, int V, bool REPLAY>
+struct SegCfg {
+  static constexpr int NSTRIPS = REPLAY ? V / 16 : (V + K) / 16;  // strips per (rec, segment)
+  static constexpr int SPW = kSegSPW;                               // strips per compute wave
+  static constexpr int SPG = kSegCompute * SPW;                     // strips per workgroup
+  static constexpr int GROUPS = NSTRIPS / SPG;                      // workgroups per (rec, segment)
+  static_assert(NSTRIPS % SPG == 0, "strips split evenly over the workgroups");
+  static constexpr int off_w = 0;                      // -W fragments, 64 x K bf16
+  static constexpr int off_kdt = off_w + 64 * K * 2;   // Kd^T fragments, K x 64 bf16
+  static constexpr int off_u = off_kdt + K * 64 * 2;   // U, C layout, SPG strips x 2 KB
+  static constexpr int off_lam = off_u + SPG * 2048;   // lam, K f32
+  static constexpr int slot = off_lam + K * 4;
+  static constexpr int n_load = (64 * K * 2) / 1024 + (K * 64 * 2) / 1024 + 2 * SPG + 1;
+  static constexpr int bytes = kSegRing * slot;
+};
+
+// Offset (in bf16 elements) of P[row][col] in the combine kernel's A-operand fragment order:
+// fragment (row / 16, col / 32), lane row % 16 + 16 * ((col % 16) / 4), element
+// 4 * ((col % 32) / 16) + col % 4 -- the permuted contraction order of the state operands.
+template <int K>
+__device__ __forceinline__ size_t segp_frag_off(int row, int col) {
+  const int lane = row % 16 + 16 * ((col % 16) / 4);
+  const int e = 4 * ((col % 32) / 16) + col % 4;
+  return (((size_t)(row / 16) * (K / 32) + col / 32) * 64 + lane) * 8 + e;
+}
+
+template <int K, int V, bool REPLAY>
+__global__ __launch_bounds__(kSegThreads) void chunk_fwd_seg_kernel(FwdArgs a, int seg_len, int max_segs) {
+  using C = SegCfg<K, V, REPLAY>;
+  constexpr int KT = K / 16, NB = K / 32, VS = V / 16, SPW = C::SPW;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int H = a.H;
+  int rs, group;
+  if (!xcd_strip_coords(a.num_seqs * H * max_segs, C::GROUPS, rs, group)) return;
+  const int rec = rs / max_segs, seg = rs % max_segs;
+  const int seq = rec / H, h = rec % H;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int n = sq.y;
+  const int nseg = (n + seg_len - 1) / seg_len;
+  const int u_first = group * C::SPG;  // the workgroup's strips, V strips first
+  int strip[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) strip[j] = u_first + (wave < kSegCompute ? wave : 0) * SPW + j;
+  if (REPLAY) {
+    if (n <= 0) {  // empty sequence: the final state is the initial one
+      if (seg == 0 && wave < kSegCompute && a.sfin) {
+        for (int j = 0; j < SPW; ++j)
+          for (int kt = 0; kt < KT; ++kt) {
+            const size_t o = (((size_t)seq * H + h) * V + 16 * strip[j] + lr) * K + 16 * kt + 4 * kg;
+            *(float4*)(a.sfin + o) = a.s0 ? *(const float4*)(a.s0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+      }
+      return;
+    }
+    if (seg >= nseg) return;
+  } else if (seg >= nseg - 1) {
+    return;  // the last segment's map is never needed
+  }
+  const int c_begin = seg * seg_len;
+  const int steps = min(n, c_begin + seg_len) - c_begin;
+
+  if (wave == kSegCompute) {
+    // ---- loader wave: direct global->LDS ring, a fixed number of loads per chunk ----
+    auto issue = [&](int ci) {
+      const int c = c_begin + (ci < steps ? ci : steps - 1);
+      const size_t tile = (size_t)(sq.x + c) * H + h;
+      char* slot = smem + (ci % kSegRing) * C::slot;
+      const char* w = (const char*)((const bf16*)a.ws.p[R_WF] + tile * 64 * K) + lane * 16;
+#pragma unroll
+      for (int b = 0; b < (64 * K * 2) / 1024; ++b) dma16(w + b * 1024, slot + C::off_w + b * 1024);
+      const char* kd = (const char*)((const bf16*)a.ws.p[R_KDTF] + tile * K * 64) + lane * 16;
+#pragma unroll
+      for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(kd + b * 1024, slot + C::off_kdt + b * 1024);
+      const char* u0 = (const char*)((const bf16*)a.ws.p[R_UF] + tile * 64 * V) + lane * 16;
+#pragma unroll
+      for (int j = 0; j < C::SPG; ++j) {
+        const int us = min(u_first + j, VS - 1);  // strips past V load a valid strip, unused
+        dma16(u0 + (size_t)us * 2048, slot + C::off_u + j * 2048);
+        dma16(u0 + (size_t)us * 2048 + 1024, slot + C::off_u + j * 2048 + 1024);
+      }
+      if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + C::off_lam);
+    };
+#pragma unroll
+    for (int d = 0; d < kSegRing - 1; ++d) issue(d);
+    for (int ci = 0; ci < steps; ++ci) {
+      wait_vmcnt<(kSegRing - 2) * C::n_load>();  // chunk ci's loads have landed
+      ring_barrier();                             // B(ci); the slot of ci - 1 fully read
+      issue(ci + kSegRing - 1);
+    }
+    ring_barrier();   // B(steps)
+    wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
+    return;
+  }
+
+  // ---- compute wave: SPW strips, all of their delta and state tiles ----
+  f32x4 S[SPW][KT];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const float* sin = nullptr;
+    size_t sin_off = 0;
+    if (REPLAY) {
+      sin = seg == 0 ? a.s0 : (const float*)a.ws.p[R_SIN] + ((size_t)rec * max_segs + seg) * V * K;
+      sin_off = (seg == 0 ? ((size_t)seq * H + h) * V * K : 0) + (size_t)(16 * strip[j] + lr) * K;
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const int k0 = 16 * kt + 4 * kg;
+      if (REPLAY) {
+        if (sin) {
+          const float4 x = *(const float4*)(sin + sin_off + k0);
+          S[j][kt][0] = x.x; S[j][kt][1] = x.y; S[j][kt][2] = x.z; S[j][kt][3] = x.w;
+        } else {
+          S[j][kt] = zero4();
+        }
+      } else {
+        // Sigma strips start at zero; P strip p starts as columns 16p.. of the identity
+        const int col = 16 * (strip[j] - VS) + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[j][kt][r] = (strip[j] >= VS && k0 + r == col) ? 1.f : 0.f;
+      }
+    }
+  }
+  for (int ci = 0; ci < steps; ++ci) {
+    ring_barrier();  // B(ci): slot ci loaded
+    const char* slot = smem + (ci % kSegRing) * C::slot;
+    // every operand of the step requested before the first product
+    bf16x8 wf[4][NB], kf[KT][2];
+    float4 lam[KT];
+    bf16x4 uf[SPW][4];
+    // (issued in the order of first use: LDS reads return in order, so the first products
+    // wait only for their own operands)
+#pragma unroll
+    for (int j = 0; j < SPW; ++j)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+        uf[j][rt] = *(const bf16x4*)(slot + C::off_u + (strip[j] - u_first) * 2048 + (rt * 64 + lane) * 8);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < NB; ++s)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) wf[rt][s] = *(const bf16x8*)(slot + C::off_w + ((rt * NB + s) * 64 + lane) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) lam[kt] = *(const float4*)(slot + C::off_lam + (16 * kt + 4 * kg) * 4);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) kf[kt][t] = *(const bf16x8*)(slot + C::off_kdt + ((kt * 2 + t) * 64 + lane) * 16);
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of every product
+    // the state as B operands: fragment s packs tiles 2s (low half) and 2s + 1 (high half)
+    bf16x8 Bs[SPW][NB];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j)
+#pragma unroll
+      for (int s = 0; s < NB; ++s) Bs[j][s] = pack_tiles(S[j][2 * s], S[j][2 * s + 1]);
+    const size_t tile = (size_t)(sq.x + c_begin + ci) * H + h;
+    if (REPLAY) {
+      // histories of the entering state: f32 [K][V] and the bf16 B-operand fragments
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        float* SH = (float*)a.ws.p[R_SH] + tile * K * V + 16 * strip[j] + lr;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) SH[(size_t)(16 * kt + 4 * kg + r) * V] = S[j][kt][r];
+        bf16* SHBF = (bf16*)a.ws.p[R_SHBF] + tile * V * K + (size_t)strip[j] * 16 * K;
+#pragma unroll
+        for (int s = 0; s < NB; ++s) *(bf16x8*)(SHBF + ((size_t)s * 64 + lane) * 8) = Bs[j][s];
+      }
+    }
+    // delta = U + (-W) S: 4 x SPW independent row-tile chains sharing each -W fragment
+    f32x4 dl[SPW][4];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dl[j][rt][r] = strip[j] < VS ? to_f32(uf[j][rt][r]) : 0.f;
+#pragma unroll
+    for (int s = 0; s < NB; ++s)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) dl[j][rt] = mfma16(wf[rt][s], Bs[j][s], dl[j][rt]);
+    // delta as B operands (fragment t packs row tiles 2t and 2t + 1)
+    bf16x8 D[SPW][2];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      D[j][0] = pack_tiles(dl[j][0], dl[j][1]);
+      D[j][1] = pack_tiles(dl[j][2], dl[j][3]);
+      if (REPLAY) {
+        bf16* DLF = (bf16*)a.ws.p[R_DLF] + tile * 64 * V + (size_t)strip[j] * 16 * 64;
+        *(bf16x8*)(DLF + (size_t)lane * 8) = D[j][0];
+        *(bf16x8*)(DLF + (size_t)(64 + lane) * 8) = D[j][1];
+      }
+    }
+    // S = lam S + Kd^T delta: KT x SPW independent chains
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        f32x4 acc;
+        acc[0] = lam[kt].x * S[j][kt][0];
+        acc[1] = lam[kt].y * S[j][kt][1];
+        acc[2] = lam[kt].z * S[j][kt][2];
+        acc[3] = lam[kt].w * S[j][kt][3];
+        S[j][kt] = mfma16(kf[kt][0], D[j][0], acc);
+      }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) S[j][kt] = mfma16(kf[kt][1], D[j][1], S[j][kt]);
+  }
+  ring_barrier();  // B(steps)
+  // segment end
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    if (REPLAY) {
+      if (seg == nseg - 1 && a.sfin) {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+          *(float4*)(a.sfin + (((size_t)seq * H + h) * V + 16 * strip[j] + lr) * K + 16 * kt + 4 * kg) =
+              make_float4(S[j][kt][0], S[j][kt][1], S[j][kt][2], S[j][kt][3]);
+      }
+    } else if (strip[j] < VS) {
+      float* sg = (float*)a.ws.p[R_SEGS] + ((size_t)rec * max_segs + seg) * V * K + (size_t)(16 * strip[j] + lr) * K;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+        *(float4*)(sg + 16 * kt + 4 * kg) = make_float4(S[j][kt][0], S[j][kt][1], S[j][kt][2], S[j][kt][3]);
+    } else {
+      // P in the combine kernel's bf16 A-operand fragment order; this lane holds column
+      // 16p + lr of rows 16kt + 4kg .. + 3
+      bf16* pg = (bf16*)a.ws.p[R_SEGP] + ((size_t)rec * max_segs + seg) * K * K;
+      const int col = 16 * (strip[j] - VS) + lr;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pg[segp_frag_off<K>(16 * kt + 4 * kg + r, col)] = to_bf16(S[j][kt][r]);
+    }
+  }
+}
+
+// S_in(j+1) = P_j S_in(j) + Sigma_j over the segments of one recurrence.  One workgroup per
+// (recurrence, V strip); wave w owns state tiles w * TPW .. (w + 1) * TPW - 1.  Each step the
+// waves publish their tiles as hi + lo bf16 B-operand halves in LDS (about 16 mantissa
+// bits of the state), one barrier, and every wave multiplies its rows of P_j (bf16
+// fragments written by the local kernel, prefetched a step ahead) by the whole state.
+constexpr int kCombThreads = 4 * kWave;
+constexpr int kCombBatch = 8;
+
+template <int K, int V>
+__global__ __launch_bounds__(kCombThreads) void chunk_fwd_combine_kernel(FwdArgs a, int seg_len, int max_segs) {
+  constexpr int KT = K / 16, NB = K / 32, VS = V / 16, TPW = KT / 4;
+  __shared__ __attribute__((aligned(16))) char sB[2][2][NB][kWave * 16];  // [parity][hi/lo][frag]
+  const int H = a.H;
+  int rec, strip;
+  if (!xcd_strip_coords(a.num_seqs * H, VS, rec, strip)) return;
+  const int seq = rec / H, h = rec % H;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, lr = lane % 16, kg = lane / 16;
+  const int n = ((const int2*)a.ws.p[R_SEQS])[seq].y;
+  const int nseg = (n + seg_len - 1) / seg_len;
+  if (nseg <= 1) return;
+  const int v = 16 * strip + lr;
+  f32x4 S[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int kt = wave * TPW + t;
+    if (a.s0) {
+      const float4 x = *(const float4*)(a.s0 + (((size_t)seq * H + h) * V + v) * K + 16 * kt + 4 * kg);
+      S[t][0] = x.x; S[t][1] = x.y; S[t][2] = x.z; S[t][3] = x.w;
+    } else {
+      S[t] = zero4();
+    }
+  }
+  const bf16* P0 = (const bf16*)a.ws.p[R_SEGP] + (size_t)rec * max_segs * K * K;
+  const float* G0 = (const float*)a.ws.p[R_SEGS] + (size_t)rec * max_segs * V * K + (size_t)v * K;
+  // every step's P rows and Sigma for this wave, requested up front in batches of
+  // kCombBatch steps (one memory round trip per batch instead of one per step)
+  bf16x8 pa[kCombBatch][TPW][NB];
+  float4 sg[kCombBatch][TPW];
+  for (int j = 0; j + 1 < nseg; ++j) {
+    const int jb = j % kCombBatch;
+    if (jb == 0) {
+#pragma unroll
+      for (int b = 0; b < kCombBatch; ++b) {
+        const int jj = min(j + b, nseg - 2);
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          const int kt = wave * TPW + t;
+#pragma unroll
+          for (int s = 0; s < NB; ++s)
+            pa[b][t][s] = *(const bf16x8*)(P0 + (size_t)jj * K * K + (((size_t)kt * NB + s) * 64 + lane) * 8);
+          sg[b][t] = *(const float4*)(G0 + (size_t)jj * V * K + 16 * kt + 4 * kg);
+        }
+      }
+    }
+    char(*buf)[NB][kWave * 16] = sB[j & 1];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int kt = wave * TPW + t;
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        hi[r] = to_bf16(S[t][r]);
+        lo[r] = to_bf16(S[t][r] - to_f32(hi[r]));
+      }
+      *(bf16x4*)(buf[0][kt / 2] + lane * 16 + (kt % 2) * 8) = hi;
+      *(bf16x4*)(buf[1][kt / 2] + lane * 16 + (kt % 2) * 8) = lo;
+    }
+    __syncthreads();
+    bf16x8 Bh[NB], Bl[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      Bh[s] = *(const bf16x8*)(buf[0][s] + lane * 16);
+      Bl[s] = *(const bf16x8*)(buf[1][s] + lane * 16);
+    }
+    // pick this step's operands (jb is uniform; unrolled select keeps them in registers)
+    bf16x8 pc[TPW][NB];
+    float4 gc[TPW];
+#pragma unroll
+    for (int b = 0; b < kCombBatch; ++b)
+      if (b == jb) {
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          gc[t] = sg[b][t];
+#pragma unroll
+          for (int s = 0; s < NB; ++s) pc[t][s] = pa[b][t][s];
+        }
+      }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      f32x4 acc;
+      acc[0] = gc[t].x; acc[1] = gc[t].y; acc[2] = gc[t].z; acc[3] = gc[t].w;
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        acc = mfma16(pc[t][s], Bh[s], acc);
+        acc = mfma16(pc[t][s], Bl[s], acc);
+      }
+      S[t] = acc;
+    }
+    float* out = (float*)a.ws.p[R_SIN] + ((size_t)rec * max_segs + j + 1) * V * K + (size_t)v * K;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+      *(float4*)(out + 16 * (wave * TPW + t) + 4 * kg) = make_float4(S[t][0], S[t][1], S[t][2], S[t][3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // output:  O = Qg S + A delta  (chunk-parallel, after the scan)
 // ---------------------------------------------------------------------------
 // One 256-thread workgroup per (chunk, head); wave w owns the 16-token row tile w and
@@ -926,6 +1300,13 @@ int validate_problem(const kda_chunk_problem* p, const char* who) {
   return KDA_OK;
 }
 
+// Segmented scans: when the (sequence, head) recurrences times the V/16 column strips are
+// too few to fill the chip and sequences are long, each sequence's chunks are cut into
+// segments of ~sqrt(chunks) chunks that are scanned in parallel (see the segmented scan
+// kernels).  A pure function of the problem, so workspace sizing and launches agree.
+constexpr int kSegMinChunks = 96;     // shorter sequences run in one pass (measured: no gain at 64)
+constexpr int kSegStripLimit = 512;   // recurrences x V/16 strips at which one pass fills the chip
+
 ChunkGeom make_geom(const kda_chunk_problem* p) {
   ChunkGeom g;
   const int nc = (p->seq_len + kChunk - 1) / kChunk;
@@ -934,6 +1315,15 @@ ChunkGeom make_geom(const kda_chunk_problem* p) {
   g.K = p->key_dim;
   g.V = p->value_dim;
   g.num_seqs = p->num_seqs;
+  g.seg_len = 0;
+  g.max_segs = 1;
+  // nc bounds the chunk count of any one sequence (a packed sequence has at most T tokens)
+  if (nc >= kSegMinChunks && (long)p->num_seqs * p->heads * (p->value_dim / 16) < kSegStripLimit) {
+    int L = 4;
+    while (L * L < nc) ++L;
+    g.seg_len = L;
+    g.max_segs = (nc + L - 1) / L;
+  }
   return g;
 }
 
@@ -965,9 +1355,34 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
       attr = true;
     }
     const int nrec = p->num_seqs * p->heads;
-    const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
-    hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), smem, stream, a);
-    KDA_LAUNCH_CHECK("chunk_forward scan");
+    if (g.seg_len == 0) {
+      const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
+      hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), smem, stream, a);
+      KDA_LAUNCH_CHECK("chunk_forward scan");
+    } else {
+      auto local = chunk_fwd_seg_kernel<K, V, false>;
+      auto replay = chunk_fwd_seg_kernel<K, V, true>;
+      using CL = SegCfg<K, V, false>;
+      using CR = SegCfg<K, V, true>;
+      static bool seg_attr = false;
+      if (!seg_attr) {
+        if (hipFuncSetAttribute((const void*)local, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CL::bytes) != hipSuccess ||
+            hipFuncSetAttribute((const void*)replay, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CR::bytes) != hipSuccess)
+          return set_error(KDA_ERR_LAUNCH, "chunk_forward: segmented scan LDS attribute failed");
+        seg_attr = true;
+      }
+      const int nrs = nrec * g.max_segs;
+      hipLaunchKernelGGL(local, dim3(kXcds * CL::GROUPS * ((nrs + kXcds - 1) / kXcds)), dim3(kSegThreads),
+                         CL::bytes, stream, a, g.seg_len, g.max_segs);
+      KDA_LAUNCH_CHECK("chunk_forward segment maps");
+      auto comb = chunk_fwd_combine_kernel<K, V>;
+      hipLaunchKernelGGL(comb, dim3(kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds)), dim3(kCombThreads), 0, stream,
+                         a, g.seg_len, g.max_segs);
+      KDA_LAUNCH_CHECK("chunk_forward segment combine");
+      hipLaunchKernelGGL(replay, dim3(kXcds * CR::GROUPS * ((nrs + kXcds - 1) / kXcds)), dim3(kSegThreads),
+                         CR::bytes, stream, a, g.seg_len, g.max_segs);
+      KDA_LAUNCH_CHECK("chunk_forward segment replay");
+    }
   }
   if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_OUTPUT))) {
     auto outk = chunk_fwd_output_kernel<K, V>;

@@ -46,6 +46,10 @@ enum WsRegion {
   R_SH,          // f32  [tile][K][V]   state entering the chunk (written by the scan)
   R_SHBF,        // bf16 the same state as B-operand fragments [V/16 strip][K/32][64][8], permuted
   R_DLF,         // bf16 delta = U - W S as B-operand fragments [V/16 strip][2][64][8] (scan), permuted
+  // segmented scan (only when ChunkGeom::seg_len > 0; [rec = seq * H + head][segment] ...)
+  R_SEGP,        // bf16 [rec][seg] K x K  P = product of the segment's chunk maps, as MFMA A fragments
+  R_SEGS,        // f32  [rec][seg][V][K]  Sigma = the segment's end state from a zero start (V-first)
+  R_SIN,         // f32  [rec][seg][V][K]  true state entering the segment (V-first; seg >= 1)
   R_COUNT
 };
 
@@ -69,6 +73,8 @@ struct ChunkGeom {
   int K;
   int V;
   int num_seqs;
+  int seg_len;   // chunks per scan segment; 0: the scans run each sequence in one pass
+  int max_segs;  // segments of the longest possible sequence (1 when seg_len == 0)
 };
 
 __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
@@ -87,6 +93,8 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
     case R_SH: return nt * K * V * 4;
     case R_SHBF: return nt * K * V * 2;
     case R_DLF: return nt * 64 * V * 2;
+    case R_SEGP: return g.seg_len ? (size_t)g.num_seqs * g.heads * g.max_segs * K * K * 2 : 0;
+    case R_SEGS: case R_SIN: return g.seg_len ? (size_t)g.num_seqs * g.heads * g.max_segs * V * K * 4 : 0;
     default: return 0;
   }
 }

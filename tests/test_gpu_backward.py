@@ -134,6 +134,24 @@ def test_long_sequences_states_and_gradients(T, KV):
     check(gpu_grads(d, "precomputed", do, dsT), oracle_grads(d, "precomputed", do, dsT))
 
 
+@pytest.mark.parametrize("B,T,H,KV,gate", [(1, 8192, 2, (128, 128), "precomputed"),
+                                            (1, 6500, 1, (64, 64), "k3")])
+def test_segmented_scan_long_sequence(B, T, H, KV, gate):
+    """Sequences of >= 96 chunks with few recurrences take the segmented forward scan
+    (segment maps, combine, replay; 11-12 chunks per segment, ragged last segment and
+    chunk): output, final state and every gradient against the float64 oracle."""
+    K, V = KV
+    d = make_kda_inputs(B, T, H, K, V, seed=T + 1, gate=gate, state=True, dist="baseline")
+    o, fin, _ = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], d["s0"],
+                                  True, -5.0, K ** -0.5, gate=gate)
+    gm = "k3" if gate == "k3" else "logdecay"
+    eo, ef = O.kda_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
+                           np64(d["A_log"]), np64(d["dt_bias"]), initial_state=np64(d["s0"]), gate_mode=gm)
+    assert rel_err(o, eo) < 2e-2 and rel_err(fin, ef) < 2e-2, (rel_err(o, eo), rel_err(fin, ef))
+    do, dsT = cotangents(d, 5)
+    check(gpu_grads(d, gate, do, dsT), oracle_grads(d, gate, do, dsT))
+
+
 def test_varlen_mixed_lengths():
     """Packed sequences of 1, 3, 58 and 2 chunks, each with its own initial state."""
     lens = [40, 150, 3700, 100]
