@@ -791,11 +791,13 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
   const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
   const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
-  // dQg/dKd/dKb of this tile; they are overwritten with dqh, dkh and dG (same lane, same
-  // address) to carry them across the barrier that completes the per-row dot products
-  float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
-  float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
-  float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
+  // dQg/dKd/dKb of this tile (from the dense role)
+  const float* DQG = (const float*)a.sc.p[S_DQG] + tile * 64 * K;
+  const float* DKD = (const float*)a.sc.p[S_DKD] + tile * 64 * K;
+  const float* DKB = (const float*)a.sc.p[S_DKB] + tile * 64 * K;
+  // each wave's dqh, dkh and dG of its item in pass 0 and pass 1, held in registers across
+  // the barrier that completes the per-row dot products
+  f32x4 keep_q[2], keep_k[2], keep_g[2];
 
   // ---- P0: stage q, k (bf16), G, dA, dM' (bf16), beta and the per-row norm factors ----
   if (tid < 4) sF[tid] = 0;
@@ -1023,9 +1025,11 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
           sPK[ct * 64 + ii] = pk;
         }
       }
-      *(f32x4*)(DQG + ((size_t)p * 64 + plane) * 4) = dqs;
-      *(f32x4*)(DKD + ((size_t)p * 64 + plane) * 4) = dks;
-      *(f32x4*)(DKB + ((size_t)p * 64 + plane) * 4) = dgs;
+      if (pass == 0) {
+        keep_q[0] = dqs; keep_k[0] = dks; keep_g[0] = dgs;
+      } else {
+        keep_q[1] = dqs; keep_k[1] = dks; keep_g[1] = dgs;
+      }
       glp = lane_stride_sum<16>(glp);
       if (kg == 0) sGL[rt * K + c] = glp;
     }
@@ -1052,15 +1056,13 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
   __syncthreads();
 
   // ---- P2: L2-norm chains; dq, dk (bf16) and dG into LDS (q, k, G are consumed) ----
+  // (the items of P1: wave w < NIH owns item (w % 4, w / 4 + pass * HALF / 16) of each pass)
 #pragma unroll
-  for (int n = 0; n < IPW; ++n) {
-    const int p = wave + n * kVjpWaves;
-    if (p >= NKT) break;
-    const int rt = p % 4, ct = p / 4;
+  for (int n = 0; n < 2; ++n) {
+    if (wave >= NIH) break;
+    const int rt = wave % 4, ct = n * (HALF / 16) + wave / 4;
     const int c = 16 * ct + lr;
-    const f32x4 dqs = *(const f32x4*)(DQG + ((size_t)p * 64 + lane) * 4);
-    const f32x4 dks = *(const f32x4*)(DKD + ((size_t)p * 64 + lane) * 4);
-    const f32x4 dgs = *(const f32x4*)(DKB + ((size_t)p * 64 + lane) * 4);
+    const f32x4 dqs = keep_q[n], dks = keep_k[n], dgs = keep_g[n];
     float dqv[4], dkv[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
