@@ -855,16 +855,6 @@ struct SegCfg {
   static constexpr int bytes = kSegRing * slot;
 };
 
-// Offset (in bf16 elements) of P[row][col] in the combine kernel's A-operand fragment order:
-// fragment (row / 16, col / 32), lane row % 16 + 16 * ((col % 16) / 4), element
-// 4 * ((col % 32) / 16) + col % 4 -- the permuted contraction order of the state operands.
-template <int K>
-__device__ __forceinline__ size_t segp_frag_off(int row, int col) {
-  const int lane = row % 16 + 16 * ((col % 16) / 4);
-  const int e = 4 * ((col % 32) / 16) + col % 4;
-  return (((size_t)(row / 16) * (K / 32) + col / 32) * 64 + lane) * 8 + e;
-}
-
 template <int K, int V, bool REPLAY>
 __global__ __launch_bounds__(kSegThreads) void chunk_fwd_seg_kernel(FwdArgs a, int seg_len, int max_segs) {
   using C = SegCfg<K, V, REPLAY>;
@@ -1071,14 +1061,15 @@ __global__ __launch_bounds__(kSegThreads) void chunk_fwd_seg_kernel(FwdArgs a, i
       for (int kt = 0; kt < KT; ++kt)
         *(float4*)(sg + 16 * kt + 4 * kg) = make_float4(S[j][kt][0], S[j][kt][1], S[j][kt][2], S[j][kt][3]);
     } else {
-      // P in the combine kernel's bf16 A-operand fragment order; this lane holds column
+      // P as bf16 A-operand fragments with the permuted contraction order of the combine
+      // kernel's state operands; this lane holds column
       // 16p + lr of rows 16kt + 4kg .. + 3
       bf16* pg = (bf16*)a.ws.p[R_SEGP] + ((size_t)rec * max_segs + seg) * K * K;
       const int col = 16 * (strip[j] - VS) + lr;
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pg[segp_frag_off<K>(16 * kt + 4 * kg + r, col)] = to_bf16(S[j][kt][r]);
+        for (int r = 0; r < 4; ++r) pg[perm_frag_elem(K, 16 * kt + 4 * kg + r, col)] = to_bf16(S[j][kt][r]);
     }
   }
 }
@@ -1150,7 +1141,9 @@ __global__ __launch_bounds__(kCombThreads) void chunk_fwd_combine_kernel(FwdArgs
       *(bf16x4*)(buf[0][kt / 2] + lane * 16 + (kt % 2) * 8) = hi;
       *(bf16x4*)(buf[1][kt / 2] + lane * 16 + (kt % 2) * 8) = lo;
     }
-    __syncthreads();
+    // LDS only: a fence-free barrier (the prefetched loads and earlier stores stay in flight)
+    wait_lgkm0();
+    ring_barrier();
     bf16x8 Bh[NB], Bl[NB];
 #pragma unroll
     for (int s = 0; s < NB; ++s) {

@@ -20,6 +20,18 @@ __host__ __device__ inline size_t frag_off(int C, int rt, int s, int lane) {
   return ((((size_t)rt * (C / 32) + s) * 64) + lane) * 8;
 }
 
+// Offsets (bf16 elements) of element X[row][col] of a C-column matrix in fragment-major
+// order, natural (contraction index 32s + 8(l/16) + e) and permuted (see below).
+__host__ __device__ inline size_t nat_frag_elem(int C, int row, int col) {
+  const int lane = row % 16 + 16 * ((col % 32) / 8);
+  return (((size_t)(row / 16) * (C / 32) + col / 32) * 64 + lane) * 8 + col % 8;
+}
+__host__ __device__ inline size_t perm_frag_elem(int C, int row, int col) {
+  const int lane = row % 16 + 16 * ((col % 16) / 4);
+  const int e = 4 * ((col % 32) / 16) + col % 4;
+  return (((size_t)(row / 16) * (C / 32) + col / 32) * 64 + lane) * 8 + e;
+}
+
 // Arrays marked "permuted" keep their fragment shape but order each 32-wide step of the
 // contraction index as 32s + 16(e/4) + 4(l/16) + e%4 for element e of lane l (instead of
 // 32s + 8(l/16) + e): the order in which a lane holds two stacked MFMA accumulator tiles,
