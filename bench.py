@@ -201,6 +201,20 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42, graphed=True)
             "execution": "hip_graph" if graphed else "eager", "reference_gb10_tok_per_s": 44942}
 
 
+def load_mfma_busy():
+    """MFMA-busy fraction per chunk kernel from the committed rocprofv3 --pmc summary
+    (SQ_VALU_MFMA_BUSY_CYCLES over dispatch cycles x 1024 SIMDs), or {}."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mfma_util_config2.txt")
+    out = {}
+    if os.path.exists(path):
+        for line in open(path):
+            if line.startswith("#") or not line.strip():
+                continue
+            f = line.split()
+            out[f[0]] = float(f[-1])
+    return out
+
+
 def load_traffic():
     """HBM bytes per dispatch from the committed rocprofv3 --pmc summary, or {}."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_config2.txt")
@@ -422,6 +436,26 @@ def main():
     traffic = load_traffic()
     dom = max(STEP_KERNELS, key=kt.get)  # the largest per-step kernel
     achieved = tiles * KERNEL_FLOP_PER_TILE[dom] / (kt[dom] * 1e-3) / 1e12
+    busy = load_mfma_busy()
+    # the bound comes from the counters: HBM bytes moved per second (FETCH + WRITE of the
+    # committed --pmc summary over the live kernel time) against the MFMA-busy fraction
+    hbm_frac = traffic[dom] / (kt[dom] * 1e-3) / 1e9 / PEAK_HBM_GBS if dom in traffic else None
+    mfma_frac = busy.get(dom, achieved / PEAK_BF16_TFLOPS)
+    if hbm_frac is not None and hbm_frac > mfma_frac:
+        # algorithmic bytes: the backward's compulsory I/O (q, k, v, dO, g, beta in; dq, dk,
+        # dv, dg, dbeta out) -- everything the VJP kernel moves beyond this is re-reads
+        elems = B * T * H
+        alg = elems * (K * 2 + K * 2 + V * 2 + V * 2 + K * 4 + 2) + elems * (K * 2 + K * 2 + V * 2 + K * 4 + 2)
+        gbs = alg / (kt[dom] * 1e-3) / 1e9
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": traffic[dom],
+                    "algorithmic_bytes": alg, "measured_hbm_frac": round(hbm_frac, 4),
+                    "mfma": {"achieved_tflops": round(achieved, 3), "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
+                             "busy_frac": busy.get(dom)}}
+    else:
+        roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom),
+                    "busy_frac": busy.get(dom), "measured_hbm_frac": None if hbm_frac is None else round(hbm_frac, 4)}
     line = {
         "metric": "KDA fwd+bwd TFLOP/s (B2 T4096 H3 D128 bf16)",
         "value": round(flop / (ms * 1e-3) / 1e12, 3),
@@ -445,9 +479,8 @@ def main():
         "k3_gate": {"ms_per_step": round(results["k3"][0], 4), "ms_fwd": round(results["k3"][1], 4),
                     "ms_per_step_eager": round(results["k3"][4], 4)},
         "kernel_ms": {n: round(v, 4) for n, v in kt.items()},
-        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom)},
+        "roofline": roofline,
+        "mfma_busy_frac": busy or None,
         "hbm_traffic_bytes": traffic or None,
         "reference_gb10_ms_fwd_bwd": 3.916,
     }
