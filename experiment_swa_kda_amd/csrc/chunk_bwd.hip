@@ -28,8 +28,14 @@
 //    tile around the first (row side) or last (column side) row of each 16-row block, so
 //    every factor is <= 1 or bounded by the block's span; a tile with a block whose decay
 //    span exceeds 80 nats runs an exact per-pair f32 loop instead.
+//  * fused launch (the whole backward in one call): the scan members and ticketed tile
+//    workgroups share one grid; a tile runs its dense and decay parts as soon as the scan
+//    has finalised its chunk, so the VJP work overlaps the latency-bound scan (see
+//    chunk_bwd_fused_kernel).  The staged entry points keep the separate launches.
 #include "chunk_host.hpp"
 #include "kda_device.hpp"
+
+#include <cstdlib>
 
 namespace kda {
 
@@ -74,6 +80,7 @@ struct BwdArgs {
 // the chunk two steps on) right after it; its W^T and lam are last read before the next S1
 // and are refilled after that.
 constexpr int kBwdRing = 2;
+constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 constexpr int kBwdThreads = 6 * kWave;
 
 template <int K, int V>
@@ -127,8 +134,52 @@ __device__ __forceinline__ void prefetch_lines(const PrefetchList& pf, int w, in
   if (acc == 0x9e3779b9u) *(unsigned*)sink = acc;  // keeps the loads; the value is irrelevant
 }
 
-template <int K, int V>
-__global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, PrefetchList pf, int scan_blocks) {
+// Scan -> dense hand-off inside the fused backward.  The histories go through memory with
+// system-coherent cache policy (sc0 sc1): stores write through the XCD's L2, loads miss in
+// the non-coherent caches.  No L2 write-back or invalidate is then needed around the
+// counts, which matters: the write-back of a whole L2 per scan step costs microseconds on
+// the scan's serial chain.  Buffer accesses take a wave-uniform base.
+constexpr int kCoherentPolicy = 1 | 16;  // sc0 | sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void store4_coherent(float* base, int off, float4 x) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = {x.x, x.y, x.z, x.w};
+  __builtin_amdgcn_raw_buffer_store_b128(v, raw_rsrc(base), off * 4, 0, kCoherentPolicy);
+}
+__device__ __forceinline__ float4 load4_coherent(const float* base, int off) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), off * 4, 0, kCoherentPolicy);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Layout of the fused backward's sync words (ints): [0] ticket, [1] abort, record rec's
+// count of finished steps at kSyncRec + 32 rec (one 128-byte line each), then per tile the
+// number of strips that finished it.
+constexpr int kSyncRec = 32;
+__host__ __device__ inline int sync_words(int nrec, int tiles) { return kSyncRec + 32 * nrec + tiles; }
+
+// One more step of this strip is in memory: every store of the step was written through
+// and waited for (vmcnt 0) before the barrier that precedes the call.  The strip that
+// completes a step on all strips of the record raises the record's count to step + 1 (the
+// strips are independent workgroups that drift apart by several steps; the last to finish
+// step r finishes after every strip's step r - 1, and atomic max keeps the count monotone
+// whatever order the raises land in).  Waiting tiles poll one word per record.
+template <int NS>
+__device__ __forceinline__ void publish_step(int* sync, int nrec, int rec, size_t tile, int step) {
+  int* arrive = sync + kSyncRec + 32 * nrec + tile;
+  if (__hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == NS - 1)
+    __hip_atomic_fetch_max(sync + kSyncRec + 32 * rec, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The scan of one (sequence, head, V strip), run by the first six waves of the workgroup.
+// PUB: the workgroup is a scan member of the fused backward launch -- waves past the six
+// only mirror the barriers, and after each step's histories (dS' and dDelta of chunk c) are
+// stored, progress[rec][strip] is raised by one: r + 1 means the strip has finished the
+// r + 1 last chunks of the sequence.
+template <int K, int V, bool PUB>
+__device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   using L = BwdScanLds<K, V>;
   constexpr int KT = K / 16 / 4;
   constexpr int SP = L::SP, DP = L::DP, OP = 16;
@@ -136,10 +187,6 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
   bf16* sDS = (bf16*)(smem + L::off_ds);
   float* sDSf = (float*)(smem + L::off_dsf);
   bf16* sDD = (bf16*)(smem + L::off_dd);
-  if ((int)blockIdx.x >= scan_blocks) {
-    prefetch_lines(pf, blockIdx.x - scan_blocks, gridDim.x - scan_blocks, smem);
-    return;
-  }
   const int H = a.H;
   int rec, strip;
   if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
@@ -159,6 +206,46 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
     seq_end = c_last.x + c_last.y;
   }
 
+  if (PUB && wave >= 6) {
+    // Waves past the six in the fused launch's scan members: the same barrier count as
+    // the six, and waves 6 and 7 pull the operands of the step kBwdPrefetch ahead into the
+    // XCD's L2 (every strip of a record runs on one XCD and reads the same per-chunk
+    // operands, so each strip takes every eighth 128-byte line): the scan's loads then hit
+    // L2 while the tile workgroups keep HBM busy.  The lines land in a scratch LDS row.
+    if (n <= 0) return;
+    const int pl = (wave - 6) * kWave + lane;
+    char* sink = smem + L::bytes + (wave & 1) * 1024;
+    auto prefetch = [&](int q) {
+      if (wave >= 8 || q >= n) return;
+      const int chunk = sq.x + n - 1 - q;
+      const size_t tile = (size_t)chunk * H + h;
+      constexpr int kAt = 64 * 64 * 2 / 128, kKd = 64 * K * 2 / 128, kLam = K * 4 / 128;
+      constexpr int kOps = kAt + 3 * kKd + kLam;  // A^T, Kd, Qg^T, W^T, lam lines
+      const int l = strip + 8 * pl;
+      const char* src = nullptr;
+      if (l < kAt) src = (const char*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64) + l * 128;
+      else if (l < kAt + kKd) src = (const char*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K) + (l - kAt) * 128;
+      else if (l < kAt + 2 * kKd) src = (const char*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64) + (l - kAt - kKd) * 128;
+      else if (l < kAt + 3 * kKd) src = (const char*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64) + (l - kAt - 2 * kKd) * 128;
+      else if (l < kOps) src = (const char*)((const float*)a.ws.p[R_LAM] + tile * K) + (l - kAt - 3 * kKd) * 128;
+      else if (l < kOps + 2 * 64) {
+        // dO rows of the chunk (each 2 V bytes, in 128-byte lines)
+        const int row0 = seq_row0 + (chunk - sq.x) * 64, len = min(64, seq_end - row0);
+        const int t = (l - kOps) / (V * 2 / 128), part = (l - kOps) % (V * 2 / 128);
+        if (t < len) src = (const char*)(a.dout + ((size_t)(row0 + t) * H + h) * V) + part * 128;
+      }
+      if (src) dma16(src, sink);
+    };
+    for (int q = 0; q < kBwdPrefetch; ++q) prefetch(q);
+    for (int b = 0; b < n; ++b) {
+      ring_barrier();  // S1(b)
+      prefetch(b + kBwdPrefetch);
+      ring_barrier();  // S2(b)
+    }
+    ring_barrier();  // final
+    wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
+    return;
+  }
   if (wave >= 4) {
     // ---- loader waves: step r's slot holds chunk sq.x + n - 1 - r ----
     const int lw = wave - 4;
@@ -202,11 +289,20 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
         ring_barrier();            // S2(r): slot r's A^T, Kd, Qg^T, dO are consumed
         issue(r + 2);
       }
+      if (PUB) ring_barrier();  // final: step n - 1 published
     } else {
       issue(0);
       for (int r = 0; r < n; ++r) {
-        wait_vmcnt<0>();  // W^T, lam of slot r complete (and last step's history stores)
+        // W^T, lam of slot r complete and the history stores of step r - 1 (step r - 2 in
+        // the fused launch, whose write-through stores may take several microseconds)
+        if (PUB && r > 0)
+          wait_vmcnt<K / 16>();
+        else
+          wait_vmcnt<0>();
         ring_barrier();   // S1(r): slot r - 1's W^T, lam are consumed
+        if (PUB && r > 1 && lane == 0) {
+          publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)(sq.x + n + 1 - r) * H + h, r - 2);  // step r - 2
+        }
         issue(r + 1);
         // f32 dS' history [K][V] of this step: element (k, v) sits in accumulator order at
         // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4; read before S2 (the compute
@@ -225,7 +321,18 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
 #pragma unroll
         for (int it = 0; it < K / 16; ++it) {
           const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
-          *(float4*)(DSH + (size_t)kk * V + c4) = hv[it];
+          if (PUB)
+            store4_coherent(DSH, kk * V + c4, hv[it]);
+          else
+            *(float4*)(DSH + (size_t)kk * V + c4) = hv[it];
+        }
+      }
+      if (PUB) {
+        wait_vmcnt<0>();  // step n - 1's history stores
+        ring_barrier();   // final: the compute waves' stores of step n - 1 are complete too
+        if (lane == 0) {
+          if (n > 1) publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)(sq.x + 1) * H + h, n - 2);
+          publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)sq.x * H + h, n - 1);
         }
       }
     }
@@ -262,6 +369,7 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
       *(f32x4*)(sDSf + ((wave * KT + kt) * 64 + lane) * 4) = dS[kt];
     }
     wait_lgkm0();
+    if (PUB) wait_vmcnt<1>();  // step r - 2's dDelta store (published after this barrier)
     ring_barrier();  // S1(r)
     // (3) dDelta rows 16*wave.. = A^T dO + Kd dS', and the dDelta-independent part of
     // (4), Qg^T dO, while the other waves finish theirs.  dO as B operand (tokens down the
@@ -294,7 +402,10 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
       }
       float* DDLT = (float*)a.sc.p[S_DDLT] + tile * V * 64;
       const f32x4 d = acc0 + acc1;
-      *(float4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = make_float4(d[0], d[1], d[2], d[3]);
+      if (PUB)
+        store4_coherent(DDLT, (v0 + lr) * 64 + 16 * wave + 4 * kg, make_float4(d[0], d[1], d[2], d[3]));
+      else
+        *(float4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = make_float4(d[0], d[1], d[2], d[3]);
       bf16x4 x;
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
@@ -318,6 +429,10 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
     }
     wait_lgkm0();  // the slot is released at the next S1
   }
+  if (PUB && n > 0) {
+    wait_vmcnt<0>();
+    ring_barrier();  // final
+  }
   if (a.ds0) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
@@ -326,6 +441,16 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
           make_float4(dS[kt][0], dS[kt][1], dS[kt][2], dS[kt][3]);
     }
   }
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, PrefetchList pf, int scan_blocks) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  if ((int)blockIdx.x >= scan_blocks) {
+    prefetch_lines(pf, blockIdx.x - scan_blocks, gridDim.x - scan_blocks, smem);
+    return;
+  }
+  bwd_scan_body<K, V, false>(a, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -369,8 +494,16 @@ struct DenseSmem {
   static constexpr size_t bytes = kAlias ? end : off_y + 64 * TP * 2;
 };
 
-template <int K, int V>
-__device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx) {
+// Gate: called by every thread of the tile once its scan-independent loads are in flight
+// and before its first read of the scan's histories (dS', dDelta); a no-op when the scan
+// completed in an earlier launch.
+struct NoGate {
+  static constexpr bool kCoherent = false;  // histories from an earlier launch: plain loads
+  __device__ void operator()() const {}
+};
+
+template <int K, int V, class Gate = NoGate>
+__device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx, const Gate& gate = Gate()) {
   using L = DenseSmem<K, V>;
   constexpr int MP = L::TP, KP = L::KP, VP = L::VP;
   constexpr int kVjpThreads = kDenseThreads, kVjpWaves = kDenseWaves;
@@ -420,14 +553,9 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx)
   static_assert(RPW >= 1 && 4 % RPW == 0, "row tiles per wave");
   const int pa_ct = wave / (4 / RPW), pa_rt0 = (wave % (4 / RPW)) * RPW;
   float xs[NVS][8], xd[NVS][8];
-  {
-    const int c = 16 * pa_ct + lr;
+  const int pa_c = 16 * pa_ct + lr;
 #pragma unroll
-    for (int sv = 0; sv < NVS; ++sv) {
-      load8f(SH + (size_t)c * V + 32 * sv + 8 * kg, xs[sv]);
-      load8f(DSH + (size_t)c * V + 32 * sv + 8 * kg, xd[sv]);
-    }
-  }
+  for (int sv = 0; sv < NVS; ++sv) load8f(SH + (size_t)pa_c * V + 32 * sv + 8 * kg, xs[sv]);
 
   // ---- P0: stage dU, delta, beta, dO, v, beta kh e^G; clear partials; T waits in
   // registers until after dA ----
@@ -451,15 +579,28 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx)
   float4 treg[64 * 64 / (4 * kDenseThreads)];
 #pragma unroll
   for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
+  bf16x8 dlf[NDL];
+#pragma unroll
+  for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
+  gate();
+#pragma unroll
+  for (int sv = 0; sv < NVS; ++sv) {
+    if (Gate::kCoherent) {
+      const float4 x0 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg);
+      const float4 x1 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg + 4);
+      xd[sv][0] = x0.x; xd[sv][1] = x0.y; xd[sv][2] = x0.z; xd[sv][3] = x0.w;
+      xd[sv][4] = x1.x; xd[sv][5] = x1.y; xd[sv][6] = x1.z; xd[sv][7] = x1.w;
+    } else {
+      load8f(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg, xd[sv]);
+    }
+  }
   float4 ddl[NDU];
 #pragma unroll
   for (int q = 0; q < NDU; ++q) {
     const int idx = min(q * kDenseThreads + tid, V * 16 - 1);
-    ddl[q] = *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
+    ddl[q] = Gate::kCoherent ? load4_coherent(DDLT, (idx / 16) * 64 + (idx % 16) * 4)
+                             : *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
   }
-  bf16x8 dlf[NDL];
-#pragma unroll
-  for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
   {
     const float bk = tk < len ? bt * rkt : 0.f;
     bf16x8 xb;
@@ -748,8 +889,8 @@ struct DecaySmem {
 // layout, the layout in which the dense kernel stored dQg, dKd and dKb, so every
 // per-element term stays in registers.  The key columns go in two passes of K/2 (the
 // operands of one pass fit in LDS beside q, k and G).
-template <int K>
-__device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx) {
+template <int K, class Gate = NoGate>
+__device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx, const Gate& gate = Gate()) {
   using L = DecaySmem<K>;
   constexpr int QP = L::QP, GP = L::GP, AP = L::AP, HALF = L::HALF, OP = L::OP, NSEG = L::NSEG;
   constexpr int NKT = 4 * (K / 16);
@@ -815,6 +956,7 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx)
     const float bt = ((const float*)a.ws.p[R_BETA])[tile * 64 + tc];
     float gv[8];
     load8f(Gg + tc * K + c0, gv);
+    gate();  // everything below reads the dense role's results
     // dA, dM': 64 x 64 f32 each, 4 consecutive per thread
     const int ai = tid * 4;
     float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xm = xa;
@@ -1186,6 +1328,107 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
 }
 
 // ---------------------------------------------------------------------------
+// fused backward: scan, dense and decay tiles in one launch
+// ---------------------------------------------------------------------------
+// The scan members (the first scan_blocks workgroups) run the reverse scan and publish each
+// step.  Every other workgroup takes a ticket from a counter and runs the dense and then
+// the decay VJP of the tile the ticket names, tiles in the order the scan finalises them
+// (last chunks of every sequence first).  The dense part waits until every strip of the
+// tile's record has passed its chunk; the decay part reads what the same workgroup's
+// dense part stored.  Every wait is on scan members, which are dispatched before any tile
+// workgroup and wait on nothing, so the launch drains; each wait is still bounded
+// (kSpinLimit of the 100 MHz wall clock), after which the abort word is set and every
+// later wait falls through.
+constexpr long long kSpinLimit = 200000000LL;  // 2 s
+
+struct SyncView {
+  int* ticket;
+  int* abort;
+  int* base;
+};
+
+__device__ __forceinline__ SyncView sync_view(const BwdArgs& a) {
+  int* base = (int*)a.sc.p[S_SYNC];
+  return {base, base + 1, base};
+}
+
+// Thread 0 waits for *p >= need, sleeping about 0.4 us per missing step between polls (the
+// scan finishes a step about every microsecond; dense polling by a couple of hundred
+// waiting workgroups slows the scan's own memory traffic), then a workgroup barrier.  The
+// data behind the count is read with coherent loads, so no cache invalidation is needed.
+struct ScanGate {
+  static constexpr bool kCoherent = true;
+  const int* p;
+  int need;
+  int* abort;
+  __device__ void operator()() const {
+    if (threadIdx.x == 0) {
+      const long long t0 = wall_clock64();
+      for (;;) {
+        const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v >= need || __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+        if (wall_clock64() - t0 > kSpinLimit) {
+          __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        for (int k = min(need - v, 8); k > 0; --k) __builtin_amdgcn_s_sleep(15);  // ~0.4 us each
+      }
+    }
+    ring_barrier();
+  }
+};
+
+// Clears the sync words and writes the chunk order: chunk c of sequence s with n chunks
+// has reverse rank r = n - 1 - (index in s); chunks go by r, then by sequence.  Position
+// of c = sum over sequences s' of min(n_s', r) + #{s' < s : n_s' > r}; chunks past the
+// last sequence keep their index.
+__global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int max_chunks, int sync_words) {
+  int* sync = (int*)a.sc.p[S_SYNC];
+  int* order = (int*)a.sc.p[S_ORDER];
+  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
+  const int2* seqs = (const int2*)a.ws.p[R_SEQS];
+  for (int i = threadIdx.x; i < sync_words; i += blockDim.x) sync[i] = 0;
+  for (int c = threadIdx.x; c < max_chunks; c += blockDim.x) {
+    const int4 ch = chunks[c];
+    if (ch.z < 0 || ch.y <= 0) {
+      order[c] = c;
+      continue;
+    }
+    const int r = seqs[ch.z].y - 1 - ch.w;
+    int pos = 0;
+    for (int s = 0; s < a.num_seqs; ++s) {
+      const int n = seqs[s].y;
+      pos += min(n, r) + (s < ch.z && n > r ? 1 : 0);
+    }
+    order[pos] = c;
+  }
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks) {
+  const SyncView sv = sync_view(a);
+  if ((int)blockIdx.x < scan_blocks) {
+    bwd_scan_body<K, V, true>(a, sv.base);
+    return;
+  }
+  __shared__ int s_ticket;
+  if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(sv.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int t = s_ticket, H = a.H;
+  const int cidx = ((const int*)a.sc.p[S_ORDER])[t / H], h = t % H;
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  int need = 0, rec = 0;
+  if (ch.y > 0) {
+    rec = ch.z * H + h;
+    need = ((const int2*)a.ws.p[R_SEQS])[ch.z].y - ch.w;
+  }
+  ScanGate gate{sv.base + kSyncRec + 32 * rec, need, sv.abort};
+  dense_tile<K, V>(a, cidx, h, gate);
+  __syncthreads();  // the dense part's stores are complete and visible to this workgroup
+  decay_tile<K>(a, cidx, h);
+}
+
+// ---------------------------------------------------------------------------
 // gate parameter reduction (fixed order)
 // ---------------------------------------------------------------------------
 constexpr int kParamThreads = 1024;
@@ -1256,9 +1499,44 @@ static int device_cu_count() {
   return cached[dev];
 }
 
+constexpr size_t cmax_sz(size_t x, size_t y) { return x > y ? x : y; }
+
+// KDA_BWD_FUSED=0 selects the three-launch backward (scan, then rounds of dense / decay
+// tiles).
+static bool fused_backward_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("KDA_BWD_FUSED");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+
 template <int K, int V>
 static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdArgs& a,
                            hipStream_t stream, int stages) {
+  const int all = (1 << (KDA_STAGE_BWD_SCAN - 10)) | (1 << (KDA_STAGE_BWD_DENSE - 10)) |
+                  (1 << (KDA_STAGE_BWD_DECAY - 10));
+  if ((stages & all) == all && p->num_seqs > 0 && g.max_chunks > 0 && fused_backward_enabled()) {
+    // one launch: scan members + ticketed dense / decay tiles (see chunk_bwd_fused_kernel)
+    constexpr size_t smem = cmax_sz(BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
+    static_assert(smem + 16 <= 160 * 1024, "fused backward LDS");
+    auto fused = chunk_bwd_fused_kernel<K, V>;
+    static bool attr_f = false;
+    if (!attr_f) {
+      if (hipFuncSetAttribute((const void*)fused, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_backward: fused LDS attribute failed");
+      attr_f = true;
+    }
+    const int nrec = p->num_seqs * p->heads;
+    const int scan_blocks = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
+    const int N = g.max_chunks * p->heads;
+    hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks, sync_words(nrec, N));
+    KDA_LAUNCH_CHECK("chunk_backward sched");
+    hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks);
+    KDA_LAUNCH_CHECK("chunk_backward fused");
+    stages &= ~all;
+  }
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     auto scan = chunk_bwd_scan_kernel<K, V>;
     constexpr size_t smem_s = BwdScanLds<K, V>::bytes;

@@ -76,6 +76,8 @@ enum ScRegion {
   S_PP,       // f32  [tile][2][K]   gate parameter partials {sum draw, sum draw*(z+b)}
   S_DGL,      // f32  [tile][K]      lam * dL/dlam (the state-decay part of dL/dG_last)
   S_DBETA,    // f32  [tile][64]     dL/dbeta from the dense VJP (U, M' terms)
+  S_SYNC,     // int  fused backward: ticket, abort, per-record step counts, per-tile strip arrivals
+  S_ORDER,    // int  [max_chunks]   chunks in the fused backward's order (reverse rank, then sequence)
   S_COUNT
 };
 
@@ -122,6 +124,8 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
     case S_PP: return nt * 2 * K * 4;
     case S_DGL: return nt * K * 4;
     case S_DBETA: return nt * 64 * 4;
+    case S_SYNC: return (32 + 32 * (size_t)g.num_seqs * g.heads + nt) * 4;
+    case S_ORDER: return (size_t)g.max_chunks * 4;
     default: return 0;
   }
 }
