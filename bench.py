@@ -37,12 +37,14 @@ KERNEL_FLOP_PER_TILE = {
     "bwd_dense": 3 * 2_097_152 + 5 * 1_048_576 + 4 * 262_144,  # dQg dKd dW; dA dT(2) dVb dKb; Y dM
     "bwd_decay": 4 * 1_048_576,                        # row/column terms of A and M'
 }
-# the step launches the dense and decay roles as one kernel
+# the staged backward launches the dense and decay roles as one kernel
 KERNEL_FLOP_PER_TILE["bwd_dense_decay"] = KERNEL_FLOP_PER_TILE["bwd_dense"] + KERNEL_FLOP_PER_TILE["bwd_decay"]
-# kernels one fwd+bwd step launches (bwd_dense / bwd_decay time one role alone)
-STEP_KERNELS = ("fwd_intra", "fwd_scan", "fwd_output", "bwd_scan", "bwd_dense_decay")
+# the whole backward (one call) is one fused launch of scan members and dense+decay tiles
+KERNEL_FLOP_PER_TILE["bwd_fused"] = KERNEL_FLOP_PER_TILE["bwd_scan"] + KERNEL_FLOP_PER_TILE["bwd_dense_decay"]
+# kernels one fwd+bwd step launches (the other entries time one stage alone)
+STEP_KERNELS = ("fwd_intra", "fwd_scan", "fwd_output", "bwd_fused")
 STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_dense": 11, "bwd_decay": 12,
-          "bwd_dense_decay": 14}
+          "bwd_dense_decay": 14, "bwd_fused": None}
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 
@@ -139,7 +141,9 @@ def kernel_times(torch, t, do, gate, reps=20):
     _lib.check(lib.kda_chunk_backward(ctypes.byref(p), *bargs), "chunk_backward")
     res = {}
     for name, stage in STAGES.items():
-        if stage < 10:
+        if stage is None:  # the full backward: chunk_bwd_sched_kernel (~2 us) + the fused launch
+            call = lambda: lib.kda_chunk_backward(ctypes.byref(p), *bargs)  # noqa: E731
+        elif stage < 10:
             call = lambda: lib.kda_chunk_forward_stage(stage, ctypes.byref(p), *fargs)  # noqa: E731
         else:
             call = lambda: lib.kda_chunk_backward_stage(stage, ctypes.byref(p), *bargs)  # noqa: E731
@@ -456,6 +460,8 @@ def main():
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom),
                     "busy_frac": busy.get(dom), "measured_hbm_frac": None if hbm_frac is None else round(hbm_frac, 4)}
+    if dom == "bwd_fused":
+        roofline["launches"] = "one kda_chunk_backward call: chunk_bwd_sched_kernel (~2 us) + chunk_bwd_fused_kernel"
     line = {
         "metric": "KDA fwd+bwd TFLOP/s (B2 T4096 H3 D128 bf16)",
         "value": round(flop / (ms * 1e-3) / 1e12, 3),
