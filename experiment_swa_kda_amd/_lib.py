@@ -49,6 +49,7 @@ SIGNATURES = {
     "kda_chunk_backward_scratch_bytes": (ctypes.c_size_t, [_PP]),
     "kda_chunk_forward": (ctypes.c_int, [_PP] + [_P] * 11 + [_P]),
     "kda_chunk_forward_norm_gate": (ctypes.c_int, [_PP] + [_P] * 13 + [_F, _P, _P, _P]),
+    "kda_chunk_forward_conv_norm_gate": (ctypes.c_int, [_PP, _P, _L, _P, _I] + [_P] * 11 + [_F, _P, _P, _P]),
     "kda_chunk_backward": (ctypes.c_int, [_PP] + [_P] * 20 + [_P]),
     "kda_chunk_backward_noalloc": (ctypes.c_int, [_PP] + [_P] * 19 + [_P]),
     "kda_chunk_backward_noalloc_max_scratch_bytes": (ctypes.c_size_t, []),

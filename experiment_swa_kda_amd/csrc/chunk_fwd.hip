@@ -58,6 +58,15 @@ struct FwdArgs {
   float ng_eps;
   bf16* ng_out;
   float* ng_inv_rms;
+  // optional short convolution + SiLU prologue of the intra kernel (conv_x null: q, k, v
+  // are the kernel's inputs).  conv_x rows are tokens (ld elements apart) holding the
+  // pre-convolution q, k, v projections side by side (columns [0, HK), [HK, 2HK),
+  // [2HK, 3HK)); conv_w is [3HK][conv_W] bf16 in the same channel order.  The intra kernel
+  // writes the post-SiLU q, k, v to q, k, v (as bf16, the values it computes with).
+  const bf16* conv_x;
+  long conv_ld;
+  const bf16* conv_w;
+  int conv_W;
 };
 
 // ---------------------------------------------------------------------------
@@ -211,7 +220,53 @@ __device__ void intra_exact_block(const FwdArgs& a, int w, int lane, int row0, i
   }
 }
 
-template <int K, int V>
+// ---------------------------------------------------------------------------
+// short convolution + SiLU prologue (fused conv path)
+// ---------------------------------------------------------------------------
+// Lane (lr, kg) of wave w holds token row i = 16 w + lr of the chunk.  The convolution of
+// row i needs rows i-1 .. i-(W-1): within the wave they are the rows of lanes lr-1 ..
+// (DPP row shift); rows before the wave's block come from a halo row that lanes 13..15
+// load (row i - 16) and a DPP row rotate hands to lanes 0..2.  Rows before the sequence
+// start are zero (no convolution state on this path).  Arithmetic and rounding follow the
+// separate convolution kernel exactly (f32 fma chain over the taps in order, sigmoid_fast,
+// one bf16 rounding), so the fused path reproduces the unfused one bit for bit.
+template <int SHIFT>
+__device__ __forceinline__ unsigned row_take(unsigned own, unsigned halo, int lr) {
+  const unsigned a = (unsigned)__builtin_amdgcn_update_dpp(0, (int)own, 0x110 + SHIFT, 0xf, 0xf, true);   // row_shr
+  const unsigned b = (unsigned)__builtin_amdgcn_update_dpp(0, (int)halo, 0x120 + SHIFT, 0xf, 0xf, false); // row_ror
+  return lr >= SHIFT ? a : b;
+}
+
+template <int W>
+__device__ __forceinline__ bf16x8 conv_silu8(bf16x8 own, bf16x8 halo, const float* wt, int lr) {
+  // xs[j] = row i - (W-1) + j, j = W-1 the own row
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const u4 o = __builtin_bit_cast(u4, own), hl = __builtin_bit_cast(u4, halo);
+  bf16x8 xs[W];
+  xs[W - 1] = own;
+#pragma unroll
+  for (int d = 1; d < W; ++d) {
+    u4 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (d == 1) r[q] = row_take<1>(o[q], hl[q], lr);
+      if (d == 2) r[q] = row_take<2>(o[q], hl[q], lr);
+      if (d == 3) r[q] = row_take<3>(o[q], hl[q], lr);
+    }
+    xs[W - 1 - d] = __builtin_bit_cast(bf16x8, r);
+  }
+  bf16x8 y;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float pre = 0.f;
+#pragma unroll
+    for (int j = 0; j < W; ++j) pre = fmaf((float)xs[j][e], wt[e * 4 + j], pre);
+    y[e] = to_bf16(pre * sigmoid_fast(pre));
+  }
+  return y;
+}
+
+template <int K, int V, bool CONV = false>
 __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdArgs a) {
   using L = IntraLds<K, V>;
   constexpr int NS = K / 32, NV = V / 32, RS = L::RS, TS = L::TS;
@@ -260,13 +315,85 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   // ---- phase 1: loads (all issued first), norms, gate, beta, cumulative decay ----
   bf16x8 qr[NS], kr[NS], vr[NV];
   float g[NS][8];
+  if constexpr (CONV) {
+    static_assert(K == V, "the fused convolution serves q, k, v of one head width");
+    // taps of this head's q, k, v channels as f32 [3][K][4] in the (still unused) X1 region
+    float* sWt = (float*)(smem + L::x1);
+    const int HK = H * K, W = a.conv_W;
+    for (int idx = tid; idx < 3 * K; idx += kIntraThreads) {
+      const int t = idx / K, c = idx % K;
+      const bf16* src = a.conv_w + (size_t)(t * HK + h * K + c) * W;
+      float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
+      wv.x = (float)src[0];
+      if (W > 1) wv.y = (float)src[1];
+      if (W > 2) wv.z = (float)src[2];
+      if (W > 3) wv.w = (float)src[3];
+      *(float4*)(sWt + idx * 4) = wv;
+    }
+    // own rows (clamped like rbase) and, for lanes 13..15, the halo row i - 16 (zero before
+    // the sequence start); every load issued before the first use
+    const int pos = ch.w * kChunk + i;  // token index in the sequence
+    const bf16* xo = a.conv_x + (size_t)(row0 + (live ? i : len - 1)) * a.conv_ld + h * K + 8 * kg;
+    // halo row i - 16 of lanes 13..15: a token of this sequence and of this chunk's rows
+    // (lanes 13..15 themselves may lie past a partial chunk's end)
+    const bool has_halo = lr >= 13 && pos >= 16 && i - 16 < len;
+    const bf16* xh = has_halo ? a.conv_x + (size_t)(row0 + i - 16) * a.conv_ld + h * K + 8 * kg
+                              : xo;  // the own row (unused)
+    bf16x8 ho[3][NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    qr[s] = *(const bf16x8*)(a.q + rbase * K + 32 * s + 8 * kg);
-    kr[s] = *(const bf16x8*)(a.k + rbase * K + 32 * s + 8 * kg);
+    for (int s = 0; s < NS; ++s) {
+      qr[s] = *(const bf16x8*)(xo + 32 * s);
+      kr[s] = *(const bf16x8*)(xo + HK + 32 * s);
+      vr[s] = *(const bf16x8*)(xo + 2 * HK + 32 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      ho[0][s] = *(const bf16x8*)(xh + 32 * s);
+      ho[1][s] = *(const bf16x8*)(xh + HK + 32 * s);
+      ho[2][s] = *(const bf16x8*)(xh + 2 * HK + 32 * s);
+      if (!has_halo)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ho[0][s][e] = ho[1][s][e] = ho[2][s][e] = to_bf16(0.f);
+    }
+    __syncthreads();  // taps staged
+    bf16* qo = (bf16*)a.q + rbase * K + 8 * kg;
+    bf16* ko = (bf16*)a.k + rbase * K + 8 * kg;
+    bf16* vo = (bf16*)a.v + rbase * V + 8 * kg;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int c0 = 32 * s + 8 * kg;
+      if (W == 4) {
+        qr[s] = conv_silu8<4>(qr[s], ho[0][s], sWt + (0 * K + c0) * 4, lr);
+        kr[s] = conv_silu8<4>(kr[s], ho[1][s], sWt + (1 * K + c0) * 4, lr);
+        vr[s] = conv_silu8<4>(vr[s], ho[2][s], sWt + (2 * K + c0) * 4, lr);
+      } else if (W == 3) {
+        qr[s] = conv_silu8<3>(qr[s], ho[0][s], sWt + (0 * K + c0) * 4, lr);
+        kr[s] = conv_silu8<3>(kr[s], ho[1][s], sWt + (1 * K + c0) * 4, lr);
+        vr[s] = conv_silu8<3>(vr[s], ho[2][s], sWt + (2 * K + c0) * 4, lr);
+      } else if (W == 2) {
+        qr[s] = conv_silu8<2>(qr[s], ho[0][s], sWt + (0 * K + c0) * 4, lr);
+        kr[s] = conv_silu8<2>(kr[s], ho[1][s], sWt + (1 * K + c0) * 4, lr);
+        vr[s] = conv_silu8<2>(vr[s], ho[2][s], sWt + (2 * K + c0) * 4, lr);
+      } else {
+        qr[s] = conv_silu8<1>(qr[s], ho[0][s], sWt + (0 * K + c0) * 4, lr);
+        kr[s] = conv_silu8<1>(kr[s], ho[1][s], sWt + (1 * K + c0) * 4, lr);
+        vr[s] = conv_silu8<1>(vr[s], ho[2][s], sWt + (2 * K + c0) * 4, lr);
+      }
+      if (live) {
+        *(bf16x8*)(qo + 32 * s) = qr[s];
+        *(bf16x8*)(ko + 32 * s) = kr[s];
+        *(bf16x8*)(vo + 32 * s) = vr[s];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qr[s] = *(const bf16x8*)(a.q + rbase * K + 32 * s + 8 * kg);
+      kr[s] = *(const bf16x8*)(a.k + rbase * K + 32 * s + 8 * kg);
+    }
+#pragma unroll
+    for (int s = 0; s < NV; ++s) vr[s] = *(const bf16x8*)(a.v + rbase * V + 32 * s + 8 * kg);
   }
-#pragma unroll
-  for (int s = 0; s < NV; ++s) vr[s] = *(const bf16x8*)(a.v + rbase * V + 32 * s + 8 * kg);
   const float bl = (float)a.beta[rbase];
   if (a.gate_mode == KDA_GATE_K3) {
     const float ea = expf(a.A_log[h]);
@@ -1327,13 +1454,14 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
     constexpr size_t smem = IntraLds<K, V>::bytes;
     static bool attr = false;
     if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)chunk_fwd_intra_kernel<K, V>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess)
-        return set_error(KDA_ERR_LAUNCH, "chunk_forward: LDS attribute: %s", hipGetErrorString(e));
+      for (const void* f : {(const void*)chunk_fwd_intra_kernel<K, V, false>, (const void*)chunk_fwd_intra_kernel<K, V, K == V>}) {
+        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess)
+          return set_error(KDA_ERR_LAUNCH, "chunk_forward: LDS attribute: %s", hipGetErrorString(e));
+      }
       attr = true;
     }
-    auto intra = chunk_fwd_intra_kernel<K, V>;
+    auto intra = a.conv_x ? chunk_fwd_intra_kernel<K, V, K == V> : chunk_fwd_intra_kernel<K, V, false>;
     hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(kIntraThreads), smem, stream, a);
     KDA_LAUNCH_CHECK("chunk_forward intra");
   }
@@ -1414,7 +1542,8 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
                                  void* workspace, hipStream_t stream,
                                  const void* norm_gate = nullptr, const float* norm_weight = nullptr,
                                  float norm_eps = 0.f, void* norm_output = nullptr,
-                                 float* norm_inv_rms = nullptr) {
+                                 float* norm_inv_rms = nullptr, const void* conv_x = nullptr,
+                                 long conv_ld = 0, const void* conv_w = nullptr, int conv_W = 0) {
   using namespace kda;
   int rc = validate_problem(p, "chunk_forward");
   if (rc != KDA_OK) return rc;
@@ -1450,6 +1579,10 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   a.ng_eps = norm_eps;
   a.ng_out = (bf16*)norm_output;
   a.ng_inv_rms = norm_inv_rms;
+  a.conv_x = (const bf16*)conv_x;
+  a.conv_ld = conv_ld;
+  a.conv_w = (const bf16*)conv_w;
+  a.conv_W = conv_W;
   // fixed-length problems with at least one chunk get their tables from the intra kernel
   a.fixed_T = (p->cu_seqlens == nullptr && g.max_chunks > 0) ? p->seq_len : 0;
   if ((stages & (1 << KDA_STAGE_PREP)) && a.fixed_T == 0) {
@@ -1490,6 +1623,35 @@ extern "C" int kda_chunk_forward_norm_gate(const kda_chunk_problem* p, const voi
   return chunk_forward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state,
                             output, final_state, workspace, stream, norm_gate, norm_weight, epsilon,
                             norm_output, inverse_rms);
+}
+
+extern "C" int kda_chunk_forward_conv_norm_gate(const kda_chunk_problem* p, const void* conv_x,
+                                                int64_t conv_ld, const void* conv_weight,
+                                                int32_t conv_width, void* q, void* k, void* v,
+                                                const void* gate, const void* beta_logits,
+                                                const float* A_log, const float* dt_bias,
+                                                void* output, void* workspace,
+                                                const void* norm_gate, const float* norm_weight,
+                                                float epsilon, void* norm_output, float* inverse_rms,
+                                                hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(p != nullptr, "chunk_forward_conv_norm_gate: null problem");
+  const bool empty = (size_t)p->batch * p->seq_len == 0;
+  KDA_REQUIRE(p->cu_seqlens == nullptr, "chunk_forward_conv_norm_gate: cu_seqlens is not supported");
+  KDA_REQUIRE(p->key_dim == p->value_dim && (p->value_dim == 64 || p->value_dim == 128),
+              "chunk_forward_conv_norm_gate: key_dim and value_dim must be equal, 64 or 128");
+  KDA_REQUIRE(conv_width >= 1 && conv_width <= 4, "chunk_forward_conv_norm_gate: conv_width must be in [1, 4]");
+  KDA_REQUIRE(empty || (conv_x && conv_weight && q && k && v),
+              "chunk_forward_conv_norm_gate: null convolution pointer");
+  KDA_REQUIRE(conv_ld >= 3 * (int64_t)p->heads * p->key_dim && conv_ld % 8 == 0,
+              "chunk_forward_conv_norm_gate: conv_ld must be a multiple of 8 and >= 3 * heads * key_dim");
+  KDA_REQUIRE(aligned16(conv_x), "chunk_forward_conv_norm_gate: conv_x must be 16-byte aligned");
+  KDA_REQUIRE(empty || (norm_gate && norm_weight && norm_output && inverse_rms),
+              "chunk_forward_conv_norm_gate: null norm pointer");
+  KDA_REQUIRE(epsilon >= 0.f, "chunk_forward_conv_norm_gate: epsilon must be non-negative");
+  return chunk_forward_impl(~0, p, q, k, v, gate, beta_logits, A_log, dt_bias, nullptr, output,
+                            nullptr, workspace, stream, norm_gate, norm_weight, epsilon, norm_output,
+                            inverse_rms, empty ? nullptr : conv_x, conv_ld, conv_weight, conv_width);
 }
 
 extern "C" int kda_chunk_forward_stage(int32_t stage, const kda_chunk_problem* p, const void* q,

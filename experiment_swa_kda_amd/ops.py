@@ -198,6 +198,61 @@ def chunk_forward_norm_gate(q, k, v, gate_values, beta_logits, A_log, dt_bias, i
     return output, normed, inv, final_state, workspace
 
 
+def chunk_forward_conv_norm_gate(qkv_in, conv_weight, gate_values, beta_logits, A_log, dt_bias,
+                                 lower_bound, scale, norm_gate, norm_weight, eps, heads, *, gate="k3"):
+    """:func:`chunk_forward_norm_gate` with the short convolution + SiLU of q, k, v computed
+    by the chunk forward's first kernel (stateless path: no convolution or recurrent state).
+    ``qkv_in`` [B,T,3HK] bf16 holds the pre-convolution q, k, v projections side by side; it
+    may be a column slice of a wider row (unit channel stride, row stride a multiple of 8).
+    ``conv_weight`` [3HK, W] bf16, W <= 4.  Returns (q, k, v, o, normed, inverse_rms,
+    workspace) with q, k, v the post-SiLU activations [B,T,H,K], bit-identical to
+    :func:`causal_conv_forward`'s."""
+    gm = GATE_MODES[gate]
+    what = "chunk_forward_conv_norm_gate"
+    dev = _require_cuda(what, qkv_in, conv_weight, gate_values, beta_logits, A_log, dt_bias, norm_gate,
+                        norm_weight)
+    _check_dtype(what, qkv_in, torch.bfloat16, "qkv_in")
+    _check_dtype(what, conv_weight, torch.bfloat16, "conv_weight")
+    B, T, C3 = qkv_in.shape
+    H = int(heads)
+    if C3 % (3 * H):
+        raise RuntimeError(f"{what}: qkv_in width {C3} is not 3 * heads * head_dim")
+    D = C3 // (3 * H)
+    if conv_weight.ndim != 2 or conv_weight.shape[0] != C3 or not 1 <= conv_weight.shape[1] <= 4:
+        raise RuntimeError(f"{what}: conv_weight must be [3HK, W] with W in [1, 4]")
+    if qkv_in.stride(2) != 1 or (T > 1 and qkv_in.stride(1) % 8) or (B > 1 and qkv_in.stride(0) != T * qkv_in.stride(1)) \
+            or qkv_in.data_ptr() % 16:
+        qkv_in = qkv_in.contiguous()
+    ld = qkv_in.stride(1) if T > 1 else C3
+    q = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
+    k, v = torch.empty_like(q), torch.empty_like(q)
+    _check_chunk_inputs(what, q, k, v, gate_values, beta_logits, A_log, dt_bias, None, None, gm)
+    _check_dtype(what, norm_gate, torch.bfloat16, "norm_gate")
+    _check_dtype(what, norm_weight, torch.float32, "norm_weight")
+    if norm_gate.shape != v.shape or norm_weight.shape != (D,):
+        raise RuntimeError(f"{what}: norm_gate must be shaped like v and norm_weight [V]")
+    gate_values, beta_logits = _c(gate_values), _c(beta_logits)
+    A_log, dt_bias, norm_gate, norm_weight = _c(A_log), _c(dt_bias), _c(norm_gate), _c(norm_weight)
+    conv_weight = _c(conv_weight)
+    p = _problem(q, v, None, gm, lower_bound, scale)
+    lib = _lib.load()
+    ws_bytes = lib.kda_chunk_workspace_bytes(ctypes.byref(p))
+    if ws_bytes == 0 and B * T > 0:
+        check(1, "chunk_workspace_bytes")
+    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    output = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
+    normed = torch.empty_like(output)
+    inv = torch.empty(B * T * H, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.kda_chunk_forward_conv_norm_gate(
+            ctypes.byref(p), ptr(qkv_in), int(ld), ptr(conv_weight), int(conv_weight.shape[1]),
+            ptr(q), ptr(k), ptr(v), ptr(gate_values), ptr(beta_logits), ptr(A_log), ptr(dt_bias),
+            ptr(output), ptr(workspace), ptr(norm_gate), ptr(norm_weight), float(eps), ptr(normed),
+            ptr(inv), _stream(dev))
+    check(rc, "kda_chunk_forward_conv_norm_gate")
+    return q, k, v, output, normed, inv, workspace
+
+
 def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace,
                    grad_output, grad_final_state, lower_bound, scale, *, cu_seqlens=None,
                    gate="k3"):

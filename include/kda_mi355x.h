@@ -102,6 +102,29 @@ int kda_chunk_forward_norm_gate(const kda_chunk_problem* p,
                                 hipStream_t stream);
 
 /*
+ * kda_chunk_forward_norm_gate with the mixer's short convolution + SiLU of q, k and v
+ * computed by the chunk forward's first kernel.  Replaces the reference's sequence
+ * causal_convolution_forward (x3) -> chunk_forward -> rmsnorm_gate_forward
+ * (nanochat/mixers/kda.py:744-770; causal_convolution_forward.cu:42-238) on the stateless
+ * training path: no convolution or recurrent state in or out, no cu_seqlens.
+ *   conv_x      bf16 rows of conv_ld elements, one per token ([B*T][conv_ld]); columns
+ *               [0, HK), [HK, 2HK), [2HK, 3HK) hold the pre-convolution q, k, v projections
+ *               (HK = heads * key_dim); conv_ld % 8 == 0, 16-byte aligned
+ *   conv_weight bf16 [3 HK][conv_width], conv_width in [1, 4], the same channel order
+ *   q, k, v     outputs: bf16 [B,T,H,K] post-SiLU activations (what kda_chunk_backward and
+ *               kda_causal_conv_backward take); bit-identical to kda_causal_conv_forward's
+ * key_dim == value_dim, 64 or 128.  The other arguments as in kda_chunk_forward_norm_gate.
+ */
+int kda_chunk_forward_conv_norm_gate(const kda_chunk_problem* p, const void* conv_x,
+                                     int64_t conv_ld, const void* conv_weight, int32_t conv_width,
+                                     void* q, void* k, void* v, const void* gate,
+                                     const void* beta_logits, const float* A_log,
+                                     const float* dt_bias, void* output, void* workspace,
+                                     const void* norm_gate, const float* norm_weight,
+                                     float epsilon, void* norm_output, float* inverse_rms,
+                                     hipStream_t stream);
+
+/*
  * Exact chunked backward.  Replaces torch.ops.nanochat_kda.chunk_backward
  * (nanochat/mixers/cuda_kda/chunk.cu:1758-2113, schema chunk.cu:2122-2129).
  *   workspace: as filled by kda_chunk_forward on the same inputs

@@ -218,3 +218,58 @@ def test_chunk_forward_norm_gate_autograd_matches_unfused():
         assert x is not None and e is not None
         cos = torch.nn.functional.cosine_similarity(x.double().flatten(), e.double().flatten(), dim=0)
         assert cos > 0.9999, float(cos)
+
+
+@pytest.mark.parametrize("B,T,H,D,W", [(2, 150, 3, 128, 4), (1, 200, 2, 64, 4), (2, 17, 1, 128, 3),
+                                       (1, 5, 2, 64, 4), (1, 1, 1, 128, 2), (1, 64, 2, 128, 1)])
+def test_chunk_forward_conv_matches_separate_conv(B, T, H, D, W):
+    """The short convolution + SiLU computed in the chunk forward's first kernel: q, k, v
+    equal kda_causal_conv_forward's bit for bit (halo rows across waves and chunks, rows
+    before the sequence start, a partial last chunk), o and the normed output equal the
+    unfused chunk forward on them, and the q activations match the oracle convolution."""
+    g = torch.Generator().manual_seed(T * 7 + D + W)
+    C = H * D
+    wide = torch.randn(B, T, 3 * C + 24, generator=g).bfloat16().cuda()   # a column slice of a wider row
+    x = wide[..., :3 * C]
+    cw = (torch.randn(3 * C, W, generator=g) * 0.5).bfloat16().cuda()
+    raw = torch.randn(B, T, H, D, generator=g).bfloat16().cuda()
+    beta = torch.randn(B, T, H, generator=g).bfloat16().cuda()
+    A_log = (torch.rand(H, generator=g) - 0.5).float().cuda()
+    dt = (0.1 * torch.randn(H * D, generator=g)).float().cuda()
+    og = torch.randn(B, T, H, D, generator=g).bfloat16().cuda()
+    nw = (1 + 0.3 * torch.randn(D, generator=g)).float().cuda()
+    q, k, v, o, normed, inv, _ = ops.chunk_forward_conv_norm_gate(x, cw, raw, beta, A_log, dt, -5.0, D ** -0.5,
+                                                                   og, nw, 1e-5, H)
+    y, _ = ops.causal_conv_forward(x.contiguous(), cw, None, False)
+    qs, ks, vs = (t.reshape(B, T, H, D) for t in y.split(C, dim=-1))
+    assert torch.equal(q, qs) and torch.equal(k, ks) and torch.equal(v, vs)
+    o2, n2, inv2, _, _ = ops.chunk_forward_norm_gate(qs.contiguous(), ks.contiguous(), vs.contiguous(), raw, beta,
+                                                     A_log, dt, None, False, -5.0, D ** -0.5, og, nw, 1e-5)
+    assert torch.equal(o, o2) and torch.equal(normed, n2) and torch.equal(inv, inv2)
+    ey, _ = O.causal_conv_forward(np64(x[..., :C]), np64(cw[:C]), None)
+    assert rel_err(q.reshape(B, T, C), ey) < 1e-2
+
+
+def test_mixer_fused_conv_equals_separate_conv():
+    """KimiDeltaAttention's stateless path with the convolutions fused into the chunk forward
+    gives the same output and the same gradient for every parameter and the input, bit for
+    bit, as the path with the separate convolution launch."""
+    from experiment_swa_kda_amd import KimiDeltaAttention
+    torch.manual_seed(0)
+    layer = KimiDeltaAttention(256, 2, 128, mode="project_chunk").cuda()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.06)
+        layer.o_norm.weight.fill_(1.0)
+    x0 = torch.randn(2, 200, 256, device="cuda").bfloat16()
+    dy = torch.randn(2, 200, 256, device="cuda").bfloat16()
+    res = []
+    for fuse in (True, False):
+        layer.fuse_conv = fuse
+        layer.zero_grad()
+        x = x0.clone().requires_grad_()
+        y, _ = layer(x)
+        y.backward(dy)
+        res.append([y, x.grad] + [p.grad.clone() for p in layer.parameters()])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
