@@ -134,25 +134,10 @@ __device__ __forceinline__ void prefetch_lines(const PrefetchList& pf, int w, in
   if (acc == 0x9e3779b9u) *(unsigned*)sink = acc;  // keeps the loads; the value is irrelevant
 }
 
-// Scan -> dense hand-off inside the fused backward.  The histories go through memory with
-// system-coherent cache policy (sc0 sc1): stores write through the XCD's L2, loads miss in
-// the non-coherent caches.  No L2 write-back or invalidate is then needed around the
-// counts, which matters: the write-back of a whole L2 per scan step costs microseconds on
-// the scan's serial chain.  Buffer accesses take a wave-uniform base.
-constexpr int kCoherentPolicy = 1 | 16;  // sc0 | sc1
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
-}
-__device__ __forceinline__ void store4_coherent(float* base, int off, float4 x) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  const f4 v = {x.x, x.y, x.z, x.w};
-  __builtin_amdgcn_raw_buffer_store_b128(v, raw_rsrc(base), off * 4, 0, kCoherentPolicy);
-}
-__device__ __forceinline__ float4 load4_coherent(const float* base, int off) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  const f4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), off * 4, 0, kCoherentPolicy);
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
+// Scan -> dense hand-off inside the fused backward: the histories go through memory with
+// the system-coherent helpers of kda_device.hpp (write-through stores, coherent loads), so no
+// L2 write-back or invalidate is needed around the counts -- the write-back of a whole L2 per
+// scan step costs microseconds on the scan's serial chain.
 
 // Layout of the fused backward's sync words (ints): [0] ticket, [1] abort, record rec's
 // count of finished steps at kSyncRec + 32 rec (one 128-byte line each), then per tile the
@@ -1485,21 +1470,6 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
     a.dA_log[h] = t;
   }
 }
-
-// Compute units of the current device (the launch granularity of the dense/decay rounds);
-// 0 if it cannot be queried.
-static int device_cu_count() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-constexpr size_t cmax_sz(size_t x, size_t y) { return x > y ? x : y; }
 
 // KDA_BWD_FUSED=0 selects the three-launch backward (scan, then rounds of dense / decay
 // tiles).

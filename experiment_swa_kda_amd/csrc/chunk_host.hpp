@@ -11,4 +11,19 @@ ChunkGeom make_geom(const kda_chunk_problem* p);
 int launch_chunk_prep(const kda_chunk_problem* p, const ChunkGeom& g, const Regions& ws,
                       hipStream_t stream);
 
+constexpr size_t cmax_sz(size_t x, size_t y) { return x > y ? x : y; }
+
+// Compute units of the current device (launch granularity of the chunk-parallel rounds and
+// the fused launches' sizing); 0 if it cannot be queried.
+inline int device_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 }  // namespace kda

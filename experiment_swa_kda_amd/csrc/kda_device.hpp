@@ -180,6 +180,28 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------
+// Cross-workgroup hand-off inside one launch.  Each XCD has its own L2, so data one
+// workgroup stores and a workgroup on another XCD loads must either go through memory with
+// system-coherent cache policy (sc0 sc1: stores write through the L2, loads miss in the
+// non-coherent caches) or be written back with an agent-scope release (which costs a write-back
+// of the XCD's whole L2).  Buffer accesses take a wave-uniform base.
+// ---------------------------------------------------------------------------
+constexpr int kCoherentPolicy = 1 | 16;  // sc0 | sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void store4_coherent(float* base, int off, float4 x) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = {x.x, x.y, x.z, x.w};
+  __builtin_amdgcn_raw_buffer_store_b128(v, raw_rsrc(base), off * 4, 0, kCoherentPolicy);
+}
+__device__ __forceinline__ float4 load4_coherent(const float* base, int off) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), off * 4, 0, kCoherentPolicy);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): two MFMAs with (hi, lo) recover
 // ~16 mantissa bits of an f32 operand.
 __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
