@@ -12,6 +12,7 @@ from __future__ import annotations
 import concurrent.futures
 import os
 import shutil
+import re
 import subprocess
 import sys
 
@@ -53,13 +54,35 @@ def _flags() -> list[str]:
     ]
 
 
+def vgpr_spills(remarks: str) -> dict[str, int]:
+    """Kernels with spilled VGPRs, from hipcc's kernel-resource-usage remarks."""
+    out, name = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"VGPRs Spill: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            out[name] = int(m.group(1))
+    return out
+
+
 def _compile(src: str) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [_hipcc(), *_flags(), *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    remarks = ["-Rpass-analysis=kernel-resource-usage"] if src.endswith(".hip") else []
+    cmd = [_hipcc(), *_flags(), *EXTRA_FLAGS.get(src, []), *remarks, "-c", os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
+    # A VGPR spill is refused: this compiler has placed a spill store in a join block
+    # before the instruction that restores the full exec mask, so only some lanes saved
+    # the value and the reload gave the others garbage (wrong dq / dk, no error).
+    spills = vgpr_spills(proc.stderr)
+    if spills:
+        os.remove(obj)
+        raise RuntimeError(f"{src}: kernels spill VGPRs (refused): {spills}")
     return obj
 
 

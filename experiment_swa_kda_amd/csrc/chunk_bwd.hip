@@ -1211,7 +1211,11 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   // ---- P3: coalesced dq, dk writes ----
   {
     constexpr int LPR = K / 8;
-    for (int idx = tid; idx < 64 * LPR; idx += kVjpThreads) {
+    // the thread index made opaque: P0's row / column of the same thread is otherwise kept
+    // alive through P1 and P2 (a spilled register at K = 64)
+    int ptid = tid;
+    asm volatile("" : "+v"(ptid));
+    for (int idx = ptid; idx < 64 * LPR; idx += kVjpThreads) {
       const int t = idx / LPR, c0 = (idx % LPR) * 8;
       if (t >= len) continue;
       const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;

@@ -259,3 +259,18 @@ def test_kv_cache_contract_on_cpu():
     assert c.get_pos() == 0 and c.get_kda_state(2) is None
     with pytest.raises(ValueError):
         KVCache(1, 3, 64, 128, 2, "cpu", torch.bfloat16, mixer_types="KS")
+
+
+def test_build_refuses_vgpr_spills():
+    """The build's spill check reads hipcc's kernel-resource-usage remarks per kernel."""
+    from experiment_swa_kda_amd.build import vgpr_spills
+
+    remarks = "\n".join([
+        "x.hip:1:1: remark: Function Name: _Z1av [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _Z1bv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     SGPRs Spill: 16 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     VGPRs Spill: 3 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert vgpr_spills(remarks) == {"_Z1bv": 3}
+    assert vgpr_spills("") == {}
