@@ -516,7 +516,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
 
-  const float* Tg = (const float*)a.ws.p[R_T] + tile * 64 * 64;
+  const bf16* Tg = (const bf16*)a.ws.p[R_T] + tile * 64 * 64;
   const float* MPg = (const float*)a.ws.p[R_MP] + tile * 64 * 64;
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
   const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
@@ -527,8 +527,8 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
   float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
   float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
-  float* DA = (float*)a.sc.p[S_DA] + tile * 64 * 64;
-  float* DMP = (float*)a.sc.p[S_DMP] + tile * 64 * 64;
+  bf16* DA = (bf16*)a.sc.p[S_DA] + tile * 64 * 64;
+  bf16* DMP = (bf16*)a.sc.p[S_DMP] + tile * 64 * 64;
 
   // PA's state rows: wave w owns key tile w / (4 / RPW) and RPW row tiles; its f32 S and
   // dS' rows are requested first, with everything P0 loads
@@ -561,9 +561,9 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   float gk[8];
   load8f(Gg + tkc * K + ck, gk);
   const float bt = ((const float*)a.ws.p[R_BETA])[tile * 64 + tkc], rkt = RK[tkc];
-  float4 treg[64 * 64 / (4 * kDenseThreads)];
+  bf16x4 treg[64 * 64 / (4 * kDenseThreads)];
 #pragma unroll
-  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const float4*)(Tg + (q * kDenseThreads + tid) * 4);
+  for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) treg[q] = *(const bf16x4*)(Tg + (q * kDenseThreads + tid) * 4);
   bf16x8 dlf[NDL];
 #pragma unroll
   for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
@@ -689,7 +689,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     const int ba = p / 4, bb = p % 4;
     if (bb > ba) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) DA[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr] = 0.f;
+      for (int rr = 0; rr < 4; ++rr) DA[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr] = to_bf16(0.f);
       continue;
     }
     const int i = 16 * ba + lr, j = 16 * bb + lr;
@@ -703,7 +703,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int ii = 16 * ba + 4 * kg + rr;
-      DA[ii * 64 + jj] = jj <= ii ? acc[rr] : 0.f;
+      DA[ii * 64 + jj] = to_bf16(jj <= ii ? acc[rr] : 0.f);
     }
   }
   __syncthreads();
@@ -712,7 +712,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) {
     const int idx = (q * kDenseThreads + tid) * 4, i = idx / 64, j = idx % 64;
     bf16* t = sT + i * MP + j;
-    t[0] = to_bf16(treg[q].x); t[1] = to_bf16(treg[q].y); t[2] = to_bf16(treg[q].z); t[3] = to_bf16(treg[q].w);
+    *(bf16x4*)t = treg[q];
     bf16* z = sDT + i * MP + j;
     z[0] = z[1] = z[2] = z[3] = to_bf16(0.f);
   }
@@ -802,7 +802,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     for (int rr = 0; rr < 4; ++rr) {
       const int ii = 16 * ba + 4 * kg + rr;
       const float dm = jj < ii ? -acc[rr] : 0.f;
-      DMP[ii * 64 + jj] = sB[ii] * dm;
+      DMP[ii * 64 + jj] = to_bf16(sB[ii] * dm);
       float part = dm * mp[rr];
       part = group_sum<16>(part);
       if (lr == 0) sPM[bb * 64 + ii] = part;
@@ -810,7 +810,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   }
   for (int idx = tid; idx < 64 * 64; idx += kVjpThreads) {
     const int ii = idx / 64, jj = idx % 64;
-    if (jj / 16 > ii / 16) DMP[idx] = 0.f;
+    if (jj / 16 > ii / 16) DMP[idx] = to_bf16(0.f);
   }
   __syncthreads();
 
@@ -915,8 +915,8 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   const int lr = lane % 16, kg = lane / 16;
 
   const float* Gg = (const float*)a.ws.p[R_G] + tile * 64 * K;
-  const float* DA = (const float*)a.sc.p[S_DA] + tile * 64 * 64;
-  const float* DMP = (const float*)a.sc.p[S_DMP] + tile * 64 * 64;
+  const bf16* DA = (const bf16*)a.sc.p[S_DA] + tile * 64 * 64;
+  const bf16* DMP = (const bf16*)a.sc.p[S_DMP] + tile * 64 * 64;
   // dQg/dKd/dKb of this tile (from the dense role)
   const float* DQG = (const float*)a.sc.p[S_DQG] + tile * 64 * K;
   const float* DKD = (const float*)a.sc.p[S_DKD] + tile * 64 * K;
@@ -944,10 +944,10 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
     gate();  // everything below reads the dense role's results
     // dA, dM': 64 x 64 f32 each, 4 consecutive per thread
     const int ai = tid * 4;
-    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xm = xa;
+    bf16x4 ya = {}, ym = {};
     if (ai < 64 * 64) {
-      xa = *(const float4*)(DA + ai);
-      xm = *(const float4*)(DMP + ai);
+      ya = *(const bf16x4*)(DA + ai);
+      ym = *(const bf16x4*)(DMP + ai);
     }
     if (act) {
       float sq = 0.f, sk = 0.f;
@@ -978,9 +978,6 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
       }
     }
     if (ai < 64 * 64) {
-      bf16x4 ya, ym;
-      ya[0] = to_bf16(xa.x); ya[1] = to_bf16(xa.y); ya[2] = to_bf16(xa.z); ya[3] = to_bf16(xa.w);
-      ym[0] = to_bf16(xm.x); ym[1] = to_bf16(xm.y); ym[2] = to_bf16(xm.z); ym[3] = to_bf16(xm.w);
       *(bf16x4*)(sDA + (ai / 64) * AP + ai % 64) = ya;
       *(bf16x4*)(sDM + (ai / 64) * AP + ai % 64) = ym;
     }
@@ -1099,8 +1096,8 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
           ck[r] *= f;
         }
       } else {
-        // a block whose decay spans more than 80 nats: exact per-pair factors (f32 dA, dM'
-        // from the dense kernel's output)
+        // a block whose decay spans more than 80 nats: exact per-pair f32 factors (dA, dM'
+        // as the dense part stored them, bf16)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int ii = 16 * rt + 4 * kg + rr;
@@ -1108,14 +1105,14 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
           float sq = 0.f, sk = 0.f;
           for (int j = 0; j <= ii; ++j) {
             const float kj = to_f32(sK[j * QP + c]) * sRk[j] * expf(gi - sG[j * GP + c]);
-            sq = fmaf(DA[ii * 64 + j], kj, sq);
-            sk = fmaf(DMP[ii * 64 + j], kj, sk);
+            sq = fmaf(to_f32(DA[ii * 64 + j]), kj, sq);
+            sk = fmaf(to_f32(DMP[ii * 64 + j]), kj, sk);
           }
           float tq = 0.f, tk = 0.f;
           for (int i = ii; i < 64; ++i) {
             const float e = expf(sG[i * GP + c] - gi);
-            tq = fmaf(DA[i * 64 + ii], to_f32(sQ[i * QP + c]) * sRq[i] * e, tq);
-            tk = fmaf(DMP[i * 64 + ii], to_f32(sK[i * QP + c]) * sRk[i] * e, tk);
+            tq = fmaf(to_f32(DA[i * 64 + ii]), to_f32(sQ[i * QP + c]) * sRq[i] * e, tq);
+            tk = fmaf(to_f32(DMP[i * 64 + ii]), to_f32(sK[i * QP + c]) * sRk[i] * e, tk);
           }
           rq[rr] = sq;
           rk[rr] = sk;

@@ -638,8 +638,14 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     __syncthreads();
   }
   {
-    float* Tout = (float*)a.ws.p[R_T] + tile * 64 * 64;
-    for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) Tout[idx] = sT[(idx / 64) * 65 + idx % 64];
+    bf16* Tout = (bf16*)a.ws.p[R_T] + tile * 64 * 64;
+    for (int idx = 4 * tid; idx < 64 * 64; idx += 4 * kIntraThreads) {
+      const float* t = sT + (idx / 64) * 65 + idx % 64;
+      bf16x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = to_bf16(t[e]);
+      *(bf16x4*)(Tout + idx) = x;
+    }
   }
 
   // ---- phase 4: U = T (beta v), W = T (beta kh e^G); wave w = row tile ----

@@ -48,7 +48,7 @@ enum WsRegion {
   R_UF,          // bf16 U = T (beta v) in MFMA C layout: [V/16 strip][4 row tile][64 lane][4]
   R_AF,          // bf16 fragments of A (64 x 64, lower incl. diagonal), permuted
   R_ATF,         // bf16 fragments of A^T
-  R_T,           // f32  [tile][64][64] T = (I + diag(beta) M')^-1
+  R_T,           // bf16 [tile][64][64] T = (I + diag(beta) M')^-1 (only ever a bf16 MFMA operand)
   R_MP,          // f32  [tile][64][64] M' (strictly lower, without beta)
   R_G,           // f32  [tile][64][K]  G = inclusive cumsum of g in the chunk
   R_LAM,         // f32  [tile][K]      exp(G_last)
@@ -68,8 +68,8 @@ enum WsRegion {
 enum ScRegion {
   S_DSH = 0,  // f32  [tile][K][V]   dL/dS at the chunk end
   S_DDLT,     // f32  [tile][V][64]  (dL/d delta)^T
-  S_DA,       // f32  [tile][64][64] dL/dA (masked lower)
-  S_DMP,      // f32  [tile][64][64] dL/dM' (strictly lower, beta folded in)
+  S_DA,       // bf16 [tile][64][64] dL/dA (masked lower; the decay VJP's MFMA operand)
+  S_DMP,      // bf16 [tile][64][64] dL/dM' (strictly lower, beta folded in; same)
   S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
   S_DKD,      // f32  [tile][item][64 lane][4]  dL/dKd  (same layout)
   S_DKB,      // f32  [tile][item][64 lane][4]  dL/d(beta kh exp(G))  (same layout)
@@ -100,7 +100,8 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
     case R_QGF: case R_QGTF: case R_KDF: case R_KDTF: case R_WF: case R_WTF: return nt * 64 * K * 2;
     case R_UF: return nt * 64 * V * 2;
     case R_AF: case R_ATF: return nt * 64 * 64 * 2;
-    case R_T: case R_MP: return nt * 64 * 64 * 4;
+    case R_T: return nt * 64 * 64 * 2;
+    case R_MP: return nt * 64 * 64 * 4;
     case R_G: return nt * 64 * K * 4;
     case R_LAM: return nt * K * 4;
     case R_RQ: case R_RK: case R_BETA: return nt * 64 * 4;
@@ -119,7 +120,7 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   switch (r) {
     case S_DSH: return nt * K * V * 4;
     case S_DDLT: return nt * 64 * V * 4;
-    case S_DA: case S_DMP: return nt * 64 * 64 * 4;
+    case S_DA: case S_DMP: return nt * 64 * 64 * 2;
     case S_DQG: case S_DKD: case S_DKB: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
     case S_DGL: return nt * K * 4;
