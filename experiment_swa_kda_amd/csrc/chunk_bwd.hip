@@ -567,25 +567,12 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   bf16x8 dlf[NDL];
 #pragma unroll
   for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
-  gate();
-#pragma unroll
-  for (int sv = 0; sv < NVS; ++sv) {
-    if (Gate::kCoherent) {
-      const float4 x0 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg);
-      const float4 x1 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg + 4);
-      xd[sv][0] = x0.x; xd[sv][1] = x0.y; xd[sv][2] = x0.z; xd[sv][3] = x0.w;
-      xd[sv][4] = x1.x; xd[sv][5] = x1.y; xd[sv][6] = x1.z; xd[sv][7] = x1.w;
-    } else {
-      load8f(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg, xd[sv]);
-    }
-  }
-  float4 ddl[NDU];
-#pragma unroll
-  for (int q = 0; q < NDU; ++q) {
-    const int idx = min(q * kDenseThreads + tid, V * 16 - 1);
-    ddl[q] = Gate::kCoherent ? load4_coherent(DDLT, (idx / 16) * 64 + (idx % 16) * 4)
-                             : *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
-  }
+  // operands of later phases, requested with the rest (each would otherwise cost a global
+  // round trip of its own after the gate): beta rows and lam of PA's key column
+  const float beta_row = ((const float*)a.ws.p[R_BETA])[tile * 64 + (tid & 63)];
+  const float lam_pa = ((const float*)a.ws.p[R_LAM])[tile * K + pa_c];
+  // ---- P0 (scan-independent, before the gate): stage dO, v, beta kh e^G, delta, beta;
+  // dQg = dO S^T and dA = tril(dO delta^T) need nothing from the scan ----
   {
     const float bk = tk < len ? bt * rkt : 0.f;
     bf16x8 xb;
@@ -601,19 +588,6 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     }
     if (tk < 64) *(bf16x8*)(sKB + tk * KP + ck) = xb;
   }
-  // dU = dDelta (hi/lo bf16 split) and delta, transposed from their [V][64] histories
-#pragma unroll
-  for (int q = 0; q < NDU; ++q) {
-    const int idx = q * kDenseThreads + tid, vv = idx / 16, t4 = (idx % 16) * 4;
-    if (idx >= V * 16) break;
-    const float dv[4] = {ddl[q].x, ddl[q].y, ddl[q].z, ddl[q].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bf16 hi = to_bf16(dv[e]);
-      sDU[(t4 + e) * VP + vv] = hi;
-      sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
-    }
-  }
   // delta from its B-operand fragments [strip][2][64 lanes][8] in the scan's permuted
   // token order: element e of lane l is t = 32 s + 16 (e/4) + 4 (l/16) + e%4
 #pragma unroll
@@ -625,63 +599,28 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
 #pragma unroll
     for (int e = 0; e < 8; ++e) sDL[(t0 + 16 * (e / 4) + e % 4) * VP + vv] = dlf[q][e];
   }
-  if (tid < 64) sB[tid] = ((const float*)a.ws.p[R_BETA])[tile * 64 + tid];
+  if (tid < 64) sB[tid] = beta_row;
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
   __syncthreads();
-
-  auto f2b8 = [&](const float* p) -> bf16x8 {
-    bf16x8 x;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = to_bf16(p[e]);
-    return x;
-  };
-
-  // ---- PA: dQg, dKd, dW over the 64 x K grid ----
-  // Wave w owns key tile ct and RPW row tiles: the f32 state rows S[c][.] and dS'[c][.] of
-  // its 16 keys (requested at the start) are split into hi + lo bf16 once and reused for
-  // every row tile.  The same rows give dlam = lam * sum_v S dS'.
+  // dQg for PA's items: wave w owns key tile pa_ct and RPW row tiles; the f32 state rows
+  // S[c][.] of its 16 keys are split into hi + lo bf16 where they are used (a few VALU
+  // operations instead of registers held across the phases)
   {
-    const int ct = pa_ct, rt0 = pa_rt0;
-    const int c = 16 * ct + lr;
-    const float lamc = ((const float*)a.ws.p[R_LAM])[tile * K + c];
-    bf16x8 sHi[NVS], sLo[NVS], dHi[NVS], dLo[NVS];
-    float dl = 0.f;
-#pragma unroll
-    for (int sv = 0; sv < NVS; ++sv) {
-      split8(xs[sv], sHi[sv], sLo[sv]);
-      split8(xd[sv], dHi[sv], dLo[sv]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dl = fmaf(xs[sv][e], xd[sv][e], dl);
-    }
-    dl = swap32_sum(swap16_sum(dl));
-    if (rt0 == 0 && kg == 0) ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lamc;
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
-      const int rt = rt0 + q, i = 16 * rt + lr;
-      const int p = rt + 4 * ct;
-      bf16x8 aO[NVS];
-#pragma unroll
-      for (int sv = 0; sv < NVS; ++sv) aO[sv] = *(const bf16x8*)(sDO + i * VP + 32 * sv + 8 * kg);
-      f32x4 accQ = zero4(), accK = zero4(), accW = zero4();
+      const int rt = pa_rt0 + q, i = 16 * rt + lr;
+      const int p = rt + 4 * pa_ct;
+      f32x4 accQ = zero4();
 #pragma unroll
       for (int sv = 0; sv < NVS; ++sv) {
-        const int vv = 32 * sv + 8 * kg;
-        const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
-        const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
-        const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
-        accQ = mfma16(aO[sv], sHi[sv], accQ);
-        accQ = mfma16(aO[sv], sLo[sv], accQ);
-        accK = mfma16(aL, dHi[sv], accK);
-        accK = mfma16(aL, dLo[sv], accK);
-        accW = mfma16(uHi, sHi[sv], accW);
-        accW = mfma16(uHi, sLo[sv], accW);
-        accW = mfma16(uLo, sHi[sv], accW);
+        bf16x8 sHi, sLo;
+        split8(xs[sv], sHi, sLo);
+        const bf16x8 aO = *(const bf16x8*)(sDO + i * VP + 32 * sv + 8 * kg);
+        accQ = mfma16(aO, sHi, accQ);
+        accQ = mfma16(aO, sLo, accQ);
       }
-      // raw dQg, dKd in C-layout item order (consumed with the same lane ownership)
+      // raw dQg in C-layout item order (consumed with the same lane ownership)
       *(f32x4*)(DQG + ((size_t)p * 64 + lane) * 4) = accQ;
-      *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = to_bf16(-accW[rr]);
     }
   }
   // dA = tril(dO delta^T), 16x16 blocks of the lower triangle; upper blocks zero
@@ -706,6 +645,87 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
       DA[ii * 64 + jj] = to_bf16(jj <= ii ? acc[rr] : 0.f);
     }
   }
+
+  // xs made opaque: PA splits it again instead of keeping this split's 32 registers alive
+#pragma unroll
+  for (int sv = 0; sv < NVS; ++sv)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(xs[sv][e]));
+
+  gate();
+  // ---- the scan's histories: dS' rows of PA's key tile, dU = dDelta (hi/lo bf16 split),
+  // transposed from its [V][64] history ----
+#pragma unroll
+  for (int sv = 0; sv < NVS; ++sv) {
+    if (Gate::kCoherent) {
+      const float4 x0 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg);
+      const float4 x1 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg + 4);
+      xd[sv][0] = x0.x; xd[sv][1] = x0.y; xd[sv][2] = x0.z; xd[sv][3] = x0.w;
+      xd[sv][4] = x1.x; xd[sv][5] = x1.y; xd[sv][6] = x1.z; xd[sv][7] = x1.w;
+    } else {
+      load8f(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg, xd[sv]);
+    }
+  }
+  float4 ddl[NDU];
+#pragma unroll
+  for (int q = 0; q < NDU; ++q) {
+    const int idx = min(q * kDenseThreads + tid, V * 16 - 1);
+    ddl[q] = Gate::kCoherent ? load4_coherent(DDLT, (idx / 16) * 64 + (idx % 16) * 4)
+                             : *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
+  }
+#pragma unroll
+  for (int q = 0; q < NDU; ++q) {
+    const int idx = q * kDenseThreads + tid, vv = idx / 16, t4 = (idx % 16) * 4;
+    if (idx >= V * 16) break;
+    const float dv[4] = {ddl[q].x, ddl[q].y, ddl[q].z, ddl[q].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16 hi = to_bf16(dv[e]);
+      sDU[(t4 + e) * VP + vv] = hi;
+      sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
+    }
+  }
+  __syncthreads();
+
+  // ---- PA: dKd, dW over the 64 x K grid (same items as dQg) ----
+  // The f32 rows S[c][.] and dS'[c][.] of the wave's 16 keys, split into hi + lo bf16 where
+  // they are used.  The same rows give dlam = lam * sum_v S dS'.
+  {
+    const int ct = pa_ct, rt0 = pa_rt0;
+    const int c = 16 * ct + lr;
+    const float lamc = lam_pa;  // c == pa_c
+    float dl = 0.f;
+#pragma unroll
+    for (int sv = 0; sv < NVS; ++sv)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dl = fmaf(xs[sv][e], xd[sv][e], dl);
+    dl = swap32_sum(swap16_sum(dl));
+    if (rt0 == 0 && kg == 0) ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lamc;
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rt = rt0 + q, i = 16 * rt + lr;
+      const int p = rt + 4 * ct;
+      f32x4 accK = zero4(), accW = zero4();
+#pragma unroll
+      for (int sv = 0; sv < NVS; ++sv) {
+        const int vv = 32 * sv + 8 * kg;
+        bf16x8 sHi, sLo, dHi, dLo;
+        split8(xs[sv], sHi, sLo);
+        split8(xd[sv], dHi, dLo);
+        const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
+        const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
+        const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
+        accK = mfma16(aL, dHi, accK);
+        accK = mfma16(aL, dLo, accK);
+        accW = mfma16(uHi, sHi, accW);
+        accW = mfma16(uHi, sLo, accW);
+        accW = mfma16(uLo, sHi, accW);
+      }
+      *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sDW[(16 * rt + 4 * kg + rr) * KP + c] = to_bf16(-accW[rr]);
+    }
+  }
   __syncthreads();
   // dU lo and delta are consumed: their region now holds T (bf16) and a zeroed dT
 #pragma unroll
@@ -717,6 +737,31 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     z[0] = z[1] = z[2] = z[3] = to_bf16(0.f);
   }
   __syncthreads();
+
+  // PD's M' entries (wave p < 10 owns PD item p), requested before PB and PC
+  static_assert(kVjpWaves >= 10, "one PD item per wave");
+  float mp_pd[4] = {0.f, 0.f, 0.f, 0.f};
+  if (wave < 10) {
+    const int ba = wave < 1 ? 0 : wave < 3 ? 1 : wave < 6 ? 2 : 3;
+    const int bb = wave - (ba * (ba + 1)) / 2;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) mp_pd[rr] = MPg[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr];
+  }
+  // The decay part's first loads (q and k rows, G of the tile) touched once per 128-byte
+  // line, so they come from L2 when the decay part starts; the value is only kept alive.
+  float warm = 0.f;
+  {
+    constexpr int LQ = K * 2 / 128, LG = K * 4 / 128;  // lines per row of q / k and of G
+    constexpr int NQK = 64 * LQ;
+    static_assert(2 * NQK + 64 * LG <= kDenseThreads, "one line per thread");
+    if (tid < 2 * NQK) {
+      const int r = min((tid % NQK) / LQ, len - 1), l = tid % LQ;
+      const bf16* base = tid < NQK ? a.q : a.k;
+      warm = *(const float*)(base + ((size_t)(row0 + r) * H + h) * K + 64 * l);
+    } else if (tid < 2 * NQK + 64 * LG) {
+      warm = Gg[(size_t)(tid - 2 * NQK) * 32];
+    }
+  }
 
   // ---- PB: dT (lower blocks), d(beta v), d(beta kh e^G) ----
   for (int p = wave; p < 10; p += kVjpWaves) {
@@ -788,9 +833,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     const int ba = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
     const int bb = p - (ba * (ba + 1)) / 2;
     const int i = 16 * ba + lr, j = 16 * bb + lr;
-    float mp[4];  // M' entries of this lane's outputs, needed after the MFMAs
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) mp[rr] = MPg[(16 * ba + 4 * kg + rr) * 64 + 16 * bb + lr];
+    const float* mp = mp_pd;  // M' entries of this lane's outputs (p == wave)
     f32x4 acc = zero4();
     const int nsteps = (16 * bb + 15) / 32 + 1;
     for (int s = 0; s < nsteps; ++s) {
@@ -821,6 +864,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     for (int b = 0; b < 4; ++b) db += sPM[b * 64 + tid];
     ((float*)a.sc.p[S_DBETA])[tile * 64 + tid] = db;
   }
+  asm volatile("" ::"v"(warm));
 }
 
 // ---------------------------------------------------------------------------
