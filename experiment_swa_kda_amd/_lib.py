@@ -37,6 +37,7 @@ class ChunkProblem(ctypes.Structure):
         ("gate_mode", ctypes.c_int32),
         ("lower_bound", ctypes.c_float),
         ("scale", ctypes.c_float),
+        ("grad_row_stride", ctypes.c_int32),
     ]
 
 
@@ -68,7 +69,7 @@ SIGNATURES = {
     "kda_weight_grad": (ctypes.c_int, [_L, _I, _I, _P, _L, _P, _L, _P, _P, _P]),
     "kda_resid_mix_backward_scratch_bytes": (ctypes.c_size_t, [_L]),
     "kda_resid_mix_forward": (ctypes.c_int, [_L, _P, _P, _P, _P, _P, _P]),
-    "kda_resid_mix_backward": (ctypes.c_int, [_L] + [_P] * 10 + [_P]),
+    "kda_resid_mix_backward": (ctypes.c_int, [_L] + [_P] * 9 + [_I, _I, _P, _P]),
     "kda_relu2_forward": (ctypes.c_int, [_L, _P, _P, _P]),
     "kda_rms_norm_forward": (ctypes.c_int, [_L, _I, _F, _P, _P, _P, _P]),
     "kda_rms_norm_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P]),

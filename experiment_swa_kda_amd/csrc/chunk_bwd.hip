@@ -64,6 +64,7 @@ struct BwdArgs {
   float* ds0;
   Regions ws;
   Regions sc;
+  long gld_qk, gld_v;  // row strides (elements per token) of dq / dk and of dv
 };
 
 // ---------------------------------------------------------------------------
@@ -797,7 +798,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
       const int jj = 16 * rt + 4 * kg + rr;
       float part = 0.f;
       if (jj < len) {
-        const size_t off = ((size_t)(row0 + jj) * H + h) * V + col;
+        const size_t off = (size_t)(row0 + jj) * a.gld_v + (size_t)h * V + col;
         a.dv[off] = to_bf16(sB[jj] * acc[rr]);
         part = acc[rr] * to_f32(sV[jj * VP + col]);
       }
@@ -1259,7 +1260,7 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
     for (int idx = ptid; idx < 64 * LPR; idx += kVjpThreads) {
       const int t = idx / LPR, c0 = (idx % LPR) * 8;
       if (t >= len) continue;
-      const size_t base = ((size_t)(row0 + t) * H + h) * K + c0;
+      const size_t base = (size_t)(row0 + t) * a.gld_qk + (size_t)h * K + c0;
       *(bf16x8*)(a.dq + base) = *(const bf16x8*)(sQ + t * QP + c0);
       *(bf16x8*)(a.dk + base) = *(const bf16x8*)(sK + t * QP + c0);
     }
@@ -1645,6 +1646,10 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
               "chunk_backward: q, k, v, gate, grad_output and the gradients must be 16-byte aligned");
   KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || (A_log && dt_bias && dA_log && ddt_bias),
               "chunk_backward: K3 gate needs A_log, dt_bias, dA_log and ddt_bias");
+  KDA_REQUIRE(p->grad_row_stride == 0 ||
+                  (p->grad_row_stride % 8 == 0 &&
+                   (long)p->grad_row_stride >= (long)p->heads * (p->key_dim > p->value_dim ? p->key_dim : p->value_dim)),
+              "chunk_backward: grad_row_stride must be 0 or a multiple of 8 of at least H * max(K, V)");
   KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,
               "chunk_backward: workspace must be non-null and 256-byte aligned");
   KDA_REQUIRE(scratch && ((uintptr_t)scratch % 256) == 0,
@@ -1668,6 +1673,8 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
   a.dq = (bf16*)dq;
   a.dk = (bf16*)dk;
   a.dv = (bf16*)dv;
+  a.gld_qk = p->grad_row_stride > 0 ? p->grad_row_stride : (long)p->heads * p->key_dim;
+  a.gld_v = p->grad_row_stride > 0 ? p->grad_row_stride : (long)p->heads * p->value_dim;
   a.dgate = dgate;
   a.dbeta = (bf16*)dbeta_logits;
   a.dA_log = dA_log;

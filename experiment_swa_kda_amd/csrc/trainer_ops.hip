@@ -112,6 +112,21 @@ __global__ __launch_bounds__(kGlueThreads) void resid_mix_bwd_kernel(
   }
 }
 
+// Both scalar gradients of the residual mix from the per-workgroup partials (rows 0 and 1 of
+// `part`), each by one wave in a fixed order, written into vectors of nslots entries: the
+// sum at `slot`, zero elsewhere (the gradient of lambda[slot] for a whole lambda vector).
+__global__ __launch_bounds__(2 * kWave) void resid_mix_reduce_kernel(int parts, const float* __restrict__ part,
+                                                                     int slot, int nslots, float* __restrict__ da,
+                                                                     float* __restrict__ db) {
+  const int row = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const float* p = part + (size_t)row * parts;
+  float acc = 0.f;
+  for (int i = lane; i < parts; i += kWave) acc += p[i];
+  acc = wave_sum(acc);
+  float* out = row == 0 ? da : db;
+  for (int j = lane; j < nslots; j += kWave) out[j] = j == slot ? acc : 0.f;
+}
+
 // y = relu(x)^2
 __global__ __launch_bounds__(kGlueThreads) void relu2_fwd_kernel(long n, const bf16* __restrict__ x,
                                                                  bf16* __restrict__ y) {
@@ -267,11 +282,13 @@ extern "C" int kda_resid_mix_forward(int64_t n, const float* a, const float* b, 
 
 extern "C" int kda_resid_mix_backward(int64_t n, const float* a, const float* b, const void* x,
                                       const void* x0, const void* grad, void* dx, void* dx0,
-                                      float* da, float* db, void* scratch, hipStream_t stream) {
+                                      float* da, float* db, int32_t slot, int32_t nslots, void* scratch,
+                                      hipStream_t stream) {
   using namespace kda;
   KDA_GLUE_CHECK(n, x, x0, grad, dx, dx0);
   KDA_REQUIRE(a && b && da && db && (n == 0 || (x && x0 && grad && dx && dx0 && scratch)),
               "resid_mix_backward: null pointer");
+  KDA_REQUIRE(nslots >= 1 && slot >= 0 && slot < nslots, "resid_mix_backward: slot out of range");
   const unsigned blocks = n > 0 ? glue_blocks(n) : 0;
   float* part = (float*)scratch;
   if (n > 0) {
@@ -279,11 +296,9 @@ extern "C" int kda_resid_mix_backward(int64_t n, const float* a, const float* b,
                        (const bf16*)x, (const bf16*)x0, (const bf16*)grad, (bf16*)dx, (bf16*)dx0, part);
     KDA_LAUNCH_CHECK("resid_mix_backward");
   }
-  // da = sum of the first row of partials, db of the second (fixed order)
-  hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3(1), dim3(256), 0, stream, (int)blocks, 1,
-                     (const float*)part, da);
-  hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3(1), dim3(256), 0, stream, (int)blocks, 1,
-                     (const float*)(part + blocks), db);
+  // da = sum of the first row of partials, db of the second (fixed order), one launch
+  hipLaunchKernelGGL(resid_mix_reduce_kernel, dim3(1), dim3(2 * kWave), 0, stream, (int)blocks,
+                     (const float*)part, (int)slot, (int)nslots, da, db);
   KDA_LAUNCH_CHECK("resid_mix_backward reduce");
   return KDA_OK;
 }

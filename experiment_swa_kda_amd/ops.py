@@ -255,9 +255,11 @@ def chunk_forward_conv_norm_gate(qkv_in, conv_weight, gate_values, beta_logits, 
 
 def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace,
                    grad_output, grad_final_state, lower_bound, scale, *, cu_seqlens=None,
-                   gate="k3"):
+                   gate="k3", packed_qkv_grad=False):
     """Exact chunked backward.  Returns the eight gradients
-    (dq, dk, dv, dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state)."""
+    (dq, dk, dv, dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state).  With
+    ``packed_qkv_grad`` (K == V) dq, dk and dv are written side by side into one
+    [B, T, 3 H K] tensor, which is returned in place of dq (dk and dv are then None)."""
     gm = GATE_MODES[gate]
     dev = _check_chunk_inputs("chunk_backward", q, k, v, gate_values, beta_logits, A_log, dt_bias,
                               initial_state, cu_seqlens, gm)
@@ -275,9 +277,16 @@ def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_st
     lib = _lib.load()
     sc_bytes = lib.kda_chunk_backward_scratch_bytes(ctypes.byref(p))
     scratch = torch.empty(max(sc_bytes, 256), dtype=torch.uint8, device=dev)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+    if packed_qkv_grad:
+        if V != K:
+            raise ValueError("chunk_backward: packed_qkv_grad needs key_dim == value_dim")
+        dqkv = torch.empty(B, T, 3 * H * K, dtype=q.dtype, device=dev)
+        p.grad_row_stride = 3 * H * K
+        dq, dk, dv = dqkv[..., :H * K], dqkv[..., H * K:2 * H * K], dqkv[..., 2 * H * K:]
+    else:
+        dq = torch.empty_like(q)
+        dk = torch.empty_like(k)
+        dv = torch.empty_like(v)
     dgate = torch.empty_like(gate_values)
     dbeta = torch.empty_like(beta_logits)
     if gm == KDA_GATE_K3:
@@ -293,6 +302,8 @@ def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_st
             ptr(grad_final_state), ptr(dq), ptr(dk), ptr(dv), ptr(dgate), ptr(dbeta), ptr(dA),
             ptr(ddt), ptr(dinit), ptr(scratch), _stream(dev))
     check(rc, "kda_chunk_backward")
+    if packed_qkv_grad:
+        return dqkv, None, None, dgate, dbeta, dA, ddt, dinit
     return dq, dk, dv, dgate, dbeta, dA, ddt, dinit
 
 
@@ -541,18 +552,23 @@ def resid_mix_forward(x, x0, a, b):
     return y
 
 
-def resid_mix_backward(x, x0, a, b, grad):
-    """Returns (dx, dx0, da [1] f32, db [1] f32)."""
+def resid_mix_backward(x, x0, lam_a, lam_b, slot, grad):
+    """Backward of y = lam_a[slot] x + lam_b[slot] x0 for f32 lambda vectors: returns
+    (dx, dx0, dlam_a, dlam_b), the lambda gradients full-length and zero except at slot."""
     dev = _glue_check("resid_mix_backward", x, x0, grad)
-    x, x0, grad, a, b = _c(x), _c(x0), _c(grad), _c(a), _c(b)
+    x, x0, grad, lam_a, lam_b = _c(x), _c(x0), _c(grad), _c(lam_a), _c(lam_b)
+    n = lam_a.numel()
+    if lam_a.dtype != torch.float32 or lam_b.dtype != torch.float32 or lam_b.numel() != n or not 0 <= slot < n:
+        raise ValueError("resid_mix_backward: f32 lambda vectors of one length and a slot inside them")
     lib = _lib.load()
     scratch = torch.empty(lib.kda_resid_mix_backward_scratch_bytes(x.numel()), dtype=torch.uint8, device=dev)
     dx, dx0 = torch.empty_like(x), torch.empty_like(x0)
-    da = torch.empty(1, dtype=torch.float32, device=dev)
-    db = torch.empty(1, dtype=torch.float32, device=dev)
+    da = torch.empty(n, dtype=torch.float32, device=dev)
+    db = torch.empty(n, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        rc = lib.kda_resid_mix_backward(x.numel(), ptr(a), ptr(b), ptr(x), ptr(x0), ptr(grad), ptr(dx),
-                                        ptr(dx0), ptr(da), ptr(db), ptr(scratch), _stream(dev))
+        rc = lib.kda_resid_mix_backward(x.numel(), ptr(lam_a) + 4 * slot, ptr(lam_b) + 4 * slot, ptr(x), ptr(x0),
+                                        ptr(grad), ptr(dx), ptr(dx0), ptr(da), ptr(db), slot, n, ptr(scratch),
+                                        _stream(dev))
     check(rc, "kda_resid_mix_backward")
     return dx, dx0, da, db
 

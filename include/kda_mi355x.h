@@ -46,6 +46,11 @@ typedef struct kda_chunk_problem {
   int32_t gate_mode;   /* KDA_GATE_K3 or KDA_GATE_LOGDECAY */
   float lower_bound;   /* K3 lower bound lb (< 0) */
   float scale;         /* query scale (resolved by the caller, normally K^-0.5) */
+  int32_t grad_row_stride; /* backward only: elements between consecutive tokens' rows of
+                              dq, dk and dv (a multiple of 8, at least H * max(K, V)); 0 for
+                              dense [.., H, K] / [.., H, V] gradients.  Lets the three land
+                              interleaved in one [B, T, 3 H K] buffer.  (No reference
+                              counterpart: the reference returns three tensors.) */
 } kda_chunk_problem;
 
 /* Last error message of the calling thread ("" when none). */
@@ -311,16 +316,18 @@ int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, int64_t ldd
  * Trainer support: fused elementwise glue of the decoder (reference nanochat/gpt.py,
  * fused there by torch.compile).  bf16 tensors of n elements (n % 8 == 0, 16-byte aligned).
  *   resid_mix: y = a x + b x0 with device scalars a, b (the per-layer resid / x0 lambdas,
- *     gpt.py:585-587); backward dx = a g, dx0 = b g, da = sum g x, db = sum g x0 (fixed-order
- *     reduction through `scratch`, kda_resid_mix_backward_scratch_bytes(n) bytes).
+ *     gpt.py:585-587); backward dx = a g, dx0 = b g and the scalar gradients sum g x, sum g x0
+ *     (fixed-order reduction through `scratch`, kda_resid_mix_backward_scratch_bytes(n)
+ *     bytes) written to da[slot], db[slot] of nslots-entry vectors that are zero elsewhere
+ *     (a, b point at lambda[slot] of the lambda vectors).
  *   relu2: y = relu(x)^2 (the MLP activation, gpt.py:151-156); backward dx = 2 relu(x) g.
  */
 size_t kda_resid_mix_backward_scratch_bytes(int64_t n);
 int kda_resid_mix_forward(int64_t n, const float* a, const float* b, const void* x, const void* x0,
                           void* y, hipStream_t stream);
 int kda_resid_mix_backward(int64_t n, const float* a, const float* b, const void* x, const void* x0,
-                           const void* grad, void* dx, void* dx0, float* da, float* db,
-                           void* scratch, hipStream_t stream);
+                           const void* grad, void* dx, void* dx0, float* da, float* db, int32_t slot,
+                           int32_t nslots, void* scratch, hipStream_t stream);
 int kda_relu2_forward(int64_t n, const void* x, void* y, hipStream_t stream);
 /* rms_norm (no weight; the decoder's norm(), gpt.py:46-48) over bf16 rows of dim = 128 J
  * (J in {1,2,3,4,6,8}): y = x / sqrt(mean(x^2) + eps), rinv [rows] f32 = 1/rms;

@@ -53,6 +53,13 @@ def test_c_abi_rejects_bad_problems_without_gpu():
     assert "multiple of 8" in lib.kda_last_error().decode()
     assert lib.kda_rmsnorm_gate_forward(4, 96, None, None, None, 1e-5, None, None, None) != 0
     assert lib.kda_recurrent_decode(1, 1, 32, 64, 0, -5.0, 0.1, *([None] * 10), None) != 0
+    # a gradient row stride shorter than a token's H * max(K, V) values is refused before any
+    # launch (the pointers are never dereferenced)
+    p = _lib.ChunkProblem(batch=1, seq_len=8, heads=2, key_dim=64, value_dim=64, num_seqs=1, cu_seqlens=None,
+                          gate_mode=1, lower_bound=-5.0, scale=0.125, grad_row_stride=64)
+    fake = ctypes.c_void_p(1 << 20)
+    rc = lib.kda_chunk_backward(ctypes.byref(p), *([fake] * 20), None)
+    assert rc != 0 and "grad_row_stride" in lib.kda_last_error().decode()
 
 
 def make(B=2, T=7, H=2, K=4, V=3, seed=1729, dtype=torch.float32):

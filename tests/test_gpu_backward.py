@@ -254,3 +254,22 @@ def test_graphed_forward_backward_replays_match_eager(gate):
                 assert static[n].grad is None, (seed, n)
             else:
                 assert torch.equal(static[n].grad, eager[n].grad), (seed, n)
+
+
+@pytest.mark.parametrize("K", [64, 128])
+def test_packed_qkv_gradients_equal_separate(K):
+    """dq, dk, dv written side by side into one [B, T, 3 H K] tensor (grad_row_stride) are
+    the separately written gradients, bit for bit; the other gradients are unchanged."""
+    d = make_kda_inputs(2, 130, 3, K, K, seed=37, gate="k3", state=False, dist="baseline")
+    do, _ = cotangents(d, 5)
+    _, _, ws = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None,
+                                 False, -5.0, K ** -0.5, gate="k3")
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None, ws, do, None, -5.0, K ** -0.5)
+    sep = ops.chunk_backward(*args, gate="k3")
+    packed = ops.chunk_backward(*args, gate="k3", packed_qkv_grad=True)
+    B, T, H = 2, 130, 3
+    dqkv = packed[0].view(B, T, 3, H, K)
+    for j in range(3):
+        assert torch.equal(dqkv[:, :, j], sep[j])
+    for a, b in zip(sep[3:7], packed[3:7]):
+        assert torch.equal(a, b)
