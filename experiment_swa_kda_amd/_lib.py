@@ -60,6 +60,7 @@ SIGNATURES = {
     "kda_causal_conv_forward": (ctypes.c_int, [_I, _I, _I, _I] + [_P] * 5 + [_P]),
     "kda_causal_conv_backward_scratch_bytes": (ctypes.c_size_t, [_I, _I, _I, _I]),
     "kda_causal_conv_backward": (ctypes.c_int, [_I, _I, _I, _I] + [_P] * 9 + [_P]),
+    "kda_causal_conv_backward_strided": (ctypes.c_int, [_I, _I, _I, _I, _P, _L] + [_P] * 5 + [_L] + [_P] * 4),
     "kda_rmsnorm_gate_forward": (ctypes.c_int, [_L, _I, _P, _P, _P, _F, _P, _P, _P]),
     "kda_rmsnorm_gate_backward_scratch_bytes": (ctypes.c_size_t, [_L, _I]),
     "kda_rmsnorm_gate_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P]),

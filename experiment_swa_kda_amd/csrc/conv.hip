@@ -41,9 +41,10 @@ template <int TOK, int CGS>
 struct ConvGeom {
   static constexpr int kTok = TOK, kCgs = CGS, kSlices = 256 / CGS, kBlockTok = TOK * kSlices;
   int B, T, C, CG, ncb, ntb;  // channel groups, channel blocks, token blocks
+  long ldx, ldd;              // row strides (elements per token) of x and of dx (default C)
   __host__ __device__ ConvGeom(int B_, int T_, int C_, int halo = 0)
       : B(B_), T(T_), C(C_), CG(C_ / 8), ncb((C_ / 8 + kCgs - 1) / kCgs),
-        ntb((T_ + kBlockTok - halo - 1) / (kBlockTok - halo)) {}
+        ntb((T_ + kBlockTok - halo - 1) / (kBlockTok - halo)), ldx(C_), ldd(C_) {}
   __host__ __device__ int blocks() const { return B * ntb * ncb; }
 };
 using FwdGeom = ConvGeom<KDA_CONV_FWD_TOK, KDA_CONV_FWD_CGS>;
@@ -81,14 +82,14 @@ __device__ __forceinline__ void load_taps(const bf16* __restrict__ w, int c0, fl
 // from the initial state (or zero), rows with t >= T are zero.
 template <int W, int N>
 __device__ __forceinline__ void load_xp_rows(const bf16* __restrict__ x, const bf16* __restrict__ st,
-                                             int b, int T, int C, int c0, int p0,
+                                             int b, int T, int C, long ldx, int c0, int p0,
                                              bf16x8 (&raw)[N]) {
-  const bf16* base = x + (size_t)b * T * C + c0;
+  const bf16* base = x + (size_t)b * T * ldx + c0;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     int t = p0 - (W - 1) + i;
     t = t < 0 ? 0 : (t >= T ? T - 1 : t);
-    raw[i] = *reinterpret_cast<const bf16x8*>(base + (size_t)t * C);
+    raw[i] = *reinterpret_cast<const bf16x8*>(base + (size_t)t * ldx);
   }
   const bf16 zero = (bf16)0.f;
   if (p0 < W - 1 || p0 - (W - 1) + N > T) {
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void conv_fwd_kernel(FwdGeom g, const bf16* __
   constexpr int kTok = FwdGeom::kTok;
   constexpr int NX = kTok + W - 1;  // xp[t0 .. t0 + kTok + W - 2]
   bf16x8 xr[NX];
-  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, P.c0, P.t0, xr);
+  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, g.ldx, P.c0, P.t0, xr);
   float wt[8][W];
   load_taps<W>(w, P.c0, wt);
   bf16* yb = y + ((size_t)P.b * g.T + P.t0) * g.C + P.c0;
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
     // dpre[s] for s = s0 .. s0+kTok-1 needs xp[s .. s+W-1], i.e. xp[s0 .. s0+kTok+W-2]
     constexpr int NX = kTok + W - 1;
     bf16x8 xr[NX], gr[kTok];
-    load_xp_rows<W, NX>(x, st, b, g.T, g.C, c0, s0, xr);
+    load_xp_rows<W, NX>(x, st, b, g.T, g.C, g.ldx, c0, s0, xr);
     const bf16* dyb = dy + (size_t)b * g.T * g.C + c0;
 #pragma unroll
     for (int u = 0; u < kTok; ++u) {
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
       dpw[i][0] = a.x; dpw[i][1] = a.y; dpw[i][2] = a.z; dpw[i][3] = a.w;
       dpw[i][4] = c.x; dpw[i][5] = c.y; dpw[i][6] = c.z; dpw[i][7] = c.w;
     }
-    bf16* dxb = dx + ((size_t)b * g.T + s0) * g.C + c0;
+    bf16* dxb = dx + ((size_t)b * g.T + s0) * g.ldd + c0;
 #pragma unroll
     for (int u = 0; u < kTok; ++u) {
       const int t = s0 + u;
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] += to_f32(dfin[((size_t)b * g.C + c0 + e) * W + jf]);
       }
-      store8(dxb + (size_t)u * g.C, o);
+      store8(dxb + (size_t)u * g.ldd, o);
     }
   }
   // reduce the kWave/kCgs token slices of each wave across lanes, then the waves via LDS
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
 // dstate[b][c][i] = dxp[i-1] for i >= 1 (0 for i = 0); dxp[p] = sum_j dpre[p-j] w[j]
 // plus the final-state gradient when xp[p] is part of the final state (short T).
 template <int W>
-__global__ void conv_dstate_kernel(int B, int T, int C, const bf16* __restrict__ x,
+__global__ void conv_dstate_kernel(int B, int T, int C, long ldx, const bf16* __restrict__ x,
                                    const bf16* __restrict__ w, const bf16* __restrict__ st,
                                    const bf16* __restrict__ dy, const bf16* __restrict__ dfin,
                                    bf16* __restrict__ dst) {
@@ -300,7 +301,7 @@ __global__ void conv_dstate_kernel(int B, int T, int C, const bf16* __restrict__
   const int b = i / C;
   auto xp = [&](int p) -> float {
     int t = p - (W - 1);
-    if (t >= 0) return t < T ? to_f32(x[((size_t)b * T + t) * C + c]) : 0.f;
+    if (t >= 0) return t < T ? to_f32(x[((size_t)b * T + t) * ldx + c]) : 0.f;
     return to_f32(st[((size_t)b * C + c) * W + p + 1]);
   };
   float wt[W];
@@ -350,10 +351,12 @@ static int conv_forward_w(int B, int T, int C, const void* x, const void* w, con
 }
 
 template <int W>
-static int conv_backward_w(int B, int T, int C, const void* x, const void* w, const void* st,
-                           const void* dy, const void* dfin, void* dx, void* dw, void* dst,
+static int conv_backward_w(int B, int T, int C, const void* x, long ldx, const void* w, const void* st,
+                           const void* dy, const void* dfin, void* dx, long ldd, void* dw, void* dst,
                            void* scratch, hipStream_t stream) {
-  const BwdGeom g(B, T, C, W - 1);
+  BwdGeom g(B, T, C, W - 1);
+  g.ldx = ldx;
+  g.ldd = ldd;
   float* part = (float*)scratch;
   const int tiles = B * g.ntb;
   if (T > 0 && B > 0) {
@@ -369,7 +372,7 @@ static int conv_backward_w(int B, int T, int C, const void* x, const void* w, co
   if (dst) {
     const long n = (long)B * C;
     hipLaunchKernelGGL(conv_dstate_kernel<W>, dim3((n + 255) / 256), dim3(256), 0, stream, B, T,
-                       C, (const bf16*)x, (const bf16*)w, (const bf16*)st, (const bf16*)dy,
+                       C, ldx, (const bf16*)x, (const bf16*)w, (const bf16*)st, (const bf16*)dy,
                        (const bf16*)dfin, (bf16*)dst);
     KDA_LAUNCH_CHECK("causal_conv_dstate");
   }
@@ -414,24 +417,38 @@ extern "C" size_t kda_causal_conv_backward_scratch_bytes(int32_t batch, int32_t 
   return kda::align256((size_t)batch * g.ntb * channels * width * sizeof(float)) + 256;
 }
 
-extern "C" int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t channels,
-                                        int32_t width, const void* x, const void* weight,
-                                        const void* initial_state, const void* grad_output,
-                                        const void* grad_final_state, void* dx, void* dweight,
-                                        void* dinitial_state, void* scratch,
-                                        hipStream_t stream) {
+extern "C" int kda_causal_conv_backward_strided(int32_t batch, int32_t seq_len, int32_t channels,
+                                                int32_t width, const void* x, int64_t x_row_stride,
+                                                const void* weight, const void* initial_state,
+                                                const void* grad_output, const void* grad_final_state,
+                                                void* dx, int64_t dx_row_stride, void* dweight,
+                                                void* dinitial_state, void* scratch, hipStream_t stream) {
   using namespace kda;
   KDA_REQUIRE(batch >= 0 && seq_len >= 0 && channels > 0, "causal_conv_backward: invalid shape");
   KDA_REQUIRE(channels % 8 == 0, "causal_conv_backward: channels must be a multiple of 8");
   KDA_REQUIRE(width >= 1 && width <= 8, "causal_conv_backward: width must be in [1, 8]");
+  KDA_REQUIRE(x_row_stride >= channels && x_row_stride % 8 == 0 && dx_row_stride >= channels &&
+                  dx_row_stride % 8 == 0,
+              "causal_conv_backward: row strides must be multiples of 8 of at least the channel count");
   KDA_REQUIRE(weight && dweight && scratch, "causal_conv_backward: null pointer");
   KDA_REQUIRE(seq_len == 0 || (x && grad_output && dx), "causal_conv_backward: null pointer");
   KDA_REQUIRE(aligned16(x, weight, grad_output, dx, scratch),
               "causal_conv_backward: x, weight, grad_output, dx and scratch must be 16-byte aligned");
   KDA_REQUIRE(!dinitial_state || initial_state,
               "causal_conv_backward: dinitial_state requires initial_state");
-#define CALL(W) conv_backward_w<W>(batch, seq_len, channels, x, weight, initial_state, grad_output, grad_final_state, dx, dweight, dinitial_state, scratch, stream)
+#define CALL(W) conv_backward_w<W>(batch, seq_len, channels, x, x_row_stride, weight, initial_state, grad_output, grad_final_state, dx, dx_row_stride, dweight, dinitial_state, scratch, stream)
   KDA_CONV_DISPATCH(width, CALL)
 #undef CALL
   return set_error(KDA_ERR_INVALID, "causal_conv_backward: unsupported width");
+}
+
+extern "C" int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t channels,
+                                        int32_t width, const void* x, const void* weight,
+                                        const void* initial_state, const void* grad_output,
+                                        const void* grad_final_state, void* dx, void* dweight,
+                                        void* dinitial_state, void* scratch,
+                                        hipStream_t stream) {
+  return kda_causal_conv_backward_strided(batch, seq_len, channels, width, x, channels, weight, initial_state,
+                                          grad_output, grad_final_state, dx, channels, dweight, dinitial_state,
+                                          scratch, stream);
 }

@@ -220,10 +220,9 @@ def chunk_forward_conv_norm_gate(qkv_in, conv_weight, gate_values, beta_logits, 
     D = C3 // (3 * H)
     if conv_weight.ndim != 2 or conv_weight.shape[0] != C3 or not 1 <= conv_weight.shape[1] <= 4:
         raise RuntimeError(f"{what}: conv_weight must be [3HK, W] with W in [1, 4]")
-    if qkv_in.stride(2) != 1 or (T > 1 and qkv_in.stride(1) % 8) or (B > 1 and qkv_in.stride(0) != T * qkv_in.stride(1)) \
-            or qkv_in.data_ptr() % 16:
+    if _row_stride(qkv_in) is None:
         qkv_in = qkv_in.contiguous()
-    ld = qkv_in.stride(1) if T > 1 else C3
+    ld = _row_stride(qkv_in)
     q = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
     k, v = torch.empty_like(q), torch.empty_like(q)
     _check_chunk_inputs(what, q, k, v, gate_values, beta_logits, A_log, dt_bias, None, None, gm)
@@ -365,11 +364,28 @@ def causal_conv_forward(x, weight, initial_state, output_final_state):
     return y, fin
 
 
-def causal_conv_backward(x, weight, initial_state, grad_output, grad_final_state):
-    """Returns (dx, dweight, dinitial_state or None)."""
+def _row_stride(t):
+    """Row stride (elements per token) with which the kernels can step through the B*T rows
+    of a [B, T, C] tensor, or None: unit channel stride, 16-byte aligned, a stride that is a
+    multiple of 8 of at least C, and batches that follow each other (a column slice of a
+    wider [B, T, N] row qualifies)."""
+    B, T, C = t.shape
+    if t.stride(2) != 1 or t.data_ptr() % 16:
+        return None
+    ld = t.stride(1) if T > 1 else (t.stride(0) if B > 1 else C)
+    if ld % 8 or ld < C or (B > 1 and t.stride(0) != T * ld):
+        return None
+    return ld
+
+
+def causal_conv_backward(x, weight, initial_state, grad_output, grad_final_state, *, dx_out=None):
+    """Returns (dx, dweight, dinitial_state or None).  ``x`` may be a column slice of wider
+    rows (read in place); ``dx_out`` may be given to receive dx, also possibly such a slice."""
     dev = _require_cuda("causal_convolution_backward", x, weight, initial_state, grad_output,
                         grad_final_state)
-    x, weight, initial_state = _c(x), _c(weight), _c(initial_state)
+    if _row_stride(x) is None:
+        x = x.contiguous()
+    weight, initial_state = _c(weight), _c(initial_state)
     B, T, C = x.shape
     W = weight.shape[-1]
     if grad_output is None:
@@ -380,13 +396,19 @@ def causal_conv_backward(x, weight, initial_state, grad_output, grad_final_state
     lib = _lib.load()
     scratch = torch.empty(lib.kda_causal_conv_backward_scratch_bytes(B, T, C, W), dtype=torch.uint8,
                           device=dev)
-    dx = torch.empty_like(x)
+    if dx_out is not None:
+        if dx_out.shape != x.shape or dx_out.dtype != torch.bfloat16 or _row_stride(dx_out) is None:
+            raise ValueError("causal_conv_backward: dx_out must be a row-strided bf16 [B, T, C] tensor")
+        dx = dx_out
+    else:
+        dx = torch.empty(B, T, C, dtype=torch.bfloat16, device=dev)
     dw = torch.empty_like(weight)
     dst = torch.empty_like(initial_state) if initial_state is not None else None
+    ldx, ldd = _row_stride(x), _row_stride(dx)
     with torch.cuda.device(dev):
-        rc = lib.kda_causal_conv_backward(B, T, C, W, ptr(x), ptr(weight), ptr(initial_state),
-                                          ptr(grad_output), ptr(grad_final_state), ptr(dx), ptr(dw),
-                                          ptr(dst), ptr(scratch), _stream(dev))
+        rc = lib.kda_causal_conv_backward_strided(B, T, C, W, ptr(x), ldx, ptr(weight), ptr(initial_state),
+                                                  ptr(grad_output), ptr(grad_final_state), ptr(dx), ldd,
+                                                  ptr(dw), ptr(dst), ptr(scratch), _stream(dev))
     check(rc, "kda_causal_conv_backward")
     return dx, dw, dst
 

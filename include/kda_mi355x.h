@@ -245,6 +245,19 @@ int kda_causal_conv_backward(int32_t batch, int32_t seq_len, int32_t channels, i
                              void* scratch, hipStream_t stream);
 
 /*
+ * kda_causal_conv_backward with row strides (elements per token) for x and dx, each a
+ * multiple of 8 of at least C: x may be a column slice of a wider row (the projection GEMM's
+ * output) and dx may land in a slice of a wider gradient row.  No counterpart in the
+ * reference (its op takes dense tensors); kda_causal_conv_backward is this with both strides C.
+ */
+int kda_causal_conv_backward_strided(int32_t batch, int32_t seq_len, int32_t channels, int32_t width,
+                                     const void* x, int64_t x_row_stride, const void* weight,
+                                     const void* initial_state, const void* grad_output,
+                                     const void* grad_final_state, void* dx, int64_t dx_row_stride,
+                                     void* dweight, void* dinitial_state, void* scratch,
+                                     hipStream_t stream);
+
+/*
  * Fused RMSNorm(x) * weight * sigmoid(gate) over rows of D = 128 (or 64).  Replaces
  * torch.ops.nanochat_kda.rmsnorm_gate_forward (nanochat/mixers/cuda_kda/rmsnorm_gate.cu:31-71,
  * schema :278-280).  x, gate, output [rows, D] bf16; weight [D] f32; inv_rms [rows] f32.

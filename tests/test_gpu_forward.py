@@ -221,7 +221,8 @@ def test_chunk_forward_norm_gate_autograd_matches_unfused():
 
 
 @pytest.mark.parametrize("B,T,H,D,W", [(2, 150, 3, 128, 4), (1, 200, 2, 64, 4), (2, 17, 1, 128, 3),
-                                       (1, 5, 2, 64, 4), (1, 1, 1, 128, 2), (1, 64, 2, 128, 1)])
+                                       (1, 5, 2, 64, 4), (1, 1, 1, 128, 2), (1, 64, 2, 128, 1),
+                                       (3, 1, 2, 64, 4)])
 def test_chunk_forward_conv_matches_separate_conv(B, T, H, D, W):
     """The short convolution + SiLU computed in the chunk forward's first kernel: q, k, v
     equal kda_causal_conv_forward's bit for bit (halo rows across waves and chunks, rows
@@ -248,6 +249,24 @@ def test_chunk_forward_conv_matches_separate_conv(B, T, H, D, W):
     assert torch.equal(o, o2) and torch.equal(normed, n2) and torch.equal(inv, inv2)
     ey, _ = O.causal_conv_forward(np64(x[..., :C]), np64(cw[:C]), None)
     assert rel_err(q.reshape(B, T, C), ey) < 1e-2
+
+
+@pytest.mark.parametrize("B,T,C,W", [(2, 300, 384, 4), (3, 1, 128, 4), (1, 70, 64, 3)])
+def test_conv_backward_strided_rows_equal_dense(B, T, C, W):
+    """x read as a column slice of wider rows and dx written into a slice of wider rows give
+    the dense convolution backward's dx and dweight bit for bit, and leave the rest of the
+    wider rows untouched."""
+    g = torch.Generator().manual_seed(B * 1000 + T + C + W)
+    wide = torch.randn(B, T, C + 40, generator=g).bfloat16().cuda()
+    x = wide[..., 8:8 + C]
+    w = (torch.randn(C, W, generator=g) * 0.5).bfloat16().cuda()
+    dy = torch.randn(B, T, C, generator=g).bfloat16().cuda()
+    dx_ref, dw_ref, _ = ops.causal_conv_backward(x.contiguous(), w, None, dy, None)
+    out = torch.full((B, T, C + 24), 7.0, dtype=torch.bfloat16, device="cuda")
+    dx, dw, _ = ops.causal_conv_backward(x, w, None, dy, None, dx_out=out[..., 16:16 + C])
+    assert torch.equal(dx, dx_ref) and torch.equal(dw, dw_ref)
+    assert torch.equal(out[..., 16:16 + C], dx_ref)
+    assert bool((out[..., :16] == 7.0).all()) and bool((out[..., 16 + C:] == 7.0).all())
 
 
 def test_mixer_fused_conv_equals_separate_conv():
