@@ -303,14 +303,14 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         }
         wait_lgkm0();
         ring_barrier();   // S2(r)
-        float* DSH = (float*)a.sc.p[S_DSH] + tile * K * V + v0;
+        bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile * K * V + v0;
 #pragma unroll
         for (int it = 0; it < K / 16; ++it) {
           const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
           if (PUB)
-            store4_coherent(DSH, kk * V + c4, hv[it]);
+            store8_coherent(DSH, (kk * V + c4) * 2, f4_to_bf16x4(hv[it]));
           else
-            *(float4*)(DSH + (size_t)kk * V + c4) = hv[it];
+            *(bf16x4*)(DSH + (size_t)kk * V + c4) = f4_to_bf16x4(hv[it]);
         }
       }
       if (PUB) {
@@ -523,7 +523,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   const float* RK = (const float*)a.ws.p[R_RK] + tile * 64;
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
   const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
-  const float* DSH = (const float*)a.sc.p[S_DSH] + tile * K * V;
+  const bf16* DSH = (const bf16*)a.sc.p[S_DSH] + tile * K * V;
   const float* DDLT = (const float*)a.sc.p[S_DDLT] + tile * V * 64;
   float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
   float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
@@ -538,7 +538,8 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   constexpr int NVS = V / 32;
   static_assert(RPW >= 1 && 4 % RPW == 0, "row tiles per wave");
   const int pa_ct = wave / (4 / RPW), pa_rt0 = (wave % (4 / RPW)) * RPW;
-  float xs[NVS][8], xd[NVS][8];
+  float xs[NVS][8];
+  bf16x8 xd[NVS];
   const int pa_c = 16 * pa_ct + lr;
 #pragma unroll
   for (int sv = 0; sv < NVS; ++sv) load8f(SH + (size_t)pa_c * V + 32 * sv + 8 * kg, xs[sv]);
@@ -659,12 +660,9 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
 #pragma unroll
   for (int sv = 0; sv < NVS; ++sv) {
     if (Gate::kCoherent) {
-      const float4 x0 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg);
-      const float4 x1 = load4_coherent(DSH, pa_c * V + 32 * sv + 8 * kg + 4);
-      xd[sv][0] = x0.x; xd[sv][1] = x0.y; xd[sv][2] = x0.z; xd[sv][3] = x0.w;
-      xd[sv][4] = x1.x; xd[sv][5] = x1.y; xd[sv][6] = x1.z; xd[sv][7] = x1.w;
+      xd[sv] = load16_coherent_bf16(DSH, (pa_c * V + 32 * sv + 8 * kg) * 2);
     } else {
-      load8f(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg, xd[sv]);
+      xd[sv] = *(const bf16x8*)(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg);
     }
   }
   float4 ddl[NDU];
@@ -699,7 +697,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
 #pragma unroll
     for (int sv = 0; sv < NVS; ++sv)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dl = fmaf(xs[sv][e], xd[sv][e], dl);
+      for (int e = 0; e < 8; ++e) dl = fmaf(xs[sv][e], to_f32(xd[sv][e]), dl);
     dl = swap32_sum(swap16_sum(dl));
     if (rt0 == 0 && kg == 0) ((float*)a.sc.p[S_DGL])[tile * K + c] = dl * lamc;
 #pragma unroll
@@ -710,14 +708,12 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
 #pragma unroll
       for (int sv = 0; sv < NVS; ++sv) {
         const int vv = 32 * sv + 8 * kg;
-        bf16x8 sHi, sLo, dHi, dLo;
+        bf16x8 sHi, sLo;
         split8(xs[sv], sHi, sLo);
-        split8(xd[sv], dHi, dLo);
         const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
         const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
         const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
-        accK = mfma16(aL, dHi, accK);
-        accK = mfma16(aL, dLo, accK);
+        accK = mfma16(aL, xd[sv], accK);
         accW = mfma16(uHi, sHi, accW);
         accW = mfma16(uHi, sLo, accW);
         accW = mfma16(uLo, sHi, accW);
