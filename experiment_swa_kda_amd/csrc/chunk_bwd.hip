@@ -386,12 +386,12 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         acc1 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s + 1, lane) * 2),
                       *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
       }
-      float* DDLT = (float*)a.sc.p[S_DDLT] + tile * V * 64;
+      bf16* DDLT = (bf16*)a.sc.p[S_DDLT] + tile * V * 64;
       const f32x4 d = acc0 + acc1;
       if (PUB)
-        store4_coherent(DDLT, (v0 + lr) * 64 + 16 * wave + 4 * kg, make_float4(d[0], d[1], d[2], d[3]));
+        store8_coherent(DDLT, ((v0 + lr) * 64 + 16 * wave + 4 * kg) * 2, f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3])));
       else
-        *(float4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = make_float4(d[0], d[1], d[2], d[3]);
+        *(bf16x4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3]));
       bf16x4 x;
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
@@ -449,7 +449,7 @@ constexpr int kVjpWaves = kVjpThreads / kWave;
 // start (dO, v and beta kh e^G rows staged in LDS, the state rows in registers), so a tile
 // waits on one global round trip instead of one per row tile and item.  T, dT, T^T dT and dW
 // only ever feed bf16 MFMA operands and are stored as bf16; T, dT and T^T dT reuse the
-// (dU lo, delta) region once the dQg / dKd / dW / dA phase is done.
+// (spare, delta) region once the dQg / dKd / dW / dA phase is done.
 constexpr int kDenseThreads = 1024;
 constexpr int kDenseWaves = kDenseThreads / kWave;
 
@@ -461,7 +461,7 @@ struct DenseSmem {
   static constexpr int KP = K + 8;    // bf16 row stride of dW
   static constexpr int VP = V + 8;
   static constexpr size_t off_du = 0;                           // bf16 [64][VP] dU
-  static constexpr size_t off_dul = off_du + 64 * VP * 2;       // bf16 [64][VP] dU - bf16(dU)
+  static constexpr size_t off_dul = off_du + 64 * VP * 2;       // bf16 [64][VP] spare (T, dT, T^T dT after PA)
   static constexpr size_t off_dl = off_dul + 64 * VP * 2;       // bf16 [64][VP] delta
   static constexpr size_t off_dw = off_dl + 64 * VP * 2;        // bf16 [64][KP] dW
   static constexpr size_t off_b = off_dw + 64 * KP * 2;         // f32 [64] beta
@@ -499,7 +499,6 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   bf16* sY = (bf16*)(smem + L::off_y);
   bf16* sDW = (bf16*)(smem + L::off_dw);
   bf16* sDU = (bf16*)(smem + L::off_du);
-  bf16* sDUl = (bf16*)(smem + L::off_dul);
   bf16* sDL = (bf16*)(smem + L::off_dl);
   float* sB = (float*)(smem + L::off_b);
   float* sPV = (float*)(smem + L::off_pv);
@@ -524,7 +523,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
   const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
   const bf16* DSH = (const bf16*)a.sc.p[S_DSH] + tile * K * V;
-  const float* DDLT = (const float*)a.sc.p[S_DDLT] + tile * V * 64;
+  const bf16* DDLT = (const bf16*)a.sc.p[S_DDLT] + tile * V * 64;
   float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
   float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
   float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
@@ -550,7 +549,6 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   // stage costs one global round trip.
   static_assert(64 * 64 % (4 * kDenseThreads) == 0, "T staging");
   static_assert(64 * V / 8 <= kDenseThreads && 64 * K / 8 <= kDenseThreads, "one row chunk per thread");
-  constexpr int NDU = (V * 16 + kDenseThreads - 1) / kDenseThreads;
   constexpr int NDL = (64 * V / 8 + kDenseThreads - 1) / kDenseThreads;
   // rows of dO, v (8 values per thread and matrix) and k, G: clamped rows, zeroed after
   const int t = tid / (V / 8), c0 = (tid % (V / 8)) * 8;
@@ -655,7 +653,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(xs[sv][e]));
 
   gate();
-  // ---- the scan's histories: dS' rows of PA's key tile, dU = dDelta (hi/lo bf16 split),
+  // ---- the scan's histories: dS' rows of PA's key tile, dU = dDelta (both bf16),
   // transposed from its [V][64] history ----
 #pragma unroll
   for (int sv = 0; sv < NVS; ++sv) {
@@ -665,23 +663,17 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
       xd[sv] = *(const bf16x8*)(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg);
     }
   }
-  float4 ddl[NDU];
+  // dU = dDelta (bf16, as the scan stored it), transposed from its [V][64] history: thread
+  // idx takes 8 consecutive tokens of column idx / 8
+  static_assert(V * 8 <= kDenseThreads, "one 16-byte piece of the history per thread");
+  {
+    const int idx = tid < V * 8 ? tid : V * 8 - 1;
+    const bf16x8 dd = Gate::kCoherent ? load16_coherent_bf16(DDLT, idx * 16)
+                                      : *(const bf16x8*)(DDLT + (size_t)idx * 8);
+    if (tid < V * 8) {
+      const int vv = idx / 8, t8 = (idx % 8) * 8;
 #pragma unroll
-  for (int q = 0; q < NDU; ++q) {
-    const int idx = min(q * kDenseThreads + tid, V * 16 - 1);
-    ddl[q] = Gate::kCoherent ? load4_coherent(DDLT, (idx / 16) * 64 + (idx % 16) * 4)
-                             : *(const float4*)(DDLT + (size_t)(idx / 16) * 64 + (idx % 16) * 4);
-  }
-#pragma unroll
-  for (int q = 0; q < NDU; ++q) {
-    const int idx = q * kDenseThreads + tid, vv = idx / 16, t4 = (idx % 16) * 4;
-    if (idx >= V * 16) break;
-    const float dv[4] = {ddl[q].x, ddl[q].y, ddl[q].z, ddl[q].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bf16 hi = to_bf16(dv[e]);
-      sDU[(t4 + e) * VP + vv] = hi;
-      sDUl[(t4 + e) * VP + vv] = to_bf16(dv[e] - to_f32(hi));
+      for (int e = 0; e < 8; ++e) sDU[(t8 + e) * VP + vv] = dd[e];
     }
   }
   __syncthreads();
@@ -711,12 +703,10 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
         bf16x8 sHi, sLo;
         split8(xs[sv], sHi, sLo);
         const bf16x8 uHi = *(const bf16x8*)(sDU + i * VP + vv);
-        const bf16x8 uLo = *(const bf16x8*)(sDUl + i * VP + vv);
         const bf16x8 aL = *(const bf16x8*)(sDL + i * VP + vv);
         accK = mfma16(aL, xd[sv], accK);
         accW = mfma16(uHi, sHi, accW);
         accW = mfma16(uHi, sLo, accW);
-        accW = mfma16(uLo, sHi, accW);
       }
       *(f32x4*)(DKD + ((size_t)p * 64 + lane) * 4) = accK;
 #pragma unroll
@@ -724,7 +714,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     }
   }
   __syncthreads();
-  // dU lo and delta are consumed: their region now holds T (bf16) and a zeroed dT
+  // delta is consumed: the spare and delta regions now hold T (bf16) and a zeroed dT
 #pragma unroll
   for (int q = 0; q < 64 * 64 / (4 * kDenseThreads); ++q) {
     const int idx = (q * kDenseThreads + tid) * 4, i = idx / 64, j = idx % 64;

@@ -67,7 +67,7 @@ enum WsRegion {
 
 enum ScRegion {
   S_DSH = 0,  // bf16 [tile][K][V]   dL/dS at the chunk end (a bf16 MFMA operand of dKd)
-  S_DDLT,     // f32  [tile][V][64]  (dL/d delta)^T
+  S_DDLT,     // bf16 [tile][V][64]  (dL/d delta)^T (the scan's own recurrence uses it in bf16)
   S_DA,       // bf16 [tile][64][64] dL/dA (masked lower; the decay VJP's MFMA operand)
   S_DMP,      // bf16 [tile][64][64] dL/dM' (strictly lower, beta folded in; same)
   S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
@@ -119,7 +119,7 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   const size_t K = g.K, V = g.V;
   switch (r) {
     case S_DSH: return nt * K * V * 2;
-    case S_DDLT: return nt * 64 * V * 4;
+    case S_DDLT: return nt * 64 * V * 2;
     case S_DA: case S_DMP: return nt * 64 * 64 * 2;
     case S_DQG: case S_DKD: case S_DKB: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
