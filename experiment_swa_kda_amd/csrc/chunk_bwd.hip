@@ -303,14 +303,16 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         }
         wait_lgkm0();
         ring_barrier();   // S2(r)
-        bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile * K * V + v0;
+        // the strip's [K][16] block of the strip-major history: each store instruction
+        // writes 512 contiguous bytes
+        bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile * K * V + (size_t)strip * K * 16;
 #pragma unroll
         for (int it = 0; it < K / 16; ++it) {
           const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
           if (PUB)
-            store8_coherent(DSH, (kk * V + c4) * 2, f4_to_bf16x4(hv[it]));
+            store8_coherent(DSH, (kk * 16 + c4) * 2, f4_to_bf16x4(hv[it]));
           else
-            *(bf16x4*)(DSH + (size_t)kk * V + c4) = f4_to_bf16x4(hv[it]);
+            *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = f4_to_bf16x4(hv[it]);
         }
       }
       if (PUB) {
@@ -386,12 +388,14 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         acc1 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s + 1, lane) * 2),
                       *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
       }
-      bf16* DDLT = (bf16*)a.sc.p[S_DDLT] + tile * V * 64;
+      // [strip][16-token block][16 columns][16 tokens]: this wave's block is 512 contiguous
+      // bytes, written by one store instruction
+      bf16* DDLT = (bf16*)a.sc.p[S_DDLT] + tile * V * 64 + (size_t)strip * 1024 + wave * 256;
       const f32x4 d = acc0 + acc1;
       if (PUB)
-        store8_coherent(DDLT, ((v0 + lr) * 64 + 16 * wave + 4 * kg) * 2, f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3])));
+        store8_coherent(DDLT, (lr * 16 + 4 * kg) * 2, f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3])));
       else
-        *(bf16x4*)(DDLT + (size_t)(v0 + lr) * 64 + 16 * wave + 4 * kg) = f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3]));
+        *(bf16x4*)(DDLT + (size_t)lr * 16 + 4 * kg) = f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3]));
       bf16x4 x;
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
@@ -653,25 +657,27 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(xs[sv][e]));
 
   gate();
-  // ---- the scan's histories: dS' rows of PA's key tile, dU = dDelta (both bf16),
-  // transposed from its [V][64] history ----
+  // ---- the scan's histories (bf16, strip-major as the scan's strips wrote them): dS'
+  // rows of PA's key tile from [V/16][K][16], dU = dDelta from [V/16][4][16 v][16 t] ----
 #pragma unroll
   for (int sv = 0; sv < NVS; ++sv) {
+    const int col = 32 * sv + 8 * kg;  // 8 columns inside strip col / 16
+    const size_t off = (size_t)(col / 16) * K * 16 + (size_t)pa_c * 16 + col % 16;
     if (Gate::kCoherent) {
-      xd[sv] = load16_coherent_bf16(DSH, (pa_c * V + 32 * sv + 8 * kg) * 2);
+      xd[sv] = load16_coherent_bf16(DSH, (int)off * 2);
     } else {
-      xd[sv] = *(const bf16x8*)(DSH + (size_t)pa_c * V + 32 * sv + 8 * kg);
+      xd[sv] = *(const bf16x8*)(DSH + off);
     }
   }
-  // dU = dDelta (bf16, as the scan stored it), transposed from its [V][64] history: thread
-  // idx takes 8 consecutive tokens of column idx / 8
+  // dU: thread idx takes the 16-byte piece idx of the history (8 consecutive tokens of one
+  // column) and writes it transposed into dU rows
   static_assert(V * 8 <= kDenseThreads, "one 16-byte piece of the history per thread");
   {
     const int idx = tid < V * 8 ? tid : V * 8 - 1;
     const bf16x8 dd = Gate::kCoherent ? load16_coherent_bf16(DDLT, idx * 16)
                                       : *(const bf16x8*)(DDLT + (size_t)idx * 8);
     if (tid < V * 8) {
-      const int vv = idx / 8, t8 = (idx % 8) * 8;
+      const int vv = (idx / 128) * 16 + (idx % 32) / 2, t8 = ((idx % 128) / 32) * 16 + (idx % 2) * 8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) sDU[(t8 + e) * VP + vv] = dd[e];
     }
@@ -679,8 +685,8 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   __syncthreads();
 
   // ---- PA: dKd, dW over the 64 x K grid (same items as dQg) ----
-  // The f32 rows S[c][.] and dS'[c][.] of the wave's 16 keys, split into hi + lo bf16 where
-  // they are used.  The same rows give dlam = lam * sum_v S dS'.
+  // The f32 rows S[c][.] of the wave's 16 keys (split into hi + lo bf16 where they are used)
+  // and their bf16 dS'[c][.]; the same rows give dlam = lam * sum_v S dS'.
   {
     const int ct = pa_ct, rt0 = pa_rt0;
     const int c = 16 * ct + lr;

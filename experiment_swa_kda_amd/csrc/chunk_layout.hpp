@@ -66,8 +66,8 @@ enum WsRegion {
 };
 
 enum ScRegion {
-  S_DSH = 0,  // bf16 [tile][K][V]   dL/dS at the chunk end (a bf16 MFMA operand of dKd)
-  S_DDLT,     // bf16 [tile][V][64]  (dL/d delta)^T (the scan's own recurrence uses it in bf16)
+  S_DSH = 0,  // bf16 [tile][V/16][K][16]  dL/dS at the chunk end, strip-major (a bf16 MFMA operand of dKd)
+  S_DDLT,     // bf16 [tile][V/16][4][16 v][16 t]  (dL/d delta)^T, per strip and 16-token block
   S_DA,       // bf16 [tile][64][64] dL/dA (masked lower; the decay VJP's MFMA operand)
   S_DMP,      // bf16 [tile][64][64] dL/dM' (strictly lower, beta folded in; same)
   S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
