@@ -191,11 +191,6 @@ constexpr int kCoherentPolicy = 1 | 16;  // sc0 | sc1
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
-__device__ __forceinline__ void store4_coherent(float* base, int off, float4 x) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  const f4 v = {x.x, x.y, x.z, x.w};
-  __builtin_amdgcn_raw_buffer_store_b128(v, raw_rsrc(base), off * 4, 0, kCoherentPolicy);
-}
 __device__ __forceinline__ bf16x4 f4_to_bf16x4(float4 x) {
   bf16x4 r;
   r[0] = to_bf16(x.x); r[1] = to_bf16(x.y); r[2] = to_bf16(x.z); r[3] = to_bf16(x.w);
@@ -209,11 +204,6 @@ __device__ __forceinline__ bf16x8 load16_coherent_bf16(const void* base, int byt
   typedef int i4 __attribute__((ext_vector_type(4)));
   const i4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), byte_off, 0, kCoherentPolicy);
   return __builtin_bit_cast(bf16x8, v);
-}
-__device__ __forceinline__ float4 load4_coherent(const float* base, int off) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  const f4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), off * 4, 0, kCoherentPolicy);
-  return make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): two MFMAs with (hi, lo) recover
