@@ -38,6 +38,9 @@ class ChunkProblem(ctypes.Structure):
         ("lower_bound", ctypes.c_float),
         ("scale", ctypes.c_float),
         ("grad_row_stride", ctypes.c_int32),
+        ("beta_row_stride", ctypes.c_int32),
+        ("beta_grad_pad", ctypes.c_int32),
+        ("norm_gate_row_stride", ctypes.c_int32),
     ]
 
 
@@ -64,6 +67,8 @@ SIGNATURES = {
     "kda_rmsnorm_gate_forward": (ctypes.c_int, [_L, _I, _P, _P, _P, _F, _P, _P, _P]),
     "kda_rmsnorm_gate_backward_scratch_bytes": (ctypes.c_size_t, [_L, _I]),
     "kda_rmsnorm_gate_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P]),
+    "kda_rmsnorm_gate_backward_strided": (ctypes.c_int, [_L, _I, _I, _P, _P, _L, _P, _P, _P, _F, _P, _P, _L, _P,
+                                                         _P, _P]),
     "kda_softcap_cross_entropy_forward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P]),
     "kda_softcap_cross_entropy_backward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P, _P]),
     "kda_weight_grad_scratch_bytes": (ctypes.c_size_t, [_L, _I, _I]),

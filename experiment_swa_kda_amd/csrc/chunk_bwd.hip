@@ -65,6 +65,8 @@ struct BwdArgs {
   Regions ws;
   Regions sc;
   long gld_qk, gld_v;  // row strides (elements per token) of dq / dk and of dv
+  long dbeta_ld;       // row stride of dbeta; the dbeta_pad elements after a row's H are zeroed
+  int dbeta_pad;
 };
 
 // ---------------------------------------------------------------------------
@@ -1211,7 +1213,10 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
     sPK[t] = dotk * sFk[t];
     if (t < len) {
       const float bt = sBeta[t];
-      a.dbeta[(size_t)(row0 + t) * H + h] = to_bf16(db * bt * (1.f - bt));
+      bf16* drow = a.dbeta + (size_t)(row0 + t) * a.dbeta_ld;
+      drow[h] = to_bf16(db * bt * (1.f - bt));
+      if (h == 0)
+        for (int e = 0; e < a.dbeta_pad; ++e) drow[H + e] = to_bf16(0.f);
     }
   }
   __syncthreads();
@@ -1669,6 +1674,8 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
   a.gld_v = p->grad_row_stride > 0 ? p->grad_row_stride : (long)p->heads * p->value_dim;
   a.dgate = dgate;
   a.dbeta = (bf16*)dbeta_logits;
+  a.dbeta_ld = p->beta_row_stride > 0 ? p->beta_row_stride : p->heads;
+  a.dbeta_pad = p->beta_grad_pad;
   a.dA_log = dA_log;
   a.ddt_bias = ddt_bias;
   a.ds0 = dinitial_state;

@@ -54,6 +54,8 @@ struct FwdArgs {
   Regions ws;
   // optional output RMSNorm * weight * sigmoid(gate) epilogue (all null / unused if ng_out is null)
   const bf16* ng_gate;
+  long ng_gate_ld;  // elements between tokens' rows of ng_gate
+  long beta_ld;     // elements between tokens' rows of beta
   const float* ng_weight;
   float ng_eps;
   bf16* ng_out;
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
 #pragma unroll
     for (int s = 0; s < NV; ++s) vr[s] = *(const bf16x8*)(a.v + rbase * V + 32 * s + 8 * kg);
   }
-  const float bl = (float)a.beta[rbase];
+  const float bl = (float)a.beta[(size_t)(row0 + (live ? i : len - 1)) * a.beta_ld + h];
   if (a.gate_mode == KDA_GATE_K3) {
     const float ea = expf(a.A_log[h]);
 #pragma unroll
@@ -1385,7 +1387,7 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = min(16 * wave + 4 * kg + r, len - 1);
-      gv[ct][r] = to_f32(a.ng_gate[((size_t)(ch.x + t) * H + h) * V + 16 * ct + lr]);
+      gv[ct][r] = to_f32(a.ng_gate[(size_t)(ch.x + t) * a.ng_gate_ld + (size_t)h * V + 16 * ct + lr]);
     }
   }
 #pragma unroll
@@ -1423,6 +1425,13 @@ int validate_problem(const kda_chunk_problem* p, const char* who) {
   }
   KDA_REQUIRE(p->gate_mode != KDA_GATE_K3 || p->lower_bound < 0.f,
               "%s: lower_bound must be negative", who);
+  KDA_REQUIRE(p->beta_grad_pad >= 0, "%s: beta_grad_pad must be non-negative", who);
+  KDA_REQUIRE(p->beta_row_stride == 0 || (long)p->beta_row_stride >= (long)p->heads + p->beta_grad_pad,
+              "%s: beta_row_stride must be 0 or at least heads + beta_grad_pad", who);
+  KDA_REQUIRE(p->beta_row_stride > 0 || p->beta_grad_pad == 0,
+              "%s: beta_grad_pad needs a beta_row_stride", who);
+  KDA_REQUIRE(p->norm_gate_row_stride == 0 || (long)p->norm_gate_row_stride >= (long)p->heads * p->value_dim,
+              "%s: norm_gate_row_stride must be 0 or at least heads * value_dim", who);
   return KDA_OK;
 }
 
@@ -1581,6 +1590,8 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   a.sfin = final_state;
   a.ws = ws_regions(g, workspace);
   a.ng_gate = (const bf16*)norm_gate;
+  a.ng_gate_ld = p->norm_gate_row_stride > 0 ? p->norm_gate_row_stride : (long)p->heads * p->value_dim;
+  a.beta_ld = p->beta_row_stride > 0 ? p->beta_row_stride : p->heads;
   a.ng_weight = norm_weight;
   a.ng_eps = norm_eps;
   a.ng_out = (bf16*)norm_output;

@@ -56,10 +56,13 @@ __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf1
 
 template <int D>
 __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
-    long rows, const bf16* __restrict__ x, const bf16* __restrict__ gate,
+    long rows, int heads, const bf16* __restrict__ x, const bf16* __restrict__ gate, long gld,
     const float* __restrict__ weight, const float* __restrict__ inv_rms,
-    const bf16* __restrict__ dy, bf16* __restrict__ dx, bf16* __restrict__ dgate,
+    const bf16* __restrict__ dy, bf16* __restrict__ dx, bf16* __restrict__ dgate, long dgld,
     float* __restrict__ dw_part) {
+  // row r = (token r / heads, head r % heads); gate and dgate rows of a token are gld / dgld
+  // elements apart (heads = 1, gld = dgld = D for dense [rows, D])
+  auto goff = [&](long r, long ld) { return (r / heads) * ld + (r % heads) * D; };
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   __shared__ float s_dw[256 / kWave][D];
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     long r = r0 + (long)i * RPP;
     r = r < rows ? r : rows - 1;
     xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
-    gr[i] = *reinterpret_cast<const bf16x8*>(gate + r * D + c0);
+    gr[i] = *reinterpret_cast<const bf16x8*>(gate + goff(r, gld) + c0);
     dr[i] = *reinterpret_cast<const bf16x8*>(dy + r * D + c0);
     ir[i] = inv_rms[r];
   }
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     for (int e = 0; e < 8; ++e) o[e] = inv * (dn[e] - n[e] * dot);
     if (live) {
       store8(dx + r * D + c0, o);
-      store8(dgate + r * D + c0, og);
+      store8(dgate + goff(r, dgld) + c0, og);
     }
   }
   // rows of one channel slot: reduce the wave's kWave/LPR row slots across lanes, then
@@ -160,15 +163,20 @@ extern "C" size_t kda_rmsnorm_gate_backward_scratch_bytes(int64_t rows, int32_t 
   return kda::align256((size_t)kda::norm_blocks(rows, dim) * dim * sizeof(float)) + 256;
 }
 
-extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* x,
-                                         const void* gate, const float* weight,
-                                         const float* inv_rms, const void* grad_output,
-                                         float eps, void* dx, void* dgate, float* dweight,
-                                         void* scratch, hipStream_t stream) {
+extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int32_t heads, const void* x,
+                                                 const void* gate, int64_t gate_row_stride,
+                                                 const float* weight, const float* inv_rms,
+                                                 const void* grad_output, float eps, void* dx, void* dgate,
+                                                 int64_t dgate_row_stride, float* dweight, void* scratch,
+                                                 hipStream_t stream) {
   using namespace kda;
   (void)eps;
   KDA_REQUIRE(rows >= 0, "rmsnorm_gate_backward: invalid rows");
   KDA_REQUIRE(dim == 64 || dim == 128, "rmsnorm_gate_backward: dim must be 64 or 128");
+  KDA_REQUIRE(heads >= 1 && rows % heads == 0, "rmsnorm_gate_backward: rows must be a multiple of heads >= 1");
+  KDA_REQUIRE(gate_row_stride >= (int64_t)heads * dim && gate_row_stride % 8 == 0 &&
+                  dgate_row_stride >= (int64_t)heads * dim && dgate_row_stride % 8 == 0,
+              "rmsnorm_gate_backward: gate / dgate row strides must be multiples of 8 of at least heads * dim");
   KDA_REQUIRE(weight && dweight && scratch, "rmsnorm_gate_backward: null pointer");
   KDA_REQUIRE(rows == 0 || (x && gate && inv_rms && grad_output && dx && dgate),
               "rmsnorm_gate_backward: null pointer");
@@ -178,17 +186,26 @@ extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* 
   float* part = (float*)scratch;
   if (rows > 0) {
     if (dim == 128)
-      hipLaunchKernelGGL(norm_gate_bwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows,
-                         (const bf16*)x, (const bf16*)gate, weight, inv_rms,
-                         (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, part);
+      hipLaunchKernelGGL(norm_gate_bwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows, (int)heads,
+                         (const bf16*)x, (const bf16*)gate, (long)gate_row_stride, weight, inv_rms,
+                         (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, (long)dgate_row_stride, part);
     else
-      hipLaunchKernelGGL(norm_gate_bwd_kernel<64>, dim3(nb), dim3(256), 0, stream, (long)rows,
-                         (const bf16*)x, (const bf16*)gate, weight, inv_rms,
-                         (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, part);
+      hipLaunchKernelGGL(norm_gate_bwd_kernel<64>, dim3(nb), dim3(256), 0, stream, (long)rows, (int)heads,
+                         (const bf16*)x, (const bf16*)gate, (long)gate_row_stride, weight, inv_rms,
+                         (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, (long)dgate_row_stride, part);
     KDA_LAUNCH_CHECK("rmsnorm_gate_backward");
   }
   hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3((dim * kDwRedLanes + 255) / 256), dim3(256), 0, stream,
                      rows > 0 ? nb : 0, dim, (const float*)part, dweight);
   KDA_LAUNCH_CHECK("rmsnorm_gate_dweight_reduce");
   return KDA_OK;
+}
+
+extern "C" int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* x,
+                                         const void* gate, const float* weight,
+                                         const float* inv_rms, const void* grad_output,
+                                         float eps, void* dx, void* dgate, float* dweight,
+                                         void* scratch, hipStream_t stream) {
+  return kda_rmsnorm_gate_backward_strided(rows, dim, 1, x, gate, dim, weight, inv_rms, grad_output, eps, dx,
+                                           dgate, dim, dweight, scratch, stream);
 }

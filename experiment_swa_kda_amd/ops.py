@@ -230,10 +230,19 @@ def chunk_forward_conv_norm_gate(qkv_in, conv_weight, gate_values, beta_logits, 
     _check_dtype(what, norm_weight, torch.float32, "norm_weight")
     if norm_gate.shape != v.shape or norm_weight.shape != (D,):
         raise RuntimeError(f"{what}: norm_gate must be shaped like v and norm_weight [V]")
-    gate_values, beta_logits = _c(gate_values), _c(beta_logits)
-    A_log, dt_bias, norm_gate, norm_weight = _c(A_log), _c(dt_bias), _c(norm_gate), _c(norm_weight)
+    gate_values = _c(gate_values)
+    A_log, dt_bias, norm_weight = _c(A_log), _c(dt_bias), _c(norm_weight)
     conv_weight = _c(conv_weight)
+    # beta_logits and norm_gate may be column slices of wider per-token rows
+    beta_ld = _token_stride(beta_logits, H)
+    if beta_ld is None:
+        beta_logits, beta_ld = beta_logits.contiguous(), H
+    gate_ld = _token_stride(norm_gate, H * D)
+    if gate_ld is None:
+        norm_gate, gate_ld = norm_gate.contiguous(), H * D
     p = _problem(q, v, None, gm, lower_bound, scale)
+    p.beta_row_stride = beta_ld
+    p.norm_gate_row_stride = gate_ld
     lib = _lib.load()
     ws_bytes = lib.kda_chunk_workspace_bytes(ctypes.byref(p))
     if ws_bytes == 0 and B * T > 0:
@@ -254,15 +263,19 @@ def chunk_forward_conv_norm_gate(qkv_in, conv_weight, gate_values, beta_logits, 
 
 def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace,
                    grad_output, grad_final_state, lower_bound, scale, *, cu_seqlens=None,
-                   gate="k3", packed_qkv_grad=False):
+                   gate="k3", packed_qkv_grad=False, dbeta_out=None, dbeta_pad=0):
     """Exact chunked backward.  Returns the eight gradients
     (dq, dk, dv, dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state).  With
     ``packed_qkv_grad`` (K == V) dq, dk and dv are written side by side into one
-    [B, T, 3 H K] tensor, which is returned in place of dq (dk and dv are then None)."""
+    [B, T, 3 H K] tensor, which is returned in place of dq (dk and dv are then None).
+    ``dbeta_out`` [B, T, H] (a column slice of wider per-token rows) receives dbeta_logits,
+    and the ``dbeta_pad`` elements after each token's H values are set to zero."""
     gm = GATE_MODES[gate]
     dev = _check_chunk_inputs("chunk_backward", q, k, v, gate_values, beta_logits, A_log, dt_bias,
                               initial_state, cu_seqlens, gm)
-    q, k, v, gate_values, beta_logits = (_c(t) for t in (q, k, v, gate_values, beta_logits))
+    q, k, v, gate_values = (_c(t) for t in (q, k, v, gate_values))
+    if dbeta_out is None:
+        beta_logits = _c(beta_logits)
     A_log, dt_bias, initial_state = _c(A_log), _c(dt_bias), _c(initial_state)
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -287,7 +300,19 @@ def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_st
         dk = torch.empty_like(k)
         dv = torch.empty_like(v)
     dgate = torch.empty_like(gate_values)
-    dbeta = torch.empty_like(beta_logits)
+    if dbeta_out is not None:
+        ld = _token_stride(dbeta_out, H)
+        if ld is None or dbeta_out.shape != beta_logits.shape or dbeta_out.dtype != torch.bfloat16 \
+                or ld < H + dbeta_pad or _token_stride(beta_logits, H) != ld:
+            raise RuntimeError("chunk_backward: dbeta_out must be a bf16 [B, T, H] slice of per-token rows "
+                               "with room for the padding, with the row stride of beta_logits")
+        dbeta = dbeta_out
+        p.beta_row_stride = ld
+        p.beta_grad_pad = int(dbeta_pad)
+    else:
+        if dbeta_pad:
+            raise RuntimeError("chunk_backward: dbeta_pad needs dbeta_out")
+        dbeta = torch.empty_like(beta_logits)
     if gm == KDA_GATE_K3:
         dA = torch.empty_like(A_log)
         ddt = torch.empty_like(dt_bias)
@@ -378,6 +403,26 @@ def _row_stride(t):
     return ld
 
 
+def _token_stride(t, inner):
+    """Elements between consecutive tokens of a [B, T, *rest] tensor whose per-token block
+    of ``inner`` elements is dense (a column slice of a wider per-token row), or None when
+    the kernels cannot step through it that way."""
+    B, T = t.shape[:2]
+    if t.numel() == 0:
+        return None
+    expect = 1
+    for d in range(t.ndim - 1, 1, -1):
+        if t.stride(d) != expect:
+            return None
+        expect *= t.shape[d]
+    if expect != inner:
+        return None
+    ld = t.stride(1) if T > 1 else (t.stride(0) if B > 1 else inner)
+    if ld < inner or (B > 1 and t.stride(0) != T * ld):
+        return None
+    return ld
+
+
 def causal_conv_backward(x, weight, initial_state, grad_output, grad_final_state, *, dx_out=None):
     """Returns (dx, dweight, dinitial_state or None).  ``x`` may be a column slice of wider
     rows (read in place); ``dx_out`` may be given to receive dx, also possibly such a slice."""
@@ -433,23 +478,42 @@ def rmsnorm_gate_forward(x, gate, weight, eps):
     return y, inv
 
 
-def rmsnorm_gate_backward(x, gate, weight, inv_rms, grad_output, eps):
-    """Returns (dx bf16, dgate bf16, dweight f32)."""
+def rmsnorm_gate_backward(x, gate, weight, inv_rms, grad_output, eps, *, dgate_out=None):
+    """Returns (dx bf16, dgate bf16, dweight f32).  For [B, T, H, D] operands the gate may
+    be a column slice of wider per-token rows, and ``dgate_out`` (same shape, also such a
+    slice) receives dgate."""
     dev = _require_cuda("rmsnorm_gate_backward", x, gate, weight, inv_rms, grad_output)
-    x, gate, weight, inv_rms = _c(x), _c(gate), _c(weight), _c(inv_rms)
+    x, weight, inv_rms = _c(x), _c(weight), _c(inv_rms)
     grad_output = grad_output.to(torch.bfloat16).contiguous()
     D = x.shape[-1]
     rows = x.numel() // D if D else 0
+    heads, gld, dgld = 1, D, D
+    if x.ndim == 4 and gate.shape == x.shape:
+        heads = x.shape[2]
+        gld = _token_stride(gate, heads * D)
+        if gld is None or gld % 8 or gate.data_ptr() % 16:
+            gate, gld = gate.contiguous(), heads * D
+        dgld = heads * D
+    else:
+        gate = _c(gate)
+    if dgate_out is not None:
+        dgld = _token_stride(dgate_out, heads * D) if dgate_out.ndim == 4 else None
+        if dgate_out.shape != gate.shape or dgate_out.dtype != torch.bfloat16 or dgld is None \
+                or dgld % 8 or dgate_out.data_ptr() % 16:
+            raise RuntimeError("rmsnorm_gate_backward: dgate_out must be a bf16 [B, T, H, D] slice of "
+                               "per-token rows (16-byte aligned, row stride a multiple of 8)")
+        dg = dgate_out
+    else:
+        dg = torch.empty(gate.shape, dtype=torch.bfloat16, device=dev)
     lib = _lib.load()
     scratch = torch.empty(lib.kda_rmsnorm_gate_backward_scratch_bytes(rows, D), dtype=torch.uint8,
                           device=dev)
     dx = torch.empty_like(x)
-    dg = torch.empty_like(gate)
     dw = torch.empty_like(weight)
     with torch.cuda.device(dev):
-        rc = lib.kda_rmsnorm_gate_backward(rows, D, ptr(x), ptr(gate), ptr(weight), ptr(inv_rms),
-                                           ptr(grad_output), float(eps), ptr(dx), ptr(dg), ptr(dw),
-                                           ptr(scratch), _stream(dev))
+        rc = lib.kda_rmsnorm_gate_backward_strided(rows, D, heads, ptr(x), ptr(gate), int(gld), ptr(weight),
+                                                   ptr(inv_rms), ptr(grad_output), float(eps), ptr(dx),
+                                                   ptr(dg), int(dgld), ptr(dw), ptr(scratch), _stream(dev))
     check(rc, "kda_rmsnorm_gate_backward")
     return dx, dg, dw
 

@@ -51,6 +51,16 @@ typedef struct kda_chunk_problem {
                               dense [.., H, K] / [.., H, V] gradients.  Lets the three land
                               interleaved in one [B, T, 3 H K] buffer.  (No reference
                               counterpart: the reference returns three tensors.) */
+  int32_t beta_row_stride; /* elements between consecutive tokens' rows of beta_logits
+                              (forward) and of dbeta_logits (backward); 0 for dense [.., H].
+                              Lets both be column slices of a wider per-token row. */
+  int32_t beta_grad_pad;   /* backward only: number of elements after each token's H
+                              dbeta_logits values that the backward sets to zero (padding
+                              columns of such a row); 0 normally */
+  int32_t norm_gate_row_stride; /* norm-gate forwards only: elements between consecutive
+                              tokens' rows of norm_gate; 0 for dense [.., H, V].  (These
+                              three have no reference counterpart: they let the training
+                              mixer pass slices of its packed projection output.) */
 } kda_chunk_problem;
 
 /* Last error message of the calling thread ("" when none). */
@@ -278,6 +288,21 @@ int kda_rmsnorm_gate_backward(int64_t rows, int32_t dim, const void* x, const vo
                               const float* weight, const float* inv_rms, const void* grad_output,
                               float eps, void* dx, void* dgate, float* dweight, void* scratch,
                               hipStream_t stream);
+
+/*
+ * kda_rmsnorm_gate_backward with gate and dgate as column slices of wider per-token rows:
+ * row r of x / grad_output / dx is (token r / heads, head r % heads); that row's gate is read
+ * at token * gate_row_stride + head * dim and its dgate written at
+ * token * dgate_row_stride + head * dim (strides multiples of 8, at least heads * dim).
+ * heads = 1 and both strides = dim is kda_rmsnorm_gate_backward.  (No reference counterpart:
+ * it lets the training mixer read the output gate from, and write its gradient into, the
+ * packed projection rows.)
+ */
+int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int32_t heads, const void* x,
+                                      const void* gate, int64_t gate_row_stride, const float* weight,
+                                      const float* inv_rms, const void* grad_output, float eps, void* dx,
+                                      void* dgate, int64_t dgate_row_stride, float* dweight, void* scratch,
+                                      hipStream_t stream);
 
 /*
  * Trainer support: soft-capped cross entropy over bf16 logits [rows, stride] (columns

@@ -60,6 +60,16 @@ def test_c_abi_rejects_bad_problems_without_gpu():
     fake = ctypes.c_void_p(1 << 20)
     rc = lib.kda_chunk_backward(ctypes.byref(p), *([fake] * 20), None)
     assert rc != 0 and "grad_row_stride" in lib.kda_last_error().decode()
+    # the beta / norm-gate row strides are checked the same way
+    for field, value, words in (("beta_row_stride", 1, "beta_row_stride"), ("beta_grad_pad", 3, "beta_grad_pad"),
+                                ("norm_gate_row_stride", 100, "norm_gate_row_stride")):
+        p = _lib.ChunkProblem(batch=1, seq_len=8, heads=2, key_dim=64, value_dim=64, num_seqs=1, cu_seqlens=None,
+                              gate_mode=1, lower_bound=-5.0, scale=0.125, **{field: value})
+        rc = lib.kda_chunk_backward(ctypes.byref(p), *([fake] * 20), None)
+        assert rc != 0 and words in lib.kda_last_error().decode()
+    rc = lib.kda_rmsnorm_gate_backward_strided(9, 64, 3, *([fake] * 2), 64, *([fake] * 3), 1e-5, fake, fake, 192,
+                                               fake, fake, None)
+    assert rc != 0 and "strides" in lib.kda_last_error().decode()
 
 
 def make(B=2, T=7, H=2, K=4, V=3, seed=1729, dtype=torch.float32):

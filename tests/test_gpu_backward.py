@@ -273,3 +273,53 @@ def test_packed_qkv_gradients_equal_separate(K):
         assert torch.equal(dqkv[:, :, j], sep[j])
     for a, b in zip(sep[3:7], packed[3:7]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_dbeta_into_packed_rows_equals_dense():
+    """dbeta_logits written as a column slice of wider per-token rows (beta_row_stride), with
+    the padding columns after it zeroed, is the dense dbeta bit for bit; the other columns of
+    the rows are left alone."""
+    B, T, H, K = 2, 130, 3, 64
+    d = make_kda_inputs(B, T, H, K, K, seed=41, gate="k3", state=False, dist="baseline")
+    do, _ = cotangents(d, 6)
+    N, off, pad = 32, 8, 5
+    rows = torch.randn(B, T, N, device="cuda").to(torch.bfloat16)
+    rows[..., off:off + H] = d["beta"]
+    beta_view = rows[..., off:off + H]
+    _, _, ws = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None,
+                                 False, -5.0, K ** -0.5, gate="k3")
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], None, ws, do, None, -5.0, K ** -0.5)
+    dense = ops.chunk_backward(*args, gate="k3")
+    out = torch.full((B, T, N), 7.0, device="cuda", dtype=torch.bfloat16)
+    sargs = (d["q"], d["k"], d["v"], d["g"], beta_view) + args[5:]
+    strided = ops.chunk_backward(*sargs, gate="k3", dbeta_out=out[..., off:off + H], dbeta_pad=pad)
+    assert torch.equal(out[..., off:off + H], dense[4])
+    assert torch.equal(out[..., off + H:off + H + pad], torch.zeros_like(out[..., :pad]))
+    assert torch.equal(out[..., :off], torch.full_like(out[..., :off], 7.0))
+    assert torch.equal(out[..., off + H + pad:], torch.full_like(out[..., off + H + pad:], 7.0))
+    for j in (0, 1, 2, 3, 5, 6):
+        assert torch.equal(strided[j], dense[j])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D", [64, 128])
+def test_norm_gate_backward_strided_gate_equals_dense(D):
+    """The norm-gate VJP reading its gate from, and writing dgate into, column slices of
+    wider per-token rows gives the dense results bit for bit."""
+    B, T, H = 2, 77, 3
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(B, T, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    N = H * D + 24
+    rows = torch.randn(B, T, N, device="cuda", generator=g).to(torch.bfloat16)
+    gate = rows[..., 8:8 + H * D].view(B, T, H, D)
+    w = torch.randn(D, device="cuda", generator=g)
+    dy = torch.randn(B, T, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    _, inv = ops.rmsnorm_gate_forward(x, gate.contiguous(), w, 1e-5)
+    ref = ops.rmsnorm_gate_backward(x, gate.contiguous(), w, inv, dy, 1e-5)
+    out = torch.full((B, T, N), 3.0, device="cuda", dtype=torch.bfloat16)
+    got = ops.rmsnorm_gate_backward(x, gate, w, inv, dy, 1e-5, dgate_out=out[..., 16:16 + H * D].view(B, T, H, D))
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[2], ref[2])
+    assert torch.equal(out[..., 16:16 + H * D].view(B, T, H, D), ref[1])
+    assert torch.equal(out[..., :16], torch.full_like(out[..., :16], 3.0))
+    assert torch.equal(out[..., 16 + H * D:], torch.full_like(out[..., 16 + H * D:], 3.0))

@@ -247,6 +247,14 @@ def test_chunk_forward_conv_matches_separate_conv(B, T, H, D, W):
     o2, n2, inv2, _, _ = ops.chunk_forward_norm_gate(qs.contiguous(), ks.contiguous(), vs.contiguous(), raw, beta,
                                                      A_log, dt, None, False, -5.0, D ** -0.5, og, nw, 1e-5)
     assert torch.equal(o, o2) and torch.equal(normed, n2) and torch.equal(inv, inv2)
+    # the output gate and beta logits read as column slices of the same packed rows as x
+    packed = torch.zeros(B, T, 4 * C + 24, dtype=torch.bfloat16, device="cuda")
+    packed[..., :3 * C] = x
+    packed[..., 3 * C:4 * C] = og.reshape(B, T, C)
+    packed[..., 4 * C + 8:4 * C + 8 + H] = beta
+    r = ops.chunk_forward_conv_norm_gate(packed[..., :3 * C], cw, raw, packed[..., 4 * C + 8:4 * C + 8 + H], A_log,
+                                         dt, -5.0, D ** -0.5, packed[..., 3 * C:4 * C].view(B, T, H, D), nw, 1e-5, H)
+    assert torch.equal(r[3], o) and torch.equal(r[4], normed) and torch.equal(r[5], inv)
     ey, _ = O.causal_conv_forward(np64(x[..., :C]), np64(cw[:C]), None)
     assert rel_err(q.reshape(B, T, C), ey) < 1e-2
 
