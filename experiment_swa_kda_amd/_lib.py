@@ -79,6 +79,8 @@ SIGNATURES = {
     "kda_relu2_forward": (ctypes.c_int, [_L, _P, _P, _P]),
     "kda_rms_norm_forward": (ctypes.c_int, [_L, _I, _F, _P, _P, _P, _P]),
     "kda_rms_norm_backward": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P]),
+    "kda_mix_rms_norm_forward": (ctypes.c_int, [_L, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "kda_rms_norm_backward_add": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P, _P]),
     "kda_relu2_backward": (ctypes.c_int, [_L, _P, _P, _P, _P]),
     "kda_softcap_cross_entropy_mean": (ctypes.c_int, [_L, _P, _P, _L, _P, _P, _P]),
     "kda_embedding_backward": (ctypes.c_int, [_L, _I, _I, _P, _P, _P, _P]),

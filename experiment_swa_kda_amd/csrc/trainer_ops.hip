@@ -186,16 +186,39 @@ inline unsigned glue_blocks(long n) { return (unsigned)((n + kGlueBlock - 1) / k
 constexpr int kNormLanes = 16;
 constexpr int kNormRowsPerBlock = 256 / kNormLanes;
 
-template <int J>
+// MIX: the normalised row is first formed as s = a x + b x2 (a = wa[0], b = wb[0], 1 where
+// the pointer is null), rounded to bf16 and stored -- a residual add or mix fused into the
+// norm that follows it.
+template <int J, bool MIX = false>
 __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(long rows, float eps, const bf16* __restrict__ x,
-                                                           bf16* __restrict__ y, float* __restrict__ rinv) {
+                                                           bf16* __restrict__ y, float* __restrict__ rinv,
+                                                           const bf16* __restrict__ x2 = nullptr,
+                                                           const float* __restrict__ wa = nullptr,
+                                                           const float* __restrict__ wb = nullptr,
+                                                           bf16* __restrict__ s = nullptr) {
   constexpr int D = 128 * J;
   const long row = (long)blockIdx.x * kNormRowsPerBlock + threadIdx.x / kNormLanes;
   const int l = threadIdx.x % kNormLanes;
   const long rc = row < rows ? row : rows - 1;
-  bf16x8 xv[J];
+  bf16x8 xv[J], x2v[J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) xv[j] = *reinterpret_cast<const bf16x8*>(x + rc * D + 128 * j + 8 * l);
+  for (int j = 0; j < J; ++j) {
+    xv[j] = *reinterpret_cast<const bf16x8*>(x + rc * D + 128 * j + 8 * l);
+    if constexpr (MIX) x2v[j] = *reinterpret_cast<const bf16x8*>(x2 + rc * D + 128 * j + 8 * l);
+  }
+  if constexpr (MIX) {
+    const float a = wa ? wa[0] : 1.f, b = wb ? wb[0] : 1.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float fx[8], fz[8], o[8];
+      unpack8(xv[j], fx);
+      unpack8(x2v[j], fz);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = fmaf(a, fx[e], b * fz[e]);  // as resid_mix_fwd_kernel
+      xv[j] = pack8(o);
+      if (row < rows) *reinterpret_cast<bf16x8*>(s + row * D + 128 * j + 8 * l) = xv[j];
+    }
+  }
   float f[J][8], ss = 0.f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -217,19 +240,23 @@ __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(long rows, float eps,
   }
 }
 
-template <int J>
+// ADD: dx also takes the gradient gadd that reaches x by another path (a residual branch),
+// added in f32 before the one rounding.
+template <int J, bool ADD = false>
 __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(long rows, const bf16* __restrict__ x,
                                                            const float* __restrict__ rinv,
-                                                           const bf16* __restrict__ g, bf16* __restrict__ dx) {
+                                                           const bf16* __restrict__ g, bf16* __restrict__ dx,
+                                                           const bf16* __restrict__ gadd = nullptr) {
   constexpr int D = 128 * J;
   const long row = (long)blockIdx.x * kNormRowsPerBlock + threadIdx.x / kNormLanes;
   const int l = threadIdx.x % kNormLanes;
   const long rc = row < rows ? row : rows - 1;
-  bf16x8 xv[J], gv[J];
+  bf16x8 xv[J], gv[J], av[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     xv[j] = *reinterpret_cast<const bf16x8*>(x + rc * D + 128 * j + 8 * l);
     gv[j] = *reinterpret_cast<const bf16x8*>(g + rc * D + 128 * j + 8 * l);
+    if constexpr (ADD) av[j] = *reinterpret_cast<const bf16x8*>(gadd + rc * D + 128 * j + 8 * l);
   }
   const float r = rinv[rc];
   float yf[J][8], gf[J][8], dot = 0.f;
@@ -250,6 +277,12 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(long rows, const bf16
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = r * (gf[j][e] - yf[j][e] * dot);
+      if constexpr (ADD) {
+        float fa[8];
+        unpack8(av[j], fa);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += fa[e];
+      }
       *reinterpret_cast<bf16x8*>(dx + row * D + 128 * j + 8 * l) = pack8(o);
     }
   }
@@ -345,6 +378,40 @@ extern "C" int kda_rms_norm_backward(int64_t rows, int32_t dim, const void* x, c
   const unsigned blocks = (unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
 #define CALL(J) hipLaunchKernelGGL(rms_norm_bwd_kernel<J>, dim3(blocks), dim3(256), 0, stream, (long)rows, \
                                    (const bf16*)x, rinv, (const bf16*)grad, (bf16*)dx)
+  KDA_NORM_DISPATCH(dim / 128, CALL)
+#undef CALL
+  KDA_LAUNCH_CHECK("rms_norm_backward");
+  return KDA_OK;
+}
+
+extern "C" int kda_mix_rms_norm_forward(int64_t rows, int32_t dim, float eps, const float* a, const float* b,
+                                        const void* x, const void* x2, void* sum, void* y, float* rinv,
+                                        hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(rows >= 0 && norm_dim_ok(dim), "mix_rms_norm_forward: dim must be 128 x {1,2,3,4,6,8}");
+  KDA_REQUIRE(aligned16(x, x2, sum, y), "mix_rms_norm_forward: tensors must be 16-byte aligned");
+  if (rows == 0) return KDA_OK;
+  KDA_REQUIRE(x && x2 && sum && y && rinv, "mix_rms_norm_forward: null pointer");
+  const unsigned blocks = (unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+#define CALL(J) hipLaunchKernelGGL((rms_norm_fwd_kernel<J, true>), dim3(blocks), dim3(256), 0, stream, (long)rows, \
+                                   eps, (const bf16*)x, (bf16*)y, rinv, (const bf16*)x2, a, b, (bf16*)sum)
+  KDA_NORM_DISPATCH(dim / 128, CALL)
+#undef CALL
+  KDA_LAUNCH_CHECK("mix_rms_norm_forward");
+  return KDA_OK;
+}
+
+extern "C" int kda_rms_norm_backward_add(int64_t rows, int32_t dim, const void* x, const float* rinv,
+                                         const void* grad, const void* grad_add, void* dx, hipStream_t stream) {
+  using namespace kda;
+  if (grad_add == nullptr) return kda_rms_norm_backward(rows, dim, x, rinv, grad, dx, stream);
+  KDA_REQUIRE(rows >= 0 && norm_dim_ok(dim), "rms_norm_backward: dim must be 128 x {1,2,3,4,6,8}");
+  KDA_REQUIRE(aligned16(x, grad, grad_add, dx), "rms_norm_backward: tensors must be 16-byte aligned");
+  if (rows == 0) return KDA_OK;
+  KDA_REQUIRE(x && rinv && grad && dx, "rms_norm_backward: null pointer");
+  const unsigned blocks = (unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+#define CALL(J) hipLaunchKernelGGL((rms_norm_bwd_kernel<J, true>), dim3(blocks), dim3(256), 0, stream, (long)rows, \
+                                   (const bf16*)x, rinv, (const bf16*)grad, (bf16*)dx, (const bf16*)grad_add)
   KDA_NORM_DISPATCH(dim / 128, CALL)
 #undef CALL
   KDA_LAUNCH_CHECK("rms_norm_backward");

@@ -693,16 +693,45 @@ def rms_norm_forward(x, eps):
     return y, rinv
 
 
-def rms_norm_backward(x, rinv, grad):
+def rms_norm_backward(x, rinv, grad, grad_add=None):
+    """dx of rms_norm, plus ``grad_add`` (the gradient reaching x by another path) when given."""
     dev = _require_cuda("rms_norm_backward", x, rinv, grad)
     x, rinv, grad = _c(x), _c(rinv), _c(grad.to(torch.bfloat16))
+    if grad_add is not None:
+        grad_add = _c(grad_add.to(torch.bfloat16))
+        if grad_add.shape != x.shape:
+            raise ValueError("rms_norm_backward: grad_add must be shaped like x")
     D = x.shape[-1]
     rows = x.numel() // D if D else 0
     dx = torch.empty_like(x)
     with torch.cuda.device(dev):
-        rc = _lib.load().kda_rms_norm_backward(rows, D, ptr(x), ptr(rinv), ptr(grad), ptr(dx), _stream(dev))
+        rc = _lib.load().kda_rms_norm_backward_add(rows, D, ptr(x), ptr(rinv), ptr(grad), ptr(grad_add), ptr(dx),
+                                                   _stream(dev))
     check(rc, "kda_rms_norm_backward")
     return dx
+
+
+def mix_rms_norm_forward(x, x2, eps, a=None, b=None):
+    """s = a x + b x2 (one-element f32 tensors a, b; None means 1) rounded to bf16, and its
+    rms_norm: returns (s, y, rinv)."""
+    dev = _require_cuda("mix_rms_norm_forward", x, x2)
+    _check_dtype("mix_rms_norm_forward", x, torch.bfloat16, "x")
+    _check_dtype("mix_rms_norm_forward", x2, torch.bfloat16, "x2")
+    if x2.shape != x.shape:
+        raise ValueError("mix_rms_norm_forward: x and x2 must have the same shape")
+    for w in (a, b):
+        if w is not None and (w.dtype != torch.float32 or w.numel() != 1 or w.device != x.device):
+            raise ValueError("mix_rms_norm_forward: a and b must be one-element f32 tensors on x's device")
+    x, x2 = _c(x), _c(x2)
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    s, y = torch.empty_like(x), torch.empty_like(x)
+    rinv = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_mix_rms_norm_forward(rows, D, float(eps), ptr(a), ptr(b), ptr(x), ptr(x2), ptr(s),
+                                                  ptr(y), ptr(rinv), _stream(dev))
+    check(rc, "kda_mix_rms_norm_forward")
+    return s, y, rinv
 
 def _op_chunk_forward(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_state,
                       output_final_state, lower_bound, scale):

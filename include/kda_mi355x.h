@@ -374,6 +374,16 @@ int kda_rms_norm_forward(int64_t rows, int32_t dim, float eps, const void* x, vo
                          hipStream_t stream);
 int kda_rms_norm_backward(int64_t rows, int32_t dim, const void* x, const float* rinv,
                           const void* grad, void* dx, hipStream_t stream);
+/* The residual add or mix fused into the norm that follows it (gpt.py:585-587 and :200-205):
+ * sum = bf16(a x + b x2) (a, b device scalars; NULL means 1, i.e. sum = x + x2) is stored and
+ * normalised as kda_rms_norm_forward does (y, rinv of the rounded sum). */
+int kda_mix_rms_norm_forward(int64_t rows, int32_t dim, float eps, const float* a, const float* b,
+                             const void* x, const void* x2, void* sum, void* y, float* rinv,
+                             hipStream_t stream);
+/* kda_rms_norm_backward plus grad_add, the gradient reaching x by another path (a residual
+ * branch), added before the one rounding; grad_add NULL is kda_rms_norm_backward. */
+int kda_rms_norm_backward_add(int64_t rows, int32_t dim, const void* x, const float* rinv,
+                              const void* grad, const void* grad_add, void* dx, hipStream_t stream);
 int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx, hipStream_t stream);
 /*
  * Gradient of the token-embedding lookup (the backward of nn.Embedding for the decoder's

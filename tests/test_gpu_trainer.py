@@ -161,6 +161,57 @@ def test_rms_norm_matches_torch(D):
     assert rel_err(y, y64) < 4e-3 and rel_err(x.grad, x64.grad) < 4e-3
 
 
+@pytest.mark.parametrize("D", [384, 128])
+def test_fused_mix_and_add_norms_match_separate_ops(D):
+    """The residual mix fused into the following norm, and the residual add fused into its
+    norm, give the values of the separate resid_mix / add / norm ops bit for bit; their
+    gradients (the residual branch added inside the norm VJP, one rounding) agree with the
+    separate ops' and with an f64 chain."""
+    from experiment_swa_kda_amd import model as M
+    g = torch.Generator().manual_seed(D + 1)
+    B, T, i = 2, 65, 2
+    mk = lambda s=1.0: (torch.randn(B, T, D, generator=g) * s).bfloat16().cuda().requires_grad_()
+    x, x0, mixed = mk(2.0), mk(), mk(0.5)
+    lam_r = (1 + 0.1 * torch.randn(4, generator=g)).cuda().requires_grad_()
+    lam_0 = (0.2 * torch.randn(4, generator=g)).cuda().requires_grad_()
+    gh, gh2, gy = (torch.randn(B, T, D, generator=g).bfloat16().cuda() for _ in range(3))
+
+    def run(fused):
+        leaves = [t.detach().clone().requires_grad_() for t in (x, x0, mixed, lam_r, lam_0)]
+        a, a0, m, lr, l0 = leaves
+        if fused:
+            s, h = M._ResidMixNorm.apply(a, a0, lr, l0, i, M._RMS_EPS)
+            y, h2 = M._AddNorm.apply(s, m, M._RMS_EPS)
+        else:
+            s = M.resid_mix(a, a0, lr, l0, i)
+            h = M.norm(s)
+            y = s + m
+            h2 = M.norm(y)
+        ((h.float() * gh.float()).sum() + (h2.float() * gh2.float()).sum() + (y.float() * gy.float()).sum()).backward()
+        return (s, h, y, h2), [t.grad for t in leaves]
+
+    (vf, gf), (vs, gs) = run(True), run(False)
+    for a, b in zip(vf, vs):
+        assert torch.equal(a, b)
+    # f64 chain of the same function
+    xd, x0d, md = (t.detach().double().requires_grad_() for t in (x, x0, mixed))
+    lrd, l0d = lam_r.detach().double().requires_grad_(), lam_0.detach().double().requires_grad_()
+    eps = torch.finfo(torch.float32).eps
+    nrm = lambda v: v * torch.rsqrt((v * v).mean(-1, keepdim=True) + eps)
+    sd = lrd[i] * xd + l0d[i] * x0d
+    sd.retain_grad()
+    yd = sd + md
+    ((nrm(sd) * gh.double()).sum() + (nrm(yd) * gh2.double()).sum() + (yd * gy.double()).sum()).backward()
+    for a, b, e in zip(gf[:3], gs[:3], (xd.grad, x0d.grad, md.grad)):
+        assert rel_err(a, e) < 1e-2 and rel_err(b, e) < 1e-2
+    # the lambda gradients are sums of many cancelling terms: bf16 rounding of the gradient of s
+    # (2^-9 relative per term) is bounded by 2^-8 of the sum of the terms' magnitudes
+    for k, (a, b, e, v) in enumerate(zip(gf[3:], gs[3:], (lrd.grad, l0d.grad), (xd, x0d))):
+        scale = float((sd.grad.abs() * v.detach().abs()).sum())
+        for got in (a, b):
+            assert float((got.double().cpu() - e.cpu()).abs().max()) < 2 ** -8 * scale, (k, got, e, scale)
+
+
 @pytest.mark.parametrize("n_tok,vocab,dim", [
     (8192, 32768, 384),   # the trainer's lookup: B2 x T4096, vocab 32768, d384
     (3000, 100, 256),     # many repeats per row, ragged last workgroup
