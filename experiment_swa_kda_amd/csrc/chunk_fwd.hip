@@ -136,6 +136,26 @@ __device__ __forceinline__ void emit_frags(bf16* dst, int tid, F val) {
   }
 }
 
+// emit_frags of the transpose of a row-major bf16 LDS matrix m (element (r, c) of the emitted
+// R x C matrix is m[c][r]): each 16-byte piece is a column fragment of m, read with two
+// transposing LDS reads instead of eight 2-byte ones.  NT must be a multiple of the wave
+// size (the reads depend on the hardware lane), the pitch a multiple of 4 elements.
+template <int R, int C, int NT, bool PERM = false>
+__device__ __forceinline__ void emit_frags_tr(bf16* dst, int tid, const bf16* m, int pitch) {
+  static_assert(NT % kWave == 0, "lanes of a piece are the hardware lanes");
+  for (int idx = tid; idx < R * C / 8; idx += NT) {
+    const int lane = idx % 64, s = (idx / 64) % (C / 32), rt = idx / (64 * (C / 32));
+    bf16x8 x;
+    if constexpr (PERM) {
+      // elements 0..3: rows 32 s + 4 kg + e; 4..7: rows 32 s + 16 + 4 kg + e (frag_col<true>)
+      x = lds_col_frag_split(m, pitch, 32 * s, 32 * s + 16, 16 * rt, lane);
+    } else {
+      x = lds_col_frag(m, pitch, 32 * s, 16 * rt, lane);  // rows 32 s + 8 kg + e
+    }
+    *(bf16x8*)(dst + (size_t)idx * 8) = x;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // intra-chunk kernel
 // ---------------------------------------------------------------------------
@@ -544,8 +564,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   // ---- phase 2b: A fragments, M' to HBM, beta v and beta kh e^G (natural rows) to LDS ----
   emit_frags<64, 64, kIntraThreads, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
                                           [&](int r, int c) { return sA[r * TS + c]; });
-  emit_frags<64, 64, kIntraThreads>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid,
-                                    [&](int r, int c) { return sA[c * TS + r]; });
+  emit_frags_tr<64, 64, kIntraThreads>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid, sA, TS);
   {
     float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
     for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) MPout[idx] = sM[(idx / 64) * 65 + idx % 64];
@@ -686,8 +705,7 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   // -W and W^T fragments; Qg and Kd staged for their transposed / permuted fragments
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return (bf16)(-(float)sW[r * RS + c]); });
-  emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid,
-                                   [&](int r, int c) { return sW[c * RS + r]; });
+  emit_frags_tr<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid, sW, RS);
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     *(bf16x8*)(sQg + i * RS + 32 * s + 8 * kg) = xq[s];
@@ -696,10 +714,8 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   __syncthreads();
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return sQg[r * RS + c]; });
-  emit_frags<K, 64, kIntraThreads>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid,
-                                   [&](int r, int c) { return sQg[c * RS + r]; });
-  emit_frags<K, 64, kIntraThreads, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid,
-                                         [&](int r, int c) { return sKd[c * RS + r]; });
+  emit_frags_tr<K, 64, kIntraThreads>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid, sQg, RS);
+  emit_frags_tr<K, 64, kIntraThreads, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, sKd, RS);
 }
 
 // ---------------------------------------------------------------------------

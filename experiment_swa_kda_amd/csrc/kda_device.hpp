@@ -145,6 +145,17 @@ __device__ __forceinline__ bf16x8 lds_col_frag(const bf16* m, int pitch, int r0,
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Column fragment whose two halves are 4-row groups from different row bases: lane
+// (l % 16, l / 16) gets m[ra + 4 (l / 16) + e][c0 + l % 16] for e < 4 and
+// m[rb + 4 (l / 16) + e - 4][c0 + l % 16] for e >= 4.
+__device__ __forceinline__ bf16x8 lds_col_frag_split(const bf16* m, int pitch, int ra, int rb, int c0, int lane) {
+  const int lr = lane % 16, kg = lane / 16;
+  const int off = (4 * kg + lr / 4) * pitch + c0 + 4 * (lr % 4);
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(m + ra * pitch + off));
+  const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(m + rb * pitch + off));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Four-row column fragment (the B operand of a 16-deep MFMA, or an A operand read down a
 // column): lane (l % 16, l / 16) gets m[r0 + 4 (l / 16) + e][c0 + l % 16], e = 0..3, from one
 // transposing read (same lane mapping as lds_col_frag, four rows per lane group).
