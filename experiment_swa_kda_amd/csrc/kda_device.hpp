@@ -202,6 +202,8 @@ constexpr int kCoherentPolicy = 1 | 16;  // sc0 | sc1
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
+// A byte offset beyond raw_rsrc's range: a buffer load from it reads zeros.
+constexpr int kDropOffset = (int)0x80000000u;
 __device__ __forceinline__ bf16x4 f4_to_bf16x4(float4 x) {
   bf16x4 r;
   r[0] = to_bf16(x.x); r[1] = to_bf16(x.y); r[2] = to_bf16(x.z); r[3] = to_bf16(x.w);

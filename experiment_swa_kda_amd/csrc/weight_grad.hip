@@ -10,7 +10,12 @@
 // atomics).
 //
 // Both operands are row-major in M, while an MFMA operand fragment holds 8 consecutive
-// contraction rows of one column.  Each thread loads an 8 x 8 block (8 rows of one 16-byte
+// contraction rows of one column.  Two kernels:
+//  - outputs of at least kWgDmaMinTiles 128 x 128 tiles with aligned operands: LDS stages
+//    filled by dedicated loader waves with global -> LDS buffer loads, fragments read down the
+//    columns with transposing LDS reads (weight_grad_dma_kernel, below);
+//  - otherwise 64 x 64 tiles (four times the tiles, so fewer ranges and partials): each
+//    thread loads an 8 x 8 block (8 rows of one 16-byte
 // column group), transposes it in registers and writes 8 16-byte rows of the transposed
 // slab [column][row] to LDS, so every global access and every LDS access is 16 bytes wide.
 // A workgroup covers kWgDepth 128-row steps of the contraction and issues all of their
@@ -198,6 +203,149 @@ __global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Aligned operands: 128 x 128 output tiles.  Two loader waves stream 32-row contraction steps
+// of dy (128 columns) and x (128 columns) into LDS with buffer loads (global -> LDS, no
+// registers), kWgStages - 1 steps ahead; four compute waves own 64 x 64 each (4 x 4 MFMA
+// accumulators) and read their operand fragments, 8 consecutive contraction rows of one
+// column, with transposing LDS reads, one step ahead of the products.  A stage row is the
+// 256 bytes of one contraction row; its 16-byte chunk q sits in slot q ^ 2 (row % 4), so the
+// four rows one transposing read touches fall on different banks.
+// ---------------------------------------------------------------------------------------
+constexpr int kWgBT = 128;                          // output tile (n and k)
+constexpr int kWgBR = 32;                           // contraction rows per step
+constexpr int kWgStages = 6;
+constexpr int kWgCompute = 4;
+constexpr int kWgDmaThreads = (kWgCompute + 2) * kWave;
+constexpr int kWgRowBytes = kWgBT * 2;              // 256
+constexpr int kWgPart = kWgBR * kWgRowBytes;        // 8 KB: one operand's step
+constexpr int kWgStage = 2 * kWgPart;
+constexpr int kWgNI = kWgPart / 1024;               // loads per step and loader (8)
+constexpr int kWgDmaLds = kWgStages * kWgStage;     // 96 KB
+static_assert((kWgStages - 2) * kWgNI < 64, "vmcnt range");
+
+__device__ __forceinline__ int wg_slot_off(int r, int col) {
+  // byte offset of column col (a multiple of 4) of stage row r
+  return r * kWgRowBytes + (((col >> 3) ^ (2 * (r & 3))) << 4) + ((col >> 2) & 1) * 8;
+}
+
+// lane (l % 16, l / 16) gets rows 8 (l / 16) + e (e < 8) of column c0 + l % 16 of one operand's
+// stage (two transposing reads; the second four rows are 4 rows = 1 KB further)
+__device__ __forceinline__ bf16x8 wg_col_frag(const char* part, int c0, int lane) {
+  const int lr = lane % 16, kg = lane / 16;
+  const char* p = part + wg_slot_off(8 * kg + lr / 4, c0 + 4 * (lr % 4));
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
+  const short4_t hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p + 4 * kWgRowBytes));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+__global__ __launch_bounds__(kWgDmaThreads) void weight_grad_dma_kernel(
+    int M, int N, int K, const bf16* __restrict__ dy, long ldd, const bf16* __restrict__ x, long ldx,
+    int rows_per_split, float* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tiles_k = (K + kWgBT - 1) / kWgBT;
+  const int tiles = tiles_k * ((N + kWgBT - 1) / kWgBT);
+  const int splits = (max(M, 1) + rows_per_split - 1) / rows_per_split;
+  const int per_xcd = (tiles * splits + kXcds - 1) / kXcds;
+  const int item = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (item >= tiles * splits) return;  // grid rounding (the whole workgroup)
+  const int tile = item % tiles, split = item / tiles;
+  const int n0 = (tile / tiles_k) * kWgBT, k0 = (tile % tiles_k) * kWgBT;
+  const int m_begin = split * rows_per_split, m_end = min(M, m_begin + rows_per_split);
+  const int nsteps = (max(m_end - m_begin, 0) + kWgBR - 1) / kWgBR;
+  // uniform wave index: the loaders' descriptors and LDS bases must be scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+
+  if (wave >= kWgCompute) {
+    // ---- loader waves: wave 4 moves dy rows (columns n0..), wave 5 x rows (k0..) ----
+    if (nsteps == 0) return;
+    const bool isd = wave == kWgCompute;
+    const __amdgpu_buffer_rsrc_t rs = raw_rsrc(isd ? (const void*)dy : (const void*)x);
+    const long ld = isd ? ldd : ldx;
+    const int c0 = isd ? n0 : k0, ncols = isd ? N : K;
+    auto issue = [&](int q) {
+      char* st = smem + (q % kWgStages) * kWgStage + (isd ? 0 : kWgPart);
+      const int m0 = m_begin + q * kWgBR;
+#pragma unroll
+      for (int i = 0; i < kWgNI; ++i) {
+        const int r = 4 * i + lane / 16, qc = (lane % 16) ^ (2 * (r & 3));
+        const int m = m0 + r, c = c0 + 8 * qc;
+        const bool ok = m < m_end && c < ncols;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(st + 4 * i * kWgRowBytes),
+                                                 16, ok ? (int)(((long)m * ld + c) * 2) : kDropOffset, 0, 0, 0);
+      }
+    };
+    constexpr int P = kWgStages - 1;
+    auto wait_landed = [&](int later) {  // step t landed: at most `later` steps issued after it
+      switch (later) {
+        case 4: wait_vmcnt<4 * kWgNI>(); break;
+        case 3: wait_vmcnt<3 * kWgNI>(); break;
+        case 2: wait_vmcnt<2 * kWgNI>(); break;
+        case 1: wait_vmcnt<kWgNI>(); break;
+        default: wait_vmcnt<0>(); break;
+      }
+    };
+    for (int q = 0; q < P && q < nsteps; ++q) issue(q);
+    wait_landed(min(P - 1, nsteps - 1));
+    ring_barrier();  // B0: step 0 visible
+    for (int q = 0; q < nsteps; ++q) {
+      wait_landed(max(0, min(P - 2, nsteps - 2 - q)));
+      ring_barrier();  // A(q): step q + 1 visible; step q - 1's slot is free
+      if (q + P < nsteps) issue(q + P);
+    }
+    return;
+  }
+
+  // ---- compute wave (wn, wk): output rows n0 + 64 wn.., columns k0 + 64 wk.. ----
+  const int wn = wave / 2, wk = wave % 2;
+  const int lr = lane % 16, kg = lane / 16;
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = zero4();
+  if (nsteps > 0) {
+    auto read_frags = [&](int q, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+      const char* st = smem + (q % kWgStages) * kWgStage;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = wg_col_frag(st, 64 * wn + 16 * t, lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = wg_col_frag(st + kWgPart, 64 * wk + 16 * u, lane);
+    };
+    auto step = [&](int q, const bf16x8 (&a)[4], const bf16x8 (&b)[4], bf16x8 (&an)[4], bf16x8 (&bn)[4]) {
+      ring_barrier();  // A(q)
+      if (q + 1 < nsteps) read_frags(q + 1, an, bn);  // overlaps the products below
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][u] = mfma16(a[t], b[u], acc[t][u]);
+    };
+    bf16x8 a0[4], b0[4], a1[4], b1[4];
+    ring_barrier();  // B0
+    read_frags(0, a0, b0);
+    int q = 0;
+    for (; q + 1 < nsteps; q += 2) {
+      step(q, a0, b0, a1, b1);
+      step(q + 1, a1, b1, a0, b0);
+    }
+    if (q < nsteps) step(q, a0, b0, a1, b1);
+  }
+  // lane (lr, kg) holds rows 16 t + 4 kg + r (n), column 16 u + lr (k) of the wave's block
+  float* o = out + (size_t)split * N * K;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = n0 + 64 * wn + 16 * t + 4 * kg + r;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = k0 + 64 * wk + 16 * u + lr;
+        if (n < N && k < K) o[(size_t)n * K + k] = acc[t][u][r];
+      }
+    }
+}
+
 // out[i] = sum_p part[p][i] in order p = 0, 1, ...; four outputs per thread, the loads of
 // kSumBatch partials issued before any is added.
 constexpr int kSumBatch = 8;
@@ -239,6 +387,24 @@ struct WgPlan {
 // ranges as that allows: every extra range adds an f32 partial of the whole output that the
 // reduction writes and reads back.  A range is a whole number of 512-row blocks.
 constexpr int kWgTarget = 1024;
+constexpr int kWgDmaTarget = 384;  // the 128 x 128 kernel: about one and a half workgroups per CU (measured best of 256, 384, 512)
+constexpr int kWgDmaMinTiles = 24;  // fewer 128 x 128 tiles: the 64 x 64 kernel (fewer partials)
+
+// The aligned kernel's plan: 128 x 128 tiles, ranges of whole 32-row steps.
+static bool use_weight_grad_dma(int N, int K) {
+  return ((N + kWgBT - 1) / kWgBT) * ((K + kWgBT - 1) / kWgBT) >= kWgDmaMinTiles;
+}
+
+static WgPlan plan_weight_grad_dma(int M, int N, int K) {
+  WgPlan p;
+  p.tiles = ((N + kWgBT - 1) / kWgBT) * ((K + kWgBT - 1) / kWgBT);
+  const int steps = max(1, (M + kWgBR - 1) / kWgBR);
+  const int want = max(1, min(steps, (kWgDmaTarget + p.tiles - 1) / p.tiles));
+  const int per_split = (steps + want - 1) / want;
+  p.rows_per_split = per_split * kWgBR;
+  p.splits = (steps + per_split - 1) / per_split;
+  return p;
+}
 
 static WgPlan plan_weight_grad(int M, int N, int K) {
   WgPlan p;
@@ -256,8 +422,10 @@ static WgPlan plan_weight_grad(int M, int N, int K) {
 
 extern "C" size_t kda_weight_grad_scratch_bytes(int64_t M, int32_t N, int32_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || M > 0x7fffffff) return 0;
-  const kda::WgPlan p = kda::plan_weight_grad((int)M, N, K);
-  return p.splits > 1 ? (size_t)p.splits * N * K * sizeof(float) : 0;
+  // enough for either kernel (which one runs depends on the operands' alignment)
+  const kda::WgPlan p = kda::plan_weight_grad((int)M, N, K), q = kda::plan_weight_grad_dma((int)M, N, K);
+  const int splits = std::max(p.splits > 1 ? p.splits : 0, q.splits > 1 ? q.splits : 0);
+  return (size_t)splits * N * K * sizeof(float);
 }
 
 extern "C" int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, int64_t ldd,
@@ -269,17 +437,32 @@ extern "C" int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, 
   KDA_REQUIRE(dweight && (M == 0 || (dy && x)), "weight_grad: null pointer");
   // M == 0: one split with no steps writes the zero gradient (no memset node, so the call
   // stays capturable)
-  const WgPlan p = M > 0 ? plan_weight_grad((int)M, N, K)
+  const bool vec = aligned16(dy, x) && ldd % 8 == 0 && ldx % 8 == 0 && N % 8 == 0 && K % 8 == 0;
+  const bool dma = vec && use_weight_grad_dma(N, K);
+  // M == 0 with the aligned kernel: one split with no steps writes zeros too
+  const WgPlan p = dma ? plan_weight_grad_dma((int)std::max<int64_t>(M, 1), N, K)
+                 : M > 0 ? plan_weight_grad((int)M, N, K)
                          : WgPlan{((N + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile), 1, 1};
   KDA_REQUIRE(p.splits == 1 || scratch, "weight_grad: scratch required (kda_weight_grad_scratch_bytes)");
   KDA_REQUIRE(aligned16(scratch, dweight), "weight_grad: dweight and scratch must be 16-byte aligned");
-  const bool vec = aligned16(dy, x) && ldd % 8 == 0 && ldx % 8 == 0 && N % 8 == 0 && K % 8 == 0;
+  KDA_REQUIRE(!dma || M == 0 || (((M - 1) * std::max(ldd, ldx) + std::max(N, K)) * 2 < 0x7fffff00LL),
+              "weight_grad: operands exceed 2 GiB");
   float* part = p.splits > 1 ? (float*)scratch : dweight;
   dim3 grid(kXcds * ((p.tiles * p.splits + kXcds - 1) / kXcds));
-  if (vec)
+  if (dma) {
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e = hipFuncSetAttribute((const void*)weight_grad_dma_kernel,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kWgDmaLds);
+      if (e != hipSuccess) return set_error(KDA_ERR_LAUNCH, "weight_grad: LDS attribute: %s", hipGetErrorString(e));
+      attr = true;
+    }
+    hipLaunchKernelGGL(weight_grad_dma_kernel, grid, dim3(kWgDmaThreads), kWgDmaLds, stream, (int)M, N, K,
+                       (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
+  } else if (vec) {
     hipLaunchKernelGGL(weight_grad_kernel<true>, grid, dim3(kWgThreads), 0, stream, (int)M, N, K,
                        (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
-  else
+  } else
     hipLaunchKernelGGL(weight_grad_kernel<false>, grid, dim3(kWgThreads), 0, stream, (int)M, N, K,
                        (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
   KDA_LAUNCH_CHECK("weight_grad");
