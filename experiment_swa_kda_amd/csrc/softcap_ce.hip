@@ -12,8 +12,9 @@
 //   d logits_j = g * (exp(z_j - lse) - [j == t]) * (1 - (z_j / softcap)^2)
 // with g = dL/dloss / (number of non-ignored rows), read from device memory so that no
 // host synchronisation is needed.  Columns vocab..stride-1 (vocabulary padding) get zero
-// gradient.  HBM-bound: one workgroup per row, 16-byte vector loads issued kCeBatch at a
-// time, row sums reduced in a fixed order (deterministic).
+// gradient.  HBM-bound: a persistent grid of one wave per row at a time, 16-byte vector
+// loads double-buffered in chunks of kCeBatch per lane, z and its factors looked up per bf16 bit
+// pattern in an LDS table, row sums reduced in a fixed order (deterministic).
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
@@ -21,103 +22,237 @@ namespace kda {
 
 constexpr int kCeThreads = 256;
 constexpr int kCeBatch = 8;  // 16-byte vectors in flight per thread
-constexpr float kLog2e = 1.4426950408889634f;
 
-// tanh(x) = 1 - 2 / (e^{2x} + 1) from v_exp_f32 / v_rcp_f32 (each about 1 ulp; absolute
-// error ~1e-7).  Saturates to +-1 through exp -> inf / 0.
-__device__ __forceinline__ float tanh_fast(float x) {
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(2.0f * kLog2e * x) + 1.0f);
+// Per-element transcendentals (tanh's exp and reciprocal, then exp(z)) at a quarter of the
+// VALU rate would cost more than the row's HBM read.  A bf16 logit has only 2^16 bit
+// patterns, so the per-pattern values are tabulated in LDS (accurate tanhf / expf), once
+// per workgroup of a persistent grid.  The table covers the binary
+// exponents kTabELo .. kTabEHi, i.e. |x| in [2^-24, 2^9); a pattern outside is clamped to
+// the nearest end of the range.  Below it exp(z) = 1 to within 2^-23; above it
+// 1 - tanh(x / cap) <= 2 e^(-2 * 512 / 60) < 1e-7 for every cap <= 60, i.e. tanh has
+// saturated to within one f32 ulp.  Inf clamps to +-(2^9 - 2); NaN logits are not
+// propagated.  Index: sign * kTabHalf + clamp(bits & 0x7fff) - (kTabELo << 7).
+constexpr int kTabELo = 127 - 24, kTabEHi = 127 + 8;
+constexpr int kTabHalf = (kTabEHi - kTabELo + 1) * 128;  // 4224 patterns per sign
+constexpr int kTabSize = 2 * kTabHalf;
+// workgroups per CU that the LDS tables allow: 33 KB forward, 66 KB backward
+constexpr int kCeFwdPerCu = 4, kCeBwdPerCu = 2;
+
+__device__ __forceinline__ float tab_pattern_value(int i) {
+  const unsigned sign = i >= kTabHalf ? 0x8000u : 0u;
+  const unsigned key = (unsigned)(i % kTabHalf) + (kTabELo << 7);
+  return __uint_as_float((sign | key) << 16);
 }
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int wave = threadIdx.x / kWave;
-  if (threadIdx.x % kWave == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.f;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Table indices of the two bf16 patterns packed in one 32-bit word, in packed 16-bit integer
+// arithmetic: clamp(bits & 0x7fff) - (kTabELo << 7) + sign * kTabHalf, both < 2^14.  The fast
+// paths drop the constant - (kTabELo << 7) (tab_index2_biased) and index a table pointer
+// moved back by it instead.
+__device__ __forceinline__ void tab_index2_biased(unsigned w, int& lo, int& hi) {
+  u16x2 k = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+  k = __builtin_elementwise_max(k, (u16x2)(kTabELo << 7));
+  k = __builtin_elementwise_min(k, (u16x2)((kTabEHi << 7) | 127));
+  const u16x2 sg = __builtin_bit_cast(u16x2, (w >> 15) & 0x00010001u);
+  const u16x2 idx = k + sg * (u16x2)kTabHalf;  // < 17408 + 4224
+  const unsigned r = __builtin_bit_cast(unsigned, idx);
+  lo = (int)(r & 0xffffu);
+  hi = (int)(r >> 16);
+}
+
+__device__ __forceinline__ void tab_index2(unsigned w, int& lo, int& hi) {
+  tab_index2_biased(w, lo, hi);
+  lo -= kTabELo << 7;
+  hi -= kTabELo << 7;
+}
+
+__device__ __forceinline__ unsigned bf16_bits(bf16 v) { return (unsigned)__builtin_bit_cast(unsigned short, v); }
+
+__device__ __forceinline__ int tab_index(unsigned bits16) {
+  int lo, hi;
+  tab_index2(bits16, lo, hi);
+  return lo;
+}
+
+// One wave per row (rows gw, gw + waves, ...), so a row's reduction is a wave reduction and
+// no barrier stalls the loads.  A row is read in chunks of kCeBatch 16-byte vectors per lane
+// (kCeChunk columns); chunks are double-buffered across the wave's whole sequence of
+// (row, chunk) items, so the next chunk's loads, also the next row's, are in flight while
+// the current one is reduced.
+constexpr int kCeChunk = kWave * 8 * kCeBatch;
+
+struct CeRows {
+  long gw, nw, nch, items;
+  __device__ CeRows(long rows, long cols) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    gw = (long)blockIdx.x * (kCeThreads / kWave) + wave;
+    nw = (long)gridDim.x * (kCeThreads / kWave);
+    nch = (cols + kCeChunk - 1) / kCeChunk;
+    items = gw < rows ? ((rows - 1 - gw) / nw + 1) * nch : 0;
+  }
+  __device__ long row(long j) const { return gw + (j / nch) * nw; }
+  __device__ long col0(long j) const { return (j % nch) * kCeChunk; }
+};
+
+// loads item j's chunk; columns past `last` re-read the vector at `last` (masked later)
+__device__ __forceinline__ void ce_load(const CeRows& it, long j, const bf16* __restrict__ base,
+                                        long stride, long last, bf16x8* x) {
+  const bf16* p = base + it.row(j) * stride;
+  const long c0 = it.col0(j) + (threadIdx.x % kWave) * 8;
 #pragma unroll
-  for (int w = 0; w < kCeThreads / kWave; ++w) s += red[w];
-  return s;
+  for (int b = 0; b < kCeBatch; ++b) {
+    const long c = c0 + b * kWave * 8;
+    x[b] = *reinterpret_cast<const bf16x8*>(p + (c < last ? c : last));
+  }
 }
 
 __global__ __launch_bounds__(kCeThreads) void softcap_ce_fwd_kernel(
-    int vocab, long stride, float cap, const bf16* __restrict__ logits,
+    long rows, int vocab, long stride, float cap, const bf16* __restrict__ logits,
     const int64_t* __restrict__ targets, int64_t ignore_index, float* __restrict__ loss_row,
     float* __restrict__ lse_row) {
-  __shared__ float red[kCeThreads / kWave];
-  const long row = blockIdx.x;
-  const bf16* p = logits + row * stride;
-  const float inv_cap = 1.0f / cap;
-  const int last = ((vocab - 1) / 8) * 8;  // last vector start that holds a vocabulary column
+  __shared__ float tab[kTabSize];
+  for (int i = threadIdx.x; i < kTabSize; i += kCeThreads)
+    tab[i] = expf(cap * tanhf(tab_pattern_value(i) / cap));
+  __syncthreads();
+  const CeRows it(rows, vocab);
+  const float* tabz = tab - (kTabELo << 7);
+  const long last = ((vocab - 1) / 8) * 8;  // last vector start that holds a vocabulary column
+  const int lane = threadIdx.x % kWave;
   float sum = 0.f;
-  for (int base = 0; base < vocab; base += kCeThreads * 8 * kCeBatch) {
-    bf16x8 x[kCeBatch];
+  auto consume = [&](long j, const bf16x8* x) {
+    const int c0 = (int)it.col0(j) + lane * 8;
+    if ((int)it.col0(j) + kCeChunk <= vocab) {  // whole chunk inside the vocabulary (uniform)
 #pragma unroll
-    for (int b = 0; b < kCeBatch; ++b) {
-      const int c = base + (b * kCeThreads + threadIdx.x) * 8;
-      x[b] = *reinterpret_cast<const bf16x8*>(p + (c < last ? c : last));
-    }
+      for (int b = 0; b < kCeBatch; ++b) {
+        const uint4 w = __builtin_bit_cast(uint4, x[b]);
+        const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+        float sb = 0.f;  // per-vector partial: short dependent-add chains
 #pragma unroll
-    for (int b = 0; b < kCeBatch; ++b) {
-      const int c = base + (b * kCeThreads + threadIdx.x) * 8;
+        for (int e = 0; e < 4; ++e) {
+          int i0, i1;
+          tab_index2_biased(ws[e], i0, i1);
+          sb += tabz[i0] + tabz[i1];
+        }
+        sum += sb;
+      }
+    } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float z = cap * tanh_fast((float)x[b][e] * inv_cap);
-        const float ez = __builtin_amdgcn_exp2f(kLog2e * z);
-        sum += (c + e < vocab) ? ez : 0.f;
+      for (int b = 0; b < kCeBatch; ++b) {
+        const int c = c0 + b * kWave * 8;
+        float sb = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float ez = tab[tab_index(bf16_bits(x[b][e]))];
+          sb += (c + e < vocab) ? ez : 0.f;
+        }
+        sum += sb;
       }
     }
-  }
-  sum = block_sum(sum, red);
-  if (threadIdx.x == 0) {
-    const float lse = __logf(sum);
-    const int64_t t = targets[row];
-    float loss;
-    if (t == ignore_index) {
-      loss = 0.f;
-    } else if (t < 0 || t >= vocab) {
-      loss = __builtin_nanf("");  // out-of-range target: poison the mean
-    } else {
-      loss = lse - cap * tanh_fast((float)p[t] * inv_cap);
+    if (j % it.nch == it.nch - 1) {
+      const float tot = wave_sum(sum);
+      sum = 0.f;
+      if (lane == 0) {
+        const long row = it.row(j);
+        const int64_t t = targets[row];
+        const float lse = __logf(tot);
+        float loss;
+        if (t == ignore_index) {
+          loss = 0.f;
+        } else if (t < 0 || t >= vocab) {
+          loss = __builtin_nanf("");  // out-of-range target: poison the mean
+        } else {
+          loss = lse - cap * tanhf((float)logits[row * stride + t] / cap);
+        }
+        loss_row[row] = loss;
+        lse_row[row] = lse;
+      }
     }
-    loss_row[row] = loss;
-    lse_row[row] = lse;
+  };
+  bf16x8 xa[kCeBatch], xb[kCeBatch];
+  if (it.items > 0) ce_load(it, 0, logits, stride, last, xa);
+  for (long j = 0; j < it.items; j += 2) {
+    if (j + 1 < it.items) ce_load(it, j + 1, logits, stride, last, xb);
+    consume(j, xa);
+    if (j + 1 >= it.items) break;
+    if (j + 2 < it.items) ce_load(it, j + 2, logits, stride, last, xa);
+    consume(j + 1, xb);
   }
 }
 
+// backward table: (exp(z), 1 - tanh^2) per pattern
 __global__ __launch_bounds__(kCeThreads) void softcap_ce_bwd_kernel(
-    int vocab, long stride, float cap, const bf16* __restrict__ logits,
+    long rows, int vocab, long stride, float cap, const bf16* __restrict__ logits,
     const int64_t* __restrict__ targets, int64_t ignore_index, const float* __restrict__ lse_row,
     const float* __restrict__ grad_scale, bf16* __restrict__ grad) {
-  const long row = blockIdx.x;
-  const bf16* p = logits + row * stride;
-  bf16* q = grad + row * stride;
-  const float inv_cap = 1.0f / cap;
-  const int64_t t = targets[row];
-  const float g = (t == ignore_index) ? 0.f : *grad_scale;
-  const float lse = lse_row[row];
-  const int tc = (t >= 0 && t < vocab) ? (int)t : -1;
-  for (long base = 0; base < stride; base += kCeThreads * 8 * kCeBatch) {
-    bf16x8 x[kCeBatch];
-#pragma unroll
-    for (int b = 0; b < kCeBatch; ++b) {
-      const long c = base + (b * kCeThreads + threadIdx.x) * 8;
-      x[b] = *reinterpret_cast<const bf16x8*>(p + (c < stride ? c : stride - 8));
+  __shared__ float2 tab[kTabSize];
+  for (int i = threadIdx.x; i < kTabSize; i += kCeThreads) {
+    const float th = tanhf(tab_pattern_value(i) / cap);
+    tab[i] = make_float2(expf(cap * th), 1.0f - th * th);
+  }
+  __syncthreads();
+  const CeRows it(rows, stride);
+  const float2* tabz = tab - (kTabELo << 7);
+  const float gs = *grad_scale;
+  const int lane = threadIdx.x % kWave;
+  float g = 0.f, einv = 0.f, ge = 0.f;
+  int tc = -1;
+  auto consume = [&](long j, const bf16x8* x) {
+    const long row = it.row(j);
+    if (j % it.nch == 0) {
+      const int64_t t = targets[row];
+      g = (t == ignore_index) ? 0.f : gs;
+      einv = __expf(-lse_row[row]);
+      tc = (t >= 0 && t < vocab) ? (int)t : -1;
+      ge = g * einv;
     }
+    bf16* q = grad + row * stride;
+    const int c0 = (int)it.col0(j) + lane * 8;
+    const bool full = (int)it.col0(j) + kCeChunk <= vocab;  // uniform over the wave
 #pragma unroll
     for (int b = 0; b < kCeBatch; ++b) {
-      const long c = base + (b * kCeThreads + threadIdx.x) * 8;
+      const int c = c0 + b * kWave * 8;
       bf16x8 y;
+      if (full && (unsigned)(tc - c) >= 8u) {  // no padding column, no target column
+        const uint4 w = __builtin_bit_cast(uint4, x[b]);
+        const unsigned ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float th = tanh_fast((float)x[b][e] * inv_cap);
-        const float pr = __builtin_amdgcn_exp2f(kLog2e * (cap * th - lse));
-        const float d = g * (pr - (c + e == tc ? 1.0f : 0.0f)) * (1.0f - th * th);
-        y[e] = to_bf16(c + e < vocab ? d : 0.f);
+        for (int e = 0; e < 4; ++e) {
+          int i0, i1;
+          tab_index2_biased(ws[e], i0, i1);
+          const float2 v0 = tabz[i0], v1 = tabz[i1];
+          y[2 * e] = to_bf16(v0.x * ge * v0.y);
+          y[2 * e + 1] = to_bf16(v1.x * ge * v1.y);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float2 v = tab[tab_index(bf16_bits(x[b][e]))];
+          const float d = g * (v.x * einv - (c + e == tc ? 1.0f : 0.0f)) * v.y;
+          y[e] = to_bf16(c + e < vocab ? d : 0.f);
+        }
       }
       if (c < stride) *reinterpret_cast<bf16x8*>(q + c) = y;
     }
+  };
+  bf16x8 xa[kCeBatch], xb[kCeBatch];
+  if (it.items > 0) ce_load(it, 0, logits, stride, stride - 8, xa);
+  for (long j = 0; j < it.items; j += 2) {
+    if (j + 1 < it.items) ce_load(it, j + 1, logits, stride, stride - 8, xb);
+    consume(j, xa);
+    if (j + 1 >= it.items) break;
+    if (j + 2 < it.items) ce_load(it, j + 2, logits, stride, stride - 8, xa);
+    consume(j + 1, xb);
   }
+}
+
+static unsigned ce_grid(int64_t rows, int per_cu) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const long g = (long)cus * per_cu;
+  const long need = (rows + kCeThreads / kWave - 1) / (kCeThreads / kWave);
+  return (unsigned)(need < g ? need : g);
 }
 
 }  // namespace kda
@@ -126,8 +261,8 @@ static int check_ce_args(int64_t rows, int32_t vocab, int64_t stride, float soft
                          const void* logits, const void* targets) {
   KDA_REQUIRE(rows >= 0 && rows <= 0x7fffffff, "softcap_cross_entropy: invalid row count");
   KDA_REQUIRE(vocab > 0 && vocab <= (1 << 24), "softcap_cross_entropy: vocab must be in [1, 2^24]");
-  KDA_REQUIRE(stride >= vocab && stride % 8 == 0,
-              "softcap_cross_entropy: row stride must be >= vocab and a multiple of 8");
+  KDA_REQUIRE(stride >= vocab && stride % 8 == 0 && stride <= (1 << 30),
+              "softcap_cross_entropy: row stride must be >= vocab, a multiple of 8 and <= 2^30");
   KDA_REQUIRE(softcap > 0.f && softcap <= 60.f, "softcap_cross_entropy: softcap must be in (0, 60]");
   KDA_REQUIRE(logits && targets, "softcap_cross_entropy: null pointer");
   KDA_REQUIRE(kda::aligned16(logits), "softcap_cross_entropy: logits must be 16-byte aligned");
@@ -144,7 +279,7 @@ extern "C" int kda_softcap_cross_entropy_forward(int64_t rows, int32_t vocab, in
   if (rc != KDA_OK) return rc;
   KDA_REQUIRE(loss_rows && lse_rows, "softcap_cross_entropy_forward: null output");
   if (rows == 0) return KDA_OK;
-  hipLaunchKernelGGL(softcap_ce_fwd_kernel, dim3((unsigned)rows), dim3(kCeThreads), 0, stream, vocab,
+  hipLaunchKernelGGL(softcap_ce_fwd_kernel, dim3(ce_grid(rows, kCeFwdPerCu)), dim3(kCeThreads), 0, stream, (long)rows, vocab,
                      (long)stride, softcap, (const bf16*)logits, targets, ignore_index, loss_rows,
                      lse_rows);
   KDA_LAUNCH_CHECK("softcap_cross_entropy_forward");
@@ -162,7 +297,7 @@ extern "C" int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, i
   KDA_REQUIRE(lse_rows && grad_scale && grad_logits, "softcap_cross_entropy_backward: null pointer");
   KDA_REQUIRE(aligned16(grad_logits), "softcap_cross_entropy_backward: grad must be 16-byte aligned");
   if (rows == 0) return KDA_OK;
-  hipLaunchKernelGGL(softcap_ce_bwd_kernel, dim3((unsigned)rows), dim3(kCeThreads), 0, stream, vocab,
+  hipLaunchKernelGGL(softcap_ce_bwd_kernel, dim3(ce_grid(rows, kCeBwdPerCu)), dim3(kCeThreads), 0, stream, (long)rows, vocab,
                      (long)stride, softcap, (const bf16*)logits, targets, ignore_index, lse_rows,
                      grad_scale, (bf16*)grad_logits);
   KDA_LAUNCH_CHECK("softcap_cross_entropy_backward");
