@@ -49,6 +49,32 @@ def test_softcap_ce_matches_oracle(rows, vocab, stride, scale, ignore_every):
         assert torch.all(d[::ignore_every] == 0)
 
 
+@pytest.mark.parametrize("cap", [15.0, 60.0])
+def test_softcap_ce_extreme_logits_match_oracle(cap):
+    """The kernels look z up per bf16 bit pattern and clamp |x| outside [2^-24, 2^9): zeros,
+    bf16 denormals, tiny, huge and infinite logits (targets on them too) still match the
+    fp64 oracle, which evaluates tanh exactly."""
+    rows, vocab = 24, 8192  # two full 4096-column chunks per row: the kernels' fast path
+    x, t = _case(rows, vocab, vocab, 4.0, seed=11)
+    specials = torch.tensor([0.0, -0.0, 1e-40, -1e-39, 3e-8, -6e-8, 1e-30, 600.0, -600.0,
+                             1e4, -3e38, float("inf"), float("-inf"), 300.0, -511.0, 2.0 ** -24])
+    g = torch.Generator().manual_seed(3)
+    for r in range(rows):
+        cols = torch.randperm(vocab, generator=g)[:64]
+        x[r, cols] = specials[torch.arange(64) % len(specials)].bfloat16()
+        if r % 3 == 0:
+            x[r, t[r]] = specials[r % len(specials)].bfloat16()
+    loss_o, rows_o, lse_o, d_o = O.softcap_cross_entropy(x.double().numpy(), t.numpy(), vocab, cap, -1)
+    xd, td = x.cuda().requires_grad_(), t.cuda()
+    loss = softcap_cross_entropy(xd, td, vocab, cap, -1)
+    loss.backward()
+    assert abs(loss.item() - loss_o) <= 1e-5 * max(1.0, abs(loss_o))
+    lr, lse = ops.softcap_cross_entropy_forward(xd.detach(), td, vocab, cap, -1)
+    np.testing.assert_allclose(lse.cpu().double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(lr.cpu().double().numpy(), rows_o, rtol=2e-5, atol=2e-5)
+    assert rel_err(xd.grad.float().cpu(), d_o) < 5e-3
+
+
 def test_softcap_ce_deterministic_and_scaled_gradient():
     x, t = _case(128, 2048, 2048, 2.0, seed=5)
     xd, td = x.cuda(), t.cuda()
