@@ -166,8 +166,9 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42, graphed=True)
     updates (the reference scores the median of steps 2-6, docs/BENCHMARK.md:33-36).
     graphed: the whole update (4 x forward + backward, optimizer step) is one HIP graph
     replay (model.GraphedUpdate); otherwise every op is dispatched eagerly."""
-    from experiment_swa_kda_amd.model import GPT, GPTConfig, GraphedUpdate, make_optimizer
+    from experiment_swa_kda_amd.model import GPT, GPTConfig, GraphedUpdate, make_optimizer, use_tuned_gemms
 
+    tuned = use_tuned_gemms()  # recorded library-GEMM solutions for the trainer's shapes
     torch.manual_seed(seed)
     cfg = GPTConfig(sequence_len=4096, vocab_size=32768, n_layer=6, n_head=3, n_embd=384)
     model = GPT(cfg).cuda()
@@ -202,7 +203,8 @@ def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42, graphed=True)
     return {"tok_per_s": round(B * T * accum / (ms * 1e-3), 1), "ms_per_update": round(ms, 3),
             "tokens_per_update": B * T * accum, "updates_timed": updates,
             "loss": round(float(loss.detach()), 4), "optimizer": "AdamW",
-            "execution": "hip_graph" if graphed else "eager", "reference_gb10_tok_per_s": 44942}
+            "execution": "hip_graph" if graphed else "eager",
+            "gemm_selection": "tuned" if tuned else "library default", "reference_gb10_tok_per_s": 44942}
 
 
 def load_mfma_busy():

@@ -291,3 +291,16 @@ def test_build_refuses_vgpr_spills():
     ])
     assert vgpr_spills(remarks) == {"_Z1bv": 3}
     assert vgpr_spills("") == {}
+
+
+def test_gemm_selection_file_is_pinned_to_gfx950():
+    """The committed TunableOp table names the stack it was tuned on and holds the
+    trainer's lm_head shape (8192 tokens x 384 -> 32768)."""
+    import os
+    from experiment_swa_kda_amd import model
+    lines = open(model.GEMM_SELECTION_FILE).read().splitlines()
+    val = {l.split(",")[1]: l.split(",", 2)[2] for l in lines if l.startswith("Validator,")}
+    assert val["GCN_ARCH_NAME"].startswith("gfx950")
+    assert {"PT_VERSION", "HIPBLASLT_VERSION", "ROCBLAS_VERSION"} <= set(val)
+    assert any(",tn_32768_8192_384_" in l for l in lines)
+    assert os.path.basename(model.GEMM_SELECTION_FILE) == "gemm_selection_gfx950.csv"

@@ -297,3 +297,19 @@ def test_scalar_scale_gradient():
     exp = (gy.double() * t.detach().double()).sum()
     assert abs(lam.grad.item() - exp.item()) < 1e-4 * max(1.0, abs(exp.item()))
     assert torch.equal(t.grad, gy * lam.detach().bfloat16())
+
+
+def test_tuned_gemm_selection_loads_and_computes_the_product():
+    """The committed TunableOp selection file matches this stack's validators, and a GEMM
+    routed through a recorded solution (the lm_head shape) still computes x @ W^T."""
+    from experiment_swa_kda_amd.model import use_tuned_gemms
+    try:
+        assert use_tuned_gemms()
+        g = torch.Generator(device="cuda").manual_seed(0)
+        x = torch.randn(8192, 384, device="cuda", generator=g).bfloat16()
+        w = torch.randn(32768, 384, device="cuda", generator=g).bfloat16()
+        y = torch.nn.functional.linear(x, w)
+        ref = x[::97].float() @ w.float().t()
+        assert rel_err(y[::97].float().cpu(), ref.cpu().double().numpy()) < 1e-2
+    finally:
+        torch.cuda.tunable.enable(False)
