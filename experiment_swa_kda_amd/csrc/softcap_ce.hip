@@ -80,18 +80,28 @@ __device__ __forceinline__ int tab_index(unsigned bits16) {
 // (kCeChunk columns); chunks are double-buffered across the wave's whole sequence of
 // (row, chunk) items, so the next chunk's loads, also the next row's, are in flight while
 // the current one is reduced.
+//
+// The forward walks the rows last to first.  It runs right after the lm_head GEMM has
+// written the logits, and the last-written rows are still dirty in the memory-side cache:
+// reading them first hits there, instead of evicting them (a write-back to HBM) to make room
+// for the first rows (in the trainer, 159 -> 137 us per 8192 x 32768 call).  The backward
+// walks first to last, so it starts on the rows the forward read last.
 constexpr int kCeChunk = kWave * 8 * kCeBatch;
 
 struct CeRows {
-  long gw, nw, nch, items;
-  __device__ CeRows(long rows, long cols) {
+  long gw, nw, nch, items, last_row;
+  bool reverse;
+  __device__ CeRows(long rows, long cols, bool rev) : last_row(rows - 1), reverse(rev) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     gw = (long)blockIdx.x * (kCeThreads / kWave) + wave;
     nw = (long)gridDim.x * (kCeThreads / kWave);
     nch = (cols + kCeChunk - 1) / kCeChunk;
     items = gw < rows ? ((rows - 1 - gw) / nw + 1) * nch : 0;
   }
-  __device__ long row(long j) const { return gw + (j / nch) * nw; }
+  __device__ long row(long j) const {
+    const long r = gw + (j / nch) * nw;
+    return reverse ? last_row - r : r;
+  }
   __device__ long col0(long j) const { return (j % nch) * kCeChunk; }
 };
 
@@ -115,7 +125,7 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_fwd_kernel(
   for (int i = threadIdx.x; i < kTabSize; i += kCeThreads)
     tab[i] = expf(cap * tanhf(tab_pattern_value(i) / cap));
   __syncthreads();
-  const CeRows it(rows, vocab);
+  const CeRows it(rows, vocab, true);
   const float* tabz = tab - (kTabELo << 7);
   const long last = ((vocab - 1) / 8) * 8;  // last vector start that holds a vocabulary column
   const int lane = threadIdx.x % kWave;
@@ -191,7 +201,7 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_bwd_kernel(
     tab[i] = make_float2(expf(cap * th), 1.0f - th * th);
   }
   __syncthreads();
-  const CeRows it(rows, stride);
+  const CeRows it(rows, stride, false);
   const float2* tabz = tab - (kTabELo << 7);
   const float gs = *grad_scale;
   const int lane = threadIdx.x % kWave;
