@@ -57,6 +57,8 @@ SIGNATURES = {
     "kda_chunk_backward": (ctypes.c_int, [_PP] + [_P] * 20 + [_P]),
     "kda_chunk_backward_noalloc": (ctypes.c_int, [_PP] + [_P] * 19 + [_P]),
     "kda_chunk_backward_noalloc_max_scratch_bytes": (ctypes.c_size_t, []),
+    "kda_chunk_backward_status": (ctypes.c_int, [_PP, _P, _P]),
+    "kda_debug_set_wait_limit": (ctypes.c_int, [_L]),
     "kda_chunk_forward_stage": (ctypes.c_int, [_I, _PP] + [_P] * 11 + [_P]),
     "kda_chunk_backward_stage": (ctypes.c_int, [_I, _PP] + [_P] * 20 + [_P]),
     "kda_recurrent_decode": (ctypes.c_int, [_I, _I, _I, _I, _I, _F, _F] + [_P] * 10 + [_P]),

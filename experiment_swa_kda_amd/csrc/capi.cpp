@@ -1,5 +1,8 @@
 // Thread-local error state and version of libkda_mi355x.
+#include <mutex>
+#include <set>
 #include <string>
+#include <tuple>
 
 #include "kda_host.hpp"
 
@@ -18,6 +21,20 @@ int set_error(int code, const char* fmt, ...) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+hipError_t ensure_lds_limit(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::tuple<const void*, int, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(kernel, dev, bytes);
+  if (done.count(key)) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert(key);
+  return e;
+}
 
 }  // namespace kda
 

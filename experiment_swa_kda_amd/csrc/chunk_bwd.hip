@@ -35,6 +35,7 @@
 #include "chunk_host.hpp"
 #include "kda_device.hpp"
 
+#include <atomic>
 #include <cstdlib>
 
 namespace kda {
@@ -1361,13 +1362,22 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
 // The scan members (the first scan_blocks workgroups) run the reverse scan and publish each
 // step.  Every other workgroup takes a ticket from a counter and runs the dense and then
 // the decay VJP of the tile the ticket names, tiles in the order the scan finalises them
-// (last chunks of every sequence first).  The dense part waits until every strip of the
-// tile's record has passed its chunk; the decay part reads what the same workgroup's
-// dense part stored.  Every wait is on scan members, which are dispatched before any tile
-// workgroup and wait on nothing, so the launch drains; each wait is still bounded
-// (kSpinLimit of the 100 MHz wall clock), after which the abort word is set and every
-// later wait falls through.
-constexpr long long kSpinLimit = 200000000LL;  // 2 s
+// (last chunks of every sequence first).  The dense part waits until every strip
+// of the tile's record has passed its chunk; the decay part reads what the same workgroup's
+// dense part stored.
+//
+// Dispatch-order assumption: every wait is on scan members, which wait on nothing.  The
+// launch drains only if the scan members are resident while tiles wait.  They are the lowest
+// workgroup indices of the grid, so the dispatcher places them first, before any tile
+// workgroup can occupy a CU slot; this is how the hardware dispatches a 1-D grid, but it is not
+// a documented guarantee.  Each wait is therefore bounded (the launch argument spin_limit,
+// in ticks of the 100 MHz wall clock; 2 s by default).  A tile whose wait gives up sets the
+// abort word (every later wait then gives up at once) and the failure is made visible:
+// the tile writes NaN over all of its gradient rows (dq, dk, dv, dgate, dbeta and its
+// K3-parameter partials, so dA_log and ddt_bias are NaN too), and the abort word stays set
+// in the scratch until the next call's scheduling kernel clears it, where
+// kda_chunk_backward_status() reads it.
+constexpr long long kSpinLimitDefault = 200000000LL;  // 2 s
 
 struct SyncView {
   int* ticket;
@@ -1384,19 +1394,27 @@ __device__ __forceinline__ SyncView sync_view(const BwdArgs& a) {
 // scan finishes a step about every microsecond; dense polling by a couple of hundred
 // waiting workgroups slows the scan's own memory traffic), then a workgroup barrier.  The
 // data behind the count is read with coherent loads, so no cache invalidation is needed.
+// A wait that gives up (or finds the abort word set) records it in *failed (LDS).
 struct ScanGate {
   static constexpr bool kCoherent = true;
   const int* p;
   int need;
   int* abort;
+  long long spin_limit;
+  int* failed;
   __device__ void operator()() const {
     if (threadIdx.x == 0) {
       const long long t0 = wall_clock64();
       for (;;) {
         const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v >= need || __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-        if (wall_clock64() - t0 > kSpinLimit) {
+        if (v >= need) break;
+        if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          *failed = 1;
+          break;
+        }
+        if (wall_clock64() - t0 > spin_limit) {
           __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          *failed = 1;
           break;
         }
         for (int k = min(need - v, 8); k > 0; --k) __builtin_amdgcn_s_sleep(15);  // ~0.4 us each
@@ -1405,6 +1423,32 @@ struct ScanGate {
     ring_barrier();
   }
 };
+
+// Overwrites every gradient of tile (cidx, h) with NaN: its rows of dq, dk, dv, dgate and
+// dbeta and its K3-parameter partials (the parameter reduction then yields NaN).
+template <int K, int V>
+__device__ void poison_tile(const BwdArgs& a, int cidx, int h) {
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  const int row0 = ch.x, len = ch.y, H = a.H;
+  const float nan = __builtin_nanf("");
+  const bf16 nanb = to_bf16(nan);
+  const size_t tile = (size_t)cidx * H + h;
+  for (int i = threadIdx.x; i < len * K; i += blockDim.x) {
+    const int t = i / K, c = i % K;
+    a.dq[(size_t)(row0 + t) * a.gld_qk + (size_t)h * K + c] = nanb;
+    a.dk[(size_t)(row0 + t) * a.gld_qk + (size_t)h * K + c] = nanb;
+    const size_t g = ((size_t)(row0 + t) * H + h) * K + c;
+    if (a.gate_mode == KDA_GATE_K3)
+      ((bf16*)a.dgate)[g] = nanb;
+    else
+      ((float*)a.dgate)[g] = nan;
+  }
+  for (int i = threadIdx.x; i < len * V; i += blockDim.x)
+    a.dv[(size_t)(row0 + i / V) * a.gld_v + (size_t)h * V + i % V] = nanb;
+  for (int t = threadIdx.x; t < len; t += blockDim.x) a.dbeta[(size_t)(row0 + t) * a.dbeta_ld + h] = nanb;
+  if (a.gate_mode == KDA_GATE_K3)
+    for (int i = threadIdx.x; i < 2 * K; i += blockDim.x) ((float*)a.sc.p[S_PP])[tile * 2 * K + i] = nan;
+}
 
 // Clears the sync words and writes the chunk order: chunk c of sequence s with n chunks
 // has reverse rank r = n - 1 - (index in s); chunks go by r, then by sequence.  Position
@@ -1433,14 +1477,18 @@ __global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int ma
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks) {
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks,
+                                                                      long long spin_limit) {
   const SyncView sv = sync_view(a);
   if ((int)blockIdx.x < scan_blocks) {
     bwd_scan_body<K, V, true>(a, sv.base);
     return;
   }
-  __shared__ int s_ticket;
-  if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(sv.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ int s_ticket, s_failed;
+  if (threadIdx.x == 0) {
+    s_ticket = __hip_atomic_fetch_add(sv.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_failed = 0;
+  }
   __syncthreads();
   const int t = s_ticket, H = a.H;
   const int cidx = ((const int*)a.sc.p[S_ORDER])[t / H], h = t % H;
@@ -1450,10 +1498,12 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
     rec = ch.z * H + h;
     need = ((const int2*)a.ws.p[R_SEQS])[ch.z].y - ch.w;
   }
-  ScanGate gate{sv.base + kSyncRec + 32 * rec, need, sv.abort};
+  ScanGate gate{sv.base + kSyncRec + 32 * rec, need, sv.abort, spin_limit, &s_failed};
   dense_tile<K, V>(a, cidx, h, gate);
   __syncthreads();  // the dense part's stores are complete and visible to this workgroup
   decay_tile<K>(a, cidx, h);
+  __syncthreads();
+  if (s_failed && ch.y > 0) poison_tile<K, V>(a, cidx, h);  // computed from unwritten histories
 }
 
 // ---------------------------------------------------------------------------
@@ -1514,6 +1564,14 @@ __global__ __launch_bounds__(kParamThreads) void chunk_bwd_params_kernel(BwdArgs
   }
 }
 
+// Bound of each wait in the fused backward (ticks of the 100 MHz wall clock), set by
+// kda_debug_set_wait_limit; negative: the default.
+static std::atomic<long long> g_wait_limit{-1};
+static long long wait_limit_ticks() {
+  const long long v = g_wait_limit.load(std::memory_order_relaxed);
+  return v < 0 ? kSpinLimitDefault : v;
+}
+
 // KDA_BWD_FUSED=0 selects the three-launch backward (scan, then rounds of dense / decay
 // tiles).
 static bool fused_backward_enabled() {
@@ -1535,30 +1593,30 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     constexpr size_t smem = cmax_sz(BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
     static_assert(smem + 16 <= 160 * 1024, "fused backward LDS");
     auto fused = chunk_bwd_fused_kernel<K, V>;
-    static bool attr_f = false;
-    if (!attr_f) {
-      if (hipFuncSetAttribute((const void*)fused, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
-        return set_error(KDA_ERR_LAUNCH, "chunk_backward: fused LDS attribute failed");
-      attr_f = true;
-    }
+    if (ensure_lds_limit((const void*)fused, (int)smem) != hipSuccess)
+      return set_error(KDA_ERR_LAUNCH, "chunk_backward: fused LDS attribute failed");
     const int nrec = p->num_seqs * p->heads;
     const int scan_blocks = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
     const int N = g.max_chunks * p->heads;
     hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks, sync_words(nrec, N));
     KDA_LAUNCH_CHECK("chunk_backward sched");
-    hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks);
+    hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks,
+                       wait_limit_ticks());
     KDA_LAUNCH_CHECK("chunk_backward fused");
     stages &= ~all;
+  } else if ((stages & all) == all && g.max_chunks > 0) {
+    // the staged backward never waits; clearing the sync words keeps
+    // kda_chunk_backward_status meaningful after it
+    const int nrec = p->num_seqs * p->heads;
+    hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks,
+                       sync_words(nrec, g.max_chunks * p->heads));
+    KDA_LAUNCH_CHECK("chunk_backward sched");
   }
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     auto scan = chunk_bwd_scan_kernel<K, V>;
     constexpr size_t smem_s = BwdScanLds<K, V>::bytes;
-    static bool attr_s = false;
-    if (!attr_s) {
-      if (hipFuncSetAttribute((const void*)scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem_s) != hipSuccess)
-        return set_error(KDA_ERR_LAUNCH, "chunk_backward: scan LDS attribute failed");
-      attr_s = true;
-    }
+    if (ensure_lds_limit((const void*)scan, (int)smem_s) != hipSuccess)
+      return set_error(KDA_ERR_LAUNCH, "chunk_backward: scan LDS attribute failed");
     const int nrec = p->num_seqs * p->heads;
     const int grid = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
     PrefetchList pf = {};
@@ -1580,12 +1638,8 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     constexpr size_t smem = DenseSmem<K, V>::bytes > DecaySmem<K>::bytes ? DenseSmem<K, V>::bytes
                                                                           : DecaySmem<K>::bytes;
     auto vjp = chunk_bwd_vjp_kernel<K, V>;
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)vjp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
-        return set_error(KDA_ERR_LAUNCH, "chunk_backward: LDS attribute failed");
-      attr = true;
-    }
+    if (ensure_lds_limit((const void*)vjp, (int)smem) != hipSuccess)
+      return set_error(KDA_ERR_LAUNCH, "chunk_backward: LDS attribute failed");
     const bool dense = stages & (1 << (KDA_STAGE_BWD_DENSE - 10));
     const bool decay = stages & (1 << (KDA_STAGE_BWD_DECAY - 10));
     const int N = g.max_chunks * p->heads;
@@ -1717,6 +1771,30 @@ extern "C" int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* 
                              initial_state, workspace, grad_output, grad_final_state, dq, dk, dv,
                              dgate, dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch,
                              stream);
+}
+
+extern "C" int kda_debug_set_wait_limit(int64_t ticks) {
+  kda::g_wait_limit.store(ticks < 0 ? -1 : ticks, std::memory_order_relaxed);
+  return KDA_OK;
+}
+
+extern "C" int kda_chunk_backward_status(const kda_chunk_problem* p, const void* scratch,
+                                         hipStream_t stream) {
+  using namespace kda;
+  int rc = validate_problem(p, "chunk_backward_status");
+  if (rc != KDA_OK) return rc;
+  KDA_REQUIRE(scratch && ((uintptr_t)scratch % 256) == 0,
+              "chunk_backward_status: scratch must be non-null and 256-byte aligned");
+  const Regions sc = sc_regions(make_geom(p), const_cast<void*>(scratch));
+  int word = 0;
+  hipError_t e = hipMemcpyAsync(&word, sc.p[S_SYNC] + sizeof(int), sizeof(int), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return set_error(KDA_ERR_LAUNCH, "chunk_backward_status: %s", hipGetErrorString(e));
+  if (word != 0)
+    return set_error(KDA_ERR_TIMEOUT,
+                     "chunk_backward: a VJP tile's wait for the reverse scan timed out; the "
+                     "affected gradients were overwritten with NaN");
+  return KDA_OK;
 }
 
 // ---------------------------------------------------------------------------------------

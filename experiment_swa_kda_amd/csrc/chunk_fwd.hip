@@ -1483,14 +1483,10 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
                           hipStream_t stream, int stages) {
   if (g.max_chunks > 0 && (stages & (1 << KDA_STAGE_FWD_INTRA))) {
     constexpr size_t smem = IntraLds<K, V>::bytes;
-    static bool attr = false;
-    if (!attr) {
-      for (const void* f : {(const void*)chunk_fwd_intra_kernel<K, V, false>, (const void*)chunk_fwd_intra_kernel<K, V, K == V>}) {
-        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e != hipSuccess)
-          return set_error(KDA_ERR_LAUNCH, "chunk_forward: LDS attribute: %s", hipGetErrorString(e));
-      }
-      attr = true;
+    for (const void* f : {(const void*)chunk_fwd_intra_kernel<K, V, false>, (const void*)chunk_fwd_intra_kernel<K, V, K == V>}) {
+      hipError_t e = ensure_lds_limit(f, (int)smem);
+      if (e != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_forward: LDS attribute: %s", hipGetErrorString(e));
     }
     auto intra = a.conv_x ? chunk_fwd_intra_kernel<K, V, K == V> : chunk_fwd_intra_kernel<K, V, false>;
     hipLaunchKernelGGL(intra, dim3(g.max_chunks, p->heads), dim3(kIntraThreads), smem, stream, a);
@@ -1499,12 +1495,10 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
   if (p->num_seqs > 0 && (stages & (1 << KDA_STAGE_FWD_SCAN))) {
     auto scan = chunk_fwd_scan_kernel<K, V>;
     constexpr size_t smem = ScanLds<K, V>::bytes;
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    {
+      hipError_t e = ensure_lds_limit((const void*)scan, (int)smem);
       if (e != hipSuccess)
         return set_error(KDA_ERR_LAUNCH, "chunk_forward: scan LDS attribute: %s", hipGetErrorString(e));
-      attr = true;
     }
     const int nrec = p->num_seqs * p->heads;
     if (g.seg_len == 0) {
@@ -1516,13 +1510,9 @@ static int launch_forward(const kda_chunk_problem* p, const ChunkGeom& g, FwdArg
       auto replay = chunk_fwd_seg_kernel<K, V, true>;
       using CL = SegCfg<K, V, false>;
       using CR = SegCfg<K, V, true>;
-      static bool seg_attr = false;
-      if (!seg_attr) {
-        if (hipFuncSetAttribute((const void*)local, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CL::bytes) != hipSuccess ||
-            hipFuncSetAttribute((const void*)replay, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CR::bytes) != hipSuccess)
-          return set_error(KDA_ERR_LAUNCH, "chunk_forward: segmented scan LDS attribute failed");
-        seg_attr = true;
-      }
+      if (ensure_lds_limit((const void*)local, (int)CL::bytes) != hipSuccess ||
+          ensure_lds_limit((const void*)replay, (int)CR::bytes) != hipSuccess)
+        return set_error(KDA_ERR_LAUNCH, "chunk_forward: segmented scan LDS attribute failed");
       const int nrs = nrec * g.max_segs;
       hipLaunchKernelGGL(local, dim3(kXcds * CL::GROUPS * ((nrs + kXcds - 1) / kXcds)), dim3(kSegThreads),
                          CL::bytes, stream, a, g.seg_len, g.max_segs);

@@ -20,6 +20,10 @@ inline int check_launch(const char* what) {
   return KDA_OK;
 }
 
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once per
+// (kernel, device); thread-safe.  Returns the HIP error of the first failing call.
+hipError_t ensure_lds_limit(const void* kernel, int bytes);
+
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // True when every pointer is null or 16-byte aligned (the kernels move 16-byte vectors).

@@ -30,8 +30,11 @@ constexpr int kCeBatch = 8;  // 16-byte vectors in flight per thread
 // exponents kTabELo .. kTabEHi, i.e. |x| in [2^-24, 2^9); a pattern outside is clamped to
 // the nearest end of the range.  Below it exp(z) = 1 to within 2^-23; above it
 // 1 - tanh(x / cap) <= 2 e^(-2 * 512 / 60) < 1e-7 for every cap <= 60, i.e. tanh has
-// saturated to within one f32 ulp.  Inf clamps to +-(2^9 - 2); NaN logits are not
-// propagated.  Index: sign * kTabHalf + clamp(bits & 0x7fff) - (kTabELo << 7).
+// saturated to within one f32 ulp.  Inf clamps to +-(2^9 - 2).  NaN patterns (magnitude bits
+// above 0x7f80) would clamp too, so the forward keeps a running packed maximum of the
+// magnitude bits per lane and makes the row's sum NaN when it exceeds 0x7f80: a NaN logit
+// gives a NaN row loss and lse (as tanh + library cross entropy would) and so a NaN gradient
+// row in the backward.  Index: sign * kTabHalf + clamp(bits & 0x7fff) - (kTabELo << 7).
 constexpr int kTabELo = 127 - 24, kTabEHi = 127 + 8;
 constexpr int kTabHalf = (kTabEHi - kTabELo + 1) * 128;  // 4224 patterns per sign
 constexpr int kTabSize = 2 * kTabHalf;
@@ -130,6 +133,7 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_fwd_kernel(
   const long last = ((vocab - 1) / 8) * 8;  // last vector start that holds a vocabulary column
   const int lane = threadIdx.x % kWave;
   float sum = 0.f;
+  u16x2 mag = (u16x2)0;  // running maximum of the magnitude bits (NaN detection)
   auto consume = [&](long j, const bf16x8* x) {
     const int c0 = (int)it.col0(j) + lane * 8;
     if ((int)it.col0(j) + kCeChunk <= vocab) {  // whole chunk inside the vocabulary (uniform)
@@ -142,6 +146,7 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_fwd_kernel(
         for (int e = 0; e < 4; ++e) {
           int i0, i1;
           tab_index2_biased(ws[e], i0, i1);
+          mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, ws[e] & 0x7fff7fffu));
           sb += tabz[i0] + tabz[i1];
         }
         sum += sb;
@@ -153,15 +158,19 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_fwd_kernel(
         float sb = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float ez = tab[tab_index(bf16_bits(x[b][e]))];
+          const unsigned bits = bf16_bits(x[b][e]);
+          const float ez = tab[tab_index(bits)];
           sb += (c + e < vocab) ? ez : 0.f;
+          if (c + e < vocab && (bits & 0x7fffu) > 0x7f80u) mag = (u16x2)0xffff;
         }
         sum += sb;
       }
     }
     if (j % it.nch == it.nch - 1) {
-      const float tot = wave_sum(sum);
+      const bool nan_here = mag.x > 0x7f80 || mag.y > 0x7f80;
+      const float tot = wave_sum(nan_here ? __builtin_nanf("") : sum);
       sum = 0.f;
+      mag = (u16x2)0;
       if (lane == 0) {
         const long row = it.row(j);
         const int64_t t = targets[row];
@@ -318,36 +327,41 @@ namespace kda {
 
 // Mean of the row losses over the rows whose target is not ignore_index, and that count,
 // in one workgroup with a fixed summation order (thread t sums rows t, t + 1024, ...; then
-// a fixed tree).  Keeps the loss reduction inside the library: a multi-block library
+// a fixed tree).  The count is kept in integers (exact for every row count the forward
+// accepts) and converted once for the division.  Keeps the loss reduction inside the library: a multi-block library
 // reduction would record memory-set nodes when captured in a HIP graph.
 constexpr int kMeanThreads = 1024;
 
 __global__ __launch_bounds__(kMeanThreads) void softcap_ce_mean_kernel(
     long rows, const float* __restrict__ loss_row, const int64_t* __restrict__ targets,
     int64_t ignore_index, float* __restrict__ loss, float* __restrict__ count) {
-  __shared__ float red_s[kMeanThreads / kWave], red_c[kMeanThreads / kWave];
-  float s = 0.f, c = 0.f;
+  __shared__ float red_s[kMeanThreads / kWave];
+  __shared__ long long red_c[kMeanThreads];
+  float s = 0.f;
+  long long c = 0;
   for (long r = threadIdx.x; r < rows; r += kMeanThreads) {
     const bool valid = targets[r] != ignore_index;
     s += valid ? loss_row[r] : 0.f;
-    c += valid ? 1.f : 0.f;
+    c += valid ? 1 : 0;
   }
   s = wave_sum(s);
-  c = wave_sum(c);
+  red_c[threadIdx.x] = c;
   const int wave = threadIdx.x / kWave;
-  if (threadIdx.x % kWave == 0) {
-    red_s[wave] = s;
-    red_c[wave] = c;
+  if (threadIdx.x % kWave == 0) red_s[wave] = s;
+  __syncthreads();
+  if (threadIdx.x < 32) {  // 32 partial counts of 32 threads each, then one sum of those
+    long long p = 0;
+    for (int t = 0; t < 32; ++t) p += red_c[threadIdx.x * 32 + t];
+    red_c[threadIdx.x * 32] = p;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float ts = 0.f, tc = 0.f;
-    for (int w = 0; w < kMeanThreads / kWave; ++w) {
-      ts += red_s[w];
-      tc += red_c[w];
-    }
-    *loss = ts / tc;  // NaN when every row is ignored, as the library cross entropy
-    *count = tc;
+    float ts = 0.f;
+    long long tc = 0;
+    for (int w = 0; w < kMeanThreads / kWave; ++w) ts += red_s[w];
+    for (int t = 0; t < 32; ++t) tc += red_c[t * 32];
+    *loss = ts / (float)tc;  // NaN when every row is ignored, as the library cross entropy
+    *count = (float)tc;
   }
 }
 

@@ -450,13 +450,8 @@ extern "C" int kda_weight_grad(int64_t M, int32_t N, int32_t K, const void* dy, 
   float* part = p.splits > 1 ? (float*)scratch : dweight;
   dim3 grid(kXcds * ((p.tiles * p.splits + kXcds - 1) / kXcds));
   if (dma) {
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)weight_grad_dma_kernel,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, kWgDmaLds);
-      if (e != hipSuccess) return set_error(KDA_ERR_LAUNCH, "weight_grad: LDS attribute: %s", hipGetErrorString(e));
-      attr = true;
-    }
+    hipError_t e = ensure_lds_limit((const void*)weight_grad_dma_kernel, kWgDmaLds);
+    if (e != hipSuccess) return set_error(KDA_ERR_LAUNCH, "weight_grad: LDS attribute: %s", hipGetErrorString(e));
     hipLaunchKernelGGL(weight_grad_dma_kernel, grid, dim3(kWgDmaThreads), kWgDmaLds, stream, (int)M, N, K,
                        (const bf16*)dy, (long)ldd, (const bf16*)x, (long)ldx, p.rows_per_split, part);
   } else if (vec) {

@@ -726,49 +726,55 @@ class KimiDeltaAttention(nn.Module):
         ``state.memory`` in place (see ``kda``); the returned state holds that tensor."""
         if hidden_states.ndim != 3 or hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"hidden_states must have shape [B,T,{self.hidden_size}]")
-        batch, length, _ = hidden_states.shape
-        requested_mode = self.mode if mode is None else mode
-        requested_fallback = self.allow_fallback if allow_fallback is None else allow_fallback
-        want_state = output_final_state
-        if (state is None and not want_state and requested_mode in ("project_chunk", "chunk")
-                and hidden_states.is_cuda and hidden_states.dtype == torch.bfloat16 and length > 0
-                and self.q_proj.weight.dtype == torch.float32):
-            return self._forward_batched(hidden_states, requested_mode, requested_fallback), None
-        q_state = None if state is None else state.q_conv
-        k_state = None if state is None else state.k_conv
-        v_state = None if state is None else state.v_conv
-        memory = None if state is None else state.memory
-        conv_backend = ("project_cuda" if requested_mode.startswith("project_")
-                        else "reference" if requested_mode == "reference" else "fla_triton")
-        q, q_final = self.q_conv1d(self.q_proj(hidden_states), q_state, output_final_state=want_state,
-                                   backend=conv_backend)
-        k, k_final = self.k_conv1d(self.k_proj(hidden_states), k_state, output_final_state=want_state,
-                                   backend=conv_backend)
-        v, v_final = self.v_conv1d(self.v_proj(hidden_states), v_state, output_final_state=want_state,
-                                   backend=conv_backend)
-        q = q.reshape(batch, length, self.num_heads, self.head_dim)
-        k = k.reshape(batch, length, self.num_heads, self.head_dim)
-        v = v.reshape(batch, length, self.num_heads, self.head_dim)
-        raw_gate = self.f_b_proj(self.f_a_proj(hidden_states)).reshape(batch, length, self.num_heads,
-                                                                       self.head_dim)
-        beta_logits = self.b_proj(hidden_states)
-        mixed, final_memory = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias,
-                                  initial_state=memory, output_final_state=want_state,
-                                  mode=requested_mode, lower_bound=self.lower_bound,
-                                  allow_fallback=requested_fallback, state_in_place=state_in_place)
-        output_gate = self.g_proj(hidden_states).reshape(batch, length, self.num_heads, self.head_dim)
-        use_fused = (requested_mode != "reference" and mixed.is_cuda and mixed.dtype == torch.bfloat16
-                     and output_gate.dtype == torch.bfloat16 and self.head_dim in (64, 128)
-                     and self.o_norm.weight.dtype == torch.float32)
-        if use_fused:
-            mixed = _ProjectRMSNormGateAutograd.apply(mixed, output_gate, self.o_norm.weight, self.o_norm.eps)
-            _record("rmsnorm_gate_forward")
-            mixed = _record_backward(mixed, "rmsnorm_gate_backward")
-        else:
-            mixed = self.o_norm(mixed, output_gate)
-        output = self.o_proj(mixed.reshape(batch, length, self.hidden_size))
-        final_state = KDAState(final_memory, q_final, k_final, v_final) if want_state else None
-        return output, final_state
+        mode = self.mode if mode is None else mode
+        fallback = self.allow_fallback if allow_fallback is None else allow_fallback
+        if state is None and not output_final_state and self._batched_ok(hidden_states, mode):
+            return self._forward_batched(hidden_states, mode, fallback), None
+        return self._forward_stepwise(hidden_states, state, output_final_state, mode, fallback,
+                                      state_in_place)
+
+    def _batched_ok(self, x, mode):
+        # the stacked-projection path needs no carried state and the HIP kernels' dtypes
+        return (mode in ("project_chunk", "chunk") and x.is_cuda and x.dtype == torch.bfloat16
+                and x.shape[1] > 0 and self.q_proj.weight.dtype == torch.float32)
+
+    def _forward_stepwise(self, x, state, keep_state, mode, fallback, state_in_place):
+        """General path (carried state, decode, CPU, reference mode): each of q, k, v is its
+        own projection followed by its short convolution, whose window is read from and
+        returned in the ``KDAState``."""
+        heads = (x.shape[0], x.shape[1], self.num_heads, self.head_dim)
+        backend = {"reference": "reference"}.get(mode, "project_cuda" if mode.startswith("project_")
+                                                 else "fla_triton")
+        branches = {}
+        for name in ("q", "k", "v"):
+            carry = getattr(state, f"{name}_conv") if state is not None else None
+            conv = getattr(self, f"{name}_conv1d")
+            seq, window = conv(getattr(self, f"{name}_proj")(x), carry, output_final_state=keep_state,
+                               backend=backend)
+            branches[name] = (seq.reshape(heads), window)
+        gate_in = self.f_b_proj(self.f_a_proj(x)).reshape(heads)
+        out, memory = kda(branches["q"][0], branches["k"][0], branches["v"][0], gate_in, self.b_proj(x),
+                          self.A_log, self.dt_bias,
+                          initial_state=state.memory if state is not None else None,
+                          output_final_state=keep_state, mode=mode, lower_bound=self.lower_bound,
+                          allow_fallback=fallback, state_in_place=state_in_place)
+        out = self._gated_norm(out, self.g_proj(x).reshape(heads), mode)
+        y = self.o_proj(out.reshape(x.shape[0], x.shape[1], self.hidden_size))
+        if not keep_state:
+            return y, None
+        return y, KDAState(memory, branches["q"][1], branches["k"][1], branches["v"][1])
+
+    def _gated_norm(self, o, gate, mode):
+        """RMSNorm(o)·sigmoid(gate): the HIP kernel pair whenever its dtypes and head size fit,
+        else the module's own (eager or per-op) path."""
+        kernel_fits = (mode != "reference" and o.is_cuda and o.dtype == torch.bfloat16
+                       and gate.dtype == torch.bfloat16 and self.head_dim in (64, 128)
+                       and self.o_norm.weight.dtype == torch.float32)
+        if not kernel_fits:
+            return self.o_norm(o, gate)
+        o = _ProjectRMSNormGateAutograd.apply(o, gate, self.o_norm.weight, self.o_norm.eps)
+        _record("rmsnorm_gate_forward")
+        return _record_backward(o, "rmsnorm_gate_backward")
 
     def _in_pad(self):
         return -(4 * self.hidden_size + self.head_dim + self.num_heads) % 8

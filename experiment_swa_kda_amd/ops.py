@@ -269,7 +269,34 @@ def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_st
     ``packed_qkv_grad`` (K == V) dq, dk and dv are written side by side into one
     [B, T, 3 H K] tensor, which is returned in place of dq (dk and dv are then None).
     ``dbeta_out`` [B, T, H] (a column slice of wider per-token rows) receives dbeta_logits,
-    and the ``dbeta_pad`` elements after each token's H values are set to zero."""
+    and the ``dbeta_pad`` elements after each token's H values are set to zero.
+
+    Outside graph capture the call then reads the launch's failure flag (a synchronisation
+    of the stream) and raises RuntimeError if an in-kernel wait gave up; under capture the
+    NaN that such a failure writes into the gradients is the report."""
+    grads, p, scratch = chunk_backward_launch(
+        q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace, grad_output,
+        grad_final_state, lower_bound, scale, cu_seqlens=cu_seqlens, gate=gate,
+        packed_qkv_grad=packed_qkv_grad, dbeta_out=dbeta_out, dbeta_pad=dbeta_pad)
+    if not torch.cuda.is_current_stream_capturing():
+        chunk_backward_status(p, scratch)
+    return grads
+
+
+def chunk_backward_status(p, scratch):
+    """Raise RuntimeError if the last backward on ``scratch`` (problem ``p``) reported a
+    wait that gave up (kda_chunk_backward_status; synchronises the stream)."""
+    lib = _lib.load()
+    with torch.cuda.device(scratch.device):
+        check(lib.kda_chunk_backward_status(ctypes.byref(p), ptr(scratch), _stream(scratch.device)),
+              "kda_chunk_backward")
+
+
+def chunk_backward_launch(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_state, workspace,
+                          grad_output, grad_final_state, lower_bound, scale, *, cu_seqlens=None,
+                          gate="k3", packed_qkv_grad=False, dbeta_out=None, dbeta_pad=0):
+    """The launch half of :func:`chunk_backward`: returns (gradients, problem, scratch)
+    without reading the failure flag."""
     gm = GATE_MODES[gate]
     dev = _check_chunk_inputs("chunk_backward", q, k, v, gate_values, beta_logits, A_log, dt_bias,
                               initial_state, cu_seqlens, gm)
@@ -327,8 +354,8 @@ def chunk_backward(q, k, v, gate_values, beta_logits, A_log, dt_bias, initial_st
             ptr(ddt), ptr(dinit), ptr(scratch), _stream(dev))
     check(rc, "kda_chunk_backward")
     if packed_qkv_grad:
-        return dqkv, None, None, dgate, dbeta, dA, ddt, dinit
-    return dq, dk, dv, dgate, dbeta, dA, ddt, dinit
+        return (dqkv, None, None, dgate, dbeta, dA, ddt, dinit), p, scratch
+    return (dq, dk, dv, dgate, dbeta, dA, ddt, dinit), p, scratch
 
 
 # ---------------------------------------------------------------------------

@@ -29,6 +29,7 @@ extern "C" {
 #define KDA_OK 0
 #define KDA_ERR_INVALID 1   /* bad shape, size, pointer or flag */
 #define KDA_ERR_LAUNCH 2    /* a HIP launch or runtime call failed */
+#define KDA_ERR_TIMEOUT 3   /* a bounded in-kernel wait gave up (kda_chunk_backward_status) */
 
 /* Gate parameterisations. */
 #define KDA_GATE_K3 0        /* g = lb*sigmoid(exp(A_log[h])*(raw+dt_bias[h,k])); gate is bf16 raw logits */
@@ -160,6 +161,27 @@ int kda_chunk_backward(const kda_chunk_problem* p,
                        void* dq, void* dk, void* dv, void* dgate, void* dbeta_logits,
                        float* dA_log, float* ddt_bias, float* dinitial_state,
                        void* scratch, hipStream_t stream);
+
+/*
+ * Failure report of the last kda_chunk_backward on `scratch` (the same problem and scratch
+ * buffer).  The fused backward launch runs the reverse scan and the per-chunk VJP tiles in
+ * one grid; a tile waits, with a bound, for the scan to finish its chunk.  A wait that gives
+ * up makes the tile overwrite all of its gradients with NaN (and dA_log / ddt_bias become NaN)
+ * and leaves a flag in the scratch, which this call reads: it synchronises `stream` and
+ * returns KDA_ERR_TIMEOUT (with kda_last_error() saying so) when the flag is set, else KDA_OK.
+ * The next kda_chunk_backward on the scratch clears the flag.  Counterpart: the reference
+ * reports launch failures through C10_CUDA_KERNEL_LAUNCH_CHECK (chunk.cu:1731); its kernels
+ * have no in-kernel waits.
+ */
+int kda_chunk_backward_status(const kda_chunk_problem* p, const void* scratch, hipStream_t stream);
+
+/*
+ * Sets the bound of every in-kernel wait of later kda_chunk_backward launches, in ticks of
+ * the 100 MHz wall clock (process-wide; negative restores the 2 s default).  For tests of
+ * the failure path: a bound of 0 makes every wait that is not already satisfied give up at
+ * once, and every kernel still exits normally.  No counterpart in the reference.
+ */
+int kda_debug_set_wait_limit(int64_t ticks);
 
 /*
  * kda_chunk_backward without the scratch argument, for callers that cannot allocate

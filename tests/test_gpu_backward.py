@@ -68,6 +68,52 @@ def test_backward_d64_boundaries(T):
     check(gpu_grads(d, "k3", do, dsT), oracle_grads(d, "k3", do, dsT))
 
 
+# the reference's frozen boundary lengths at its production head dim
+# (configs/research/kda_cuda_ownership.toml:42-43)
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 63, 64, 65, 127, 128, 129, 257])
+def test_backward_d128_boundaries(T):
+    d = make_kda_inputs(1, T, 3, 128, 128, seed=300 + T, state=True)
+    do, dsT = cotangents(d, 1000 + T)
+    check(gpu_grads(d, "k3", do, dsT), oracle_grads(d, "k3", do, dsT))
+
+
+def test_backward_wait_timeout_is_reported():
+    """With the fused backward's wait bound set to 0 from the host, every tile whose chunk
+    the reverse scan has not yet finished gives up at once (every kernel still exits
+    normally): the status call must report it, the given-up tiles' gradients must be NaN,
+    ops.chunk_backward must raise, and a later call with the default bound must be correct."""
+    from experiment_swa_kda_amd import _lib
+
+    lib = _lib.load()
+    d = make_kda_inputs(2, 1024, 3, 128, 128, seed=77, state=True)
+    do, dsT = cotangents(d, 77)
+    K = 128
+    _, _, ws = ops.chunk_forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], d["s0"],
+                                 True, -5.0, K ** -0.5, gate="k3")
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["A_log"], d["dt_bias"], d["s0"], ws, do, dsT, -5.0,
+            K ** -0.5)
+    print("wait-timeout test: B2 T1024 H3 D128, wait limit 0", flush=True)
+    assert lib.kda_debug_set_wait_limit(0) == 0
+    try:
+        grads, p, scratch = ops.chunk_backward_launch(*args, gate="k3")
+        with pytest.raises(RuntimeError, match="timed out"):
+            ops.chunk_backward_status(p, scratch)
+        dq, dk, dv, dg, db, dA, ddt, _ = grads
+        # the first tiles (the sequences' last chunks) start before the scan's first step
+        assert torch.isnan(dq.float()).any() and torch.isnan(dv.float()).any()
+        assert torch.isnan(dg.float()).any() and torch.isnan(db.float()).any()
+        assert torch.isnan(dA).all() and torch.isnan(ddt).any()
+        # every token row is either fully NaN or fully finite (whole tiles are poisoned)
+        rows = torch.isnan(dq.float()).any(-1)
+        assert torch.equal(rows, torch.isnan(dq.float()).all(-1))
+        with pytest.raises(RuntimeError, match="timed out"):
+            ops.chunk_backward(*args, gate="k3")
+    finally:
+        lib.kda_debug_set_wait_limit(-1)
+    grads = ops.chunk_backward(*args, gate="k3")  # default bound: no failure, flag cleared
+    check(grads, oracle_grads(d, "k3", do, dsT))
+
+
 @pytest.mark.parametrize("gate", ["k3", "precomputed"])
 @pytest.mark.parametrize("KV", [(128, 128), (64, 128), (128, 64)])
 def test_backward_d128(gate, KV):

@@ -96,6 +96,25 @@ def test_config2_k3_gate_forward_full_size():
     assert rel_err(out, eo) <= 2e-2 and rel_err(fin, ef) <= 2e-2
 
 
+def test_config2_k3_gate_backward_full_size():
+    # the reference's gradient-lane inputs: K3 gate, every activation ~ N(0,1) (seed
+    # 4100 + T + 1 there), A_log = dt_bias = 0, upstream gradient ~ N(0,1); all eight
+    # gradients against the fp64 oracle
+    g = torch.Generator().manual_seed(4100 + 4096 + 1)
+    B, T, H, K = 2, 4096, 3, 128
+    q, k, v, z = (torch.randn(B, T, H, K, generator=g).bfloat16().cuda() for _ in range(4))
+    bl = torch.randn(B, T, H, generator=g).bfloat16().cuda()
+    do = torch.randn(B, T, H, K, generator=g).bfloat16().cuda()
+    A_log, dt = torch.zeros(H, device="cuda"), torch.zeros(H * K, device="cuda")
+    out, fin, ws = ops.chunk_forward(q, k, v, z, bl, A_log, dt, None, True, -5.0, K ** -0.5, gate="k3")
+    grads = ops.chunk_backward(q, k, v, z, bl, A_log, dt, None, ws, do, None, -5.0, K ** -0.5, gate="k3")
+    args = (np64(q), np64(k), np64(v), np64(z), np64(bl), np64(A_log), np64(dt))
+    eo, ef = O.kda_forward(*args)
+    assert rel_err(out, eo) <= 2e-2 and rel_err(fin, ef) <= 2e-2
+    eg = O.kda_backward(*args, grad_output=np64(do))
+    check_grads(grads, eg, "config2-k3")
+
+
 def test_config3_decode_continues_chunked_prefill():
     # B64 H3 D128: chunked prefill of T=1024 -> state, then 256 single-token steps; the
     # decode outputs must match the chunked forward over T+256 (and the fp64 oracle)

@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import math
 import numpy as np
 import pytest
 import torch
@@ -73,6 +74,33 @@ def test_softcap_ce_extreme_logits_match_oracle(cap):
     np.testing.assert_allclose(lse.cpu().double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
     np.testing.assert_allclose(lr.cpu().double().numpy(), rows_o, rtol=2e-5, atol=2e-5)
     assert rel_err(xd.grad.float().cpu(), d_o) < 5e-3
+
+
+@pytest.mark.parametrize("vocab", [8192, 8200])
+def test_softcap_ce_nan_logit_poisons_row(vocab):
+    """A NaN logit anywhere in a row (fast full-chunk path at vocab 8192, masked tail at 8200)
+    makes that row's loss and lse NaN and its gradient row NaN, as tanh followed by the library
+    cross entropy does; the other rows stay finite and match the oracle."""
+    rows = 8
+    x, t = _case(rows, vocab, vocab + (-vocab % 8), 4.0, seed=13)
+    x[2, 17] = float("nan")
+    x[5, vocab - 1] = float("nan")  # in the tail chunk when vocab = 8200
+    xd, td = x.cuda(), t.cuda()
+    lr, lse = ops.softcap_cross_entropy_forward(xd, td, vocab, 15.0, -1)
+    lr, lse = lr.cpu(), lse.cpu()
+    bad = torch.zeros(rows, dtype=torch.bool)
+    bad[[2, 5]] = True
+    assert torch.isnan(lr[bad]).all() and torch.isnan(lse[bad]).all()
+    assert torch.isfinite(lr[~bad]).all() and torch.isfinite(lse[~bad]).all()
+    good = (~bad).nonzero().flatten()
+    _, rows_o, lse_o, _ = O.softcap_cross_entropy(x[good].double().numpy(), t[good].numpy(), vocab, 15.0, -1)
+    np.testing.assert_allclose(lse[good].double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(lr[good].double().numpy(), rows_o, rtol=2e-5, atol=2e-5)
+    g = ops.softcap_cross_entropy_backward(xd, td, lse.cuda(), torch.tensor(1.0, device="cuda"), vocab, 15.0)
+    g = g.float().cpu()[:, :vocab]
+    assert torch.isnan(g[bad]).all()
+    assert torch.isfinite(g[~bad]).all()
+    assert math.isnan(softcap_cross_entropy(xd, td, vocab, 15.0, -1).item())
 
 
 def test_softcap_ce_deterministic_and_scaled_gradient():
