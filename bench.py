@@ -47,6 +47,9 @@ STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_d
           "bwd_dense_decay": 14, "bwd_fused": None}
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+# the backward's compulsory HBM I/O at config 2 (q, k, v, dO, g, beta and the output in;
+# dq, dk, dv, dg, dbeta out), the secondary bytes figure of the dominant kernel
+BWD_COMPULSORY_BYTES = 56_700_000
 
 
 def parse():
@@ -58,6 +61,8 @@ def parse():
     ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
     ap.add_argument("--hbm-sweep", action="store_true",
                     help="print the HBM-peak fraction of conv / norm-gate / copy over batch sizes and exit")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="print the bf16 MFMA rate kda_mfma_probe sustains on this device and exit")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run each kernel once (plus a 64 MiB calibration copy) for rocprofv3 --pmc; no timing")
     ap.add_argument("--cpu-sample-len", type=int, default=1024,
@@ -157,6 +162,45 @@ def kernel_times(torch, t, do, gate, reps=20):
         torch.cuda.synchronize()
         res[name] = s.elapsed_time(e) / reps
     return res
+
+
+def mfma_probe(torch, shape=0, iters=20000, per_cu=8):
+    """bf16 MFMA rate that kda_mfma_probe sustains (shape 0: 16x16x32, the chunk kernels'
+    shape; 1: 32x32x16), best of three launches timed between HIP events on the launch
+    stream, with the sustained shader clock and cycles per MFMA from workgroup 0's counters."""
+    from experiment_swa_kda_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs = per_cu * cus
+    sink = torch.zeros(wgs + 2, device=dev)
+    flop = ctypes.c_double()
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        _lib.check(lib.kda_mfma_probe(shape, wgs, iters, sink.data_ptr(), ctypes.byref(flop), stream.cuda_stream),
+                   "kda_mfma_probe")
+    best = 0.0
+    for _ in range(3):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        lib.kda_mfma_probe(shape, wgs, iters, sink.data_ptr(), ctypes.byref(flop), stream.cuda_stream)
+        end.record(stream)
+        end.synchronize()
+        best = max(best, flop.value / (start.elapsed_time(end) * 1e-3) / 1e12)
+    cyc, ticks = sink[:2].tolist()
+    clock_ghz = cyc / ticks * 0.1 if ticks > 0 else None
+    return {"tflops": round(best, 1), "shape": "16x16x32" if shape == 0 else "32x32x16",
+            "workgroups": wgs, "waves_per_simd": per_cu,
+            "wg0_clock_ghz": None if clock_ghz is None else round(clock_ghz, 3)}
+
+
+def mfma_peak_measured(torch):
+    """The measured bf16 MFMA peak (TFLOP/s): the larger of the two probe shapes' rates
+    (32x32x16 sustains more than 16x16x32, the chunk kernels' shape), so the fraction
+    against it is the conservative one; both rates are returned."""
+    r = {s: mfma_probe(torch, s, per_cu=4)["tflops"] for s in (0, 1)}
+    return max(r.values()), r
 
 
 def train_throughput(torch, updates=5, warmup=2, accum=4, seed=42, graphed=True):
@@ -267,10 +311,17 @@ def hbm_kernels(torch):
     g = torch.Generator(device="cuda").manual_seed(42)
     out = {}
 
-    def rec(name, us, nbytes):
+    def rec(name, us, nbytes, n_copy=50):
         gbs = nbytes / (us * 1e-6) / 1e9
+        # a plain device copy moving the same bytes (half read, half written), timed the same way
+        src = torch.empty(nbytes // 2 // 16 * 16, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        cus = graph_time_us(torch, lambda: dst.copy_(src), n=n_copy)
+        copy_gbs = 2 * src.numel() / (cus * 1e-6) / 1e9
         out[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_per_s": round(gbs, 1),
-                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     "copy_same_bytes_frac_hbm_peak": round(copy_gbs / PEAK_HBM_GBS, 4),
+                     "ratio_to_copy": round(gbs / copy_gbs, 3)}
 
     B, T, C, W = 2, 4096, 384, 4
     x = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
@@ -278,6 +329,16 @@ def hbm_kernels(torch):
     dy = torch.randn(B, T, C, device="cuda", generator=g).bfloat16()
     rec("conv_fwd", graph_time_us(torch, lambda: ops.causal_conv_forward(x, w, None, False)), 2 * x.numel() * 2)
     rec("conv_bwd", graph_time_us(torch, lambda: ops.causal_conv_backward(x, w, None, dy, None)), 3 * x.numel() * 2)
+    # the trainer's launch: the three projections' 1,152 channels read in place from the
+    # packed projection output (row stride 2312 columns) and dx written back into its columns
+    ld = 2312
+    packed = torch.randn(B, T, ld, device="cuda", generator=g).bfloat16()
+    w3 = torch.randn(3 * C, W, device="cuda", generator=g).bfloat16()
+    dy3 = torch.randn(B, T, 3 * C, device="cuda", generator=g).bfloat16()
+    dxp = torch.zeros_like(packed)
+    xs, dxs = packed[..., :3 * C], dxp[..., :3 * C]
+    rec("conv_bwd_trainer_3proj", graph_time_us(
+        torch, lambda: ops.causal_conv_backward(xs, w3, None, dy3, None, dx_out=dxs)), 3 * B * T * 3 * C * 2)
     o = torch.randn(B, T, 3, 128, device="cuda", generator=g).bfloat16()
     gt = torch.randn(B, T, 3, 128, device="cuda", generator=g).bfloat16()
     nw = torch.ones(128, device="cuda")
@@ -408,6 +469,12 @@ def main():
     if args.pmc_workload:
         pmc_workload(torch)
         return
+    if args.mfma_probe:
+        for shape in (0, 1):
+            for per_cu in (4, 8):
+                print(json.dumps(dict(mfma_probe(torch, shape, per_cu=per_cu),
+                                      peak_published_tflops=PEAK_BF16_TFLOPS)), flush=True)
+        return
     if args.hbm_sweep:
         hbm_sweep(torch)
         return
@@ -443,25 +510,22 @@ def main():
     dom = max(STEP_KERNELS, key=kt.get)  # the largest per-step kernel
     achieved = tiles * KERNEL_FLOP_PER_TILE[dom] / (kt[dom] * 1e-3) / 1e12
     busy = load_mfma_busy()
-    # the bound comes from the counters: HBM bytes moved per second (FETCH + WRITE of the
-    # committed --pmc summary over the live kernel time) against the MFMA-busy fraction
+    # The chunk kernels are priced on the bf16 MFMA roofline: algorithmic FLOPs of the
+    # kernel's products over its live time, against the published dense peak and against
+    # the rate an MFMA-only probe sustains on this device.  The HBM side (copy-calibrated
+    # FETCH + WRITE bytes of the committed --pmc summary over the live time) and the
+    # MFMA-busy counter are reported beside it.
+    peak_meas, peak_shapes = mfma_peak_measured(torch)
     hbm_frac = traffic[dom] / (kt[dom] * 1e-3) / 1e9 / PEAK_HBM_GBS if dom in traffic else None
-    mfma_frac = busy.get(dom, achieved / PEAK_BF16_TFLOPS)
-    if hbm_frac is not None and hbm_frac > mfma_frac:
-        # algorithmic bytes: the backward's compulsory I/O (q, k, v, dO, g, beta in; dq, dk,
-        # dv, dg, dbeta out) -- everything the VJP kernel moves beyond this is re-reads
-        elems = B * T * H
-        alg = elems * (K * 2 + K * 2 + V * 2 + V * 2 + K * 4 + 2) + elems * (K * 2 + K * 2 + V * 2 + K * 4 + 2)
-        gbs = alg / (kt[dom] * 1e-3) / 1e9
-        roofline = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": traffic[dom],
-                    "algorithmic_bytes": alg, "measured_hbm_frac": round(hbm_frac, 4),
-                    "mfma": {"achieved_tflops": round(achieved, 3), "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
-                             "busy_frac": busy.get(dom)}}
-    else:
-        roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom),
-                    "busy_frac": busy.get(dom), "measured_hbm_frac": None if hbm_frac is None else round(hbm_frac, 4)}
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 5), "traffic": traffic.get(dom),
+                "flop_per_launch": tiles * KERNEL_FLOP_PER_TILE[dom], "kernel_ms": round(kt[dom], 5),
+                "peak_measured": round(peak_meas, 1),
+                "peak_measured_by_shape": {"16x16x32": peak_shapes[0], "32x32x16": peak_shapes[1]},
+                "frac_of_measured_peak": round(achieved / peak_meas, 5),
+                "busy_frac": busy.get(dom),
+                "measured_hbm_frac": None if hbm_frac is None else round(hbm_frac, 4),
+                "compulsory_bytes": BWD_COMPULSORY_BYTES if dom == "bwd_fused" else None}
     if dom == "bwd_fused":
         roofline["launches"] = "one kda_chunk_backward call: chunk_bwd_sched_kernel (~2 us) + chunk_bwd_fused_kernel"
     line = {

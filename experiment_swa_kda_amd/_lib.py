@@ -85,6 +85,7 @@ SIGNATURES = {
     "kda_rms_norm_backward_add": (ctypes.c_int, [_L, _I, _P, _P, _P, _P, _P, _P]),
     "kda_relu2_backward": (ctypes.c_int, [_L, _P, _P, _P, _P]),
     "kda_softcap_cross_entropy_mean": (ctypes.c_int, [_L, _P, _P, _L, _P, _P, _P]),
+    "kda_mfma_probe": (ctypes.c_int, [_I, _I, _I, _P, ctypes.POINTER(ctypes.c_double), _P]),
     "kda_embedding_backward": (ctypes.c_int, [_L, _I, _I, _P, _P, _P, _P]),
 }
 

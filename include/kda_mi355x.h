@@ -417,6 +417,17 @@ int kda_relu2_backward(int64_t n, const void* x, const void* grad, void* dx, hip
 int kda_embedding_backward(int64_t n_tokens, int32_t vocab, int32_t dim, const int64_t* idx,
                            const void* grad_output, void* grad_weight, hipStream_t stream);
 
+/*
+ * Measurement only (no counterpart in the reference): launches `workgroups` workgroups of
+ * four waves; each wave runs `iters` rounds of 8 x 16,384 FLOP of bf16 MFMAs in independent
+ * chains with no memory traffic (shape 0: v_mfma_f32_16x16x32_bf16, 8 chains; shape 1:
+ * v_mfma_f32_32x32x16_bf16, 4 chains) and *flop receives the launch's FLOP count.  sink:
+ * >= workgroups + 2 floats; sink[0] and sink[1] receive workgroup 0's shader-clock cycles and
+ * 100 MHz wall-clock ticks over its loop.  bench.py times it between HIP events to obtain the
+ * bf16 MFMA rate the device sustains.
+ */
+int kda_mfma_probe(int32_t shape, int32_t workgroups, int32_t iters, float* sink, double* flop, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
