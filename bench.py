@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
     ap.add_argument("--hbm-sweep", action="store_true",
                     help="print the HBM-peak fraction of conv / norm-gate / copy over batch sizes and exit")
+    ap.add_argument("--hbm-kernels", action="store_true",
+                    help="print only the conv / norm-gate / decode HBM figures and exit")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="print the bf16 MFMA rate kda_mfma_probe sustains on this device and exit")
     ap.add_argument("--pmc-workload", action="store_true",
@@ -468,6 +470,9 @@ def main():
 
     if args.pmc_workload:
         pmc_workload(torch)
+        return
+    if args.hbm_kernels:
+        print(json.dumps(hbm_kernels(torch)), flush=True)
         return
     if args.mfma_probe:
         for shape in (0, 1):

@@ -122,10 +122,11 @@ __global__ __launch_bounds__(256) void conv_fwd_kernel(FwdGeom g, const bf16* __
   if (P.cg >= g.CG || P.t0 >= g.T) return;
   constexpr int kTok = FwdGeom::kTok;
   constexpr int NX = kTok + W - 1;  // xp[t0 .. t0 + kTok + W - 2]
-  bf16x8 xr[NX];
-  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, g.ldx, P.c0, P.t0, xr);
+  // the taps first: every token's arithmetic needs them, and loads complete in order
   float wt[8][W];
   load_taps<W>(w, P.c0, wt);
+  bf16x8 xr[NX];
+  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, g.ldx, P.c0, P.t0, xr);
   bf16* yb = y + ((size_t)P.b * g.T + P.t0) * g.C + P.c0;
 #pragma unroll
   for (int u = 0; u < kTok; ++u) {
@@ -198,7 +199,9 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
     for (int j = 0; j < W; ++j) dwacc[e][j] = 0.f;
   float wt[8][W];
   if (active) {
+    // the taps first (loads complete in order and every token needs them); then
     // dpre[s] for s = s0 .. s0+kTok-1 needs xp[s .. s+W-1], i.e. xp[s0 .. s0+kTok+W-2]
+    load_taps<W>(w, c0, wt);
     constexpr int NX = kTok + W - 1;
     bf16x8 xr[NX], gr[kTok];
     load_xp_rows<W, NX>(x, st, b, g.T, g.C, g.ldx, c0, s0, xr);
@@ -208,7 +211,6 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
       const int sc = s0 + u < g.T ? s0 + u : g.T - 1;
       gr[u] = *reinterpret_cast<const bf16x8*>(dyb + (size_t)sc * g.C);
     }
-    load_taps<W>(w, c0, wt);
 #pragma unroll
     for (int u = 0; u < kTok; ++u) {
       const bool live = s0 + u < g.T;

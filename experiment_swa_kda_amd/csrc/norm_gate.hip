@@ -3,9 +3,9 @@
 // nanochat/mixers/kda.py:46-59 (F.rms_norm(x, weight) * sigmoid(gate)).
 //
 // HBM-bound.  D/8 lanes own one row (one 16-byte bf16x8 vector each); a thread handles
-// kRows rows spaced one row-pass apart, so every load instruction of a wave is coalesced
+// a few rows (kRowsFwd, kRowsBwd) spaced one row-pass apart, so every load instruction of a wave is coalesced
 // and all of a thread's loads are issued before any is consumed.  A workgroup owns a
-// contiguous block of 256 / (D/8) * kRows rows; reductions over a row are in-wave
+// contiguous block of 256 / (D/8) rows per row pass; reductions over a row are in-wave
 // shuffles.  The per-workgroup weight-gradient partials are summed in a fixed order
 // (deterministic).  Arithmetic is f32 with one rounding to bf16 at the store.
 #include "kda_device.hpp"
@@ -13,7 +13,17 @@
 
 namespace kda {
 
-constexpr int kRows = 4;  // rows per thread
+// Rows per thread.  Forward: 3 gives 48 rows per workgroup at D = 128, i.e. 512 workgroups
+// (two per CU, evenly) for the 24,576 rows of B2 T4096 H3 (4 left half the CUs with one more
+// workgroup than the rest).  Backward: 6, one workgroup per CU, and half the weight-gradient
+// partials for the reduction launch (measured: 9.5 us against 10.0 with 3 and 10.3 with 4).
+#ifndef KDA_NORM_ROWS_FWD
+#define KDA_NORM_ROWS_FWD 3
+#endif
+#ifndef KDA_NORM_ROWS_BWD
+#define KDA_NORM_ROWS_BWD 6
+#endif
+constexpr int kRowsFwd = KDA_NORM_ROWS_FWD, kRowsBwd = KDA_NORM_ROWS_BWD;
 
 template <int D>
 __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf16* __restrict__ x,
@@ -25,19 +35,20 @@ __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf1
   constexpr int RPP = 256 / LPR;  // rows per pass of the workgroup
   const int lane = threadIdx.x % LPR;
   const int c0 = lane * 8;
-  const long r0 = (long)blockIdx.x * RPP * kRows + threadIdx.x / LPR;
-  bf16x8 xr[kRows], gr[kRows];
+  const long r0 = (long)blockIdx.x * RPP * kRowsFwd + threadIdx.x / LPR;
+  // the weight first: loads complete in order, and every row's arithmetic needs it
+  float w[8];
+  load8f(weight + c0, w);
+  bf16x8 xr[kRowsFwd], gr[kRowsFwd];
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+  for (int i = 0; i < kRowsFwd; ++i) {
     long r = r0 + (long)i * RPP;
     r = r < rows ? r : rows - 1;
     xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
     gr[i] = *reinterpret_cast<const bf16x8*>(gate + r * D + c0);
   }
-  float w[8];
-  load8f(weight + c0, w);
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+  for (int i = 0; i < kRowsFwd; ++i) {
     const long r = r0 + (long)i * RPP;
     float ss = 0.f;
 #pragma unroll
@@ -61,49 +72,64 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     const bf16* __restrict__ dy, bf16* __restrict__ dx, bf16* __restrict__ dgate, long dgld,
     float* __restrict__ dw_part) {
   // row r = (token r / heads, head r % heads); gate and dgate rows of a token are gld / dgld
-  // elements apart (heads = 1, gld = dgld = D for dense [rows, D])
-  auto goff = [&](long r, long ld) { return (r / heads) * ld + (r % heads) * D; };
+  // elements apart (heads = 1, gld = dgld = D for dense [rows, D]).  32-bit division by the
+  // uniform head count (rows < 2^31): a 64-bit division expands to a long branchy sequence
+  // per row that sat between the row loads.
+  auto goff = [&](long r, long ld) {
+    const unsigned tok = (unsigned)r / (unsigned)heads;
+    return (long)tok * ld + (long)((unsigned)r - tok * (unsigned)heads) * D;
+  };
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   __shared__ float s_dw[256 / kWave][D];
   const int lane = threadIdx.x % LPR;
   const int c0 = lane * 8;
-  const long r0 = (long)blockIdx.x * RPP * kRows + threadIdx.x / LPR;
-  bf16x8 xr[kRows], gr[kRows], dr[kRows];
-  float ir[kRows];
+  const long r0 = (long)blockIdx.x * RPP * kRowsBwd + threadIdx.x / LPR;
+  // the weight and the rows' 1/rms first (loads complete in order; row i's arithmetic
+  // then waits only for its own three vectors)
+  float w[8], dwacc[8];
+  load8f(weight + c0, w);
+  float ir[kRowsBwd];
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+  for (int i = 0; i < kRowsBwd; ++i) {
+    const long r = r0 + (long)i * RPP;
+    ir[i] = inv_rms[r < rows ? r : rows - 1];
+  }
+  bf16x8 xr[kRowsBwd], gr[kRowsBwd], dr[kRowsBwd];
+#pragma unroll
+  for (int i = 0; i < kRowsBwd; ++i) {
     long r = r0 + (long)i * RPP;
     r = r < rows ? r : rows - 1;
     xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
     gr[i] = *reinterpret_cast<const bf16x8*>(gate + goff(r, gld) + c0);
     dr[i] = *reinterpret_cast<const bf16x8*>(dy + r * D + c0);
-    ir[i] = inv_rms[r];
   }
-  float w[8], dwacc[8];
-  load8f(weight + c0, w);
 #pragma unroll
   for (int e = 0; e < 8; ++e) dwacc[e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+  for (int i = 0; i < kRowsBwd; ++i) {
     const long r = r0 + (long)i * RPP;
     const bool live = r < rows;
     const float inv = ir[i];
+    // with gs = dy s, dn = gs w, t = dn n:  dgate = t (1 - s),  dw += gs n,
+    // dx = inv (dn - n mean(t))
     float dn[8], n[8], o[8], og[8];
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float g = live ? (float)dr[i][e] : 0.f;
       const float s = sigmoid_fast((float)gr[i][e]);
+      const float gs = g * s;
       n[e] = (float)xr[i][e] * inv;
-      dn[e] = g * s * w[e];
-      dot = fmaf(dn[e], n[e], dot);
-      og[e] = g * n[e] * w[e] * s * (1.f - s);
-      dwacc[e] = fmaf(g * s, n[e], dwacc[e]);
+      dn[e] = gs * w[e];
+      const float t = dn[e] * n[e];
+      dot += t;
+      og[e] = fmaf(-t, s, t);
+      dwacc[e] = fmaf(gs, n[e], dwacc[e]);
     }
-    dot = group_sum<LPR>(dot) / D;
+    dot = group_sum<LPR>(dot) * (1.0f / D);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = inv * (dn[e] - n[e] * dot);
+    for (int e = 0; e < 8; ++e) o[e] = inv * fmaf(-n[e], dot, dn[e]);
     if (live) {
       store8(dx + r * D + c0, o);
       store8(dgate + goff(r, dgld) + c0, og);
@@ -127,8 +153,8 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
   }
 }
 
-static int norm_blocks(long rows, int dim) {
-  const long rpb = 256 / (dim / 8) * kRows;
+static int norm_blocks(long rows, int dim, int rows_per_thread) {
+  const long rpb = 256 / (dim / 8) * rows_per_thread;
   long nb = (rows + rpb - 1) / rpb;
   if (nb < 1) nb = 1;
   return (int)nb;
@@ -148,7 +174,7 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
   KDA_REQUIRE(aligned16(x, gate, weight, output),
               "rmsnorm_gate_forward: x, gate, weight and output must be 16-byte aligned");
   if (rows == 0) return KDA_OK;
-  const int nb = norm_blocks(rows, dim);
+  const int nb = norm_blocks(rows, dim, kRowsFwd);
   if (dim == 128)
     hipLaunchKernelGGL(norm_gate_fwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows,
                        (const bf16*)x, (const bf16*)gate, weight, eps, (bf16*)output, inv_rms);
@@ -160,7 +186,7 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
 }
 
 extern "C" size_t kda_rmsnorm_gate_backward_scratch_bytes(int64_t rows, int32_t dim) {
-  return kda::align256((size_t)kda::norm_blocks(rows, dim) * dim * sizeof(float)) + 256;
+  return kda::align256((size_t)kda::norm_blocks(rows, dim, kda::kRowsBwd) * dim * sizeof(float)) + 256;
 }
 
 extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int32_t heads, const void* x,
@@ -171,7 +197,7 @@ extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int3
                                                  hipStream_t stream) {
   using namespace kda;
   (void)eps;
-  KDA_REQUIRE(rows >= 0, "rmsnorm_gate_backward: invalid rows");
+  KDA_REQUIRE(rows >= 0 && rows < (1LL << 31), "rmsnorm_gate_backward: rows must be in [0, 2^31)");
   KDA_REQUIRE(dim == 64 || dim == 128, "rmsnorm_gate_backward: dim must be 64 or 128");
   KDA_REQUIRE(heads >= 1 && rows % heads == 0, "rmsnorm_gate_backward: rows must be a multiple of heads >= 1");
   KDA_REQUIRE(gate_row_stride >= (int64_t)heads * dim && gate_row_stride % 8 == 0 &&
@@ -182,7 +208,7 @@ extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int3
               "rmsnorm_gate_backward: null pointer");
   KDA_REQUIRE(aligned16(x, gate, weight, grad_output, dx, dgate, scratch),
               "rmsnorm_gate_backward: x, gate, weight, grad_output, dx, dgate and scratch must be 16-byte aligned");
-  const int nb = norm_blocks(rows, dim);
+  const int nb = norm_blocks(rows, dim, kRowsBwd);
   float* part = (float*)scratch;
   if (rows > 0) {
     if (dim == 128)
