@@ -71,47 +71,179 @@ struct BwdArgs {
 };
 
 // ---------------------------------------------------------------------------
-// reverse state-gradient scan
+// reverse state-gradient scan (transition form)
 // ---------------------------------------------------------------------------
+// With X_c = dL/dS at the end of chunk c (X_{n-1} = the final-state gradient),
+//   dDelta_c = A^T dO + Kd X_c,   X_{c-1} = lam o X_c + Qg^T dO - W^T dDelta_c
+//            = lam o X_c - G_c X_c + E_c,   G_c = W_c^T Kd_c,  E_c = Qg_c^T dO - W_c^T (A_c^T dO),
+// and X_{-1} is the initial-state gradient.  G and E need nothing from the recurrence, so a
+// chunk-parallel kernel forms them first (chunk_bwd_prep_kernel); the sequential scan then
+// streams per chunk only -G (K x K bf16), its strip of E (K x 16 f32) and lam, and its chain
+// is one K/32-deep MFMA product with one barrier per chunk.  dDelta_c is formed by the VJP
+// tile of chunk c from X_c (dense_tile).
+//
+// Prep: one workgroup (four waves) per tile.  -G is emitted as permuted A fragments straight
+// from the accumulators of -G^T = Kd^T (-W) (the accumulator tiles 2s and 2s + 1 of column
+// block b give a lane exactly the 8 contraction values of fragment (b, s)); E in the scan's
+// accumulator order [strip][key tile][lane][4].
+constexpr int kPrepThreads = 256;
+
+template <int K, int V>
+struct PrepLds {
+  static constexpr int OP = V + 8, KP = K + 8;  // row pitches (bf16), 16-byte aligned rows
+  static constexpr int off_do = 0;                       // dO [64][OP], rows >= len zero
+  static constexpr int off_ado = off_do + 64 * OP * 2;   // bf16(A^T dO) [64][OP]
+  static constexpr int off_kd = off_ado + 64 * OP * 2;   // Kd [64][KP]
+  static constexpr int off_w = off_kd + 64 * KP * 2;     // -W [64][KP]
+  static constexpr int bytes = off_w + 64 * KP * 2;
+};
+
+template <int K, int V>
+__global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a) {
+  using L = PrepLds<K, V>;
+  constexpr int OP = L::OP, KP = L::KP, KB = K / 16, VB = V / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* sDO = (bf16*)(smem + L::off_do);
+  bf16* sADO = (bf16*)(smem + L::off_ado);
+  bf16* sKd = (bf16*)(smem + L::off_kd);
+  bf16* sW = (bf16*)(smem + L::off_w);
+  const int cidx = blockIdx.x, h = blockIdx.y, H = a.H;
+  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  const int len = ch.y, row0 = ch.x;
+  if (len <= 0) return;
+  const size_t tile = (size_t)cidx * H + h;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lr = lane % 16, kg = lane / 16;
+  const bf16* KDF = (const bf16*)a.ws.p[R_KDF] + tile * 64 * K;
+  const bf16* WF = (const bf16*)a.ws.p[R_WF] + tile * 64 * K;
+  // ---- every global load first: dO rows, Kd and -W fragments (4 x 16 bytes per thread
+  // each at K = V = 128), this wave's A^T, Qg^T and W^T fragments ----
+  constexpr int NDO = 64 * V / 8 / kPrepThreads, NKF = 64 * K / 8 / kPrepThreads;
+  bf16x8 xo[NDO], xk[NKF], xw[NKF];
+#pragma unroll
+  for (int q = 0; q < NDO; ++q) {
+    const int idx = q * kPrepThreads + tid, t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
+    xo[q] = *(const bf16x8*)(a.dout + ((size_t)(row0 + (t < len ? t : len - 1)) * H + h) * V + c0);
+  }
+#pragma unroll
+  for (int q = 0; q < NKF; ++q) {
+    xk[q] = *(const bf16x8*)(KDF + (size_t)(q * kPrepThreads + tid) * 8);
+    xw[q] = *(const bf16x8*)(WF + (size_t)(q * kPrepThreads + tid) * 8);
+  }
+  bf16x8 atf[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    atf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64 + frag_off(64, wave, s, lane));
+  // ---- stage dO (rows past the chunk zero), Kd and -W as row-major [t][k] ----
+#pragma unroll
+  for (int q = 0; q < NDO; ++q) {
+    const int idx = q * kPrepThreads + tid, t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
+    bf16x8 x = xo[q];
+    if (t >= len) x = bf16x8{};
+    *(bf16x8*)(sDO + t * OP + c0) = x;
+  }
+#pragma unroll
+  for (int q = 0; q < NKF; ++q) {
+    // natural fragment piece idx: row 16 rt + l % 16, columns 32 s + 8 (l / 16) ..
+    const int idx = q * kPrepThreads + tid, l = idx % 64, fs = (idx / 64) % (K / 32), rt = idx / (64 * (K / 32));
+    const int r = 16 * rt + l % 16, g = l / 16;
+    *(bf16x8*)(sKd + r * KP + 32 * fs + 8 * g) = xk[q];
+    // -W is stored permuted: element e is column 32 s + 16 (e / 4) + 4 (l / 16) + e % 4
+    bf16x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = xw[q][e];
+      hi[e] = xw[q][4 + e];
+    }
+    *(bf16x4*)(sW + r * KP + 32 * fs + 4 * g) = lo;
+    *(bf16x4*)(sW + r * KP + 32 * fs + 16 + 4 * g) = hi;
+  }
+  __syncthreads();
+  // ---- A^T dO: wave w owns row tile w (tokens 16 w ..), every column tile ----
+#pragma unroll
+  for (int ct = 0; ct < VB; ++ct) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) acc = mfma16(atf[s], lds_col_frag(sDO, OP, 32 * s, 16 * ct, lane), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sADO[(16 * wave + 4 * kg + r) * OP + 16 * ct + lr] = to_bf16(acc[r]);
+  }
+  // ---- -G fragments: fragment (b, s) packs the accumulator tiles (2s, b), (2s+1, b) of
+  // -G^T = Kd^T (-W); wave w owns fragment rows b = w, w + 4, ... ----
+  bf16* NG = (bf16*)a.sc.p[S_NG] + tile * K * K;
+  for (int b = wave; b < KB; b += 4) {
+    bf16x8 wb[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) wb[s] = lds_col_frag(sW, KP, 32 * s, 16 * b, lane);
+#pragma unroll
+    for (int fs = 0; fs < K / 32; ++fs) {
+      f32x4 lo = zero4(), hi = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        lo = mfma16(lds_col_frag(sKd, KP, 32 * s, 16 * (2 * fs), lane), wb[s], lo);
+        hi = mfma16(lds_col_frag(sKd, KP, 32 * s, 16 * (2 * fs + 1), lane), wb[s], hi);
+      }
+      bf16x8 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = to_bf16(lo[r]);
+        x[4 + r] = to_bf16(hi[r]);
+      }
+      *(bf16x8*)(NG + frag_off(K, b, fs, lane)) = x;
+    }
+  }
+  __syncthreads();  // A^T dO staged
+  // ---- E = Qg^T dO - W^T bf16(A^T dO): wave w owns key tiles w, w + 4, ... ----
+  float* E = (float*)a.sc.p[S_E] + tile * K * V;
+  for (int kt = wave; kt < KB; kt += 4) {
+    bf16x8 qf[2], wf[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      qf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64 + frag_off(64, kt, s, lane));
+      wf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64 + frag_off(64, kt, s, lane));
+    }
+#pragma unroll
+    for (int ct = 0; ct < VB; ++ct) {
+      f32x4 pq = zero4(), pw = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        pq = mfma16(qf[s], lds_col_frag(sDO, OP, 32 * s, 16 * ct, lane), pq);
+        pw = mfma16(wf[s], lds_col_frag(sADO, OP, 32 * s, 16 * ct, lane), pw);
+      }
+      *(f32x4*)(E + (((size_t)ct * KB + kt) * 64 + lane) * 4) = pq - pw;
+    }
+  }
+}
+
 // One workgroup per (sequence, head, 16-wide V strip) walks the chunks backwards: four
-// compute waves (wave w owns the dDelta row tile w and the dS tiles w K/64 .., as MFMA
-// accumulators) and two loader waves.  The loaders stream each chunk's A^T, Kd, Qg^T and W^T
-// fragments, lam and the dO strip into a kBwdRing-deep LDS ring with direct global->LDS
-// loads, so the compute waves' instruction streams hold no global loads (issuing ~70 KB of
-// loads per chunk from the compute waves themselves serialised with the chain).  Per chunk
-// the six waves meet at two barriers: S1 (dS' published, slot complete) and S2 (dDelta
-// published).  A slot's A^T, Kd, Qg^T and dO are last read before S2 and are refilled (for
-// the chunk two steps on) right after it; its W^T and lam are last read before the next S1
-// and are refilled after that.
-constexpr int kBwdRing = 2;
+// compute waves (wave w owns the X tiles w K/64 .., as MFMA accumulators), a loader wave
+// that streams each chunk's -G fragments, E strip and lam into a kBwdRing-deep LDS ring with
+// direct global->LDS loads (two chunks ahead), and a history wave that copies X_c out of
+// LDS to the strip-major history and, in the fused launch, publishes the step.  Per chunk
+// the waves meet at one barrier S(r): X_c staged (bf16 B operand in the permuted contraction
+// order -G was emitted in, f32 in accumulator order for the history), slot r loaded.
+constexpr int kBwdRing = 3;
 constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 constexpr int kBwdThreads = 6 * kWave;
 
 template <int K, int V>
 struct BwdScanLds {
-  static constexpr int off_at = 0;                        // A^T fragments, 64 x 64 bf16
-  static constexpr int off_kd = off_at + 64 * 64 * 2;     // Kd fragments, 64 x K bf16
-  static constexpr int off_qgt = off_kd + 64 * K * 2;     // Qg^T fragments, K x 64 bf16
-  static constexpr int off_wt = off_qgt + K * 64 * 2;     // W^T fragments, K x 64 bf16
-  static constexpr int off_lam = off_wt + K * 64 * 2;     // lam, K f32
-  static constexpr int off_do = off_lam + K * 4;          // dO strip [64 t][16 v] bf16 (rows >= len undefined)
-  static constexpr int slot = off_do + 64 * 16 * 2;
-  static constexpr int n_load0 = (64 * 64 * 2 + 2 * 64 * K * 2) / 1024 + 2;  // A^T, Kd, Qg^T, dO
-  static constexpr int n_load1 = (K * 64 * 2) / 1024 + 1;                    // W^T, lam
-  static constexpr int SP = K + 8, DP = 64 + 8;
-  static constexpr int off_ds = kBwdRing * slot;           // dS' as [v][k] bf16
-  static constexpr int off_dsf = off_ds + 16 * SP * 2;     // f32 dS' in accumulator order [K/16][64][4]
-  static constexpr int off_dd = off_dsf + K * 16 * 4;      // dDelta strip as [v][t] bf16
-  static constexpr int bytes = off_dd + 16 * DP * 2;
-  static_assert(n_load0 < 64 && n_load1 < 64, "vmcnt range");
+  static constexpr int off_g = 0;                         // -G fragments, K x K bf16
+  static constexpr int off_e = off_g + K * K * 2;         // E strip [K/16][64][4] f32
+  static constexpr int off_lam = off_e + K * 16 * 4;      // lam, K f32
+  static constexpr int slot = off_lam + K * 4;
+  static constexpr int n_load = (K * K * 2 + K * 16 * 4) / 1024 + 1;
+  static constexpr int SP = K + 8;
+  static constexpr int off_ds = kBwdRing * slot;          // X_c bf16 [v][k] (x2, by step parity)
+  static constexpr int off_dsf = off_ds + 2 * 16 * SP * 2;  // X_c f32 in accumulator order [K/16][64][4] (x2)
+  static constexpr int bytes = off_dsf + 2 * K * 16 * 4;
+  static_assert(n_load < 64, "vmcnt range");
 };
 
 // The scan's per-chunk operands.  Workgroups of the scan launch past the scan's own touch
 // one word of every 128-byte line of them while the scan runs on its few CUs, so the scan's
-// latency-bound loads find their lines in the caches (the forward wrote them long before
-// the backward in training).  Loads only: the results are folded into a value that is never
-// stored.  (Warming the dense/decay inputs as well measured slower, cold and warm: the extra
-// requests delay the scan's own.)
+// latency-bound loads find their lines in the caches.  Loads only: the results are folded
+// into a value that is never stored.
 constexpr int kMaxPrefetch = 20;
 struct PrefetchList {
   const char* p[kMaxPrefetch];
@@ -164,18 +296,14 @@ __device__ __forceinline__ void publish_step(int* sync, int nrec, int rec, size_
 
 // The scan of one (sequence, head, V strip), run by the first six waves of the workgroup.
 // PUB: the workgroup is a scan member of the fused backward launch -- waves past the six
-// only mirror the barriers, and after each step's histories (dS' and dDelta of chunk c) are
-// stored, progress[rec][strip] is raised by one: r + 1 means the strip has finished the
-// r + 1 last chunks of the sequence.
+// only mirror the barriers (waves 6 and 7 pull operands into L2 ahead of the ring), and
+// after each step's history (X_c) is stored, progress[rec][strip] is raised by one: r + 1
+// means the strip has finished the r + 1 last chunks of the sequence.
 template <int K, int V, bool PUB>
 __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   using L = BwdScanLds<K, V>;
-  constexpr int KT = K / 16 / 4;
-  constexpr int SP = L::SP, DP = L::DP, OP = 16;
+  constexpr int KT = K / 16 / 4, NB = K / 32, SP = L::SP;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* sDS = (bf16*)(smem + L::off_ds);
-  float* sDSf = (float*)(smem + L::off_dsf);
-  bf16* sDD = (bf16*)(smem + L::off_dd);
   const int H = a.H;
   int rec, strip;
   if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
@@ -183,255 +311,174 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
-  const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
-
-  // Chunks of one sequence are consecutive 64-token blocks: chunk ci starts at
-  // seq_row0 + 64 ci, so no per-chunk table read sits in front of the dO load.
   const int n = sq.y;
-  int seq_row0 = 0, seq_end = 0;
-  if (n > 0) {
-    const int4 c_first = chunks[sq.x], c_last = chunks[sq.x + n - 1];
-    seq_row0 = c_first.x;
-    seq_end = c_last.x + c_last.y;
-  }
+  auto tile_of = [&](int r) { return (size_t)(sq.x + max(n - 1 - r, 0)) * H + h; };  // step r's chunk
 
   if (PUB && wave >= 6) {
-    // Waves past the six in the fused launch's scan members: the same barrier count as
-    // the six, and waves 6 and 7 pull the operands of the step kBwdPrefetch ahead into the
-    // XCD's L2 (every strip of a record runs on one XCD and reads the same per-chunk
-    // operands, so each strip takes every eighth 128-byte line): the scan's loads then hit
-    // L2 while the tile workgroups keep HBM busy.  The lines land in a scratch LDS row.
+    // Waves 6 and 7 pull the operands of the step kBwdPrefetch ahead into the XCD's L2: the
+    // shared -G and lam lines split over the record's strips (every strip of a record runs
+    // on one XCD), plus this strip's own E lines.  The lines land in a scratch LDS row.
     if (n <= 0) return;
     const int pl = (wave - 6) * kWave + lane;
     char* sink = smem + L::bytes + (wave & 1) * 1024;
     auto prefetch = [&](int q) {
       if (wave >= 8 || q >= n) return;
-      const int chunk = sq.x + n - 1 - q;
-      const size_t tile = (size_t)chunk * H + h;
-      constexpr int kAt = 64 * 64 * 2 / 128, kKd = 64 * K * 2 / 128, kLam = K * 4 / 128;
-      constexpr int kOps = kAt + 3 * kKd + kLam;  // A^T, Kd, Qg^T, W^T, lam lines
-      const int l = strip + 8 * pl;
+      const size_t tile = tile_of(q);
+      constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * 4 / 128;
+      constexpr int kShared = (kG + kLam + 7) / 8;  // lanes for this strip's share
       const char* src = nullptr;
-      if (l < kAt) src = (const char*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64) + l * 128;
-      else if (l < kAt + kKd) src = (const char*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K) + (l - kAt) * 128;
-      else if (l < kAt + 2 * kKd) src = (const char*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64) + (l - kAt - kKd) * 128;
-      else if (l < kAt + 3 * kKd) src = (const char*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64) + (l - kAt - 2 * kKd) * 128;
-      else if (l < kOps) src = (const char*)((const float*)a.ws.p[R_LAM] + tile * K) + (l - kAt - 3 * kKd) * 128;
-      else if (l < kOps + 2 * 64) {
-        // dO rows of the chunk (each 2 V bytes, in 128-byte lines)
-        const int row0 = seq_row0 + (chunk - sq.x) * 64, len = min(64, seq_end - row0);
-        const int t = (l - kOps) / (V * 2 / 128), part = (l - kOps) % (V * 2 / 128);
-        if (t < len) src = (const char*)(a.dout + ((size_t)(row0 + t) * H + h) * V) + part * 128;
+      if (pl < kShared) {
+        const int l = strip + 8 * pl;
+        if (l < kG) src = (const char*)((const bf16*)a.sc.p[S_NG] + tile * K * K) + l * 128;
+        else if (l < kG + kLam) src = (const char*)((const float*)a.ws.p[R_LAM] + tile * K) + (l - kG) * 128;
+      } else if (pl - kShared < kE) {
+        src = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)strip * K * 16) + (pl - kShared) * 128;
       }
       if (src) dma16(src, sink);
     };
     for (int q = 0; q < kBwdPrefetch; ++q) prefetch(q);
     for (int b = 0; b < n; ++b) {
-      ring_barrier();  // S1(b)
+      ring_barrier();  // S(b)
       prefetch(b + kBwdPrefetch);
-      ring_barrier();  // S2(b)
     }
     ring_barrier();  // final
     wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
     return;
   }
-  if (wave >= 4) {
-    // ---- loader waves: step r's slot holds chunk sq.x + n - 1 - r ----
-    const int lw = wave - 4;
-    auto issue = [&](int r) {
-      const int chunk = sq.x + max(n - 1 - r, 0);  // clamped: fixed load count
-      const size_t tile = (size_t)chunk * H + h;
-      char* slot = smem + (r % kBwdRing) * L::slot;
-      if (lw == 0) {
-        const char* at = (const char*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64) + lane * 16;
-#pragma unroll
-        for (int b = 0; b < (64 * 64 * 2) / 1024; ++b) dma16(at + b * 1024, slot + L::off_at + b * 1024);
-        const char* kd = (const char*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K) + lane * 16;
-#pragma unroll
-        for (int b = 0; b < (64 * K * 2) / 1024; ++b) dma16(kd + b * 1024, slot + L::off_kd + b * 1024);
-        const char* qg = (const char*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64) + lane * 16;
-#pragma unroll
-        for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(qg + b * 1024, slot + L::off_qgt + b * 1024);
-        // dO strip: lane -> token (lane / 2 + 32 i), half lane % 2 of its 16 values; rows past
-        // the chunk end read row 0 of the chunk (masked by the compute waves)
-        const int row0 = seq_row0 + (chunk - sq.x) * 64;
-        const int len = min(64, seq_end - row0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int t = lane / 2 + 32 * i, tr = t < len ? t : 0;
-          dma16(a.dout + ((size_t)(row0 + tr) * H + h) * V + v0 + 8 * (lane % 2), slot + L::off_do + i * 1024);
-        }
-      } else {
-        const char* wt = (const char*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64) + lane * 16;
-#pragma unroll
-        for (int b = 0; b < (K * 64 * 2) / 1024; ++b) dma16(wt + b * 1024, slot + L::off_wt + b * 1024);
-        if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
-      }
-    };
-    if (n <= 0) return;  // an empty sequence: no steps, no barriers, nothing to load
-    if (lw == 0) {
-      issue(0);
-      issue(1);
-      for (int r = 0; r < n; ++r) {
-        wait_vmcnt<L::n_load0>();  // part of slot r complete (step r + 1's loads may be in flight)
-        ring_barrier();            // S1(r)
-        ring_barrier();            // S2(r): slot r's A^T, Kd, Qg^T, dO are consumed
-        issue(r + 2);
-      }
-      if (PUB) ring_barrier();  // final: step n - 1 published
-    } else {
-      issue(0);
-      for (int r = 0; r < n; ++r) {
-        // W^T, lam of slot r complete and the history stores of step r - 1 (step r - 2 in
-        // the fused launch, whose write-through stores may take several microseconds)
-        if (PUB && r > 0)
-          wait_vmcnt<K / 16>();
-        else
-          wait_vmcnt<0>();
-        ring_barrier();   // S1(r): slot r - 1's W^T, lam are consumed
-        if (PUB && r > 1 && lane == 0) {
-          publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)(sq.x + n + 1 - r) * H + h, r - 2);  // step r - 2
-        }
-        issue(r + 1);
-        // f32 dS' history [K][V] of this step: element (k, v) sits in accumulator order at
-        // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4; read before S2 (the compute
-        // waves republish after it), stored after
-        const size_t tile = (size_t)(sq.x + n - 1 - r) * H + h;
-        float4 hv[K / 16];
-#pragma unroll
-        for (int it = 0; it < K / 16; ++it) {
-          const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
-          const float* f = sDSf + ((kk / 16) * 64 + 16 * ((kk % 16) / 4) + c4) * 4 + kk % 4;
-          hv[it] = make_float4(f[0], f[4], f[8], f[12]);
-        }
-        wait_lgkm0();
-        ring_barrier();   // S2(r)
-        // the strip's [K][16] block of the strip-major history: each store instruction
-        // writes 512 contiguous bytes
-        bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile * K * V + (size_t)strip * K * 16;
-#pragma unroll
-        for (int it = 0; it < K / 16; ++it) {
-          const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
-          if (PUB)
-            store8_coherent(DSH, (kk * 16 + c4) * 2, f4_to_bf16x4(hv[it]));
-          else
-            *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = f4_to_bf16x4(hv[it]);
-        }
-      }
-      if (PUB) {
-        wait_vmcnt<0>();  // step n - 1's history stores
-        ring_barrier();   // final: the compute waves' stores of step n - 1 are complete too
-        if (lane == 0) {
-          if (n > 1) publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)(sq.x + 1) * H + h, n - 2);
-          publish_step<V / 16>(progress, a.num_seqs * H, rec, (size_t)sq.x * H + h, n - 1);
-        }
+  if (n <= 0) {
+    // an empty sequence: the initial-state gradient is the final-state gradient
+    if (wave == 0 && a.ds0) {
+      for (int kt = 0; kt < K / 16; ++kt) {
+        const size_t o = (((size_t)seq * H + h) * V + v0 + lr) * K + 16 * kt + 4 * kg;
+        *(float4*)(a.ds0 + o) = a.dsfin ? *(const float4*)(a.dsfin + o) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
+    return;
+  }
+  if (wave == 4) {
+    // ---- loader wave: step r's slot (r % kBwdRing) holds -G, the E strip and lam ----
+    auto issue = [&](int r) {
+      const size_t tile = tile_of(r);  // clamped past the last step: a fixed load count
+      char* slot = smem + (r % kBwdRing) * L::slot;
+      const char* g = (const char*)((const bf16*)a.sc.p[S_NG] + tile * K * K) + lane * 16;
+#pragma unroll
+      for (int b = 0; b < (K * K * 2) / 1024; ++b) dma16(g + b * 1024, slot + L::off_g + b * 1024);
+      const char* e = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)strip * K * 16) + lane * 16;
+#pragma unroll
+      for (int b = 0; b < (K * 16 * 4) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
+      if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
+    };
+    issue(0);
+    issue(1);
+    for (int r = 0; r < n; ++r) {
+      wait_vmcnt<L::n_load>();  // slot r complete (step r + 1's loads may be in flight)
+      ring_barrier();           // S(r): slot r - 1 is consumed
+      issue(r + 2);
+    }
+    if (PUB) ring_barrier();  // final
     wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
     return;
   }
+  if (wave == 5) {
+    // ---- history wave: X_c of step r (f32 staging, accumulator order: element (k, v) at
+    // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4) is read after S(r) and stored as
+    // bf16 into the strip's [K][16] block of the strip-major history, 512 contiguous bytes
+    // per store instruction.  In the fused launch step r - 2 is published once its stores
+    // have completed (write-through stores may take microseconds) ----
+    for (int r = 0; r < n; ++r) {
+      if (PUB && r >= 2) wait_vmcnt<K / 16>();  // step r - 2's stores
+      ring_barrier();  // S(r)
+      if (PUB && r >= 2 && lane == 0)
+        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r - 2), r - 2);
+      const float* dsf = (const float*)(smem + L::off_dsf + (r & 1) * K * 16 * 4);
+      float4 hv[K / 16];
+#pragma unroll
+      for (int it = 0; it < K / 16; ++it) {
+        const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
+        const float* f = dsf + ((kk / 16) * 64 + 16 * ((kk % 16) / 4) + c4) * 4 + kk % 4;
+        hv[it] = make_float4(f[0], f[4], f[8], f[12]);
+      }
+      bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile_of(r) * K * V + (size_t)strip * K * 16;
+#pragma unroll
+      for (int it = 0; it < K / 16; ++it) {
+        const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
+        if (PUB)
+          store8_coherent(DSH, (kk * 16 + c4) * 2, f4_to_bf16x4(hv[it]));
+        else
+          *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = f4_to_bf16x4(hv[it]);
+      }
+    }
+    if (PUB) {
+      wait_vmcnt<0>();
+      if (lane == 0) {
+        if (n > 1) publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(n - 2), n - 2);
+        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(n - 1), n - 1);
+      }
+      ring_barrier();  // final
+    }
+    return;
+  }
 
-  // ---- compute waves ----
-  f32x4 dS[KT];
+  // ---- compute waves: X tiles wave * KT .. (rows 16 kt + 4 (l / 16) + r, column l % 16) ----
+  f32x4 X[KT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
     const int k0 = 16 * (wave * KT + kt) + 4 * kg;
     if (a.dsfin) {
       const float4 s = *(const float4*)(a.dsfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
-      dS[kt][0] = s.x; dS[kt][1] = s.y; dS[kt][2] = s.z; dS[kt][3] = s.w;
+      X[kt][0] = s.x; X[kt][1] = s.y; X[kt][2] = s.z; X[kt][3] = s.w;
     } else {
-      dS[kt] = zero4();
+      X[kt] = zero4();
     }
   }
   for (int r = 0; r < n; ++r) {
-    const int chunk = sq.x + n - 1 - r;
-    const size_t tile = (size_t)chunk * H + h;
-    const int len = min(64, seq_end - (seq_row0 + (chunk - sq.x) * 64));
     const char* slot = smem + (r % kBwdRing) * L::slot;
-    const bf16* sO = (const bf16*)(slot + L::off_do);
-    // (1) publish dS' (bf16 [v][k] operand, f32 [k][v] staging)
+    bf16* sDS = (bf16*)(smem + L::off_ds + (r & 1) * 16 * SP * 2);
+    float* sDSf = (float*)(smem + L::off_dsf + (r & 1) * K * 16 * 4);
+    // stage X_c: bf16 [v][k] (B operand) and f32 accumulator order (history)
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       bf16x4 x;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) x[q] = to_bf16(dS[kt][q]);
+      for (int q = 0; q < 4; ++q) x[q] = to_bf16(X[kt][q]);
       *(bf16x4*)(sDS + lr * SP + k0) = x;
-      *(f32x4*)(sDSf + ((wave * KT + kt) * 64 + lane) * 4) = dS[kt];
+      *(f32x4*)(sDSf + ((wave * KT + kt) * 64 + lane) * 4) = X[kt];
     }
     wait_lgkm0();
-    if (PUB) wait_vmcnt<1>();  // step r - 2's dDelta store (published after this barrier)
-    ring_barrier();  // S1(r)
-    // (3) dDelta rows 16*wave.. = A^T dO + Kd dS', and the dDelta-independent part of
-    // (4), Qg^T dO, while the other waves finish theirs.  dO as B operand (tokens down the
-    // contraction): transposing reads of the [t][v] strip, tokens past the chunk end zeroed
-    bf16x8 oB0 = lds_col_frag(sO, OP, 0, 0, lane), oB1 = lds_col_frag(sO, OP, 32, 0, lane);
-    if (len < 64) {  // uniform: only a sequence's last chunk can be partial
+    ring_barrier();  // S(r)
+    // B fragments of X_c in the permuted contraction order of -G's fragments: element e of
+    // lane l is key 32 s + 16 (e / 4) + 4 (l / 16) + e % 4
+    bf16x8 xb[NB];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (8 * kg + e >= len) oB0[e] = to_bf16(0.f);
-        if (32 + 8 * kg + e >= len) oB1[e] = to_bf16(0.f);
-      }
+    for (int s = 0; s < NB; ++s) {
+      const bf16x4 lo = *(const bf16x4*)(sDS + lr * SP + 32 * s + 4 * kg);
+      const bf16x4 hi = *(const bf16x4*)(sDS + lr * SP + 32 * s + 16 + 4 * kg);
+      xb[s] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    f32x4 pq[KT];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const bf16x8 q0 = *(const bf16x8*)(slot + L::off_qgt + frag_off(64, wave * KT + kt, 0, lane) * 2);
-      const bf16x8 q1 = *(const bf16x8*)(slot + L::off_qgt + frag_off(64, wave * KT + kt, 1, lane) * 2);
-      pq[kt] = mfma16(q1, oB1, mfma16(q0, oB0, zero4()));
+      const int ktg = wave * KT + kt;
+      const float4 lam = *(const float4*)(slot + L::off_lam + (16 * ktg + 4 * kg) * 4);
+      const f32x4 e = *(const f32x4*)(slot + L::off_e + (ktg * 64 + lane) * 16);
+      f32x4 acc;
+      acc[0] = fmaf(lam.x, X[kt][0], e[0]);
+      acc[1] = fmaf(lam.y, X[kt][1], e[1]);
+      acc[2] = fmaf(lam.z, X[kt][2], e[2]);
+      acc[3] = fmaf(lam.w, X[kt][3], e[3]);
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        acc = mfma16(*(const bf16x8*)(slot + L::off_g + frag_off(K, ktg, s, lane) * 2), xb[s], acc);
+      X[kt] = acc;
     }
-    {
-      f32x4 acc0 = zero4(), acc1 = zero4();
-      acc0 = mfma16(*(const bf16x8*)(slot + L::off_at + frag_off(64, wave, 0, lane) * 2), oB0, acc0);
-      acc1 = mfma16(*(const bf16x8*)(slot + L::off_at + frag_off(64, wave, 1, lane) * 2), oB1, acc1);
-#pragma unroll
-      for (int s = 0; s < K / 32; s += 2) {
-        acc0 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s, lane) * 2),
-                      *(const bf16x8*)(sDS + lr * SP + 32 * s + 8 * kg), acc0);
-        acc1 = mfma16(*(const bf16x8*)(slot + L::off_kd + frag_off(K, wave, s + 1, lane) * 2),
-                      *(const bf16x8*)(sDS + lr * SP + 32 * (s + 1) + 8 * kg), acc1);
-      }
-      // [strip][16-token block][16 columns][16 tokens]: this wave's block is 512 contiguous
-      // bytes, written by one store instruction
-      bf16* DDLT = (bf16*)a.sc.p[S_DDLT] + tile * V * 64 + (size_t)strip * 1024 + wave * 256;
-      const f32x4 d = acc0 + acc1;
-      if (PUB)
-        store8_coherent(DDLT, (lr * 16 + 4 * kg) * 2, f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3])));
-      else
-        *(bf16x4*)(DDLT + (size_t)lr * 16 + 4 * kg) = f4_to_bf16x4(make_float4(d[0], d[1], d[2], d[3]));
-      bf16x4 x;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) x[q] = to_bf16(d[q]);
-      *(bf16x4*)(sDD + lr * DP + 16 * wave + 4 * kg) = x;
-    }
-    wait_lgkm0();
-    ring_barrier();  // S2(r)
-    // (4) dS = lam dS' + Qg^T dO - W^T dDelta
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      f32x4 pw = zero4();
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        pw = mfma16(*(const bf16x8*)(slot + L::off_wt + frag_off(64, wave * KT + kt, s, lane) * 2),
-                    *(const bf16x8*)(sDD + lr * DP + 32 * s + 8 * kg), pw);
-      const float4 lam = *(const float4*)(slot + L::off_lam + (16 * (wave * KT + kt) + 4 * kg) * 4);
-      dS[kt][0] = fmaf(lam.x, dS[kt][0], pq[kt][0] - pw[0]);
-      dS[kt][1] = fmaf(lam.y, dS[kt][1], pq[kt][1] - pw[1]);
-      dS[kt][2] = fmaf(lam.z, dS[kt][2], pq[kt][2] - pw[2]);
-      dS[kt][3] = fmaf(lam.w, dS[kt][3], pq[kt][3] - pw[3]);
-    }
-    wait_lgkm0();  // the slot is released at the next S1
   }
-  if (PUB && n > 0) {
-    wait_vmcnt<0>();
-    ring_barrier();  // final
-  }
+  if (PUB) ring_barrier();  // final
   if (a.ds0) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
       *(float4*)(a.ds0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
-          make_float4(dS[kt][0], dS[kt][1], dS[kt][2], dS[kt][3]);
+          make_float4(X[kt][0], X[kt][1], X[kt][2], X[kt][3]);
     }
   }
 }
@@ -530,7 +577,11 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   const float* SH = (const float*)a.ws.p[R_SH] + tile * K * V;
   const bf16* DLF = (const bf16*)a.ws.p[R_DLF] + tile * 64 * V;
   const bf16* DSH = (const bf16*)a.sc.p[S_DSH] + tile * K * V;
-  const bf16* DDLT = (const bf16*)a.sc.p[S_DDLT] + tile * V * 64;
+  // X_c (dS' at the chunk end, K x V) staged for dU = dDelta = A^T dO + Kd X_c after the gate:
+  // keys 0..63 in the spare region, keys 64.. in the dW region (both free until PA), pitch VP
+  static_assert(K <= 64 || V <= K, "X_c's second key half fits the dW region");
+  bf16* sX0 = (bf16*)(smem + L::off_dul);
+  bf16* sX1 = (bf16*)(smem + L::off_dw);
   float* DQG = (float*)a.sc.p[S_DQG] + tile * 64 * K;
   float* DKD = (float*)a.sc.p[S_DKD] + tile * 64 * K;
   float* DKB = (float*)a.sc.p[S_DKB] + tile * 64 * K;
@@ -574,6 +625,18 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   bf16x8 dlf[NDL];
 #pragma unroll
   for (int q = 0; q < NDL; ++q) dlf[q] = *(const bf16x8*)(DLF + (size_t)min(q * kDenseThreads + tid, 64 * V / 8 - 1) * 8);
+  // dU tiles of this wave: tile id = wave + 16 j -> row tile id % 4, column tile id / 4; the
+  // A^T and Kd fragments of its row tile
+  constexpr int NDU = (4 * V / 16) / kDenseWaves;  // 2 at V = 128, 1 at V = 64
+  static_assert(NDU >= 1 && NDU * kDenseWaves == 4 * V / 16, "dU tiles per wave");
+  const int du_rt = wave % 4;
+  bf16x8 du_at[2], du_kd[K / 32];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+    du_at[s2] = *(const bf16x8*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64 + frag_off(64, du_rt, s2, lane));
+#pragma unroll
+  for (int s2 = 0; s2 < K / 32; ++s2)
+    du_kd[s2] = *(const bf16x8*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K + frag_off(K, du_rt, s2, lane));
   // operands of later phases, requested with the rest (each would otherwise cost a global
   // round trip of its own after the gate): beta rows and lam of PA's key column
   const float beta_row = ((const float*)a.ws.p[R_BETA])[tile * 64 + (tid & 63)];
@@ -653,6 +716,16 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     }
   }
 
+  // the scan-independent half of dU: A^T dO (dO staged above, tokens down the contraction)
+  f32x4 du_acc[NDU];
+#pragma unroll
+  for (int j = 0; j < NDU; ++j) {
+    const int ct = (wave + kDenseWaves * j) / 4;
+    du_acc[j] = zero4();
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) du_acc[j] = mfma16(du_at[s2], lds_col_frag(sDO, VP, 32 * s2, 16 * ct, lane), du_acc[j]);
+  }
+
   // xs made opaque: PA splits it again instead of keeping this split's 32 registers alive
 #pragma unroll
   for (int sv = 0; sv < NVS; ++sv)
@@ -672,18 +745,37 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
       xd[sv] = *(const bf16x8*)(DSH + off);
     }
   }
-  // dU: thread idx takes the 16-byte piece idx of the history (8 consecutive tokens of one
-  // column) and writes it transposed into dU rows
-  static_assert(V * 8 <= kDenseThreads, "one 16-byte piece of the history per thread");
+  // X_c from the strip-major history [V/16][K][16]: 16-byte piece p = (strip, key, half)
+  // -> row key, columns 16 strip + 8 half of the staged [key][VP] matrix
   {
-    const int idx = tid < V * 8 ? tid : V * 8 - 1;
-    const bf16x8 dd = Gate::kCoherent ? load16_coherent_bf16(DDLT, idx * 16)
-                                      : *(const bf16x8*)(DDLT + (size_t)idx * 8);
-    if (tid < V * 8) {
-      const int vv = (idx / 128) * 16 + (idx % 32) / 2, t8 = ((idx % 128) / 32) * 16 + (idx % 2) * 8;
+    constexpr int NP = K * V / 8, NPT = (NP + kDenseThreads - 1) / kDenseThreads;
+    bf16x8 xp[NPT];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sDU[(t8 + e) * VP + vv] = dd[e];
+    for (int q = 0; q < NPT; ++q) {
+      const int p = min(q * kDenseThreads + tid, NP - 1);
+      xp[q] = Gate::kCoherent ? load16_coherent_bf16(DSH, p * 16) : *(const bf16x8*)(DSH + (size_t)p * 8);
     }
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      const int p = q * kDenseThreads + tid;
+      if (p >= NP) break;
+      const int st = p / (K * 2), key = (p / 2) % K, half = p % 2;
+      bf16* row = key < 64 ? sX0 + key * VP : sX1 + (key - 64) * VP;
+      *(bf16x8*)(row + 16 * st + 8 * half) = xp[q];
+    }
+  }
+  __syncthreads();
+  // dU = A^T dO + Kd X_c (bf16, the operand of PA and PB)
+#pragma unroll
+  for (int j = 0; j < NDU; ++j) {
+    const int ct = (wave + kDenseWaves * j) / 4;
+#pragma unroll
+    for (int s2 = 0; s2 < K / 32; ++s2) {
+      const bf16* xm = s2 < 2 ? sX0 : sX1;
+      du_acc[j] = mfma16(du_kd[s2], lds_col_frag(xm, VP, 32 * (s2 % 2), 16 * ct, lane), du_acc[j]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sDU[(16 * du_rt + 4 * kg + r) * VP + 16 * ct + lr] = to_bf16(du_acc[j][r]);
   }
   __syncthreads();
 
@@ -1588,6 +1680,16 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
                            hipStream_t stream, int stages) {
   const int all = (1 << (KDA_STAGE_BWD_SCAN - 10)) | (1 << (KDA_STAGE_BWD_DENSE - 10)) |
                   (1 << (KDA_STAGE_BWD_DECAY - 10));
+  // the reverse scan's per-chunk transition -G and inhomogeneous term E (chunk-parallel)
+  auto launch_prep = [&]() -> int {
+    auto prep = chunk_bwd_prep_kernel<K, V>;
+    constexpr int smem_p = PrepLds<K, V>::bytes;
+    if (ensure_lds_limit((const void*)prep, smem_p) != hipSuccess)
+      return set_error(KDA_ERR_LAUNCH, "chunk_backward: prep LDS attribute failed");
+    hipLaunchKernelGGL(prep, dim3(g.max_chunks, p->heads), dim3(kPrepThreads), smem_p, stream, a);
+    KDA_LAUNCH_CHECK("chunk_backward prep");
+    return KDA_OK;
+  };
   if ((stages & all) == all && p->num_seqs > 0 && g.max_chunks > 0 && fused_backward_enabled()) {
     // one launch: scan members + ticketed dense / decay tiles (see chunk_bwd_fused_kernel)
     constexpr size_t smem = cmax_sz(BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
@@ -1598,6 +1700,8 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     const int nrec = p->num_seqs * p->heads;
     const int scan_blocks = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
     const int N = g.max_chunks * p->heads;
+    int rc = launch_prep();
+    if (rc != KDA_OK) return rc;
     hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks, sync_words(nrec, N));
     KDA_LAUNCH_CHECK("chunk_backward sched");
     hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks,
@@ -1613,6 +1717,10 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     KDA_LAUNCH_CHECK("chunk_backward sched");
   }
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
+    if (g.max_chunks > 0) {
+      int rc = launch_prep();
+      if (rc != KDA_OK) return rc;
+    }
     auto scan = chunk_bwd_scan_kernel<K, V>;
     constexpr size_t smem_s = BwdScanLds<K, V>::bytes;
     if (ensure_lds_limit((const void*)scan, (int)smem_s) != hipSuccess)
@@ -1627,8 +1735,10 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
         pf.lines[pf.n++] = bytes / 128;
       }
     };
-    for (int r : {R_ATF, R_KDF, R_QGTF, R_WTF, R_LAM}) add(a.ws.p[r], ws_region_bytes(g, r));
-    add(a.dout, rows * V * 2);
+    (void)rows;
+    add(a.sc.p[S_NG], sc_region_bytes(g, S_NG));
+    add(a.sc.p[S_E], sc_region_bytes(g, S_E));
+    add(a.ws.p[R_LAM], ws_region_bytes(g, R_LAM));
     const int cus = device_cu_count();
     const int extra = cus > grid ? cus - grid : 0;
     hipLaunchKernelGGL(scan, dim3(grid + extra), dim3(kBwdThreads), smem_s, stream, a, pf, grid);

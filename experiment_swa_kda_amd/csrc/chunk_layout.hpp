@@ -67,7 +67,8 @@ enum WsRegion {
 
 enum ScRegion {
   S_DSH = 0,  // bf16 [tile][V/16][K][16]  dL/dS at the chunk end, strip-major (a bf16 MFMA operand of dKd)
-  S_DDLT,     // bf16 [tile][V/16][4][16 v][16 t]  (dL/d delta)^T, per strip and 16-token block
+  S_NG,       // bf16 [tile] K x K  -G = -(W^T Kd) as MFMA A fragments, permuted (the reverse scan's transition)
+  S_E,        // f32  [tile][V/16][K/16][64 lane][4]  E = Qg^T dO - W^T (A^T dO) in the scan's accumulator order
   S_DA,       // bf16 [tile][64][64] dL/dA (masked lower; the decay VJP's MFMA operand)
   S_DMP,      // bf16 [tile][64][64] dL/dM' (strictly lower, beta folded in; same)
   S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
@@ -119,7 +120,8 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   const size_t K = g.K, V = g.V;
   switch (r) {
     case S_DSH: return nt * K * V * 2;
-    case S_DDLT: return nt * 64 * V * 2;
+    case S_NG: return nt * K * K * 2;
+    case S_E: return nt * K * V * 4;
     case S_DA: case S_DMP: return nt * 64 * 64 * 2;
     case S_DQG: case S_DKD: case S_DKB: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
