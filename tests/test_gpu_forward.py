@@ -37,6 +37,18 @@ def test_chunk_forward_boundary_lengths_d64(T):
     torch.testing.assert_close(fin.double().cpu(), torch.tensor(ef), atol=5e-3, rtol=5e-3)
 
 
+# the reference's frozen boundary lengths at its production head dim
+# (configs/research/kda_cuda_ownership.toml:42-43)
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 63, 64, 65, 127, 128, 129, 257])
+def test_chunk_forward_boundary_lengths_d128(T):
+    d = make_kda_inputs(1, T, 3, 128, 128, seed=400 + T, state=True)
+    out, fin = run_chunk(d, "k3")
+    eo, ef = oracle_fwd(d, "k3")
+    assert rel_err(out, eo) < 2e-2 and rel_err(fin, ef) < 2e-2
+    torch.testing.assert_close(out.double().cpu(), torch.tensor(eo), atol=5e-3, rtol=5e-3)
+    torch.testing.assert_close(fin.double().cpu(), torch.tensor(ef), atol=5e-3, rtol=5e-3)
+
+
 @pytest.mark.parametrize("gate", ["k3", "precomputed"])
 @pytest.mark.parametrize("KV", [(128, 128), (64, 128), (128, 64)])
 def test_chunk_forward_d128(gate, KV):
