@@ -24,7 +24,7 @@ LIB_NAME = "libkda_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
 SOURCES = ["capi.cpp", "decode.hip", "conv.hip", "norm_gate.hip", "chunk_fwd.hip", "chunk_bwd.hip", "softcap_ce.hip",
-           "weight_grad.hip", "trainer_ops.hip", "mfma_probe.hip"]
+           "weight_grad.hip", "trainer_ops.hip", "mfma_probe.hip", "generic.hip"]
 # Per-source extra flags.  The chunk kernels keep MFMA accumulators in VGPRs: their
 # accumulators feed VALU work every step, and the AGPR form costs a copy per element.
 EXTRA_FLAGS = {

@@ -1429,8 +1429,9 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
 int validate_problem(const kda_chunk_problem* p, const char* who) {
   KDA_REQUIRE(p, "%s: null problem", who);
   KDA_REQUIRE(p->batch >= 0 && p->seq_len >= 0 && p->heads > 0, "%s: invalid B/T/H", who);
-  KDA_REQUIRE(p->key_dim == 64 || p->key_dim == 128, "%s: key_dim must be 64 or 128", who);
-  KDA_REQUIRE(p->value_dim == 64 || p->value_dim == 128, "%s: value_dim must be 64 or 128", who);
+  // 64 / 128 run the chunked kernels; other sizes the token-serial kernels (generic.hip)
+  KDA_REQUIRE(p->key_dim >= 1 && p->key_dim <= 256, "%s: key_dim must be in [1, 256]", who);
+  KDA_REQUIRE(p->value_dim >= 1 && p->value_dim <= 4096, "%s: value_dim must be in [1, 4096]", who);
   KDA_REQUIRE(p->gate_mode == KDA_GATE_K3 || p->gate_mode == KDA_GATE_LOGDECAY,
               "%s: invalid gate_mode", who);
   if (p->cu_seqlens) {
@@ -1548,11 +1549,13 @@ int launch_chunk_prep(const kda_chunk_problem* p, const ChunkGeom& g, const Regi
 
 extern "C" size_t kda_chunk_workspace_bytes(const kda_chunk_problem* p) {
   if (kda::validate_problem(p, "chunk_workspace_bytes") != KDA_OK) return 0;
+  if (kda::generic_dims(p)) return kda::generic_ws_bytes(p);
   return kda::ws_total_bytes(kda::make_geom(p));
 }
 
 extern "C" size_t kda_chunk_backward_scratch_bytes(const kda_chunk_problem* p) {
   if (kda::validate_problem(p, "chunk_backward_scratch_bytes") != KDA_OK) return 0;
+  if (kda::generic_dims(p)) return kda::generic_sc_bytes(p);
   return kda::sc_total_bytes(kda::make_geom(p));
 }
 
@@ -1577,6 +1580,12 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
               "chunk_forward: K3 gate needs A_log and dt_bias");
   KDA_REQUIRE(workspace && ((uintptr_t)workspace % 256) == 0,
               "chunk_forward: workspace must be non-null and 256-byte aligned");
+  if (generic_dims(p)) {
+    KDA_REQUIRE(stages == ~0 && !norm_gate && !conv_x,
+                "chunk_forward: stage entry points and fused epilogues need head dims 64 or 128");
+    return generic_forward(p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state, output, final_state,
+                           workspace, stream);
+  }
   const ChunkGeom g = make_geom(p);
   FwdArgs a;
   a.H = p->heads;

@@ -11,6 +11,19 @@ ChunkGeom make_geom(const kda_chunk_problem* p);
 int launch_chunk_prep(const kda_chunk_problem* p, const ChunkGeom& g, const Regions& ws,
                       hipStream_t stream);
 
+// Token-serial path for head dims other than 64 / 128 (generic.hip).
+bool generic_dims(const kda_chunk_problem* p);
+size_t generic_ws_bytes(const kda_chunk_problem* p);
+size_t generic_sc_bytes(const kda_chunk_problem* p);
+int generic_forward(const kda_chunk_problem* p, const void* q, const void* k, const void* v, const void* gate,
+                    const void* beta_logits, const float* A_log, const float* dt_bias, const float* initial_state,
+                    void* output, float* final_state, void* workspace, hipStream_t stream);
+int generic_backward(const kda_chunk_problem* p, const void* q, const void* k, const void* v, const void* gate,
+                     const void* beta_logits, const float* A_log, const float* dt_bias, const void* workspace,
+                     const void* grad_output, const float* grad_final_state, void* dq, void* dk, void* dv,
+                     void* dgate, void* dbeta_logits, float* dA_log, float* ddt_bias, float* dinitial_state,
+                     void* scratch, hipStream_t stream);
+
 constexpr size_t cmax_sz(size_t x, size_t y) { return x > y ? x : y; }
 
 // Compute units of the current device (launch granularity of the chunk-parallel rounds and

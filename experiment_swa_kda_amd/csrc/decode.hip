@@ -11,6 +11,7 @@
 // four keys each, and handed to every wave through LDS: done per lane, it was most of the
 // kernel's VALU time.  Its inputs are loaded before the state rows (loads complete in
 // order), so it runs while the state rows are in flight.
+#include "chunk_host.hpp"
 #include "kda_device.hpp"
 #include "kda_host.hpp"
 
@@ -173,7 +174,7 @@ extern "C" int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_di
                                     float* final_state, hipStream_t stream) {
   using namespace kda;
   KDA_REQUIRE(batch >= 0 && heads > 0, "recurrent_decode: invalid batch/heads");
-  KDA_REQUIRE(key_dim == 64 || key_dim == 128, "recurrent_decode: key_dim must be 64 or 128");
+  KDA_REQUIRE(key_dim >= 1 && key_dim <= 256, "recurrent_decode: key_dim must be in [1, 256]");
   KDA_REQUIRE(value_dim > 0 && value_dim <= 4096, "recurrent_decode: invalid value_dim");
   KDA_REQUIRE(gate_mode == KDA_GATE_K3 || gate_mode == KDA_GATE_LOGDECAY,
               "recurrent_decode: invalid gate_mode");
@@ -183,6 +184,23 @@ extern "C" int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_di
   KDA_REQUIRE(aligned16(q, k, gate, dt_bias, initial_state, final_state),
               "recurrent_decode: q, k, gate, dt_bias and the states must be 16-byte aligned");
   if (batch == 0) return KDA_OK;
+  if (key_dim != 64 && key_dim != 128) {
+    // other key dims: one step of the token-serial kernel (generic.hip); it reads each
+    // state element before writing it from the same lane, so final_state may alias the
+    // initial state
+    kda_chunk_problem one = {};
+    one.batch = batch;
+    one.seq_len = 1;
+    one.heads = heads;
+    one.key_dim = key_dim;
+    one.value_dim = value_dim;
+    one.num_seqs = batch;
+    one.gate_mode = gate_mode;
+    one.lower_bound = lower_bound;
+    one.scale = scale;
+    return generic_forward(&one, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state, output,
+                           final_state, nullptr, stream);
+  }
   dim3 grid(batch * heads, (value_dim + kDecodeRowsPerBlock - 1) / kDecodeRowsPerBlock);
   auto args = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), 0, stream, heads, value_dim, lower_bound, scale,

@@ -1,4 +1,5 @@
-// Fused output RMSNorm * weight * sigmoid(gate) over rows of D channels (D = 64 or 128).
+// Fused output RMSNorm * weight * sigmoid(gate) over rows of D channels (D = 64 or 128 on
+// the vector kernels below; any D <= 1024 on the one-wave-per-row kernels).
 // Reference: nanochat/mixers/cuda_kda/rmsnorm_gate.cu:31-184; semantics
 // nanochat/mixers/kda.py:46-59 (F.rms_norm(x, weight) * sigmoid(gate)).
 //
@@ -153,6 +154,105 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
   }
 }
 
+// Any other row width D <= 1024 (the reference takes any): one wave per row, lane l owning
+// channels l + 64 i (scalar bf16 accesses), wave-wide sums.  The backward's workgroups
+// stride over the rows and leave one weight-gradient partial each (kGenNormBlocks at most).
+constexpr int kGenNormMaxD = 1024;
+constexpr int kGenNormBlocks = 512;
+
+template <int NI>
+__global__ __launch_bounds__(256) void norm_gate_fwd_generic_kernel(long rows, int D, const bf16* __restrict__ x,
+                                                                    const bf16* __restrict__ gate,
+                                                                    const float* __restrict__ weight, float eps,
+                                                                    bf16* __restrict__ y, float* __restrict__ inv_rms) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const long r = (long)blockIdx.x * 4 + wave;
+  if (r >= rows) return;  // whole wave
+  float xv[NI], gv[NI], ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int c = lane + 64 * i;
+    xv[i] = c < D ? (float)x[r * D + c] : 0.f;
+    gv[i] = c < D ? (float)gate[r * D + c] : 0.f;
+    ss = fmaf(xv[i], xv[i], ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / D + eps);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int c = lane + 64 * i;
+    if (c < D) y[r * D + c] = to_bf16(xv[i] * inv * weight[c] * sigmoid_fast(gv[i]));
+  }
+  if (lane == 0) inv_rms[r] = inv;
+}
+
+template <int NI>
+__global__ __launch_bounds__(256) void norm_gate_bwd_generic_kernel(
+    long rows, int D, int heads, const bf16* __restrict__ x, const bf16* __restrict__ gate, long gld,
+    const float* __restrict__ weight, const float* __restrict__ inv_rms, const bf16* __restrict__ dy,
+    bf16* __restrict__ dx, bf16* __restrict__ dgate, long dgld, float* __restrict__ dw_part) {
+  __shared__ float s_dw[4][kGenNormMaxD];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  float dwacc[NI], w[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int c = lane + 64 * i;
+    dwacc[i] = 0.f;
+    w[i] = c < D ? weight[c] : 0.f;
+  }
+  for (long r = (long)blockIdx.x * 4 + wave; r < rows; r += (long)gridDim.x * 4) {
+    const long tok = r / heads, hh = r - tok * heads;
+    const long go = tok * gld + hh * D, dgo = tok * dgld + hh * D;
+    const float inv = inv_rms[r];
+    float n[NI], dn[NI], s[NI], gs[NI], dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int c = lane + 64 * i;
+      const bool ok = c < D;
+      const float g = ok ? (float)dy[r * D + c] : 0.f;
+      s[i] = ok ? sigmoid_fast((float)gate[go + c]) : 0.f;
+      n[i] = ok ? (float)x[r * D + c] * inv : 0.f;
+      gs[i] = g * s[i];
+      dn[i] = gs[i] * w[i];
+      dot = fmaf(dn[i], n[i], dot);
+      dwacc[i] = fmaf(gs[i], n[i], dwacc[i]);
+    }
+    dot = wave_sum(dot) / D;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int c = lane + 64 * i;
+      if (c < D) {
+        const float t = dn[i] * n[i];
+        dx[r * D + c] = to_bf16(inv * fmaf(-n[i], dot, dn[i]));
+        dgate[dgo + c] = to_bf16(fmaf(-t, s[i], t));
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    if (lane + 64 * i < D) s_dw[wave][lane + 64 * i] = dwacc[i];
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += 256)
+    dw_part[(size_t)blockIdx.x * D + c] = ((s_dw[0][c] + s_dw[1][c]) + s_dw[2][c]) + s_dw[3][c];
+}
+
+static int gen_norm_ni(int D) { return D <= 64 ? 1 : D <= 128 ? 2 : D <= 256 ? 4 : D <= 512 ? 8 : 16; }
+
+static int gen_norm_blocks(long rows) {
+  const long nb = (rows + 3) / 4;
+  return (int)(nb < 1 ? 1 : (nb > kGenNormBlocks ? kGenNormBlocks : nb));
+}
+
+#define KDA_GEN_NORM_DISPATCH(D_, CALL) \
+  switch (gen_norm_ni(D_)) {            \
+    case 1: CALL(1); break;             \
+    case 2: CALL(2); break;             \
+    case 4: CALL(4); break;             \
+    case 8: CALL(8); break;             \
+    default: CALL(16); break;           \
+  }
+
+static bool fast_dim(int dim) { return dim == 64 || dim == 128; }
+
 static int norm_blocks(long rows, int dim, int rows_per_thread) {
   const long rpb = 256 / (dim / 8) * rows_per_thread;
   long nb = (rows + rpb - 1) / rpb;
@@ -167,13 +267,22 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
                                         void* output, float* inv_rms, hipStream_t stream) {
   using namespace kda;
   KDA_REQUIRE(rows >= 0, "rmsnorm_gate_forward: invalid rows");
-  KDA_REQUIRE(dim == 64 || dim == 128, "rmsnorm_gate_forward: dim must be 64 or 128");
+  KDA_REQUIRE(dim >= 1 && dim <= kGenNormMaxD, "rmsnorm_gate_forward: dim must be in [1, %d]", kGenNormMaxD);
   KDA_REQUIRE(eps > 0.f, "rmsnorm_gate_forward: eps must be positive");
   KDA_REQUIRE(weight && (rows == 0 || (x && gate && output && inv_rms)),
               "rmsnorm_gate_forward: null pointer");
-  KDA_REQUIRE(aligned16(x, gate, weight, output),
+  KDA_REQUIRE(!fast_dim(dim) || aligned16(x, gate, weight, output),
               "rmsnorm_gate_forward: x, gate, weight and output must be 16-byte aligned");
   if (rows == 0) return KDA_OK;
+  if (!fast_dim(dim)) {
+#define KDA_GEN_NORM_FWD(NI)                                                                                  \
+  hipLaunchKernelGGL(norm_gate_fwd_generic_kernel<NI>, dim3((rows + 3) / 4), dim3(256), 0, stream, (long)rows, \
+                     (int)dim, (const bf16*)x, (const bf16*)gate, weight, eps, (bf16*)output, inv_rms)
+    KDA_GEN_NORM_DISPATCH(dim, KDA_GEN_NORM_FWD)
+#undef KDA_GEN_NORM_FWD
+    KDA_LAUNCH_CHECK("rmsnorm_gate_forward");
+    return KDA_OK;
+  }
   const int nb = norm_blocks(rows, dim, kRowsFwd);
   if (dim == 128)
     hipLaunchKernelGGL(norm_gate_fwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows,
@@ -186,7 +295,9 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
 }
 
 extern "C" size_t kda_rmsnorm_gate_backward_scratch_bytes(int64_t rows, int32_t dim) {
-  return kda::align256((size_t)kda::norm_blocks(rows, dim, kda::kRowsBwd) * dim * sizeof(float)) + 256;
+  if (dim < 1 || dim > kda::kGenNormMaxD) return 0;
+  const size_t nb = kda::fast_dim(dim) ? kda::norm_blocks(rows, dim, kda::kRowsBwd) : kda::gen_norm_blocks(rows);
+  return kda::align256(nb * dim * sizeof(float)) + 256;
 }
 
 extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int32_t heads, const void* x,
@@ -198,18 +309,35 @@ extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int3
   using namespace kda;
   (void)eps;
   KDA_REQUIRE(rows >= 0 && rows < (1LL << 31), "rmsnorm_gate_backward: rows must be in [0, 2^31)");
-  KDA_REQUIRE(dim == 64 || dim == 128, "rmsnorm_gate_backward: dim must be 64 or 128");
+  KDA_REQUIRE(dim >= 1 && dim <= kGenNormMaxD, "rmsnorm_gate_backward: dim must be in [1, %d]", kGenNormMaxD);
   KDA_REQUIRE(heads >= 1 && rows % heads == 0, "rmsnorm_gate_backward: rows must be a multiple of heads >= 1");
-  KDA_REQUIRE(gate_row_stride >= (int64_t)heads * dim && gate_row_stride % 8 == 0 &&
-                  dgate_row_stride >= (int64_t)heads * dim && dgate_row_stride % 8 == 0,
-              "rmsnorm_gate_backward: gate / dgate row strides must be multiples of 8 of at least heads * dim");
+  KDA_REQUIRE(gate_row_stride >= (int64_t)heads * dim && dgate_row_stride >= (int64_t)heads * dim &&
+                  (!fast_dim(dim) || (gate_row_stride % 8 == 0 && dgate_row_stride % 8 == 0)),
+              "rmsnorm_gate_backward: gate / dgate row strides must be at least heads * dim (multiples of 8 "
+              "for dim 64 / 128)");
   KDA_REQUIRE(weight && dweight && scratch, "rmsnorm_gate_backward: null pointer");
   KDA_REQUIRE(rows == 0 || (x && gate && inv_rms && grad_output && dx && dgate),
               "rmsnorm_gate_backward: null pointer");
-  KDA_REQUIRE(aligned16(x, gate, weight, grad_output, dx, dgate, scratch),
+  KDA_REQUIRE(aligned16(scratch) && (!fast_dim(dim) || aligned16(x, gate, weight, grad_output, dx, dgate)),
               "rmsnorm_gate_backward: x, gate, weight, grad_output, dx, dgate and scratch must be 16-byte aligned");
-  const int nb = norm_blocks(rows, dim, kRowsBwd);
   float* part = (float*)scratch;
+  if (!fast_dim(dim)) {
+    const int gnb = gen_norm_blocks(rows);
+    if (rows > 0) {
+#define KDA_GEN_NORM_BWD(NI)                                                                                  \
+  hipLaunchKernelGGL(norm_gate_bwd_generic_kernel<NI>, dim3(gnb), dim3(256), 0, stream, (long)rows, (int)dim, \
+                     (int)heads, (const bf16*)x, (const bf16*)gate, (long)gate_row_stride, weight, inv_rms,   \
+                     (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, (long)dgate_row_stride, part)
+      KDA_GEN_NORM_DISPATCH(dim, KDA_GEN_NORM_BWD)
+#undef KDA_GEN_NORM_BWD
+      KDA_LAUNCH_CHECK("rmsnorm_gate_backward");
+    }
+    hipLaunchKernelGGL(dw_reduce_kernel<float>, dim3((dim * kDwRedLanes + 255) / 256), dim3(256), 0, stream,
+                       rows > 0 ? gnb : 0, dim, (const float*)part, dweight);
+    KDA_LAUNCH_CHECK("rmsnorm_gate_dweight_reduce");
+    return KDA_OK;
+  }
+  const int nb = norm_blocks(rows, dim, kRowsBwd);
   if (rows > 0) {
     if (dim == 128)
       hipLaunchKernelGGL(norm_gate_bwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows, (int)heads,

@@ -329,8 +329,9 @@ def _backend_reason(q, k, v, raw_gate, beta_logits, A_log, dt_bias, initial_stat
             return "safe-gate lower_bound must be in [-5, 0)"
     elif raw_gate.dtype != torch.float32:
         return "a precomputed log decay must be float32"
-    if q.shape[-1] not in (64, 128) or v.shape[-1] not in (64, 128):
-        return "head dimensions must be 64 or 128"
+    # 64 / 128 run the chunked kernels, other sizes the token-serial ones
+    if not (1 <= q.shape[-1] <= 256 and 1 <= v.shape[-1] <= 4096):
+        return "head dimensions must be K in [1, 256] and V in [1, 4096]"
     if initial_state is not None:
         if initial_state.device != q.device:
             return "initial_state must be on the same device as q"
@@ -501,10 +502,15 @@ def kda_norm_gate(q, k, v, raw_gate, beta_logits, A_log, dt_bias, output_gate, n
         _gate_shapes(raw_gate, A_log, dt_bias)
     reason = _backend_reason(q, k, v, raw_gate, beta_logits, A_log, dt_bias, None,
                              lower_bound=lower_bound, gate=gate)
-    if reason is None and v.shape[-1] not in (64, 128):
-        reason = "the fused norm needs head_dim 64 or 128"
     if reason is not None:
         raise RuntimeError(f"project CUDA KDA backend unavailable: {reason}")
+    if q.shape[-1] not in (64, 128) or v.shape[-1] not in (64, 128):
+        # the token-serial kernels have no fused epilogue: the norm runs as its own kernel
+        out, _ = kda(q, k, v, raw_gate, beta_logits, A_log, dt_bias, mode="project_chunk",
+                     lower_bound=lower_bound, scale=scale, gate=gate)
+        out = _ProjectRMSNormGateAutograd.apply(out, output_gate, norm_weight, float(eps))
+        _record("rmsnorm_gate_forward")
+        return _record_backward(out, "rmsnorm_gate_backward")
     resolved_scale = float(scale if scale is not None else q.shape[-1] ** -0.5)
     out = _ProjectKDANormGateAutograd.apply(q, k, v, raw_gate, beta_logits, A_log, dt_bias,
                                             output_gate, norm_weight, float(eps),
@@ -768,7 +774,7 @@ class KimiDeltaAttention(nn.Module):
         """RMSNorm(o)·sigmoid(gate): the HIP kernel pair whenever its dtypes and head size fit,
         else the module's own (eager or per-op) path."""
         kernel_fits = (mode != "reference" and o.is_cuda and o.dtype == torch.bfloat16
-                       and gate.dtype == torch.bfloat16 and self.head_dim in (64, 128)
+                       and gate.dtype == torch.bfloat16 and self.head_dim <= 1024
                        and self.o_norm.weight.dtype == torch.float32)
         if not kernel_fits:
             return self.o_norm(o, gate)
@@ -830,7 +836,7 @@ class KimiDeltaAttention(nn.Module):
         mixed, _ = kda(q, k, v, raw_gate, beta_logits, self.A_log, self.dt_bias, initial_state=None,
                        output_final_state=False, mode=mode, lower_bound=self.lower_bound,
                        allow_fallback=allow_fallback)
-        return self.o_proj(self.o_norm(mixed, output_gate).reshape(batch, length, C))
+        return self.o_proj(self._gated_norm(mixed, output_gate, mode).reshape(batch, length, C))
 
 
 __all__ = ["KDAState", "KimiDeltaAttention", "k3_decay_gate", "kda", "kda_norm_gate", "prepare_kda_backend",

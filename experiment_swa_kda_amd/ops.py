@@ -98,8 +98,9 @@ def _check_chunk_inputs(what, q, k, v, gate, beta_logits, A_log, dt_bias, initia
         raise RuntimeError(f"{what}: v must have shape [B, T, H, V]")
     if beta_logits.shape != q.shape[:3]:
         raise RuntimeError(f"{what}: beta_logits must have shape [B, T, H]")
-    if K not in (64, 128) or v.shape[-1] not in (64, 128):
-        raise RuntimeError(f"{what}: head dimensions must be 64 or 128 (got K={K}, V={v.shape[-1]})")
+    if not (1 <= K <= 256 and 1 <= v.shape[-1] <= 4096):
+        raise RuntimeError(f"{what}: head dimensions must be K in [1, 256] and V in [1, 4096] "
+                           f"(got K={K}, V={v.shape[-1]})")
     n = B if cu_seqlens is None else cu_seqlens.numel() - 1
     if cu_seqlens is not None:
         if B != 1:

@@ -38,10 +38,19 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.skipif(not _lib.is_built(), reason="library not built")
 def test_c_abi_rejects_bad_problems_without_gpu():
     lib = _lib.load()
-    p = _lib.ChunkProblem(batch=1, seq_len=8, heads=1, key_dim=96, value_dim=64, num_seqs=1,
+    p = _lib.ChunkProblem(batch=1, seq_len=8, heads=1, key_dim=257, value_dim=64, num_seqs=1,
                           cu_seqlens=None, gate_mode=0, lower_bound=-5.0, scale=0.1)
     assert lib.kda_chunk_workspace_bytes(ctypes.byref(p)) == 0
     assert "key_dim" in lib.kda_last_error().decode()
+    # head dims other than 64 / 128 take the token-serial kernels: state checkpoints every
+    # 16 tokens as the workspace, per-wave gradient partials as the backward scratch
+    p.key_dim = 96
+    assert lib.kda_chunk_workspace_bytes(ctypes.byref(p)) >= 1 * 1 * 64 * 96 * 4
+    assert lib.kda_chunk_backward_scratch_bytes(ctypes.byref(p)) >= 16 * 8 * (3 * 96 + 1) * 4
+    p.value_dim = 0
+    assert lib.kda_chunk_workspace_bytes(ctypes.byref(p)) == 0
+    assert "value_dim" in lib.kda_last_error().decode()
+    p.value_dim = 64
     p.key_dim = 64
     assert lib.kda_chunk_workspace_bytes(ctypes.byref(p)) > 0
     rc = lib.kda_chunk_forward(ctypes.byref(p), *([None] * 11), None)
@@ -52,7 +61,12 @@ def test_c_abi_rejects_bad_problems_without_gpu():
     assert lib.kda_causal_conv_forward(1, 4, 12, 4, None, None, None, None, None, None) != 0
     assert "multiple of 8" in lib.kda_last_error().decode()
     assert lib.kda_rmsnorm_gate_forward(4, 96, None, None, None, 1e-5, None, None, None) != 0
+    assert "null" in lib.kda_last_error().decode()
+    assert lib.kda_rmsnorm_gate_forward(4, 1025, None, None, None, 1e-5, None, None, None) != 0
+    assert "dim" in lib.kda_last_error().decode()
     assert lib.kda_recurrent_decode(1, 1, 32, 64, 0, -5.0, 0.1, *([None] * 10), None) != 0
+    assert lib.kda_recurrent_decode(1, 1, 257, 64, 0, -5.0, 0.1, *([None] * 10), None) != 0
+    assert "key_dim" in lib.kda_last_error().decode()
     # a gradient row stride shorter than a token's H * max(K, V) values is refused before any
     # launch (the pointers are never dereferenced)
     p = _lib.ChunkProblem(batch=1, seq_len=8, heads=2, key_dim=64, value_dim=64, num_seqs=1, cu_seqlens=None,
