@@ -1817,6 +1817,9 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
               "chunk_backward: scratch must be non-null and 256-byte aligned");
   if (generic_dims(p)) {
     KDA_REQUIRE(stages == ~0, "chunk_backward_stage: stage entry points need head dims 64 or 128");
+    if (padded_route(p))
+      return padded_backward(p, beta_logits, A_log, workspace, grad_output, grad_final_state, dq, dk, dv, dgate,
+                             dbeta_logits, dA_log, ddt_bias, dinitial_state, scratch, stream);
     return generic_backward(p, q, k, v, gate, beta_logits, A_log, dt_bias, workspace, grad_output,
                             grad_final_state, dq, dk, dv, dgate, dbeta_logits, dA_log, ddt_bias,
                             dinitial_state, scratch, stream);
@@ -1901,6 +1904,7 @@ extern "C" int kda_chunk_backward_status(const kda_chunk_problem* p, const void*
   if (rc != KDA_OK) return rc;
   KDA_REQUIRE(scratch && ((uintptr_t)scratch % 256) == 0,
               "chunk_backward_status: scratch must be non-null and 256-byte aligned");
+  if (padded_route(p)) return padded_status(p, scratch, stream);
   if (generic_dims(p)) return KDA_OK;  // the token-serial backward has no waits
   const Regions sc = sc_regions(make_geom(p), const_cast<void*>(scratch));
   int word = 0;
@@ -1967,7 +1971,8 @@ extern "C" int kda_chunk_backward_noalloc(const kda_chunk_problem* p, const void
   using namespace kda;
   int rc = validate_problem(p, "chunk_backward_noalloc");
   if (rc != KDA_OK) return rc;
-  const size_t need = generic_dims(p) ? generic_sc_bytes(p) : sc_total_bytes(make_geom(p));
+  const size_t need = !generic_dims(p) ? sc_total_bytes(make_geom(p))
+                                        : padded_route(p) ? padded_sc_bytes(p) : generic_sc_bytes(p);
   KDA_REQUIRE(need <= kNoAllocScratchBytes,
               "chunk_backward_noalloc: problem needs %zu bytes of scratch, more than the %zu-byte "
               "static array (use kda_chunk_backward with a caller buffer)",

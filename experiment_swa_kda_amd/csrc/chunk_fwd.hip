@@ -1549,13 +1549,13 @@ int launch_chunk_prep(const kda_chunk_problem* p, const ChunkGeom& g, const Regi
 
 extern "C" size_t kda_chunk_workspace_bytes(const kda_chunk_problem* p) {
   if (kda::validate_problem(p, "chunk_workspace_bytes") != KDA_OK) return 0;
-  if (kda::generic_dims(p)) return kda::generic_ws_bytes(p);
+  if (kda::generic_dims(p)) return kda::padded_route(p) ? kda::padded_ws_bytes(p) : kda::generic_ws_bytes(p);
   return kda::ws_total_bytes(kda::make_geom(p));
 }
 
 extern "C" size_t kda_chunk_backward_scratch_bytes(const kda_chunk_problem* p) {
   if (kda::validate_problem(p, "chunk_backward_scratch_bytes") != KDA_OK) return 0;
-  if (kda::generic_dims(p)) return kda::generic_sc_bytes(p);
+  if (kda::generic_dims(p)) return kda::padded_route(p) ? kda::padded_sc_bytes(p) : kda::generic_sc_bytes(p);
   return kda::sc_total_bytes(kda::make_geom(p));
 }
 
@@ -1583,6 +1583,9 @@ static int chunk_forward_impl(int stages, const kda_chunk_problem* p, const void
   if (generic_dims(p)) {
     KDA_REQUIRE(stages == ~0 && !norm_gate && !conv_x,
                 "chunk_forward: stage entry points and fused epilogues need head dims 64 or 128");
+    if (padded_route(p))
+      return padded_forward(p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state, output, final_state,
+                            workspace, stream);
     return generic_forward(p, q, k, v, gate, beta_logits, A_log, dt_bias, initial_state, output, final_state,
                            workspace, stream);
   }

@@ -24,6 +24,20 @@ int generic_backward(const kda_chunk_problem* p, const void* q, const void* k, c
                      void* dgate, void* dbeta_logits, float* dA_log, float* ddt_bias, float* dinitial_state,
                      void* scratch, hipStream_t stream);
 
+// Zero-padded route (generic.hip): K, V <= 128 other than 64 / 128 run the chunked kernels
+// at K, V rounded up to 64 or 128.
+bool padded_route(const kda_chunk_problem* p);
+size_t padded_ws_bytes(const kda_chunk_problem* p);
+size_t padded_sc_bytes(const kda_chunk_problem* p);
+int padded_forward(const kda_chunk_problem* p, const void* q, const void* k, const void* v, const void* gate,
+                   const void* beta_logits, const float* A_log, const float* dt_bias, const float* initial_state,
+                   void* output, float* final_state, void* workspace, hipStream_t stream);
+int padded_backward(const kda_chunk_problem* p, const void* beta_logits, const float* A_log, const void* workspace,
+                    const void* grad_output, const float* grad_final_state, void* dq, void* dk, void* dv,
+                    void* dgate, void* dbeta_logits, float* dA_log, float* ddt_bias, float* dinitial_state,
+                    void* scratch, hipStream_t stream);
+int padded_status(const kda_chunk_problem* p, const void* scratch, hipStream_t stream);
+
 constexpr size_t cmax_sz(size_t x, size_t y) { return x > y ? x : y; }
 
 // Compute units of the current device (launch granularity of the chunk-parallel rounds and

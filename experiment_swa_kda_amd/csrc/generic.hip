@@ -745,4 +745,184 @@ int generic_backward(const kda_chunk_problem* p, const void* q, const void* k, c
   return KDA_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// zero-padded route: K <= 128 and V <= 128 run the chunked kernels at K, V rounded up to 64
+// or 128.  Zero keys and zero value columns are exact: a zero key row of q and k leaves the
+// L2 norms, every k^T S and q^T S and the state rows of the real keys unchanged, and its own
+// state row never leaves zero; a zero value column (v = 0, no state, dO = 0) keeps its state
+// column and every gradient contribution at zero.  The padded copies of q, k, v and the gate
+// live behind the chunked workspace, so the backward reads the same padded inputs.
+// ---------------------------------------------------------------------------
+
+// dst[t][h][c] = c < w_src ? src[t][h][c] : 0 for c < w_dst, rows of H heads; token strides
+// ld_src / ld_dst (elements), head strides w_src / w_dst.  One wave per (token, head) row.
+template <typename T>
+__global__ __launch_bounds__(256) void pad_rows_kernel(int nrows, int H, int w_src, long ld_src, int w_dst,
+                                                       long ld_dst, const T* __restrict__ src, T* __restrict__ dst) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int r = blockIdx.x * 4 + wave; r < nrows; r += gridDim.x * 4) {
+    const int t = r / H, h = r - t * H;
+    const T* s = src + (size_t)t * ld_src + (size_t)h * w_src;
+    T* d = dst + (size_t)t * ld_dst + (size_t)h * w_dst;
+    for (int c = lane; c < w_dst; c += kWave) d[c] = c < w_src ? s[c] : T(0.f);
+  }
+}
+
+template <typename T>
+static int pad_rows(long nrows, int H, int w_src, long ld_src, int w_dst, long ld_dst, const void* src, void* dst,
+                    hipStream_t stream) {
+  if (nrows <= 0) return KDA_OK;
+  KDA_REQUIRE(nrows < (1L << 31), "padded KDA: too many rows");
+  const long blocks = (nrows + 3) / 4;
+  hipLaunchKernelGGL(pad_rows_kernel<T>, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, stream,
+                     (int)nrows, H, w_src, ld_src, w_dst, ld_dst, (const T*)src, (T*)dst);
+  KDA_LAUNCH_CHECK("padded KDA copy");
+  return KDA_OK;
+}
+
+bool padded_route(const kda_chunk_problem* p) {
+  return generic_dims(p) && p->key_dim <= 128 && p->value_dim <= 128;
+}
+
+static kda_chunk_problem padded_problem(const kda_chunk_problem* p) {
+  kda_chunk_problem pp = *p;
+  pp.key_dim = p->key_dim <= 64 ? 64 : 128;
+  pp.value_dim = p->value_dim <= 64 ? 64 : 128;
+  pp.grad_row_stride = 0;
+  pp.norm_gate_row_stride = 0;
+  return pp;
+}
+
+// Regions behind the chunked workspace: qp, kp, vp, gp, dtp, s0p, outp, sfinp.
+enum { PW_FAST, PW_Q, PW_K, PW_V, PW_G, PW_DT, PW_S0, PW_OUT, PW_SFIN, PW_END };
+// Regions of the backward scratch: the chunked scratch, then dop, dsfp, dqp, dkp, dvp, dgp, ddtp, ds0p.
+enum { PS_FAST, PS_DO, PS_DSF, PS_DQ, PS_DK, PS_DV, PS_DG, PS_DDT, PS_DS0, PS_END };
+
+static void padded_ws_layout(const kda_chunk_problem* p, size_t off[PW_END + 1]) {
+  const kda_chunk_problem pp = padded_problem(p);
+  const size_t rowsH = (size_t)p->batch * p->seq_len * p->heads;
+  const size_t gsz = p->gate_mode == KDA_GATE_K3 ? 2 : 4;
+  const size_t st = (size_t)p->num_seqs * p->heads * pp.value_dim * pp.key_dim * 4;
+  const size_t sz[PW_END] = {kda_chunk_workspace_bytes(&pp), rowsH * pp.key_dim * 2, rowsH * pp.key_dim * 2,
+                             rowsH * pp.value_dim * 2,        rowsH * pp.key_dim * gsz,
+                             (size_t)p->heads * pp.key_dim * 4, st, rowsH * pp.value_dim * 2, st};
+  off[0] = 0;
+  for (int i = 0; i < PW_END; ++i) off[i + 1] = off[i] + align256(sz[i]);
+}
+
+static void padded_sc_layout(const kda_chunk_problem* p, size_t off[PS_END + 1]) {
+  const kda_chunk_problem pp = padded_problem(p);
+  const size_t rowsH = (size_t)p->batch * p->seq_len * p->heads;
+  const size_t gsz = p->gate_mode == KDA_GATE_K3 ? 2 : 4;
+  const size_t st = (size_t)p->num_seqs * p->heads * pp.value_dim * pp.key_dim * 4;
+  const size_t sz[PS_END] = {kda_chunk_backward_scratch_bytes(&pp), rowsH * pp.value_dim * 2, st,
+                             rowsH * pp.key_dim * 2, rowsH * pp.key_dim * 2, rowsH * pp.value_dim * 2,
+                             rowsH * pp.key_dim * gsz, (size_t)p->heads * pp.key_dim * 4, st};
+  off[0] = 0;
+  for (int i = 0; i < PS_END; ++i) off[i + 1] = off[i] + align256(sz[i]);
+}
+
+size_t padded_ws_bytes(const kda_chunk_problem* p) {
+  size_t off[PW_END + 1];
+  padded_ws_layout(p, off);
+  return off[PW_END] + 256;
+}
+
+size_t padded_sc_bytes(const kda_chunk_problem* p) {
+  size_t off[PS_END + 1];
+  padded_sc_layout(p, off);
+  return off[PS_END] + 256;
+}
+
+#define KDA_TRY(call)              \
+  do {                             \
+    const int _rc = (call);        \
+    if (_rc != KDA_OK) return _rc; \
+  } while (0)
+
+int padded_forward(const kda_chunk_problem* p, const void* q, const void* k, const void* v, const void* gate,
+                   const void* beta_logits, const float* A_log, const float* dt_bias, const float* initial_state,
+                   void* output, float* final_state, void* workspace, hipStream_t stream) {
+  const kda_chunk_problem pp = padded_problem(p);
+  size_t off[PW_END + 1];
+  padded_ws_layout(p, off);
+  char* w = (char*)workspace;
+  const int K = p->key_dim, V = p->value_dim, Kp = pp.key_dim, Vp = pp.value_dim, H = p->heads;
+  const long toks = (long)p->batch * p->seq_len, nst = (long)p->num_seqs * H * V;
+  const bool k3 = p->gate_mode == KDA_GATE_K3;
+  KDA_TRY(pad_rows<bf16>(toks * H, H, K, (long)H * K, Kp, (long)H * Kp, q, w + off[PW_Q], stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, K, (long)H * K, Kp, (long)H * Kp, k, w + off[PW_K], stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, V, (long)H * V, Vp, (long)H * Vp, v, w + off[PW_V], stream));
+  if (k3) {
+    KDA_TRY(pad_rows<bf16>(toks * H, H, K, (long)H * K, Kp, (long)H * Kp, gate, w + off[PW_G], stream));
+    KDA_TRY(pad_rows<float>(H, H, K, (long)H * K, Kp, (long)H * Kp, dt_bias, w + off[PW_DT], stream));
+  } else {
+    KDA_TRY(pad_rows<float>(toks * H, H, K, (long)H * K, Kp, (long)H * Kp, gate, w + off[PW_G], stream));
+  }
+  float* s0p = nullptr;
+  if (initial_state) {
+    // [N][H][V][K] -> [N][H][Vp][Kp]: rows (n, h, v) padded to Kp, then the Vp - V zero rows
+    s0p = (float*)(w + off[PW_S0]);
+    KDA_TRY(pad_rows<float>((long)p->num_seqs * H, 1, V * K, (long)V * K, Vp * Kp, (long)Vp * Kp, initial_state,
+                            s0p, stream));  // zero tail of each (n, h) block
+    KDA_TRY(pad_rows<float>(nst, V, K, (long)V * K, Kp, (long)Vp * Kp, initial_state, s0p, stream));
+  }
+  float* sfp = final_state ? (float*)(w + off[PW_SFIN]) : nullptr;
+  bf16* outp = (bf16*)(w + off[PW_OUT]);
+  KDA_TRY(kda_chunk_forward(&pp, w + off[PW_Q], w + off[PW_K], w + off[PW_V], w + off[PW_G], beta_logits, A_log,
+                            k3 ? (const float*)(w + off[PW_DT]) : dt_bias, s0p, outp, sfp, w + off[PW_FAST],
+                            stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, Vp, (long)H * Vp, V, (long)H * V, outp, output, stream));
+  if (final_state) KDA_TRY(pad_rows<float>(nst, V, Kp, (long)Vp * Kp, K, (long)V * K, sfp, final_state, stream));
+  return KDA_OK;
+}
+
+int padded_backward(const kda_chunk_problem* p, const void* beta_logits, const float* A_log, const void* workspace,
+                    const void* grad_output, const float* grad_final_state, void* dq, void* dk, void* dv,
+                    void* dgate, void* dbeta_logits, float* dA_log, float* ddt_bias, float* dinitial_state,
+                    void* scratch, hipStream_t stream) {
+  const kda_chunk_problem pp = padded_problem(p);
+  size_t wo[PW_END + 1], so[PS_END + 1];
+  padded_ws_layout(p, wo);
+  padded_sc_layout(p, so);
+  const char* w = (const char*)workspace;
+  char* sc = (char*)scratch;
+  const int K = p->key_dim, V = p->value_dim, Kp = pp.key_dim, Vp = pp.value_dim, H = p->heads;
+  const long toks = (long)p->batch * p->seq_len, nst = (long)p->num_seqs * H * V;
+  const bool k3 = p->gate_mode == KDA_GATE_K3;
+  const long gld_qk = p->grad_row_stride > 0 ? p->grad_row_stride : (long)H * K;
+  const long gld_v = p->grad_row_stride > 0 ? p->grad_row_stride : (long)H * V;
+  KDA_TRY(pad_rows<bf16>(toks * H, H, V, (long)H * V, Vp, (long)H * Vp, grad_output, sc + so[PS_DO], stream));
+  float* dsfp = nullptr;
+  if (grad_final_state) {
+    dsfp = (float*)(sc + so[PS_DSF]);
+    KDA_TRY(pad_rows<float>((long)p->num_seqs * H, 1, V * K, (long)V * K, Vp * Kp, (long)Vp * Kp,
+                            grad_final_state, dsfp, stream));
+    KDA_TRY(pad_rows<float>(nst, V, K, (long)V * K, Kp, (long)Vp * Kp, grad_final_state, dsfp, stream));
+  }
+  float* ds0p = dinitial_state ? (float*)(sc + so[PS_DS0]) : nullptr;
+  KDA_TRY(kda_chunk_backward(&pp, w + wo[PW_Q], w + wo[PW_K], w + wo[PW_V], w + wo[PW_G], beta_logits, A_log,
+                             k3 ? (const float*)(w + wo[PW_DT]) : nullptr, nullptr, w + wo[PW_FAST],
+                             sc + so[PS_DO], dsfp, sc + so[PS_DQ], sc + so[PS_DK], sc + so[PS_DV],
+                             sc + so[PS_DG], dbeta_logits, dA_log, k3 ? (float*)(sc + so[PS_DDT]) : nullptr,
+                             ds0p, sc + so[PS_FAST], stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, Kp, (long)H * Kp, K, gld_qk, sc + so[PS_DQ], dq, stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, Kp, (long)H * Kp, K, gld_qk, sc + so[PS_DK], dk, stream));
+  KDA_TRY(pad_rows<bf16>(toks * H, H, Vp, (long)H * Vp, V, gld_v, sc + so[PS_DV], dv, stream));
+  if (k3) {
+    KDA_TRY(pad_rows<bf16>(toks * H, H, Kp, (long)H * Kp, K, (long)H * K, sc + so[PS_DG], dgate, stream));
+    KDA_TRY(pad_rows<float>(H, H, Kp, (long)H * Kp, K, (long)H * K, sc + so[PS_DDT], ddt_bias, stream));
+  } else {
+    KDA_TRY(pad_rows<float>(toks * H, H, Kp, (long)H * Kp, K, (long)H * K, sc + so[PS_DG], dgate, stream));
+  }
+  if (dinitial_state) KDA_TRY(pad_rows<float>(nst, V, Kp, (long)Vp * Kp, K, (long)V * K, ds0p, dinitial_state, stream));
+  return KDA_OK;
+}
+
+int padded_status(const kda_chunk_problem* p, const void* scratch, hipStream_t stream) {
+  const kda_chunk_problem pp = padded_problem(p);
+  return kda_chunk_backward_status(&pp, scratch, stream);
+}
+
 }  // namespace kda

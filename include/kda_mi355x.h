@@ -40,8 +40,9 @@ typedef struct kda_chunk_problem {
   int32_t batch;       /* B */
   int32_t seq_len;     /* T (total packed length when cu_seqlens != NULL) */
   int32_t heads;       /* H */
-  int32_t key_dim;     /* K: 64 or 128 */
-  int32_t value_dim;   /* V: 64 or 128 */
+  int32_t key_dim;     /* K in [1, 256]: 64 and 128 run the chunked kernels, other sizes the
+                          token-serial ones (as the reference's generic lane, chunk.cu:135-213) */
+  int32_t value_dim;   /* V in [1, 4096] (chunked kernels when K and V are 64 or 128) */
   int32_t num_seqs;    /* B without cu_seqlens; number of packed sequences with it */
   const int32_t* cu_seqlens; /* device pointer or NULL */
   int32_t gate_mode;   /* KDA_GATE_K3 or KDA_GATE_LOGDECAY */
@@ -107,7 +108,8 @@ int kda_chunk_forward(const kda_chunk_problem* p,
  *   norm_gate bf16 [B,T,H,V], norm_weight f32 [V], epsilon >= 0,
  *   norm_output bf16 [B,T,H,V] = rms_norm(bf16(o), weight, eps) * sigmoid(norm_gate),
  *   inverse_rms f32 [B*T*H] (what kda_rmsnorm_gate_backward takes).
- * value_dim must be 64 or 128.
+ * key_dim and value_dim must be 64 or 128 (other sizes: kda_chunk_forward, then
+ * kda_rmsnorm_gate_forward).
  */
 int kda_chunk_forward_norm_gate(const kda_chunk_problem* p,
                                 const void* q, const void* k, const void* v, const void* gate,
@@ -239,7 +241,8 @@ int kda_chunk_backward_stage(int32_t stage, const kda_chunk_problem* p, const vo
  * (nanochat/mixers/cuda_kda/recurrent_decode.cu:24-181, schema :186-189).
  *   q, k, gate [B,1,H,K] bf16 (gate K3 raw logits), v [B,1,H,V] bf16, beta_logits [B,1,H] bf16
  *   initial_state f32 [B,H,V,K] or NULL; output bf16 [B,1,H,V]; final_state f32 [B,H,V,K]
- *   or NULL.  final_state may alias initial_state (in-place update).
+ *   or NULL.  final_state may alias initial_state (in-place update).  key_dim in [1, 256]
+ *   (64 and 128 on the vector kernel, other sizes one step of the token-serial kernel).
  */
 int kda_recurrent_decode(int32_t batch, int32_t heads, int32_t key_dim, int32_t value_dim,
                          int32_t gate_mode, float lower_bound, float scale,
@@ -290,7 +293,8 @@ int kda_causal_conv_backward_strided(int32_t batch, int32_t seq_len, int32_t cha
                                      hipStream_t stream);
 
 /*
- * Fused RMSNorm(x) * weight * sigmoid(gate) over rows of D = 128 (or 64).  Replaces
+ * Fused RMSNorm(x) * weight * sigmoid(gate) over rows of D in [1, 1024] (16-byte vector
+ * kernels for D = 64 and 128, one wave per row otherwise).  Replaces
  * torch.ops.nanochat_kda.rmsnorm_gate_forward (nanochat/mixers/cuda_kda/rmsnorm_gate.cu:31-71,
  * schema :278-280).  x, gate, output [rows, D] bf16; weight [D] f32; inv_rms [rows] f32.
  */

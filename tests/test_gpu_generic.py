@@ -1,6 +1,7 @@
-"""GPU parity of the token-serial kernels (head dims other than 64 / 128) against the float64
-oracle: forward, backward, packed sequences, decode, the norm-gate kernels and the mixer
-paths that route to them.  The reference takes any head dim through its generic lane
+"""GPU parity of the head dims other than 64 / 128 against the float64 oracle: the
+zero-padded chunked route (K, V <= 128) and the token-serial kernels (larger K or V):
+forward, backward, packed sequences, decode, the norm-gate kernels and the mixer paths that
+route to them.  The reference takes any head dim through its generic lane
 (nanochat/mixers/cuda_kda/chunk.cu:135-213, :578-870)."""
 
 from __future__ import annotations
@@ -18,9 +19,12 @@ pytestmark = pytest.mark.gpu
 if torch.cuda.is_available():
     from experiment_swa_kda_amd import kda, ops
 
-# (K, V) pairs covering every keys-per-lane instance (K <= 16, 32, 64, 128, 256), V not a
-# multiple of 16 (partial column groups) and the fast sizes mixed with generic ones
-SHAPES = [(16, 16), (32, 48), (96, 96), (200, 40), (256, 64), (128, 96), (64, 200), (7, 5)]
+# K, V <= 128 take the zero-padded chunked route: (16, 16), (32, 48), (96, 96), (128, 96), (7, 5).
+# The rest take the token-serial kernels, one pair per keys-per-lane instance (K <= 16, 32,
+# 64, 128, 256), with V not a multiple of 16 (partial column groups): (16, 136), (32, 144),
+# (64, 200), (100, 130), (200, 40), (256, 64).
+SHAPES = [(16, 16), (32, 48), (96, 96), (128, 96), (7, 5),
+          (16, 136), (32, 144), (64, 200), (100, 130), (200, 40), (256, 64)]
 
 
 def oracle_fwd(d, gate):
@@ -99,13 +103,15 @@ def test_generic_backward_deterministic():
         assert x is None or torch.equal(x, y)
 
 
+@pytest.mark.parametrize("KV", [(48, 80), (160, 24)])
 @pytest.mark.parametrize("gate", ["k3", "precomputed"])
-def test_generic_varlen(gate):
+def test_generic_varlen(gate, KV):
     # packed sequences of ragged lengths, one of them empty
+    K, V = KV
     cu = torch.tensor([0, 5, 5, 40, 57, 100], dtype=torch.int32, device="cuda")
-    d = make_kda_inputs(1, 100, 2, 48, 80, seed=11, gate=gate)
+    d = make_kda_inputs(1, 100, 2, K, V, seed=11, gate=gate)
     g = torch.Generator().manual_seed(12)
-    d["s0"] = (torch.randn(5, 2, 80, 48, generator=g) * 0.05).cuda()
+    d["s0"] = (torch.randn(5, 2, V, K, generator=g) * 0.05).cuda()
     out, fin = run_fwd(d, gate, cu)
     gm = "k3" if gate == "k3" else "logdecay"
     eo, ef = O.kda_varlen_forward(np64(d["q"]), np64(d["k"]), np64(d["v"]), np64(d["g"]), np64(d["beta"]),
