@@ -47,9 +47,10 @@ STAGES = {"fwd_intra": 1, "fwd_scan": 2, "fwd_output": 3, "bwd_scan": 10, "bwd_d
           "bwd_dense_decay": 14, "bwd_fused": None}
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
-# the backward's compulsory HBM I/O at config 2 (q, k, v, dO, g, beta and the output in;
-# dq, dk, dv, dg, dbeta out), the secondary bytes figure of the dominant kernel
-BWD_COMPULSORY_BYTES = 56_700_000
+# the backward's compulsory HBM I/O at config 2 with the precomputed gate: q, k, v, dO bf16,
+# g f32 and beta bf16 in; dq, dk, dv bf16, dg f32 and dbeta bf16 out (the secondary bytes
+# figure of the dominant kernel)
+BWD_COMPULSORY_BYTES = 4 * 6_291_456 + 12_582_912 + 49_152 + 3 * 6_291_456 + 12_582_912 + 49_152
 
 
 def parse():
