@@ -98,8 +98,11 @@ struct PrepLds {
   static constexpr int bytes = off_w + 64 * KP * 2;
 };
 
+// The fused launch's scheduling (sync words, tile order; defined with chunk_bwd_sched_kernel).
+__device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks, int sync_words);
+
 template <int K, int V>
-__global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a, int sched_words) {
   using L = PrepLds<K, V>;
   constexpr int OP = L::OP, KP = L::KP, KB = K / 16, VB = V / 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -108,6 +111,12 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a)
   bf16* sKd = (bf16*)(smem + L::off_kd);
   bf16* sW = (bf16*)(smem + L::off_w);
   const int cidx = blockIdx.x, h = blockIdx.y, H = a.H;
+  if (sched_words > 0 && cidx == (int)gridDim.x - 1) {
+    // one extra column of workgroups: (x = last, y = 0) does the fused launch's scheduling
+    // (sync words, tile order), saving a launch of its own
+    if (h == 0) bwd_sched_body(a, cidx, sched_words);
+    return;
+  }
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
   const int len = ch.y, row0 = ch.x;
   if (len <= 0) return;
@@ -1546,7 +1555,7 @@ __device__ void poison_tile(const BwdArgs& a, int cidx, int h) {
 // has reverse rank r = n - 1 - (index in s); chunks go by r, then by sequence.  Position
 // of c = sum over sequences s' of min(n_s', r) + #{s' < s : n_s' > r}; chunks past the
 // last sequence keep their index.
-__global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int max_chunks, int sync_words) {
+__device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks, int sync_words) {
   int* sync = (int*)a.sc.p[S_SYNC];
   int* order = (int*)a.sc.p[S_ORDER];
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
@@ -1566,6 +1575,10 @@ __global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int ma
     }
     order[pos] = c;
   }
+}
+
+__global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int max_chunks, int sync_words) {
+  bwd_sched_body(a, max_chunks, sync_words);
 }
 
 template <int K, int V>
@@ -1681,12 +1694,15 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
   const int all = (1 << (KDA_STAGE_BWD_SCAN - 10)) | (1 << (KDA_STAGE_BWD_DENSE - 10)) |
                   (1 << (KDA_STAGE_BWD_DECAY - 10));
   // the reverse scan's per-chunk transition -G and inhomogeneous term E (chunk-parallel)
-  auto launch_prep = [&]() -> int {
+  // sched_words > 0: the prep launch also clears the fused launch's sync words and writes
+  // its tile order (one extra column of workgroups)
+  auto launch_prep = [&](int sched_words) -> int {
     auto prep = chunk_bwd_prep_kernel<K, V>;
     constexpr int smem_p = PrepLds<K, V>::bytes;
     if (ensure_lds_limit((const void*)prep, smem_p) != hipSuccess)
       return set_error(KDA_ERR_LAUNCH, "chunk_backward: prep LDS attribute failed");
-    hipLaunchKernelGGL(prep, dim3(g.max_chunks, p->heads), dim3(kPrepThreads), smem_p, stream, a);
+    hipLaunchKernelGGL(prep, dim3(g.max_chunks + (sched_words > 0 ? 1 : 0), p->heads), dim3(kPrepThreads), smem_p,
+                       stream, a, sched_words);
     KDA_LAUNCH_CHECK("chunk_backward prep");
     return KDA_OK;
   };
@@ -1700,10 +1716,8 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     const int nrec = p->num_seqs * p->heads;
     const int scan_blocks = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
     const int N = g.max_chunks * p->heads;
-    int rc = launch_prep();
+    int rc = launch_prep(sync_words(nrec, N));
     if (rc != KDA_OK) return rc;
-    hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks, sync_words(nrec, N));
-    KDA_LAUNCH_CHECK("chunk_backward sched");
     hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks,
                        wait_limit_ticks());
     KDA_LAUNCH_CHECK("chunk_backward fused");
@@ -1718,7 +1732,7 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
   }
   if (p->num_seqs > 0 && (stages & (1 << (KDA_STAGE_BWD_SCAN - 10)))) {
     if (g.max_chunks > 0) {
-      int rc = launch_prep();
+      int rc = launch_prep(0);
       if (rc != KDA_OK) return rc;
     }
     auto scan = chunk_bwd_scan_kernel<K, V>;
