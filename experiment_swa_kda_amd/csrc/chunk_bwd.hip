@@ -233,6 +233,13 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
 // order -G was emitted in, f32 in accumulator order for the history), slot r loaded.
 constexpr int kBwdRing = 3;
 constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
+#ifndef KDA_PUB_LAG
+#define KDA_PUB_LAG 3
+#endif
+// fused launch: the history wave publishes step r - kPubLag at step r, so the write-through
+// stores of kPubLag - 1 steps stay in flight (their completion takes longer than a step when
+// the VJP tiles load the memory system)
+constexpr int kPubLag = KDA_PUB_LAG;
 constexpr int kBwdThreads = 6 * kWave;
 
 template <int K, int V>
@@ -392,13 +399,13 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     // ---- history wave: X_c of step r (f32 staging, accumulator order: element (k, v) at
     // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4) is read after S(r) and stored as
     // bf16 into the strip's [K][16] block of the strip-major history, 512 contiguous bytes
-    // per store instruction.  In the fused launch step r - 2 is published once its stores
+    // per store instruction.  In the fused launch step r - kPubLag is published once its stores
     // have completed (write-through stores may take microseconds) ----
     for (int r = 0; r < n; ++r) {
-      if (PUB && r >= 2) wait_vmcnt<K / 16>();  // step r - 2's stores
+      if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * (K / 16)>();  // step r - kPubLag's stores
       ring_barrier();  // S(r)
-      if (PUB && r >= 2 && lane == 0)
-        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r - 2), r - 2);
+      if (PUB && r >= kPubLag && lane == 0)
+        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r - kPubLag), r - kPubLag);
       const float* dsf = (const float*)(smem + L::off_dsf + (r & 1) * K * 16 * 4);
       float4 hv[K / 16];
 #pragma unroll
@@ -420,8 +427,8 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     if (PUB) {
       wait_vmcnt<0>();
       if (lane == 0) {
-        if (n > 1) publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(n - 2), n - 2);
-        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(n - 1), n - 1);
+        for (int r = n > kPubLag ? n - kPubLag : 0; r < n; ++r)
+          publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r), r);
       }
       ring_barrier();  // final
     }
