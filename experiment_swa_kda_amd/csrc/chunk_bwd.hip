@@ -225,13 +225,13 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
 }
 
 // One workgroup per (sequence, head, 16-wide V strip) walks the chunks backwards: four
-// compute waves (wave w owns the X tiles w K/64 .., as MFMA accumulators), a loader wave
-// that streams each chunk's -G fragments, E strip and lam into a kBwdRing-deep LDS ring with
-// direct global->LDS loads (two chunks ahead), and a history wave that copies X_c out of
-// LDS to the strip-major history and, in the fused launch, publishes the step.  Per chunk
-// the waves meet at one barrier S(r): X_c staged (bf16 B operand in the permuted contraction
-// order -G was emitted in, f32 in accumulator order for the history), slot r loaded.
-constexpr int kBwdRing = 3;
+// compute waves (wave w owns the X tiles w K/64 .., as MFMA accumulators, and loads its own
+// rows of each chunk's -G into registers one step ahead), a loader wave that streams each
+// chunk's E strip and lam into a kBwdRing-deep LDS ring with direct global->LDS loads (two
+// chunks ahead), and a history wave that copies X_c out of LDS to the strip-major history
+// and, in the fused launch, publishes the step.  Per chunk the waves meet at one barrier
+// S(r): X_c staged as bf16 (the B operand, in the permuted contraction order -G was emitted
+// in), slot r loaded.
 constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 #ifndef KDA_PUB_LAG
 #define KDA_PUB_LAG 3
@@ -240,19 +240,22 @@ constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 // stores of kPubLag - 1 steps stay in flight (their completion takes longer than a step when
 // the VJP tiles load the memory system)
 constexpr int kPubLag = KDA_PUB_LAG;
-constexpr int kBwdThreads = 6 * kWave;
+#ifndef KDA_SCAN_CW
+#define KDA_SCAN_CW 4
+#endif
+constexpr int kScanCW = KDA_SCAN_CW;              // compute waves of a scan workgroup
+constexpr int kBwdThreads = (kScanCW + 2) * kWave;  // + the loader and the history wave
 
+constexpr int kBwdRing = 3;
 template <int K, int V>
 struct BwdScanLds {
-  static constexpr int off_g = 0;                         // -G fragments, K x K bf16
-  static constexpr int off_e = off_g + K * K * 2;         // E strip [K/16][64][4] f32
+  static constexpr int off_e = 0;                         // E strip [K/16][64][4] f32
   static constexpr int off_lam = off_e + K * 16 * 4;      // lam, K f32
   static constexpr int slot = off_lam + K * 4;
-  static constexpr int n_load = (K * K * 2 + K * 16 * 4) / 1024 + 1;
+  static constexpr int n_load = (K * 16 * 4) / 1024 + 1;
   static constexpr int SP = K + 8;
   static constexpr int off_ds = kBwdRing * slot;          // X_c bf16 [v][k] (x2, by step parity)
-  static constexpr int off_dsf = off_ds + 2 * 16 * SP * 2;  // X_c f32 in accumulator order [K/16][64][4] (x2)
-  static constexpr int bytes = off_dsf + 2 * K * 16 * 4;
+  static constexpr int bytes = off_ds + 2 * 16 * SP * 2;
   static_assert(n_load < 64, "vmcnt range");
 };
 
@@ -291,34 +294,31 @@ __device__ __forceinline__ void prefetch_lines(const PrefetchList& pf, int w, in
 // L2 write-back or invalidate is needed around the counts -- the write-back of a whole L2 per
 // scan step costs microseconds on the scan's serial chain.
 
-// Layout of the fused backward's sync words (ints): [0] ticket, [1] abort, record rec's
-// count of finished steps at kSyncRec + 32 rec (one 128-byte line each), then per tile the
-// number of strips that finished it.
+// Layout of the fused backward's sync words (ints): [0] ticket, [1] abort, then per record
+// rec one 128-byte line at kSyncRec + 32 rec holding each V strip's count of finished steps
+// (the tail of the buffer, one word per tile, is cleared but unused).
 constexpr int kSyncRec = 32;
 __host__ __device__ inline int sync_words(int nrec, int tiles) { return kSyncRec + 32 * nrec + tiles; }
 
-// One more step of this strip is in memory: every store of the step was written through
-// and waited for (vmcnt 0) before the barrier that precedes the call.  The strip that
-// completes a step on all strips of the record raises the record's count to step + 1 (the
-// strips are independent workgroups that drift apart by several steps; the last to finish
-// step r finishes after every strip's step r - 1, and atomic max keeps the count monotone
-// whatever order the raises land in).  Waiting tiles poll one word per record.
-template <int NS>
-__device__ __forceinline__ void publish_step(int* sync, int nrec, int rec, size_t tile, int step) {
-  int* arrive = sync + kSyncRec + 32 * nrec + tile;
-  if (__hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == NS - 1)
-    __hip_atomic_fetch_max(sync + kSyncRec + 32 * rec, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// One more step of this strip is in memory: every store of the step was written through and
+// waited for (vmcnt) before the call.  Each strip raises its own word (a store, nothing to
+// wait for on the scan's chain); a waiting tile takes the minimum over the record's strips.
+__device__ __forceinline__ void publish_strip(int* sync, int rec, int strip, int step) {
+  __hip_atomic_store(sync + kSyncRec + 32 * rec + strip, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The scan of one (sequence, head, V strip), run by the first six waves of the workgroup.
 // PUB: the workgroup is a scan member of the fused backward launch -- waves past the six
 // only mirror the barriers (waves 6 and 7 pull operands into L2 ahead of the ring), and
-// after each step's history (X_c) is stored, progress[rec][strip] is raised by one: r + 1
+// after each step's history (X_c) is stored, the strip's progress word is raised: r + 1
 // means the strip has finished the r + 1 last chunks of the sequence.
 template <int K, int V, bool PUB>
 __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   using L = BwdScanLds<K, V>;
-  constexpr int KT = K / 16 / 4, NB = K / 32, SP = L::SP;
+  // CW waves own the K / 16 X tiles (KT each); at K = 64 with eight compute-wave slots the
+  // last four only mirror the barriers
+  constexpr int CW = K / 16 < kScanCW ? K / 16 : kScanCW;
+  constexpr int KT = K / 16 / CW, NB = K / 32, SP = L::SP;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int H = a.H;
   int rec, strip;
@@ -330,15 +330,16 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   const int n = sq.y;
   auto tile_of = [&](int r) { return (size_t)(sq.x + max(n - 1 - r, 0)) * H + h; };  // step r's chunk
 
-  if (PUB && wave >= 6) {
-    // Waves 6 and 7 pull the operands of the step kBwdPrefetch ahead into the XCD's L2: the
+  if (PUB && wave >= kScanCW + 2) {
+    // The two waves after the history wave pull the operands of the step kBwdPrefetch ahead
+    // into the XCD's L2: the
     // shared -G and lam lines split over the record's strips (every strip of a record runs
     // on one XCD), plus this strip's own E lines.  The lines land in a scratch LDS row.
     if (n <= 0) return;
-    const int pl = (wave - 6) * kWave + lane;
+    const int pl = (wave - kScanCW - 2) * kWave + lane;
     char* sink = smem + L::bytes + (wave & 1) * 1024;
     auto prefetch = [&](int q) {
-      if (wave >= 8 || q >= n) return;
+      if (wave >= kScanCW + 4 || q >= n) return;
       const size_t tile = tile_of(q);
       constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * 4 / 128;
       constexpr int kShared = (kG + kLam + 7) / 8;  // lanes for this strip's share
@@ -371,14 +372,11 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     }
     return;
   }
-  if (wave == 4) {
-    // ---- loader wave: step r's slot (r % kBwdRing) holds -G, the E strip and lam ----
+  if (wave == kScanCW) {
+    // ---- loader wave: step r's slot (r % kBwdRing) holds the E strip and lam ----
     auto issue = [&](int r) {
       const size_t tile = tile_of(r);  // clamped past the last step: a fixed load count
       char* slot = smem + (r % kBwdRing) * L::slot;
-      const char* g = (const char*)((const bf16*)a.sc.p[S_NG] + tile * K * K) + lane * 16;
-#pragma unroll
-      for (int b = 0; b < (K * K * 2) / 1024; ++b) dma16(g + b * 1024, slot + L::off_g + b * 1024);
       const char* e = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)strip * K * 16) + lane * 16;
 #pragma unroll
       for (int b = 0; b < (K * 16 * 4) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
@@ -395,46 +393,45 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
     return;
   }
-  if (wave == 5) {
-    // ---- history wave: X_c of step r (f32 staging, accumulator order: element (k, v) at
-    // tile k / 16, lane v + 16 ((k % 16) / 4), value k % 4) is read after S(r) and stored as
-    // bf16 into the strip's [K][16] block of the strip-major history, 512 contiguous bytes
-    // per store instruction.  In the fused launch step r - kPubLag is published once its stores
+  if (wave == kScanCW + 1) {
+    // ---- history wave: X_c of step r (bf16 [v][k] in LDS) is read after S(r) and stored
+    // into the strip's [K][16] block of the strip-major history, 512 contiguous bytes per
+    // store instruction.  In the fused launch step r - kPubLag is published once its stores
     // have completed (write-through stores may take microseconds) ----
     for (int r = 0; r < n; ++r) {
-      if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * (K / 16)>();  // step r - kPubLag's stores
+      // step r - kPubLag's stores (each later step added K / 16 stores and one publish)
+      if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * (K / 16 + 1)>();
       ring_barrier();  // S(r)
-      if (PUB && r >= kPubLag && lane == 0)
-        publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r - kPubLag), r - kPubLag);
-      const float* dsf = (const float*)(smem + L::off_dsf + (r & 1) * K * 16 * 4);
-      float4 hv[K / 16];
+      if (PUB && r >= kPubLag && lane == 0) publish_strip(progress, rec, strip, r - kPubLag);
+      // X_c as bf16 [v][k] (the compute waves' B-operand staging): one transposing read per
+      // 16 keys gives lane l keys 16 it + l % 16, values 4 (l / 16) .. + 3
+      const bf16* sx = (const bf16*)(smem + L::off_ds + (r & 1) * 16 * SP * 2);
+      bf16x4 hv[K / 16];
 #pragma unroll
-      for (int it = 0; it < K / 16; ++it) {
-        const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
-        const float* f = dsf + ((kk / 16) * 64 + 16 * ((kk % 16) / 4) + c4) * 4 + kk % 4;
-        hv[it] = make_float4(f[0], f[4], f[8], f[12]);
-      }
+      for (int it = 0; it < K / 16; ++it) hv[it] = lds_col_frag4(sx, SP, 0, 16 * it, lane);
       bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile_of(r) * K * V + (size_t)strip * K * 16;
 #pragma unroll
       for (int it = 0; it < K / 16; ++it) {
-        const int idx = it * 64 + lane, kk = idx / 4, c4 = (idx % 4) * 4;
+        const int kk = 16 * it + lr, c4 = 4 * kg;
         if (PUB)
-          store8_coherent(DSH, (kk * 16 + c4) * 2, f4_to_bf16x4(hv[it]));
+          store8_coherent(DSH, (kk * 16 + c4) * 2, hv[it]);
         else
-          *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = f4_to_bf16x4(hv[it]);
+          *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = hv[it];
       }
     }
     if (PUB) {
       wait_vmcnt<0>();
-      if (lane == 0) {
-        for (int r = n > kPubLag ? n - kPubLag : 0; r < n; ++r)
-          publish_step<V / 16>(progress, a.num_seqs * H, rec, tile_of(r), r);
-      }
+      if (lane == 0) publish_strip(progress, rec, strip, n - 1);
       ring_barrier();  // final
     }
     return;
   }
 
+  if (wave >= CW) {
+    for (int r = 0; r < n; ++r) ring_barrier();
+    if (PUB) ring_barrier();  // final
+    return;
+  }
   // ---- compute waves: X tiles wave * KT .. (rows 16 kt + 4 (l / 16) + r, column l % 16) ----
   f32x4 X[KT];
 #pragma unroll
@@ -447,11 +444,24 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
       X[kt] = zero4();
     }
   }
-  for (int r = 0; r < n; ++r) {
-    const char* slot = smem + (r % kBwdRing) * L::slot;
+  // Step r's -G rows of this wave's X tiles (permuted A fragments, 8 KB per wave) go straight
+  // from memory into registers, one step ahead of their use: staged in LDS (a DMA write and a
+  // read of 32 KB per step) they made the CU's LDS bandwidth the bound of the step.  The prep
+  // launch wrote them; the fused launch's look-ahead waves pull them into L2 a few steps
+  // earlier.
+  struct Ops {
+    bf16x8 g[KT][NB];
+  };
+  auto load_ops = [&](Ops& o, int r) {
+    const bf16* G = (const bf16*)a.sc.p[S_NG] + tile_of(r) * K * K;  // clamped past the last step
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int s = 0; s < NB; ++s) o.g[kt][s] = *(const bf16x8*)(G + frag_off(K, wave * KT + kt, s, lane));
+  };
+  auto step = [&](int r, const Ops& o) {
     bf16* sDS = (bf16*)(smem + L::off_ds + (r & 1) * 16 * SP * 2);
-    float* sDSf = (float*)(smem + L::off_dsf + (r & 1) * K * 16 * 4);
-    // stage X_c: bf16 [v][k] (B operand) and f32 accumulator order (history)
+    // stage X_c as bf16 [v][k]: the B operand of every compute wave, and the history's source
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int k0 = 16 * (wave * KT + kt) + 4 * kg;
@@ -459,7 +469,6 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(X[kt][q]);
       *(bf16x4*)(sDS + lr * SP + k0) = x;
-      *(f32x4*)(sDSf + ((wave * KT + kt) * 64 + lane) * 4) = X[kt];
     }
     wait_lgkm0();
     ring_barrier();  // S(r)
@@ -472,6 +481,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
       const bf16x4 hi = *(const bf16x4*)(sDS + lr * SP + 32 * s + 16 + 4 * kg);
       xb[s] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+    const char* slot = smem + (r % kBwdRing) * L::slot;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const int ktg = wave * KT + kt;
@@ -483,9 +493,18 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
       acc[2] = fmaf(lam.z, X[kt][2], e[2]);
       acc[3] = fmaf(lam.w, X[kt][3], e[3]);
 #pragma unroll
-      for (int s = 0; s < NB; ++s)
-        acc = mfma16(*(const bf16x8*)(slot + L::off_g + frag_off(K, ktg, s, lane) * 2), xb[s], acc);
+      for (int s = 0; s < NB; ++s) acc = mfma16(o.g[kt][s], xb[s], acc);
       X[kt] = acc;
+    }
+  };
+  Ops o0, o1;
+  load_ops(o0, 0);
+  for (int r = 0; r < n; r += 2) {
+    load_ops(o1, r + 1);
+    step(r, o0);
+    if (r + 1 < n) {
+      load_ops(o0, r + 2);
+      step(r + 1, o1);
     }
   }
   if (PUB) ring_barrier();  // final
@@ -1505,7 +1524,8 @@ __device__ __forceinline__ SyncView sync_view(const BwdArgs& a) {
 // A wait that gives up (or finds the abort word set) records it in *failed (LDS).
 struct ScanGate {
   static constexpr bool kCoherent = true;
-  const int* p;
+  const int* p;  // the record's strip counts
+  int nstrips;
   int need;
   int* abort;
   long long spin_limit;
@@ -1514,7 +1534,14 @@ struct ScanGate {
     if (threadIdx.x == 0) {
       const long long t0 = wall_clock64();
       for (;;) {
-        const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // up to 8 strips (V <= 128): the loads are issued together, then reduced
+        int w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          w[i] = i < nstrips ? __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : INT_MAX;
+        int v = w[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) v = min(v, w[i]);
         if (v >= need) break;
         if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
           *failed = 1;
@@ -1610,7 +1637,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
     rec = ch.z * H + h;
     need = ((const int2*)a.ws.p[R_SEQS])[ch.z].y - ch.w;
   }
-  ScanGate gate{sv.base + kSyncRec + 32 * rec, need, sv.abort, spin_limit, &s_failed};
+  ScanGate gate{sv.base + kSyncRec + 32 * rec, V / 16, need, sv.abort, spin_limit, &s_failed};
   dense_tile<K, V>(a, cidx, h, gate);
   __syncthreads();  // the dense part's stores are complete and visible to this workgroup
   decay_tile<K>(a, cidx, h);
