@@ -240,11 +240,12 @@ constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 // stores of kPubLag - 1 steps stay in flight (their completion takes longer than a step when
 // the VJP tiles load the memory system)
 constexpr int kPubLag = KDA_PUB_LAG;
-#ifndef KDA_SCAN_CW
-#define KDA_SCAN_CW 4
+constexpr int kScanCW = 4;                        // compute waves per V strip
+constexpr int kBwdThreads = (kScanCW + 2) * kWave;  // one strip + the loader and the history wave
+#ifndef KDA_FUSED_SPW
+#define KDA_FUSED_SPW 1
 #endif
-constexpr int kScanCW = KDA_SCAN_CW;              // compute waves of a scan workgroup
-constexpr int kBwdThreads = (kScanCW + 2) * kWave;  // + the loader and the history wave
+constexpr int kFusedSPW = KDA_FUSED_SPW;           // V strips per scan member of the fused launch
 
 constexpr int kBwdRing = 3;
 template <int K, int V>
@@ -307,49 +308,57 @@ __device__ __forceinline__ void publish_strip(int* sync, int rec, int strip, int
   __hip_atomic_store(sync + kSyncRec + 32 * rec + strip, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The scan of one (sequence, head, V strip), run by the first six waves of the workgroup.
-// PUB: the workgroup is a scan member of the fused backward launch -- waves past the six
-// only mirror the barriers (waves 6 and 7 pull operands into L2 ahead of the ring), and
-// after each step's history (X_c) is stored, the strip's progress word is raised: r + 1
-// means the strip has finished the r + 1 last chunks of the sequence.
-template <int K, int V, bool PUB>
+// The scan of SPW V strips of one (sequence, head) per workgroup: per strip four compute
+// waves (X tiles in MFMA accumulators), then one loader wave and one history wave for all
+// strips.  PUB: the workgroup is a scan member of the fused backward launch, where it takes
+// a whole CU like every tile workgroup (two strips per workgroup would leave half the scan's
+// CUs to the VJP tiles, but measured slower: 123 against 98 us for the backward call, the
+// scan's step lengthening with two compute waves per SIMD).  Its next waves pull the
+// operands into L2 ahead of the steps, the rest exit, and after each step's history (X_c)
+// is stored the strip's progress word is raised: r + 1 means the strip has finished the
+// r + 1 last chunks of the sequence.
+template <int K, int V, bool PUB, int SPW>
 __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   using L = BwdScanLds<K, V>;
-  // CW waves own the K / 16 X tiles (KT each); at K = 64 with eight compute-wave slots the
-  // last four only mirror the barriers
-  constexpr int CW = K / 16 < kScanCW ? K / 16 : kScanCW;
-  constexpr int KT = K / 16 / CW, NB = K / 32, SP = L::SP;
+  constexpr int CW = kScanCW, KT = K / 16 / CW, NB = K / 32, SP = L::SP;
+  static_assert(KT >= 1 && KT * CW == K / 16, "X tiles split evenly over the compute waves");
+  constexpr int NSG = V / 16 / SPW;  // strip groups (workgroups) per record
+  constexpr int kLoader = CW * SPW, kHistory = kLoader + 1, kPrefetch0 = kLoader + 2;
+  constexpr int kPrefetchWaves = 2 * SPW;  // look-ahead lanes: this group's shared lines + its E lines
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int H = a.H;
-  int rec, strip;
-  if (!xcd_strip_coords(a.num_seqs * H, V / 16, rec, strip)) return;
-  const int seq = rec / H, h = rec % H, v0 = strip * 16;
+  int rec, sg;
+  if (!xcd_strip_coords(a.num_seqs * H, NSG, rec, sg)) return;
+  const int seq = rec / H, h = rec % H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
   const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
   const int n = sq.y;
   auto tile_of = [&](int r) { return (size_t)(sq.x + max(n - 1 - r, 0)) * H + h; };  // step r's chunk
+  auto group = [&](int g) { return smem + g * L::bytes; };  // a strip's LDS (E ring, X staging)
 
-  if (PUB && wave >= kScanCW + 2) {
-    // The two waves after the history wave pull the operands of the step kBwdPrefetch ahead
-    // into the XCD's L2: the
-    // shared -G and lam lines split over the record's strips (every strip of a record runs
-    // on one XCD), plus this strip's own E lines.  The lines land in a scratch LDS row.
-    if (n <= 0) return;
-    const int pl = (wave - kScanCW - 2) * kWave + lane;
-    char* sink = smem + L::bytes + (wave & 1) * 1024;
+  if (PUB && wave >= kPrefetch0) {
+    // Look-ahead waves pull the operands of the step kBwdPrefetch ahead into the XCD's L2:
+    // the shared -G and lam lines split over the record's strip groups (every strip of a
+    // record runs on one XCD), plus this group's own E lines.  The lines land in a scratch
+    // LDS row.
+    if (n <= 0 || wave >= kPrefetch0 + kPrefetchWaves) return;
+    const int pl = (wave - kPrefetch0) * kWave + lane;
+    char* sink = smem + SPW * L::bytes + (wave & 1) * 1024;
+    constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * 4 / 128;
+    constexpr int kShared = (kG + kLam + NSG - 1) / NSG;  // lanes for this group's share
+    // (a hint: when the lanes are fewer than the lines, the last lines are not pulled ahead)
     auto prefetch = [&](int q) {
-      if (wave >= kScanCW + 4 || q >= n) return;
+      if (q >= n) return;
       const size_t tile = tile_of(q);
-      constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * 4 / 128;
-      constexpr int kShared = (kG + kLam + 7) / 8;  // lanes for this strip's share
       const char* src = nullptr;
       if (pl < kShared) {
-        const int l = strip + 8 * pl;
+        const int l = sg + NSG * pl;
         if (l < kG) src = (const char*)((const bf16*)a.sc.p[S_NG] + tile * K * K) + l * 128;
         else if (l < kG + kLam) src = (const char*)((const float*)a.ws.p[R_LAM] + tile * K) + (l - kG) * 128;
-      } else if (pl - kShared < kE) {
-        src = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)strip * K * 16) + (pl - kShared) * 128;
+      } else if (pl - kShared < SPW * kE) {
+        const int g = (pl - kShared) / kE, l = (pl - kShared) % kE;
+        src = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)(sg * SPW + g) * K * 16) + l * 128;
       }
       if (src) dma16(src, sink);
     };
@@ -364,7 +373,8 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   }
   if (n <= 0) {
     // an empty sequence: the initial-state gradient is the final-state gradient
-    if (wave == 0 && a.ds0) {
+    if (wave < kLoader && wave % CW == 0 && a.ds0) {
+      const int v0 = (sg * SPW + wave / CW) * 16;
       for (int kt = 0; kt < K / 16; ++kt) {
         const size_t o = (((size_t)seq * H + h) * V + v0 + lr) * K + 16 * kt + 4 * kg;
         *(float4*)(a.ds0 + o) = a.dsfin ? *(const float4*)(a.dsfin + o) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -372,71 +382,82 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     }
     return;
   }
-  if (wave == kScanCW) {
-    // ---- loader wave: step r's slot (r % kBwdRing) holds the E strip and lam ----
+  if (wave == kLoader) {
+    // ---- loader wave: step r's slot (r % kBwdRing) of each strip holds its E strip and lam ----
     auto issue = [&](int r) {
       const size_t tile = tile_of(r);  // clamped past the last step: a fixed load count
-      char* slot = smem + (r % kBwdRing) * L::slot;
-      const char* e = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)strip * K * 16) + lane * 16;
 #pragma unroll
-      for (int b = 0; b < (K * 16 * 4) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
-      if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
+      for (int g = 0; g < SPW; ++g) {
+        char* slot = group(g) + (r % kBwdRing) * L::slot;
+        const char* e = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)(sg * SPW + g) * K * 16) +
+                        lane * 16;
+#pragma unroll
+        for (int b = 0; b < (K * 16 * 4) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
+        if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
+      }
     };
     issue(0);
     issue(1);
     for (int r = 0; r < n; ++r) {
-      wait_vmcnt<L::n_load>();  // slot r complete (step r + 1's loads may be in flight)
-      ring_barrier();           // S(r): slot r - 1 is consumed
+      wait_vmcnt<SPW * L::n_load>();  // slot r complete (step r + 1's loads may be in flight)
+      ring_barrier();                 // S(r): slot r - 1 is consumed
       issue(r + 2);
     }
     if (PUB) ring_barrier();  // final
     wait_vmcnt<0>();  // no LDS write may land after the workgroup ends
     return;
   }
-  if (wave == kScanCW + 1) {
+  if (wave == kHistory) {
     // ---- history wave: X_c of step r (bf16 [v][k] in LDS) is read after S(r) and stored
-    // into the strip's [K][16] block of the strip-major history, 512 contiguous bytes per
+    // into each strip's [K][16] block of the strip-major history, 512 contiguous bytes per
     // store instruction.  In the fused launch step r - kPubLag is published once its stores
     // have completed (write-through stores may take microseconds) ----
     for (int r = 0; r < n; ++r) {
-      // step r - kPubLag's stores (each later step added K / 16 stores and one publish)
-      if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * (K / 16 + 1)>();
+      // step r - kPubLag's stores (each later step added SPW (K / 16 stores + one publish))
+      if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * SPW * (K / 16 + 1)>();
       ring_barrier();  // S(r)
-      if (PUB && r >= kPubLag && lane == 0) publish_strip(progress, rec, strip, r - kPubLag);
-      // X_c as bf16 [v][k] (the compute waves' B-operand staging): one transposing read per
-      // 16 keys gives lane l keys 16 it + l % 16, values 4 (l / 16) .. + 3
-      const bf16* sx = (const bf16*)(smem + L::off_ds + (r & 1) * 16 * SP * 2);
-      bf16x4 hv[K / 16];
+      if (PUB && r >= kPubLag && lane == 0)
 #pragma unroll
-      for (int it = 0; it < K / 16; ++it) hv[it] = lds_col_frag4(sx, SP, 0, 16 * it, lane);
-      bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile_of(r) * K * V + (size_t)strip * K * 16;
+        for (int g = 0; g < SPW; ++g) publish_strip(progress, rec, sg * SPW + g, r - kPubLag);
 #pragma unroll
-      for (int it = 0; it < K / 16; ++it) {
-        const int kk = 16 * it + lr, c4 = 4 * kg;
-        if (PUB)
-          store8_coherent(DSH, (kk * 16 + c4) * 2, hv[it]);
-        else
-          *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = hv[it];
+      for (int g = 0; g < SPW; ++g) {
+        // X_c as bf16 [v][k] (the compute waves' B-operand staging): one transposing read
+        // per 16 keys gives lane l keys 16 it + l % 16, values 4 (l / 16) .. + 3
+        const bf16* sx = (const bf16*)(group(g) + L::off_ds + (r & 1) * 16 * SP * 2);
+        bf16x4 hv[K / 16];
+#pragma unroll
+        for (int it = 0; it < K / 16; ++it) hv[it] = lds_col_frag4(sx, SP, 0, 16 * it, lane);
+        bf16* DSH = (bf16*)a.sc.p[S_DSH] + tile_of(r) * K * V + (size_t)(sg * SPW + g) * K * 16;
+#pragma unroll
+        for (int it = 0; it < K / 16; ++it) {
+          const int kk = 16 * it + lr, c4 = 4 * kg;
+          if (PUB)
+            store8_coherent(DSH, (kk * 16 + c4) * 2, hv[it]);
+          else
+            *(bf16x4*)(DSH + (size_t)kk * 16 + c4) = hv[it];
+        }
       }
     }
     if (PUB) {
       wait_vmcnt<0>();
-      if (lane == 0) publish_strip(progress, rec, strip, n - 1);
+      if (lane == 0)
+#pragma unroll
+        for (int g = 0; g < SPW; ++g) publish_strip(progress, rec, sg * SPW + g, n - 1);
       ring_barrier();  // final
     }
     return;
   }
+  if (wave > kHistory) return;  // (only in a launch with more waves than the roles need)
 
-  if (wave >= CW) {
-    for (int r = 0; r < n; ++r) ring_barrier();
-    if (PUB) ring_barrier();  // final
-    return;
-  }
-  // ---- compute waves: X tiles wave * KT .. (rows 16 kt + 4 (l / 16) + r, column l % 16) ----
+  // ---- compute waves of strip g: X tiles cw * KT .. (rows 16 kt + 4 (l / 16) + r, column
+  // l % 16) ----
+  const int g = wave / CW, cw = wave % CW;
+  const int v0 = (sg * SPW + g) * 16;
+  char* gl = group(g);
   f32x4 X[KT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
-    const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+    const int k0 = 16 * (cw * KT + kt) + 4 * kg;
     if (a.dsfin) {
       const float4 s = *(const float4*)(a.dsfin + (((size_t)seq * H + h) * V + v0 + lr) * K + k0);
       X[kt][0] = s.x; X[kt][1] = s.y; X[kt][2] = s.z; X[kt][3] = s.w;
@@ -457,14 +478,15 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int s = 0; s < NB; ++s) o.g[kt][s] = *(const bf16x8*)(G + frag_off(K, wave * KT + kt, s, lane));
+      for (int s = 0; s < NB; ++s) o.g[kt][s] = *(const bf16x8*)(G + frag_off(K, cw * KT + kt, s, lane));
   };
   auto step = [&](int r, const Ops& o) {
-    bf16* sDS = (bf16*)(smem + L::off_ds + (r & 1) * 16 * SP * 2);
-    // stage X_c as bf16 [v][k]: the B operand of every compute wave, and the history's source
+    bf16* sDS = (bf16*)(gl + L::off_ds + (r & 1) * 16 * SP * 2);
+    // stage X_c as bf16 [v][k]: the B operand of the strip's compute waves, and the history's
+    // source
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      const int k0 = 16 * (cw * KT + kt) + 4 * kg;
       bf16x4 x;
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[q] = to_bf16(X[kt][q]);
@@ -481,10 +503,10 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
       const bf16x4 hi = *(const bf16x4*)(sDS + lr * SP + 32 * s + 16 + 4 * kg);
       xb[s] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    const char* slot = smem + (r % kBwdRing) * L::slot;
+    const char* slot = gl + (r % kBwdRing) * L::slot;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const int ktg = wave * KT + kt;
+      const int ktg = cw * KT + kt;
       const float4 lam = *(const float4*)(slot + L::off_lam + (16 * ktg + 4 * kg) * 4);
       const f32x4 e = *(const f32x4*)(slot + L::off_e + (ktg * 64 + lane) * 16);
       f32x4 acc;
@@ -511,7 +533,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   if (a.ds0) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const int k0 = 16 * (wave * KT + kt) + 4 * kg;
+      const int k0 = 16 * (cw * KT + kt) + 4 * kg;
       *(float4*)(a.ds0 + (((size_t)seq * H + h) * V + v0 + lr) * K + k0) =
           make_float4(X[kt][0], X[kt][1], X[kt][2], X[kt][3]);
     }
@@ -525,7 +547,7 @@ __global__ __launch_bounds__(kBwdThreads) void chunk_bwd_scan_kernel(BwdArgs a, 
     prefetch_lines(pf, blockIdx.x - scan_blocks, gridDim.x - scan_blocks, smem);
     return;
   }
-  bwd_scan_body<K, V, false>(a, nullptr);
+  bwd_scan_body<K, V, false, 1>(a, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1620,7 +1642,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
                                                                       long long spin_limit) {
   const SyncView sv = sync_view(a);
   if ((int)blockIdx.x < scan_blocks) {
-    bwd_scan_body<K, V, true>(a, sv.base);
+    bwd_scan_body<K, V, true, kFusedSPW>(a, sv.base);
     return;
   }
   __shared__ int s_ticket, s_failed;
@@ -1742,13 +1764,14 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
   };
   if ((stages & all) == all && p->num_seqs > 0 && g.max_chunks > 0 && fused_backward_enabled()) {
     // one launch: scan members + ticketed dense / decay tiles (see chunk_bwd_fused_kernel)
-    constexpr size_t smem = cmax_sz(BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
+    constexpr size_t smem =
+        cmax_sz(kFusedSPW * BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
     static_assert(smem + 16 <= 160 * 1024, "fused backward LDS");
     auto fused = chunk_bwd_fused_kernel<K, V>;
     if (ensure_lds_limit((const void*)fused, (int)smem) != hipSuccess)
       return set_error(KDA_ERR_LAUNCH, "chunk_backward: fused LDS attribute failed");
     const int nrec = p->num_seqs * p->heads;
-    const int scan_blocks = kXcds * (V / 16) * ((nrec + kXcds - 1) / kXcds);
+    const int scan_blocks = kXcds * (V / 16 / kFusedSPW) * ((nrec + kXcds - 1) / kXcds);
     const int N = g.max_chunks * p->heads;
     int rc = launch_prep(sync_words(nrec, N));
     if (rc != KDA_OK) return rc;
