@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
   }
   __syncthreads();  // A^T dO staged
   // ---- E = Qg^T dO - W^T bf16(A^T dO): wave w owns key tiles w, w + 4, ... ----
-  float* E = (float*)a.sc.p[S_E] + tile * K * V;
+  char* E = (char*)a.sc.p[S_E] + tile * K * V * kEBytes;
   for (int kt = wave; kt < KB; kt += 4) {
     bf16x8 qf[2], wf[2];
 #pragma unroll
@@ -219,7 +219,16 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
         pq = mfma16(qf[s], lds_col_frag(sDO, OP, 32 * s, 16 * ct, lane), pq);
         pw = mfma16(wf[s], lds_col_frag(sADO, OP, 32 * s, 16 * ct, lane), pw);
       }
-      *(f32x4*)(E + (((size_t)ct * KB + kt) * 64 + lane) * 4) = pq - pw;
+      const f32x4 ev = pq - pw;
+      const size_t eo = (((size_t)ct * KB + kt) * 64 + lane) * 4;
+      if constexpr (kEBytes == 2) {
+        bf16x4 eb;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) eb[q] = to_bf16(ev[q]);
+        *(bf16x4*)(E + eo * 2) = eb;
+      } else {
+        *(f32x4*)(E + eo * 4) = ev;
+      }
     }
   }
 }
@@ -250,10 +259,10 @@ constexpr int kFusedSPW = KDA_FUSED_SPW;           // V strips per scan member o
 constexpr int kBwdRing = 3;
 template <int K, int V>
 struct BwdScanLds {
-  static constexpr int off_e = 0;                         // E strip [K/16][64][4] f32
-  static constexpr int off_lam = off_e + K * 16 * 4;      // lam, K f32
+  static constexpr int off_e = 0;                         // E strip [K/16][64][4] (f32 or bf16)
+  static constexpr int off_lam = off_e + K * 16 * kEBytes;  // lam, K f32
   static constexpr int slot = off_lam + K * 4;
-  static constexpr int n_load = (K * 16 * 4) / 1024 + 1;
+  static constexpr int n_load = (K * 16 * kEBytes) / 1024 + 1;
   static constexpr int SP = K + 8;
   static constexpr int off_ds = kBwdRing * slot;          // X_c bf16 [v][k] (x2, by step parity)
   static constexpr int bytes = off_ds + 2 * 16 * SP * 2;
@@ -345,7 +354,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     if (n <= 0 || wave >= kPrefetch0 + kPrefetchWaves) return;
     const int pl = (wave - kPrefetch0) * kWave + lane;
     char* sink = smem + SPW * L::bytes + (wave & 1) * 1024;
-    constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * 4 / 128;
+    constexpr int kG = K * K * 2 / 128, kLam = K * 4 / 128, kE = K * 16 * kEBytes / 128;
     constexpr int kShared = (kG + kLam + NSG - 1) / NSG;  // lanes for this group's share
     // (a hint: when the lanes are fewer than the lines, the last lines are not pulled ahead)
     auto prefetch = [&](int q) {
@@ -358,7 +367,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         else if (l < kG + kLam) src = (const char*)((const float*)a.ws.p[R_LAM] + tile * K) + (l - kG) * 128;
       } else if (pl - kShared < SPW * kE) {
         const int g = (pl - kShared) / kE, l = (pl - kShared) % kE;
-        src = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)(sg * SPW + g) * K * 16) + l * 128;
+        src = (const char*)a.sc.p[S_E] + (tile * K * V + (size_t)(sg * SPW + g) * K * 16) * kEBytes + l * 128;
       }
       if (src) dma16(src, sink);
     };
@@ -389,10 +398,9 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
 #pragma unroll
       for (int g = 0; g < SPW; ++g) {
         char* slot = group(g) + (r % kBwdRing) * L::slot;
-        const char* e = (const char*)((const float*)a.sc.p[S_E] + tile * K * V + (size_t)(sg * SPW + g) * K * 16) +
-                        lane * 16;
+        const char* e = (const char*)a.sc.p[S_E] + (tile * K * V + (size_t)(sg * SPW + g) * K * 16) * kEBytes + lane * 16;
 #pragma unroll
-        for (int b = 0; b < (K * 16 * 4) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
+        for (int b = 0; b < (K * 16 * kEBytes) / 1024; ++b) dma16(e + b * 1024, slot + L::off_e + b * 1024);
         if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
       }
     };
@@ -508,7 +516,14 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     for (int kt = 0; kt < KT; ++kt) {
       const int ktg = cw * KT + kt;
       const float4 lam = *(const float4*)(slot + L::off_lam + (16 * ktg + 4 * kg) * 4);
-      const f32x4 e = *(const f32x4*)(slot + L::off_e + (ktg * 64 + lane) * 16);
+      f32x4 e;
+      if constexpr (kEBytes == 2) {
+        const bf16x4 eb = *(const bf16x4*)(slot + L::off_e + (ktg * 64 + lane) * 8);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) e[q] = (float)eb[q];
+      } else {
+        e = *(const f32x4*)(slot + L::off_e + (ktg * 64 + lane) * 16);
+      }
       f32x4 acc;
       acc[0] = fmaf(lam.x, X[kt][0], e[0]);
       acc[1] = fmaf(lam.y, X[kt][1], e[1]);

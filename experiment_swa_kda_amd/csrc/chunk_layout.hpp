@@ -11,6 +11,12 @@
 
 namespace kda {
 
+// Element size of the reverse scan's per-chunk input E (f32, or bf16 with KDA_E_BF16).
+#ifndef KDA_E_BF16
+#define KDA_E_BF16 1
+#endif
+constexpr int kEBytes = KDA_E_BF16 ? 2 : 4;
+
 // "Fragment-major" arrays hold a matrix in the exact order the MFMA A/B operand registers
 // of v_mfma_f32_16x16x32_bf16 consume it: for a row-major R x C matrix X, fragment
 // (rt, s) is the 16 x 32 block rows 16rt.., columns 32s..; lane l holds
@@ -68,7 +74,7 @@ enum WsRegion {
 enum ScRegion {
   S_DSH = 0,  // bf16 [tile][V/16][K][16]  dL/dS at the chunk end, strip-major (a bf16 MFMA operand of dKd)
   S_NG,       // bf16 [tile] K x K  -G = -(W^T Kd) as MFMA A fragments, permuted (the reverse scan's transition)
-  S_E,        // f32  [tile][V/16][K/16][64 lane][4]  E = Qg^T dO - W^T (A^T dO) in the scan's accumulator order
+  S_E,        // f32 (bf16: KDA_E_BF16) [tile][V/16][K/16][64 lane][4]  E = Qg^T dO - W^T (A^T dO) in the scan's accumulator order
   S_DA,       // bf16 [tile][64][64] dL/dA (masked lower; the decay VJP's MFMA operand)
   S_DMP,      // bf16 [tile][64][64] dL/dM' (strictly lower, beta folded in; same)
   S_DQG,      // f32  [tile][item][64 lane][4]  dL/dQg  in MFMA C layout (item = row tile + 4 col tile)
@@ -121,7 +127,7 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
   switch (r) {
     case S_DSH: return nt * K * V * 2;
     case S_NG: return nt * K * K * 2;
-    case S_E: return nt * K * V * 4;
+    case S_E: return nt * K * V * kEBytes;
     case S_DA: case S_DMP: return nt * 64 * 64 * 2;
     case S_DQG: case S_DKD: case S_DKB: return nt * 64 * K * 4;
     case S_PP: return nt * 2 * K * 4;
