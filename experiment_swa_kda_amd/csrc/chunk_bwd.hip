@@ -90,13 +90,30 @@ constexpr int kPrepThreads = 256;
 
 template <int K, int V>
 struct PrepLds {
-  static constexpr int OP = V + 8, KP = K + 8;  // row pitches (bf16), 16-byte aligned rows
+  static constexpr int OP = V + 8, KP = K + 8, AP = 64 + 8;  // row pitches (bf16), 16-byte aligned rows
   static constexpr int off_do = 0;                       // dO [64][OP], rows >= len zero
   static constexpr int off_ado = off_do + 64 * OP * 2;   // bf16(A^T dO) [64][OP]
-  static constexpr int off_kd = off_ado + 64 * OP * 2;   // Kd [64][KP]
+  static constexpr int off_kd = off_ado + 64 * OP * 2;   // Kd [64][KP], then Qg [64][KP]
   static constexpr int off_w = off_kd + 64 * KP * 2;     // -W [64][KP]
-  static constexpr int bytes = off_w + 64 * KP * 2;
+  static constexpr int off_a = off_w + 64 * KP * 2;      // A [64][AP]
+  static constexpr int bytes = off_a + 64 * AP * 2;
 };
+
+// Row-major staging of a permuted fragment array (64 rows; fragment (rt, s) element e of lane
+// l is row 16 rt + l % 16, column 32 s + 16 (e / 4) + 4 (l / 16) + e % 4): one 16-byte piece
+// (fragment-major index idx) written as two 8-byte row pieces.
+__device__ __forceinline__ void stage_permuted_piece(bf16* m, int pitch, int ncols, int idx, const bf16x8& x) {
+  const int l = idx % 64, fs = (idx / 64) % (ncols / 32), rt = idx / (64 * (ncols / 32));
+  const int r = 16 * rt + l % 16, g = l / 16;
+  bf16x4 lo, hi;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo[e] = x[e];
+    hi[e] = x[4 + e];
+  }
+  *(bf16x4*)(m + r * pitch + 32 * fs + 4 * g) = lo;
+  *(bf16x4*)(m + r * pitch + 32 * fs + 16 + 4 * g) = hi;
+}
 
 // The fused launch's scheduling (sync words, tile order; defined with chunk_bwd_sched_kernel).
 __device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks, int sync_words);
@@ -104,12 +121,14 @@ __device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks,
 template <int K, int V>
 __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a, int sched_words) {
   using L = PrepLds<K, V>;
-  constexpr int OP = L::OP, KP = L::KP, KB = K / 16, VB = V / 16;
+  constexpr int OP = L::OP, KP = L::KP, AP = L::AP, KB = K / 16, VB = V / 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* sDO = (bf16*)(smem + L::off_do);
   bf16* sADO = (bf16*)(smem + L::off_ado);
   bf16* sKd = (bf16*)(smem + L::off_kd);
+  bf16* sQg = sKd;  // Qg replaces Kd once -G is formed
   bf16* sW = (bf16*)(smem + L::off_w);
+  bf16* sA = (bf16*)(smem + L::off_a);
   const int cidx = blockIdx.x, h = blockIdx.y, H = a.H;
   if (sched_words > 0 && cidx == (int)gridDim.x - 1) {
     // one extra column of workgroups: (x = last, y = 0) does the fused launch's scheduling
@@ -125,10 +144,13 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
   const int lr = lane % 16, kg = lane / 16;
   const bf16* KDF = (const bf16*)a.ws.p[R_KDF] + tile * 64 * K;
   const bf16* WF = (const bf16*)a.ws.p[R_WF] + tile * 64 * K;
-  // ---- every global load first: dO rows, Kd and -W fragments (4 x 16 bytes per thread
-  // each at K = V = 128), this wave's A^T, Qg^T and W^T fragments ----
-  constexpr int NDO = 64 * V / 8 / kPrepThreads, NKF = 64 * K / 8 / kPrepThreads;
-  bf16x8 xo[NDO], xk[NKF], xw[NKF];
+  const bf16* QGF = (const bf16*)a.ws.p[R_QGF] + tile * 64 * K;
+  const bf16* AF = (const bf16*)a.ws.p[R_AF] + tile * 64 * 64;
+  // ---- every global load first: dO rows, Kd, -W, Qg and A fragments (4 x 16 bytes per
+  // thread each of Kd, -W and Qg, 2 x 16 of A at K = V = 128).  A^T, W^T and Qg^T are
+  // formed from the row-major stagings with transposing LDS reads ----
+  constexpr int NDO = 64 * V / 8 / kPrepThreads, NKF = 64 * K / 8 / kPrepThreads, NAF = 64 * 64 / 8 / kPrepThreads;
+  bf16x8 xo[NDO], xk[NKF], xw[NKF], xq[NKF], xa[NAF];
 #pragma unroll
   for (int q = 0; q < NDO; ++q) {
     const int idx = q * kPrepThreads + tid, t = idx / (V / 8), c0 = (idx % (V / 8)) * 8;
@@ -139,10 +161,10 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
     xk[q] = *(const bf16x8*)(KDF + (size_t)(q * kPrepThreads + tid) * 8);
     xw[q] = *(const bf16x8*)(WF + (size_t)(q * kPrepThreads + tid) * 8);
   }
-  bf16x8 atf[2];
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
-    atf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64 + frag_off(64, wave, s, lane));
+  for (int q = 0; q < NAF; ++q) xa[q] = *(const bf16x8*)(AF + (size_t)(q * kPrepThreads + tid) * 8);
+#pragma unroll
+  for (int q = 0; q < NKF; ++q) xq[q] = *(const bf16x8*)(QGF + (size_t)(q * kPrepThreads + tid) * 8);
   // ---- stage dO (rows past the chunk zero), Kd and -W as row-major [t][k] ----
 #pragma unroll
   for (int q = 0; q < NDO; ++q) {
@@ -157,18 +179,16 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
     const int idx = q * kPrepThreads + tid, l = idx % 64, fs = (idx / 64) % (K / 32), rt = idx / (64 * (K / 32));
     const int r = 16 * rt + l % 16, g = l / 16;
     *(bf16x8*)(sKd + r * KP + 32 * fs + 8 * g) = xk[q];
-    // -W is stored permuted: element e is column 32 s + 16 (e / 4) + 4 (l / 16) + e % 4
-    bf16x4 lo, hi;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      lo[e] = xw[q][e];
-      hi[e] = xw[q][4 + e];
-    }
-    *(bf16x4*)(sW + r * KP + 32 * fs + 4 * g) = lo;
-    *(bf16x4*)(sW + r * KP + 32 * fs + 16 + 4 * g) = hi;
+    stage_permuted_piece(sW, KP, K, idx, xw[q]);  // -W and A are stored permuted
   }
+#pragma unroll
+  for (int q = 0; q < NAF; ++q) stage_permuted_piece(sA, AP, 64, q * kPrepThreads + tid, xa[q]);
   __syncthreads();
-  // ---- A^T dO: wave w owns row tile w (tokens 16 w ..), every column tile ----
+  // ---- A^T dO: wave w owns row tile w (tokens 16 w ..), every column tile; the A^T
+  // fragments are column reads of A ----
+  bf16x8 atf[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) atf[s] = lds_col_frag(sA, AP, 32 * s, 16 * wave, lane);
 #pragma unroll
   for (int ct = 0; ct < VB; ++ct) {
     f32x4 acc = zero4();
@@ -201,15 +221,19 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
       *(bf16x8*)(NG + frag_off(K, b, fs, lane)) = x;
     }
   }
-  __syncthreads();  // A^T dO staged
-  // ---- E = Qg^T dO - W^T bf16(A^T dO): wave w owns key tiles w, w + 4, ... ----
+  __syncthreads();  // A^T dO staged, every read of Kd done
+#pragma unroll
+  for (int q = 0; q < NKF; ++q) stage_permuted_piece(sQg, KP, K, q * kPrepThreads + tid, xq[q]);
+  __syncthreads();
+  // ---- E = Qg^T dO - W^T bf16(A^T dO) = Qg^T dO + (-W)^T bf16(A^T dO): wave w owns key
+  // tiles w, w + 4, ...; Qg^T and (-W)^T fragments are column reads of the stagings ----
   char* E = (char*)a.sc.p[S_E] + tile * K * V * kEBytes;
   for (int kt = wave; kt < KB; kt += 4) {
     bf16x8 qf[2], wf[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      qf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_QGTF] + tile * K * 64 + frag_off(64, kt, s, lane));
-      wf[s] = *(const bf16x8*)((const bf16*)a.ws.p[R_WTF] + tile * K * 64 + frag_off(64, kt, s, lane));
+      qf[s] = lds_col_frag(sQg, KP, 32 * s, 16 * kt, lane);
+      wf[s] = lds_col_frag(sW, KP, 32 * s, 16 * kt, lane);
     }
 #pragma unroll
     for (int ct = 0; ct < VB; ++ct) {
@@ -219,7 +243,7 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
         pq = mfma16(qf[s], lds_col_frag(sDO, OP, 32 * s, 16 * ct, lane), pq);
         pw = mfma16(wf[s], lds_col_frag(sADO, OP, 32 * s, 16 * ct, lane), pw);
       }
-      const f32x4 ev = pq - pw;
+      const f32x4 ev = pq + pw;
       const size_t eo = (((size_t)ct * KB + kt) * 64 + lane) * 4;
       if constexpr (kEBytes == 2) {
         bf16x4 eb;
@@ -596,7 +620,8 @@ struct DenseSmem {
   static constexpr size_t off_do = off_pm + 4 * 64 * 4;        // bf16 [64][VP] dO (rows >= len zero)
   static constexpr size_t off_v = off_do + 64 * VP * 2;          // bf16 [64][VP] v (rows >= len zero)
   static constexpr size_t off_kb = off_v + 64 * VP * 2;          // bf16 [64][KP] beta kh e^G
-  static constexpr size_t end = off_kb + 64 * KP * 2;
+  static constexpr size_t off_a = off_kb + 64 * KP * 2;          // bf16 [64][TP] A (its A^T fragments)
+  static constexpr size_t end = off_a + 64 * TP * 2;
   // T, dT, T^T dT (bf16 [64][TP] each, after dA): in the dU-lo / delta region when it is
   // large enough (V = 128), else behind everything
   static constexpr bool kAlias = 3 * 64 * TP * 2 <= 2 * 64 * VP * 2;
@@ -703,9 +728,10 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   static_assert(NDU >= 1 && NDU * kDenseWaves == 4 * V / 16, "dU tiles per wave");
   const int du_rt = wave % 4;
   bf16x8 du_at[2], du_kd[K / 32];
-#pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2)
-    du_at[s2] = *(const bf16x8*)((const bf16*)a.ws.p[R_ATF] + tile * 64 * 64 + frag_off(64, du_rt, s2, lane));
+  // A (permuted fragments, one 16-byte piece per thread of the first 512), staged row-major
+  // in P0: the A^T fragments of dU = A^T dO are column reads of it
+  const bf16x8 xa = tid < 512 ? *(const bf16x8*)((const bf16*)a.ws.p[R_AF] + tile * 64 * 64 + (size_t)tid * 8)
+                              : bf16x8{};
 #pragma unroll
   for (int s2 = 0; s2 < K / 32; ++s2)
     du_kd[s2] = *(const bf16x8*)((const bf16*)a.ws.p[R_KDF] + tile * 64 * K + frag_off(K, du_rt, s2, lane));
@@ -742,6 +768,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
     for (int e = 0; e < 8; ++e) sDL[(t0 + 16 * (e / 4) + e % 4) * VP + vv] = dlf[q][e];
   }
   if (tid < 64) sB[tid] = beta_row;
+  if (tid < 512) stage_permuted_piece((bf16*)(smem + L::off_a), L::TP, 64, tid, xa);
   for (int idx = tid; idx < 4 * 64; idx += kVjpThreads) sPM[idx] = 0.f;
   __syncthreads();
   // dQg for PA's items: wave w owns key tile pa_ct and RPW row tiles; the f32 state rows
@@ -789,6 +816,8 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   }
 
   // the scan-independent half of dU: A^T dO (dO staged above, tokens down the contraction)
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) du_at[s2] = lds_col_frag((const bf16*)(smem + L::off_a), L::TP, 32 * s2, 16 * du_rt, lane);
   f32x4 du_acc[NDU];
 #pragma unroll
   for (int j = 0; j < NDU; ++j) {

@@ -564,7 +564,6 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   // ---- phase 2b: A fragments, M' to HBM, beta v and beta kh e^G (natural rows) to LDS ----
   emit_frags<64, 64, kIntraThreads, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
                                           [&](int r, int c) { return sA[r * TS + c]; });
-  emit_frags_tr<64, 64, kIntraThreads>((bf16*)a.ws.p[R_ATF] + tile * 64 * 64, tid, sA, TS);
   {
     float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
     for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) MPout[idx] = sM[(idx / 64) * 65 + idx % 64];
@@ -702,10 +701,11 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     }
   }
   __syncthreads();
-  // -W and W^T fragments; Qg and Kd staged for their transposed / permuted fragments
+  // -W fragments; Qg and Kd staged for their permuted / transposed fragments (the
+  // backward forms W^T, Qg^T and A^T operands with transposing LDS reads, so only Kd^T, which
+  // the forward scan streams, is stored in both orientations)
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return (bf16)(-(float)sW[r * RS + c]); });
-  emit_frags_tr<K, 64, kIntraThreads>((bf16*)a.ws.p[R_WTF] + tile * K * 64, tid, sW, RS);
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     *(bf16x8*)(sQg + i * RS + 32 * s + 8 * kg) = xq[s];
@@ -714,7 +714,6 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   __syncthreads();
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return sQg[r * RS + c]; });
-  emit_frags_tr<K, 64, kIntraThreads>((bf16*)a.ws.p[R_QGTF] + tile * K * 64, tid, sQg, RS);
   emit_frags_tr<K, 64, kIntraThreads, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, sKd, RS);
 }
 

@@ -46,14 +46,11 @@ enum WsRegion {
   R_CHUNKS = 0,  // int4 [max_chunks]   {row0, len, seq, index_in_seq}
   R_SEQS,        // int2 [num_seqs]     {first_chunk, n_chunks}
   R_QGF,         // bf16 fragments of Qg = q_hat exp(G) (64 x K; q_hat includes the scale), permuted
-  R_QGTF,        // bf16 fragments of Qg^T (K x 64)
   R_KDF,         // bf16 fragments of Kd = k_hat exp(G_last - G) (64 x K)
   R_KDTF,        // bf16 fragments of Kd^T (K x 64), permuted
   R_WF,          // bf16 fragments of -W, W = T (beta k_hat exp(G)) (64 x K), permuted
-  R_WTF,         // bf16 fragments of W^T (K x 64)
   R_UF,          // bf16 U = T (beta v) in MFMA C layout: [V/16 strip][4 row tile][64 lane][4]
   R_AF,          // bf16 fragments of A (64 x 64, lower incl. diagonal), permuted
-  R_ATF,         // bf16 fragments of A^T
   R_T,           // bf16 [tile][64][64] T = (I + diag(beta) M')^-1 (only ever a bf16 MFMA operand)
   R_MP,          // f32  [tile][64][64] M' (strictly lower, without beta)
   R_G,           // f32  [tile][64][K]  G = inclusive cumsum of g in the chunk
@@ -104,9 +101,9 @@ __host__ __device__ inline size_t ws_region_bytes(const ChunkGeom& g, int r) {
   switch (r) {
     case R_CHUNKS: return (size_t)g.max_chunks * 16;
     case R_SEQS: return (size_t)g.num_seqs * 8;
-    case R_QGF: case R_QGTF: case R_KDF: case R_KDTF: case R_WF: case R_WTF: return nt * 64 * K * 2;
+    case R_QGF: case R_KDF: case R_KDTF: case R_WF: return nt * 64 * K * 2;
     case R_UF: return nt * 64 * V * 2;
-    case R_AF: case R_ATF: return nt * 64 * 64 * 2;
+    case R_AF: return nt * 64 * 64 * 2;
     case R_T: return nt * 64 * 64 * 2;
     case R_MP: return nt * 64 * 64 * 4;
     case R_G: return nt * 64 * K * 4;
