@@ -118,8 +118,11 @@ __device__ __forceinline__ void stage_permuted_piece(bf16* m, int pitch, int nco
 // The fused launch's scheduling (sync words, tile order; defined with chunk_bwd_sched_kernel).
 __device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks, int sync_words);
 
-template <int K, int V>
-__global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a, int sched_words) {
+// The prep of tile (cidx, h), run by kPrepThreads threads.  COHERENT: its outputs (-G, E)
+// are read by scan members of the same launch on other XCDs, so they are written through
+// to memory (the caller waits for the stores before it publishes the tile).
+template <int K, int V, bool COHERENT>
+__device__ __forceinline__ void bwd_prep_body(const BwdArgs& a, int cidx, int h) {
   using L = PrepLds<K, V>;
   constexpr int OP = L::OP, KP = L::KP, AP = L::AP, KB = K / 16, VB = V / 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -129,13 +132,7 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
   bf16* sQg = sKd;  // Qg replaces Kd once -G is formed
   bf16* sW = (bf16*)(smem + L::off_w);
   bf16* sA = (bf16*)(smem + L::off_a);
-  const int cidx = blockIdx.x, h = blockIdx.y, H = a.H;
-  if (sched_words > 0 && cidx == (int)gridDim.x - 1) {
-    // one extra column of workgroups: (x = last, y = 0) does the fused launch's scheduling
-    // (sync words, tile order), saving a launch of its own
-    if (h == 0) bwd_sched_body(a, cidx, sched_words);
-    return;
-  }
+  const int H = a.H;
   const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
   const int len = ch.y, row0 = ch.x;
   if (len <= 0) return;
@@ -218,7 +215,10 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
         x[r] = to_bf16(lo[r]);
         x[4 + r] = to_bf16(hi[r]);
       }
-      *(bf16x8*)(NG + frag_off(K, b, fs, lane)) = x;
+      if constexpr (COHERENT)
+        store16_coherent(NG, (int)frag_off(K, b, fs, lane) * 2, x);
+      else
+        *(bf16x8*)(NG + frag_off(K, b, fs, lane)) = x;
     }
   }
   __syncthreads();  // A^T dO staged, every read of Kd done
@@ -249,12 +249,27 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
         bf16x4 eb;
 #pragma unroll
         for (int q = 0; q < 4; ++q) eb[q] = to_bf16(ev[q]);
-        *(bf16x4*)(E + eo * 2) = eb;
+        if constexpr (COHERENT)
+          store8_coherent(E, (int)eo * 2, eb);
+        else
+          *(bf16x4*)(E + eo * 2) = eb;
       } else {
         *(f32x4*)(E + eo * 4) = ev;
       }
     }
   }
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a, int sched_words) {
+  const int cidx = blockIdx.x, h = blockIdx.y;
+  if (sched_words > 0 && cidx == (int)gridDim.x - 1) {
+    // one extra column of workgroups: (x = last, y = 0) does the fused launch's scheduling
+    // (sync words, tile order), saving a launch of its own
+    if (h == 0) bwd_sched_body(a, cidx, sched_words);
+    return;
+  }
+  bwd_prep_body<K, V, false>(a, cidx, h);
 }
 
 // One workgroup per (sequence, head, 16-wide V strip) walks the chunks backwards: four
@@ -275,6 +290,9 @@ constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
 constexpr int kPubLag = KDA_PUB_LAG;
 constexpr int kScanCW = 4;                        // compute waves per V strip
 constexpr int kBwdThreads = (kScanCW + 2) * kWave;  // one strip + the loader and the history wave
+#ifndef KDA_FUSED_PREP
+#define KDA_FUSED_PREP 1  // the prep inside the fused launch (0: a launch of its own before it)
+#endif
 #ifndef KDA_FUSED_SPW
 #define KDA_FUSED_SPW 1
 #endif
@@ -351,7 +369,8 @@ __device__ __forceinline__ void publish_strip(int* sync, int rec, int strip, int
 // is stored the strip's progress word is raised: r + 1 means the strip has finished the
 // r + 1 last chunks of the sequence.
 template <int K, int V, bool PUB, int SPW>
-__device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
+__device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress, const int* prep_flags = nullptr,
+                                              long long spin_limit = 0) {
   using L = BwdScanLds<K, V>;
   constexpr int CW = kScanCW, KT = K / 16 / CW, NB = K / 32, SP = L::SP;
   static_assert(KT >= 1 && KT * CW == K / 16, "X tiles split evenly over the compute waves");
@@ -369,6 +388,27 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
   const int n = sq.y;
   auto tile_of = [&](int r) { return (size_t)(sq.x + max(n - 1 - r, 0)) * H + h; };  // step r's chunk
   auto group = [&](int g) { return smem + g * L::bytes; };  // a strip's LDS (E ring, X staging)
+  // Fused launch with the prep inside it: a chunk's -G and E exist once its prep workgroup
+  // raised the chunk's flag (after its write-through stores completed).  The loader waits for
+  // the flag of step r + 2 before the barrier S(r) after which it, and (one step later) the
+  // compute waves, load that step's operands; a first barrier S(-1) covers steps 0 and 1.
+  const bool prep_wait = PUB && prep_flags != nullptr;
+  auto prep_ready = [&](int q) {
+    return __hip_atomic_load(prep_flags + tile_of(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  };
+  auto wait_prep = [&](int q) {
+    if (!prep_wait || q >= n || lane != 0) return;
+    const long long t0 = wall_clock64();
+    int* abort_word = progress + 1;
+    while (!prep_ready(q)) {
+      if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+          wall_clock64() - t0 > spin_limit) {
+        __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+  };
 
   if (PUB && wave >= kPrefetch0) {
     // Look-ahead waves pull the operands of the step kBwdPrefetch ahead into the XCD's L2:
@@ -383,6 +423,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     // (a hint: when the lanes are fewer than the lines, the last lines are not pulled ahead)
     auto prefetch = [&](int q) {
       if (q >= n) return;
+      if (prep_wait && !prep_ready(q)) return;  // not written yet: no stale line pulled into L2
       const size_t tile = tile_of(q);
       const char* src = nullptr;
       if (pl < kShared) {
@@ -395,6 +436,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
       }
       if (src) dma16(src, sink);
     };
+    if (prep_wait) ring_barrier();  // S(-1)
     for (int q = 0; q < kBwdPrefetch; ++q) prefetch(q);
     for (int b = 0; b < n; ++b) {
       ring_barrier();  // S(b)
@@ -428,10 +470,16 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
         if (lane < K / 4) dma16((const float*)a.ws.p[R_LAM] + tile * K + lane * 4, slot + L::off_lam);
       }
     };
+    if (prep_wait) {
+      wait_prep(0);
+      wait_prep(1);
+      ring_barrier();  // S(-1)
+    }
     issue(0);
     issue(1);
     for (int r = 0; r < n; ++r) {
       wait_vmcnt<SPW * L::n_load>();  // slot r complete (step r + 1's loads may be in flight)
+      wait_prep(r + 2);
       ring_barrier();                 // S(r): slot r - 1 is consumed
       issue(r + 2);
     }
@@ -444,6 +492,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     // into each strip's [K][16] block of the strip-major history, 512 contiguous bytes per
     // store instruction.  In the fused launch step r - kPubLag is published once its stores
     // have completed (write-through stores may take microseconds) ----
+    if (prep_wait) ring_barrier();  // S(-1)
     for (int r = 0; r < n; ++r) {
       // step r - kPubLag's stores (each later step added SPW (K / 16 stores + one publish))
       if (PUB && r >= kPubLag) wait_vmcnt<(kPubLag - 1) * SPW * (K / 16 + 1)>();
@@ -559,6 +608,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress) {
     }
   };
   Ops o0, o1;
+  if (prep_wait) ring_barrier();  // S(-1)
   load_ops(o0, 0);
   for (int r = 0; r < n; r += 2) {
     load_ops(o1, r + 1);
@@ -1682,11 +1732,25 @@ __global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int ma
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks,
+__global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks, int prep_blocks,
                                                                       long long spin_limit) {
   const SyncView sv = sync_view(a);
+  int* prep_flags = sv.base + kSyncRec + 32 * a.num_seqs * a.H;  // one word per tile
   if ((int)blockIdx.x < scan_blocks) {
-    bwd_scan_body<K, V, true, kFusedSPW>(a, sv.base);
+    bwd_scan_body<K, V, true, kFusedSPW>(a, sv.base, prep_blocks > 0 ? prep_flags : nullptr, spin_limit);
+    return;
+  }
+  if ((int)blockIdx.x < scan_blocks + prep_blocks) {
+    // a prep workgroup: tile number blockIdx - scan_blocks in the scan's order, so the scan's
+    // first steps find their operands first
+    if (threadIdx.x >= kPrepThreads) return;
+    const int i = blockIdx.x - scan_blocks;
+    const int cidx = ((const int*)a.sc.p[S_ORDER])[i / a.H], h = i % a.H;
+    bwd_prep_body<K, V, true>(a, cidx, h);
+    wait_vmcnt<0>();  // every write-through store of the tile is complete
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(prep_flags + (size_t)cidx * a.H + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   __shared__ int s_ticket, s_failed;
@@ -1811,16 +1875,26 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     constexpr size_t smem =
         cmax_sz(kFusedSPW * BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
     static_assert(smem + 16 <= 160 * 1024, "fused backward LDS");
+    static_assert(PrepLds<K, V>::bytes <= smem, "fused backward LDS (prep workgroups)");
     auto fused = chunk_bwd_fused_kernel<K, V>;
     if (ensure_lds_limit((const void*)fused, (int)smem) != hipSuccess)
       return set_error(KDA_ERR_LAUNCH, "chunk_backward: fused LDS attribute failed");
     const int nrec = p->num_seqs * p->heads;
     const int scan_blocks = kXcds * (V / 16 / kFusedSPW) * ((nrec + kXcds - 1) / kXcds);
     const int N = g.max_chunks * p->heads;
+#if KDA_FUSED_PREP
+    // the prep runs inside the fused launch (workgroups between the scan members and the
+    // VJP tiles); a one-workgroup launch clears the sync words and writes the tile order
+    hipLaunchKernelGGL(chunk_bwd_sched_kernel, dim3(1), dim3(1024), 0, stream, a, g.max_chunks, sync_words(nrec, N));
+    KDA_LAUNCH_CHECK("chunk_backward sched");
+    hipLaunchKernelGGL(fused, dim3(scan_blocks + 2 * N), dim3(kVjpThreads), smem, stream, a, scan_blocks, N,
+                       wait_limit_ticks());
+#else
     int rc = launch_prep(sync_words(nrec, N));
     if (rc != KDA_OK) return rc;
-    hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks,
+    hipLaunchKernelGGL(fused, dim3(scan_blocks + N), dim3(kVjpThreads), smem, stream, a, scan_blocks, 0,
                        wait_limit_ticks());
+#endif
     KDA_LAUNCH_CHECK("chunk_backward fused");
     stages &= ~all;
   } else if ((stages & all) == all && g.max_chunks > 0) {

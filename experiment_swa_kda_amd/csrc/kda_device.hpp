@@ -213,6 +213,10 @@ __device__ __forceinline__ void store8_coherent(void* base, int byte_off, bf16x4
   typedef int i2 __attribute__((ext_vector_type(2)));
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2, x), raw_rsrc(base), byte_off, 0, kCoherentPolicy);
 }
+__device__ __forceinline__ void store16_coherent(void* base, int byte_off, bf16x8 x) {
+  typedef int i4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4, x), raw_rsrc(base), byte_off, 0, kCoherentPolicy);
+}
 __device__ __forceinline__ bf16x8 load16_coherent_bf16(const void* base, int byte_off) {
   typedef int i4 __attribute__((ext_vector_type(4)));
   const i4 v = __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(base), byte_off, 0, kCoherentPolicy);
