@@ -159,19 +159,27 @@ __device__ __forceinline__ void emit_frags_tr(bf16* dst, int tid, const bf16* m,
 // ---------------------------------------------------------------------------
 // intra-chunk kernel
 // ---------------------------------------------------------------------------
-// One 256-thread workgroup per (chunk, head) tile; wave w owns the 16-row block w.  Lane
-// (lr, kg) holds row 16w + lr on the channels 32s + 8kg + e (s < K/32, e < 8): exactly
+// One workgroup per (chunk, head) tile of 4 x kIntraNH waves; wave w owns the 16-row block
+// rb = w % 4 and the channel part hh = w / 4 (K / kIntraNH channels; V likewise).  Lane
+// (lr, kg) holds row 16rb + lr on the channels 32s + 8kg + e of its part (e < 8): exactly
 // the A-operand fragments of its row block, so the bf16 MFMA operands of A and M' are
 // formed in registers.  The in-chunk cumulative decay is a DPP scan across the 16 rows of
-// a wave plus a 3-term prefix of the block totals; row norms are two permlane swaps.
-// LDS stays under 80 KB so two tiles share a CU.
-constexpr int kIntraThreads = 256;
+// a wave plus a 3-term prefix of the block totals; row norms are two permlane swaps and a
+// sum over the parts through LDS.  A tile is a chain of short dependent phases (one tile
+// alone on a CU is latency-bound), so the elementwise work, the A / M' products (partial
+// sums over the channel parts, added in a fixed order) and the U / W products are split
+// over the parts; the 16 x 16 triangular solves stay with part 0.  LDS stays under 80 KB
+// so two tiles share a CU.
+#ifndef KDA_INTRA_NH
+#define KDA_INTRA_NH 2
+#endif
+constexpr int kIntraNH = KDA_INTRA_NH;
+constexpr int kIntraThreads = 256 * kIntraNH;
 
 template <int K, int V>
 struct IntraLds {
   static constexpr int NS = K / 32;
   static constexpr int RS = K + 8;   // bf16 row stride of [64][K] staging
-  static constexpr int TS = 64 + 8;  // bf16 row stride of [*][64] staging
   static constexpr int cmax(int a, int b) { return a > b ? a : b; }
   static constexpr int VS = V + 8;   // bf16 row stride of [64][V] staging
   static_assert(RS % 8 == 0 && VS % 8 == 0, "vector rows and transposing reads need 16-byte rows");
@@ -181,16 +189,18 @@ struct IntraLds {
   // X3: M' f32 [64][65] -> W bf16 [64][RS]
   static constexpr int x3 = x1 + x1_bytes;
   static constexpr int x3_bytes = cmax(64 * 65 * 4, 64 * RS * 2);
-  // X4: A bf16 [64][TS] -> T f32 [64][65]
+  // X4: A f32 [64][65] -> T f32 [64][65]
   static constexpr int x4 = x3 + x3_bytes;
-  static constexpr int x4_bytes = cmax(64 * TS * 2, 64 * 65 * 4);
+  static constexpr int x4_bytes = 64 * 65 * 4;
   // per-wave 16 x 17 f32 product scratch (T solve)
   static constexpr int scr = x4 + x4_bytes;
   static constexpr int scr_bytes = 4 * 16 * 17 * 4;
   static constexpr int gref = scr + scr_bytes;   // f32 [5][K]: G of rows 0, 16, 32, 48 and 63
   static constexpr int tot = gref + 5 * K * 4;   // f32 [4][K]: block totals of g
   static constexpr int beta = tot + 4 * K * 4;   // f32 [64]
-  static constexpr int bytes = beta + 64 * 4;
+  static constexpr int nrm = beta + 64 * 4;      // f32 [parts][64][2]: per-part sums of q^2, k^2
+  static constexpr int wide = nrm + kIntraNH * 64 * 2 * 4;  // int [8]: per-wave wide-diagonal flags
+  static constexpr int bytes = wide + 8 * 4;
 };
 
 template <int CTRL>
@@ -224,16 +234,15 @@ __device__ void intra_exact_block(const FwdArgs& a, int w, int lane, int row0, i
     if (j <= i && i < len) {
       const size_t bi = ((size_t)(row0 + i) * H + h) * K, bj = ((size_t)(row0 + j) * H + h) * K;
       const float rqi = RQ[i], rki = RK[i], rkj = RK[j];
+#pragma unroll 1
       for (int c0 = 0; c0 < K; c0 += 8) {
-        float qi[8], ki[8], kj[8];
-        load8(a.q + bi + c0, qi);
-        load8(a.k + bi + c0, ki);
-        load8(a.k + bj + c0, kj);
+        const bf16x8 qi = *(const bf16x8*)(a.q + bi + c0), ki = *(const bf16x8*)(a.k + bi + c0),
+                     kj = *(const bf16x8*)(a.k + bj + c0);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float d = expf(G[i * K + c0 + e] - G[j * K + c0 + e]) * kj[e] * rkj;
-          sa = fmaf(qi[e] * rqi, d, sa);
-          sm = fmaf(ki[e] * rki, d, sm);
+          const float d = expf(G[i * K + c0 + e] - G[j * K + c0 + e]) * (float)kj[e] * rkj;
+          sa = fmaf((float)qi[e] * rqi, d, sa);
+          sm = fmaf((float)ki[e] * rki, d, sm);
         }
       }
     }
@@ -289,9 +298,13 @@ __device__ __forceinline__ bf16x8 conv_silu8(bf16x8 own, bf16x8 halo, const floa
 }
 
 template <int K, int V, bool CONV = false>
-__global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kIntraThreads, 2 * kIntraNH) void chunk_fwd_intra_kernel(FwdArgs a) {
   using L = IntraLds<K, V>;
-  constexpr int NS = K / 32, NV = V / 32, RS = L::RS, TS = L::TS;
+  constexpr int NH = kIntraNH;
+  constexpr int NS = K / 32, NV = V / 32, RS = L::RS;
+  constexpr int NSH = NS / NH, NVH = NV / NH;  // 32-channel steps of this wave's part (K, V)
+  static_assert(NH == 1 || NH == 2, "one or two channel parts");
+  static_assert(NS % NH == 0 && NV % NH == 0 && (V / 16) % NH == 0 && (K / 16) % NH == 0, "even channel parts");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* sF = (bf16*)(smem + L::x1);        // Fq / Fk fragments
   constexpr int VS = L::VS;
@@ -301,12 +314,14 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   bf16* sKd = sQg + 64 * RS;               // Kd [64][RS]
   float* sM = (float*)(smem + L::x3);      // M' [64][65]
   bf16* sW = (bf16*)(smem + L::x3);        // W [64][RS]
-  bf16* sA = (bf16*)(smem + L::x4);        // A [64][TS]
+  float* sA = (float*)(smem + L::x4);      // A [64][65]
   float* sT = (float*)(smem + L::x4);      // T [64][65]
   float* sScr = (float*)(smem + L::scr);
   float* sGref = (float*)(smem + L::gref);
   float* sTot = (float*)(smem + L::tot);
   float* sBeta = (float*)(smem + L::beta);
+  float* sNrm = (float*)(smem + L::nrm);
+  int* sWide = (int*)(smem + L::wide);
 
   // Fixed-length problems derive their chunk from the index and publish the chunk and
   // sequence tables for the later kernels (which run after this one on the stream);
@@ -329,14 +344,18 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   const size_t tile = (size_t)blockIdx.x * H + h;
   const int row0 = ch.x;
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const int rb = w % 4, hh = w / 4;  // row block, channel part
   const int lr = lane % 16, kg = lane / 16;
-  const int i = 16 * w + lr;
+  const int i = 16 * rb + lr;
   const bool live = i < len;
   const size_t rbase = (size_t)(row0 + (live ? i : len - 1)) * H + h;
+  // channel step s' of this wave's part is the global step S(s') = NSH hh + s' (V: NVH hh + s')
+  auto S = [&](int s) { return NSH * hh + s; };
+  auto SV = [&](int s) { return NVH * hh + s; };
 
   // ---- phase 1: loads (all issued first), norms, gate, beta, cumulative decay ----
-  bf16x8 qr[NS], kr[NS], vr[NV];
-  float g[NS][8];
+  bf16x8 qr[NSH], kr[NSH];
+  float g[NSH][8];
   if constexpr (CONV) {
     static_assert(K == V, "the fused convolution serves q, k, v of one head width");
     // taps of this head's q, k, v channels as f32 [3][K][4] in the (still unused) X1 region
@@ -361,18 +380,18 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     const bool has_halo = lr >= 13 && pos >= 16 && i - 16 < len;
     const bf16* xh = has_halo ? a.conv_x + (size_t)(row0 + i - 16) * a.conv_ld + h * K + 8 * kg
                               : xo;  // the own row (unused)
-    bf16x8 ho[3][NS];
+    bf16x8 ho[3][NSH], vr[NSH];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qr[s] = *(const bf16x8*)(xo + 32 * s);
-      kr[s] = *(const bf16x8*)(xo + HK + 32 * s);
-      vr[s] = *(const bf16x8*)(xo + 2 * HK + 32 * s);
+    for (int s = 0; s < NSH; ++s) {
+      qr[s] = *(const bf16x8*)(xo + 32 * S(s));
+      kr[s] = *(const bf16x8*)(xo + HK + 32 * S(s));
+      vr[s] = *(const bf16x8*)(xo + 2 * HK + 32 * S(s));
     }
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      ho[0][s] = *(const bf16x8*)(xh + 32 * s);
-      ho[1][s] = *(const bf16x8*)(xh + HK + 32 * s);
-      ho[2][s] = *(const bf16x8*)(xh + 2 * HK + 32 * s);
+    for (int s = 0; s < NSH; ++s) {
+      ho[0][s] = *(const bf16x8*)(xh + 32 * S(s));
+      ho[1][s] = *(const bf16x8*)(xh + HK + 32 * S(s));
+      ho[2][s] = *(const bf16x8*)(xh + 2 * HK + 32 * S(s));
       if (!has_halo)
 #pragma unroll
         for (int e = 0; e < 8; ++e) ho[0][s][e] = ho[1][s][e] = ho[2][s][e] = to_bf16(0.f);
@@ -382,8 +401,8 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     bf16* ko = (bf16*)a.k + rbase * K + 8 * kg;
     bf16* vo = (bf16*)a.v + rbase * V + 8 * kg;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int c0 = 32 * s + 8 * kg;
+    for (int s = 0; s < NSH; ++s) {
+      const int c0 = 32 * S(s) + 8 * kg;
       if (W == 4) {
         qr[s] = conv_silu8<4>(qr[s], ho[0][s], sWt + (0 * K + c0) * 4, lr);
         kr[s] = conv_silu8<4>(kr[s], ho[1][s], sWt + (1 * K + c0) * 4, lr);
@@ -402,26 +421,24 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
         vr[s] = conv_silu8<1>(vr[s], ho[2][s], sWt + (2 * K + c0) * 4, lr);
       }
       if (live) {
-        *(bf16x8*)(qo + 32 * s) = qr[s];
-        *(bf16x8*)(ko + 32 * s) = kr[s];
-        *(bf16x8*)(vo + 32 * s) = vr[s];
+        *(bf16x8*)(qo + 32 * S(s)) = qr[s];
+        *(bf16x8*)(ko + 32 * S(s)) = kr[s];
+        *(bf16x8*)(vo + 32 * S(s)) = vr[s];
       }
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qr[s] = *(const bf16x8*)(a.q + rbase * K + 32 * s + 8 * kg);
-      kr[s] = *(const bf16x8*)(a.k + rbase * K + 32 * s + 8 * kg);
+    for (int s = 0; s < NSH; ++s) {
+      qr[s] = *(const bf16x8*)(a.q + rbase * K + 32 * S(s) + 8 * kg);
+      kr[s] = *(const bf16x8*)(a.k + rbase * K + 32 * S(s) + 8 * kg);
     }
-#pragma unroll
-    for (int s = 0; s < NV; ++s) vr[s] = *(const bf16x8*)(a.v + rbase * V + 32 * s + 8 * kg);
   }
   const float bl = (float)a.beta[(size_t)(row0 + (live ? i : len - 1)) * a.beta_ld + h];
   if (a.gate_mode == KDA_GATE_K3) {
     const float ea = expf(a.A_log[h]);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int c0 = 32 * s + 8 * kg;
+    for (int s = 0; s < NSH; ++s) {
+      const int c0 = 32 * S(s) + 8 * kg;
       const bf16x8 raw = *(const bf16x8*)((const bf16*)a.gate + rbase * K + c0);
       float db[8];
       load8f(a.dt_bias + h * K + c0, db);
@@ -430,71 +447,77 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) load8f((const float*)a.gate + rbase * K + 32 * s + 8 * kg, g[s]);
+    for (int s = 0; s < NSH; ++s) load8f((const float*)a.gate + rbase * K + 32 * S(s) + 8 * kg, g[s]);
   }
-  float qh[NS][8], kh[NS][8];
+  // q and k stay bf16 in registers (rows past the chunk end zeroed); the normalised values
+  // qh = q rq, kh = k rk are formed in f32 where they are used
   float sq = 0.f, sk = 0.f;
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < NSH; ++s)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      qh[s][e] = live ? (float)qr[s][e] : 0.f;
-      kh[s][e] = live ? (float)kr[s][e] : 0.f;
-      if (!live) g[s][e] = 0.f;
-      sq = fmaf(qh[s][e], qh[s][e], sq);
-      sk = fmaf(kh[s][e], kh[s][e], sk);
+      if (!live) {
+        qr[s][e] = to_bf16(0.f);
+        kr[s][e] = to_bf16(0.f);
+        g[s][e] = 0.f;
+      }
+      sq = fmaf((float)qr[s][e], (float)qr[s][e], sq);
+      sk = fmaf((float)kr[s][e], (float)kr[s][e], sk);
+      g[s][e] = row_prefix16(g[s][e]);  // inclusive in-block prefix over the 16 rows
     }
   sq = swap32_sum(swap16_sum(sq));
   sk = swap32_sum(swap16_sum(sk));
-  const float rq = a.scale / fmaxf(sqrtf(sq), 1e-12f);
-  const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
-  const float beta = live ? sigmoid_acc(bl) : 0.f;
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qh[s][e] *= rq;
-      kh[s][e] *= rk;
-      g[s][e] = row_prefix16(g[s][e]);  // inclusive in-block prefix over the 16 rows
-    }
-  if (kg == 0) {
-    sBeta[i] = beta;
-    ((float*)a.ws.p[R_RQ])[tile * 64 + i] = rq;
-    ((float*)a.ws.p[R_RK])[tile * 64 + i] = rk;
-    ((float*)a.ws.p[R_BETA])[tile * 64 + i] = beta;
+  if (NH > 1 && kg == 0) {  // this part's sums of squares; the parts add up after the barrier
+    sNrm[(hh * 64 + i) * 2] = sq;
+    sNrm[(hh * 64 + i) * 2 + 1] = sk;
   }
   if (lr == 15) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      float* t = sTot + w * K + 32 * s + 8 * kg;
+    for (int s = 0; s < NSH; ++s) {
+      float* t = sTot + rb * K + 32 * S(s) + 8 * kg;
       *(float4*)t = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
       *(float4*)(t + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
     }
   }
   __syncthreads();
+  if (NH > 1) {  // fixed order: part 0 + part 1 in every wave
+    sq = sNrm[i * 2] + sNrm[(64 + i) * 2];
+    sk = sNrm[i * 2 + 1] + sNrm[(64 + i) * 2 + 1];
+  }
+  const float rq = a.scale / fmaxf(sqrtf(sq), 1e-12f);
+  const float rk = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+  const float beta = live ? sigmoid_acc(bl) : 0.f;
+  auto qh = [&](int s, int e) { return (float)qr[s][e] * rq; };
+  auto kh = [&](int s, int e) { return (float)kr[s][e] * rk; };
+  if (hh == 0 && kg == 0) {
+    sBeta[i] = beta;
+    ((float*)a.ws.p[R_RQ])[tile * 64 + i] = rq;
+    ((float*)a.ws.p[R_RK])[tile * 64 + i] = rk;
+    ((float*)a.ws.p[R_BETA])[tile * 64 + i] = beta;
+  }
   // G = in-block prefix + totals of the preceding blocks (fixed order)
-  for (int b = 0; b < w; ++b) {
+  for (int b = 0; b < rb; ++b) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NSH; ++s) {
       float t[8];
-      load8f(sTot + b * K + 32 * s + 8 * kg, t);
+      load8f(sTot + b * K + 32 * S(s) + 8 * kg, t);
 #pragma unroll
       for (int e = 0; e < 8; ++e) g[s][e] += t[e];
     }
   }
   float* Gout = (float*)a.ws.p[R_G] + tile * 64 * K;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    float* o = Gout + i * K + 32 * s + 8 * kg;
+  for (int s = 0; s < NSH; ++s) {
+    float* o = Gout + i * K + 32 * S(s) + 8 * kg;
     *(float4*)o = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
     *(float4*)(o + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
     if (lr == 0 || i == 63) {
-      float* r = sGref + (lr == 0 ? w : 4) * K + 32 * s + 8 * kg;
+      float* r = sGref + (lr == 0 ? rb : 4) * K + 32 * S(s) + 8 * kg;
       *(float4*)r = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
       *(float4*)(r + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
     }
     if (i == 63) {
-      float* lam = (float*)a.ws.p[R_LAM] + tile * K + 32 * s + 8 * kg;
+      float* lam = (float*)a.ws.p[R_LAM] + tile * K + 32 * S(s) + 8 * kg;
       *(float4*)lam = make_float4(expf(g[s][0]), expf(g[s][1]), expf(g[s][2]), expf(g[s][3]));
       *(float4*)(lam + 4) = make_float4(expf(g[s][4]), expf(g[s][5]), expf(g[s][6]), expf(g[s][7]));
     }
@@ -502,126 +525,161 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   __syncthreads();
 
   // ---- phase 2: A and M' = (factorised) 16 x 16 blocks; row factors e^{G_i - G_r} ----
-  bool wide = false;  // this wave's diagonal block spans more than 80 nats on some channel
+  bool wide = false;  // this row block's diagonal block spans more than 80 nats on some channel
   {
-    float gr[NS][8];
+    float gr[NSH][8];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) load8f(sGref + w * K + 32 * s + 8 * kg, gr[s]);
+    for (int s = 0; s < NSH; ++s) load8f(sGref + rb * K + 32 * S(s) + 8 * kg, gr[s]);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NSH; ++s) {
       bf16x8 fq, fk;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float f = __expf(g[s][e] - gr[s][e]);
-        fq[e] = (bf16)(qh[s][e] * f);
-        fk[e] = (bf16)(kh[s][e] * f);
+        fq[e] = (bf16)(qh(s, e) * f);
+        fk[e] = (bf16)(kh(s, e) * f);
         wide |= (lr == 15) && (gr[s][e] - g[s][e] > 80.f);
       }
-      *(bf16x8*)(sF + ((size_t)(w * NS + s) * 64 + lane) * 8) = fq;
-      *(bf16x8*)(sF + ((size_t)((4 + w) * NS + s) * 64 + lane) * 8) = fk;
+      *(bf16x8*)(sF + ((size_t)(rb * NS + S(s)) * 64 + lane) * 8) = fq;
+      *(bf16x8*)(sF + ((size_t)((4 + rb) * NS + S(s)) * 64 + lane) * 8) = fk;
     }
   }
   wide = __builtin_amdgcn_ballot_w64(wide) != 0;
-  __syncthreads();
-  // wave w = column block bb computes the pairs (ba, bb) for ba >= w
-  for (int ba = w; ba < 4; ++ba) {
+  if (NH > 1 && lane == 0) sWide[w] = wide;
+  // A and M' start as zero: entries outside the masks (and the blocks above the diagonal)
+  // are never written
+  for (int idx = tid; idx < 64 * 65 / 4; idx += kIntraThreads) {
+    ((float4*)sA)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ((float4*)sM)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __syncthreads();  // also drains the G, RQ, RK stores: the exact diagonal path reads them back
+  if (NH > 1) wide = (sWide[rb] | sWide[4 + rb]) != 0;
+  // wave (rb, hh) computes the pairs (ba, rb) for ba >= rb over its channel part, one pair
+  // per round: part 0 stores its partial products, part 1 adds its own after the round's
+  // barrier (fixed order; one pair's accumulators held at a time)
+  const int jj = 16 * rb + lr;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int ba = rb + q;
+    const bool pair = ba < 4 && !(ba == rb && wide);  // a wide diagonal block: exact path below
     f32x4 accA = zero4(), accM = zero4();
-    if (ba == w && wide) {
-      __threadfence_block();
-      intra_exact_block<K>(a, w, lane, row0, len, h, Gout, (const float*)a.ws.p[R_RQ] + tile * 64,
-                           (const float*)a.ws.p[R_RK] + tile * 64, accA, accM);
-    } else {
-      float gr[NS][8];
+    if (pair) {
+      float gr[NSH][8];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) load8f(sGref + ba * K + 32 * s + 8 * kg, gr[s]);
+      for (int s = 0; s < NSH; ++s) load8f(sGref + ba * K + 32 * S(s) + 8 * kg, gr[s]);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
+      for (int s = 0; s < NSH; ++s) {
         bf16x8 cf;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) cf[e] = (bf16)(kh[s][e] * __expf(gr[s][e] - g[s][e]));
-        accA = mfma16(*(const bf16x8*)(sF + ((size_t)(ba * NS + s) * 64 + lane) * 8), cf, accA);
-        accM = mfma16(*(const bf16x8*)(sF + ((size_t)((4 + ba) * NS + s) * 64 + lane) * 8), cf, accM);
+        for (int e = 0; e < 8; ++e) cf[e] = (bf16)(kh(s, e) * __expf(gr[s][e] - g[s][e]));
+        accA = mfma16(*(const bf16x8*)(sF + ((size_t)(ba * NS + S(s)) * 64 + lane) * 8), cf, accA);
+        accM = mfma16(*(const bf16x8*)(sF + ((size_t)((4 + ba) * NS + S(s)) * 64 + lane) * 8), cf, accM);
+      }
+      if (hh == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ii = 16 * ba + 4 * kg + r;
+          if (jj <= ii) sA[ii * 65 + jj] = accA[r];
+          if (jj < ii) sM[ii * 65 + jj] = accM[r];
+        }
       }
     }
-    const int jj = 16 * w + lr;
+    if (NH > 1) {
+      __syncthreads();
+      if (hh == 1 && pair) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ii = 16 * ba + 4 * kg + r;
-      sA[ii * TS + jj] = (bf16)(jj <= ii ? accA[r] : 0.f);
-      sM[ii * 65 + jj] = jj < ii ? accM[r] : 0.f;
+        for (int r = 0; r < 4; ++r) {
+          const int ii = 16 * ba + 4 * kg + r;
+          if (jj <= ii) sA[ii * 65 + jj] += accA[r];
+          if (jj < ii) sM[ii * 65 + jj] += accM[r];
+        }
+      }
     }
   }
-  for (int ba = 0; ba < w; ++ba) {  // blocks above the diagonal are zero
+  if (wide && hh == 0) {  // part 0 computes the whole exact diagonal block (rare)
+    f32x4 accA, accM;
+    __threadfence_block();
+    intra_exact_block<K>(a, rb, lane, row0, len, h, Gout, (const float*)a.ws.p[R_RQ] + tile * 64,
+                         (const float*)a.ws.p[R_RK] + tile * 64, accA, accM);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int ii = 16 * ba + 4 * kg + r, jj = 16 * w + lr;
-      sA[ii * TS + jj] = (bf16)0.f;
-      sM[ii * 65 + jj] = 0.f;
+      const int ii = 16 * rb + 4 * kg + r;
+      if (jj <= ii) sA[ii * 65 + jj] = accA[r];
+      if (jj < ii) sM[ii * 65 + jj] = accM[r];
     }
   }
   __syncthreads();
 
   // ---- phase 2b: A fragments, M' to HBM, beta v and beta kh e^G (natural rows) to LDS ----
+  // v again (from L2; the fused convolution wrote it above): not held across phases 1-2
+  bf16x8 vr2[NVH];
+#pragma unroll
+  for (int s = 0; s < NVH; ++s) vr2[s] = *(const bf16x8*)(a.v + rbase * V + 32 * SV(s) + 8 * kg);
   emit_frags<64, 64, kIntraThreads, true>((bf16*)a.ws.p[R_AF] + tile * 64 * 64, tid,
-                                          [&](int r, int c) { return sA[r * TS + c]; });
+                                          [&](int r, int c) { return (bf16)sA[r * 65 + c]; });
   {
     float* MPout = (float*)a.ws.p[R_MP] + tile * 64 * 64;
     for (int idx = tid; idx < 64 * 64; idx += kIntraThreads) MPout[idx] = sM[(idx / 64) * 65 + idx % 64];
   }
+  // beta v and beta kh e^G overwrite the Fq / Fk fragments (read by every wave above)
 #pragma unroll
-  for (int s = 0; s < NV; ++s) {
+  for (int s = 0; s < NVH; ++s) {
     bf16x8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * (live ? (float)vr[s][e] : 0.f));
-    *(bf16x8*)(sBV + i * VS + 32 * s + 8 * kg) = x;
+    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * (live ? (float)vr2[s][e] : 0.f));
+    *(bf16x8*)(sBV + i * VS + 32 * SV(s) + 8 * kg) = x;
   }
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
+  for (int s = 0; s < NSH; ++s) {
     bf16x8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * kh[s][e] * __expf(g[s][e]));
-    *(bf16x8*)(sBK + i * RS + 32 * s + 8 * kg) = x;
+    for (int e = 0; e < 8; ++e) x[e] = (bf16)(beta * kh(s, e) * __expf(g[s][e]));
+    *(bf16x8*)(sBK + i * RS + 32 * S(s) + 8 * kg) = x;
   }
   // Qg = qh e^G and Kd = kh e^{G_last - G} (bf16) are all that phase 5 needs of this row;
   // Kd's natural fragments are exactly what this lane holds
-  bf16x8 xq[NS], xk[NS];
+  bf16x8 xq[NSH], xk[NSH];
   {
     bf16* KDF = (bf16*)a.ws.p[R_KDF] + tile * 64 * K;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NSH; ++s) {
       float gl[8];
-      load8f(sGref + 4 * K + 32 * s + 8 * kg, gl);
+      load8f(sGref + 4 * K + 32 * S(s) + 8 * kg, gl);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        xq[s][e] = (bf16)(qh[s][e] * __expf(g[s][e]));
-        xk[s][e] = (bf16)(kh[s][e] * __expf(gl[e] - g[s][e]));
+        xq[s][e] = (bf16)(qh(s, e) * __expf(g[s][e]));
+        xk[s][e] = (bf16)(kh(s, e) * __expf(gl[e] - g[s][e]));
       }
-      *(bf16x8*)(KDF + frag_off(K, w, s, lane)) = xk[s];
+      *(bf16x8*)(KDF + frag_off(K, rb, S(s), lane)) = xk[s];
     }
   }
   __syncthreads();
 
-  // ---- phase 3: T = (I + diag(beta) M')^-1 ----
+  // ---- phase 3: T = (I + diag(beta) M')^-1 (waves of part 0) ----
   // diagonal blocks by forward substitution, one column per lane (lanes of group kg = 0)
   {
-    const int o = 16 * w, j = lr;
+    const int o = 16 * rb, j = lr;
     float x[16];
+    if (hh == 0) {
 #pragma unroll
-    for (int ii = 0; ii < 16; ++ii) {
-      float sacc = (ii == j) ? 1.f : 0.f;
-      const float bi = sBeta[o + ii];
+      for (int ii = 0; ii < 16; ++ii) {
+        float sacc = (ii == j) ? 1.f : 0.f;
+        const float bi = sBeta[o + ii];
 #pragma unroll
-      for (int m = 0; m < ii; ++m) sacc = fmaf(-bi * sM[(o + ii) * 65 + o + m], x[m], sacc);
-      x[ii] = (ii < j) ? 0.f : sacc;
+        for (int m = 0; m < ii; ++m) sacc = fmaf(-bi * sM[(o + ii) * 65 + o + m], x[m], sacc);
+        x[ii] = (ii < j) ? 0.f : sacc;
+      }
     }
     __syncthreads();  // sA (aliasing sT) is no longer read
-    if (kg == 0) {
+    if (hh == 0) {
+      if (kg == 0) {
 #pragma unroll
-      for (int ii = 0; ii < 16; ++ii) sT[(o + ii) * 65 + o + j] = x[ii];
-    }
-    for (int idx = lane; idx < 16 * 16 * (3 - w); idx += kWave) {  // zero blocks right of the diagonal
-      const int cb = w + 1 + idx / 256, rr = (idx % 256) / 16, cc = idx % 16;
-      sT[(o + rr) * 65 + 16 * cb + cc] = 0.f;
+        for (int ii = 0; ii < 16; ++ii) sT[(o + ii) * 65 + o + j] = x[ii];
+      }
+      for (int idx = lane; idx < 16 * 16 * (3 - rb); idx += kWave) {  // zero blocks right of the diagonal
+        const int cb = rb + 1 + idx / 256, rr = (idx % 256) / 16, cc = idx % 16;
+        sT[(o + rr) * 65 + 16 * cb + cc] = 0.f;
+      }
     }
   }
   __syncthreads();
@@ -637,10 +695,10 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     }
     return acc;
   };
-  float* scr = sScr + w * 16 * 17;
+  float* scr = sScr + rb * 16 * 17;
   for (int lvl = 1; lvl < 4; ++lvl) {
-    const int b = w, ra = w + lvl;
-    if (ra < 4) {
+    const int b = rb, ra = rb + lvl;
+    if (hh == 0 && ra < 4) {
       f32x4 z = zero4();
       for (int m = b; m < ra; ++m) z = prod_NT(ra, m, b, z);
 #pragma unroll
@@ -668,9 +726,10 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
     }
   }
 
-  // ---- phase 4: U = T (beta v), W = T (beta kh e^G); wave w = row tile ----
+  // ---- phase 4: U = T (beta v), W = T (beta kh e^G); wave (rb, hh) = row tile rb, column
+  // tiles of part hh ----
   {
-    const int rt = w, nst = (16 * rt + 15) / 32 + 1;
+    const int rt = rb, nst = (16 * rt + 15) / 32 + 1;
     bf16x8 fa[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -680,7 +739,10 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
       fa[st] = x;
     }
     bf16* Uout = (bf16*)a.ws.p[R_UF] + tile * 64 * V;
-    for (int ct = 0; ct < V / 16; ++ct) {
+    constexpr int UCT = V / 16 / NH, WCT = K / 16 / NH;
+#pragma unroll
+    for (int c = 0; c < UCT; ++c) {
+      const int ct = UCT * hh + c;
       f32x4 acc = zero4();
 #pragma unroll
       for (int st = 0; st < 2; ++st)  // T is lower triangular: row tile rt needs nst steps
@@ -691,7 +753,9 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
       *(bf16x4*)(Uout + ((size_t)(ct * 4 + rt) * 64 + lane) * 4) = x;
     }
     __syncthreads();  // M' (aliasing W) is no longer read
-    for (int ct = 0; ct < K / 16; ++ct) {
+#pragma unroll
+    for (int c = 0; c < WCT; ++c) {
+      const int ct = WCT * hh + c;
       f32x4 acc = zero4();
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -707,9 +771,9 @@ __global__ __launch_bounds__(kIntraThreads, 2) void chunk_fwd_intra_kernel(FwdAr
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_WF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return (bf16)(-(float)sW[r * RS + c]); });
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    *(bf16x8*)(sQg + i * RS + 32 * s + 8 * kg) = xq[s];
-    *(bf16x8*)(sKd + i * RS + 32 * s + 8 * kg) = xk[s];
+  for (int s = 0; s < NSH; ++s) {
+    *(bf16x8*)(sQg + i * RS + 32 * S(s) + 8 * kg) = xq[s];
+    *(bf16x8*)(sKd + i * RS + 32 * S(s) + 8 * kg) = xk[s];
   }
   __syncthreads();
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid,
