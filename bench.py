@@ -149,7 +149,7 @@ def kernel_times(torch, t, do, gate, reps=20):
     _lib.check(lib.kda_chunk_backward(ctypes.byref(p), *bargs), "chunk_backward")
     res = {}
     for name, stage in STAGES.items():
-        if stage is None:  # the full backward: prep (with the scheduling) + the fused launch
+        if stage is None:  # the full backward: the scheduling launch + the fused launch
             call = lambda: lib.kda_chunk_backward(ctypes.byref(p), *bargs)  # noqa: E731
         elif stage < 10:
             call = lambda: lib.kda_chunk_forward_stage(stage, ctypes.byref(p), *fargs)  # noqa: E731
@@ -533,9 +533,10 @@ def main():
                 "measured_hbm_frac": None if hbm_frac is None else round(hbm_frac, 4),
                 "compulsory_bytes": BWD_COMPULSORY_BYTES if dom == "bwd_fused" else None}
     if dom == "bwd_fused":
-        roofline["launches"] = ("one kda_chunk_backward call: chunk_bwd_prep_kernel (its extra workgroup "
-                                "clears the sync words and writes the tile order) + chunk_bwd_fused_kernel "
-                                "(kernel_ms, traffic and busy_frac cover both)")
+        roofline["launches"] = ("one kda_chunk_backward call: chunk_bwd_sched_kernel (clears the sync words "
+                                "and writes the tile order) + chunk_bwd_fused_kernel (scan members, prep "
+                                "workgroups and ticketed dense / decay tiles; kernel_ms, traffic and busy_frac "
+                                "cover both launches)")
     line = {
         "metric": "KDA fwd+bwd TFLOP/s (B2 T4096 H3 D128 bf16)",
         "value": round(flop / (ms * 1e-3) / 1e12, 3),
