@@ -28,8 +28,8 @@
 //    tile around the first (row side) or last (column side) row of each 16-row block, so
 //    every factor is <= 1 or bounded by the block's span; a tile with a block whose decay
 //    span exceeds 80 nats runs an exact per-pair f32 loop instead.
-//  * fused launch (the whole backward in one call): the scan members and ticketed tile
-//    workgroups share one grid; a tile runs its dense and decay parts as soon as the scan
+//  * fused launch (the whole backward in one call): the scan members, the prep workgroups
+//    and the tile workgroups share one grid; a tile runs its dense and decay parts as soon as the scan
 //    has finalised its chunk, so the VJP work overlaps the latency-bound scan (see
 //    chunk_bwd_fused_kernel).  The staged entry points keep the separate launches.
 #include "chunk_host.hpp"
@@ -280,7 +280,10 @@ __global__ __launch_bounds__(kPrepThreads) void chunk_bwd_prep_kernel(BwdArgs a,
 // and, in the fused launch, publishes the step.  Per chunk the waves meet at one barrier
 // S(r): X_c staged as bf16 (the B operand, in the permuted contraction order -G was emitted
 // in), slot r loaded.
-constexpr int kBwdPrefetch = 4;  // fused launch: steps of L2 look-ahead
+#ifndef KDA_BWD_PREFETCH
+#define KDA_BWD_PREFETCH 4
+#endif
+constexpr int kBwdPrefetch = KDA_BWD_PREFETCH;  // fused launch: steps of L2 look-ahead
 #ifndef KDA_PUB_LAG
 #define KDA_PUB_LAG 3
 #endif
@@ -346,9 +349,9 @@ __device__ __forceinline__ void prefetch_lines(const PrefetchList& pf, int w, in
 // L2 write-back or invalidate is needed around the counts -- the write-back of a whole L2 per
 // scan step costs microseconds on the scan's serial chain.
 
-// Layout of the fused backward's sync words (ints): [0] ticket, [1] abort, then per record
-// rec one 128-byte line at kSyncRec + 32 rec holding each V strip's count of finished steps
-// (the tail of the buffer, one word per tile, is cleared but unused).
+// Layout of the fused backward's sync words (ints): [0] unused, [1] abort, then per record
+// rec one 128-byte line at kSyncRec + 32 rec holding each V strip's count of finished steps,
+// then one word per tile: the prep workgroups' ready flags.
 constexpr int kSyncRec = 32;
 __host__ __device__ inline int sync_words(int nrec, int tiles) { return kSyncRec + 32 * nrec + tiles; }
 
@@ -690,7 +693,7 @@ struct NoGate {
 };
 
 template <int K, int V, class Gate = NoGate>
-__device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx, const Gate& gate = Gate()) {
+__device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx, int4 ch, const Gate& gate = Gate()) {
   using L = DenseSmem<K, V>;
   constexpr int MP = L::TP, KP = L::KP, VP = L::VP;
   constexpr int kVjpThreads = kDenseThreads, kVjpWaves = kDenseWaves;
@@ -708,7 +711,7 @@ __device__ __forceinline__ void dense_tile(const BwdArgs& a, int cidx, int hidx,
   bf16* sV = (bf16*)(smem + L::off_v);
   bf16* sKB = (bf16*)(smem + L::off_kb);
 
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  // ch: the chunk's table entry {row0, len, ...}
   const int len = ch.y;
   if (len <= 0) return;
   const int H = a.H, h = hidx;
@@ -1158,7 +1161,7 @@ struct DecaySmem {
 // per-element term stays in registers.  The key columns go in two passes of K/2 (the
 // operands of one pass fit in LDS beside q, k and G).
 template <int K, class Gate = NoGate>
-__device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx, const Gate& gate = Gate()) {
+__device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx, int4 ch, const Gate& gate = Gate()) {
   using L = DecaySmem<K>;
   constexpr int QP = L::QP, GP = L::GP, AP = L::AP, HALF = L::HALF, OP = L::OP, NSEG = L::NSEG;
   constexpr int NKT = 4 * (K / 16);
@@ -1188,7 +1191,7 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   float* sFk = sBeta + 256;
   int* sF = (int*)(smem + L::off_f);
 
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  // ch: the chunk's table entry {row0, len, ...}
   const int len = ch.y;
   if (len <= 0) return;
   const int H = a.H, h = hidx;
@@ -1592,10 +1595,10 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
   const int item = blockIdx.x;
   if (item < dense_count) {
     const int t = dense_begin + item;
-    dense_tile<K, V>(a, t / a.H, t % a.H);
+    dense_tile<K, V>(a, t / a.H, t % a.H, ((const int4*)a.ws.p[R_CHUNKS])[t / a.H]);
   } else {
     const int t = decay_begin + item - dense_count;
-    decay_tile<K>(a, t / a.H, t % a.H);
+    decay_tile<K>(a, t / a.H, t % a.H, ((const int4*)a.ws.p[R_CHUNKS])[t / a.H]);
   }
 }
 
@@ -1603,11 +1606,14 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
 // fused backward: scan, dense and decay tiles in one launch
 // ---------------------------------------------------------------------------
 // The scan members (the first scan_blocks workgroups) run the reverse scan and publish each
-// step.  Every other workgroup takes a ticket from a counter and runs the dense and then
-// the decay VJP of the tile the ticket names, tiles in the order the scan finalises them
-// (last chunks of every sequence first).  The dense part waits until every strip
-// of the tile's record has passed its chunk; the decay part reads what the same workgroup's
-// dense part stored.
+// step; the next prep_blocks workgroups form the scan's per-chunk inputs.  Every other
+// workgroup runs the dense and then the decay VJP of one tile, workgroup index order = the
+// order the scan finalises the tiles (last chunks of every sequence first), each reading
+// its position's record {chunk, row0, len, sequence, steps to wait for} written by the
+// scheduling launch: one load before the tile's own loads (a ticket counter and the chunk
+// table lookups were three dependent round trips, ≈3 µs under the launch's load).  The
+// dense part waits until every strip of the tile's record has passed its chunk; the decay
+// part reads what the same workgroup's dense part stored.
 //
 // Dispatch-order assumption: every wait is on scan members, which wait on nothing.  The
 // launch drains only if the scan members are resident while tiles wait.  They are the lowest
@@ -1623,14 +1629,13 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
 constexpr long long kSpinLimitDefault = 200000000LL;  // 2 s
 
 struct SyncView {
-  int* ticket;
   int* abort;
   int* base;
 };
 
 __device__ __forceinline__ SyncView sync_view(const BwdArgs& a) {
   int* base = (int*)a.sc.p[S_SYNC];
-  return {base, base + 1, base};
+  return {base + 1, base};
 }
 
 // Thread 0 waits for *p >= need, sleeping about 0.4 us per missing step between polls (the
@@ -1704,17 +1709,19 @@ __device__ void poison_tile(const BwdArgs& a, int cidx, int h) {
 // Clears the sync words and writes the chunk order: chunk c of sequence s with n chunks
 // has reverse rank r = n - 1 - (index in s); chunks go by r, then by sequence.  Position
 // of c = sum over sequences s' of min(n_s', r) + #{s' < s : n_s' > r}; chunks past the
-// last sequence keep their index.
+// last sequence keep their index.  Each position holds the chunk's table entry and the
+// step count its tiles wait for, so a tile reads one record before its loads.
 __device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks, int sync_words) {
   int* sync = (int*)a.sc.p[S_SYNC];
-  int* order = (int*)a.sc.p[S_ORDER];
+  int4* order = (int4*)a.sc.p[S_ORDER];
   const int4* chunks = (const int4*)a.ws.p[R_CHUNKS];
   const int2* seqs = (const int2*)a.ws.p[R_SEQS];
   for (int i = threadIdx.x; i < sync_words; i += blockDim.x) sync[i] = 0;
   for (int c = threadIdx.x; c < max_chunks; c += blockDim.x) {
     const int4 ch = chunks[c];
     if (ch.z < 0 || ch.y <= 0) {
-      order[c] = c;
+      order[2 * c] = make_int4(c, ch.x, ch.y, -1);
+      order[2 * c + 1] = make_int4(0, 0, 0, 0);
       continue;
     }
     const int r = seqs[ch.z].y - 1 - ch.w;
@@ -1723,7 +1730,8 @@ __device__ __forceinline__ void bwd_sched_body(const BwdArgs& a, int max_chunks,
       const int n = seqs[s].y;
       pos += min(n, r) + (s < ch.z && n > r ? 1 : 0);
     }
-    order[pos] = c;
+    order[2 * pos] = make_int4(c, ch.x, ch.y, ch.z);
+    order[2 * pos + 1] = make_int4(r + 1, 0, 0, 0);
   }
 }
 
@@ -1745,7 +1753,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
     // first steps find their operands first
     if (threadIdx.x >= kPrepThreads) return;
     const int i = blockIdx.x - scan_blocks;
-    const int cidx = ((const int*)a.sc.p[S_ORDER])[i / a.H], h = i % a.H;
+    const int cidx = ((const int4*)a.sc.p[S_ORDER])[2 * (i / a.H)].x, h = i % a.H;
     bwd_prep_body<K, V, true>(a, cidx, h);
     wait_vmcnt<0>();  // every write-through store of the tile is complete
     __syncthreads();
@@ -1753,24 +1761,24 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
       __hip_atomic_store(prep_flags + (size_t)cidx * a.H + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  __shared__ int s_ticket, s_failed;
-  if (threadIdx.x == 0) {
-    s_ticket = __hip_atomic_fetch_add(sv.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_failed = 0;
-  }
-  __syncthreads();
-  const int t = s_ticket, H = a.H;
-  const int cidx = ((const int*)a.sc.p[S_ORDER])[t / H], h = t % H;
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  __shared__ int s_failed;
+  if (threadIdx.x == 0) s_failed = 0;  // ordered before the gate by the dense part's barriers
+  // tile t in the scan's order: workgroups are dispatched in index order, so the tiles start
+  // in the order the scan finalises them (a tile waits only on scan members)
+  const int t = blockIdx.x - scan_blocks - prep_blocks, H = a.H, h = t % H;
+  const int4* rec4 = (const int4*)a.sc.p[S_ORDER] + 2 * (t / H);
+  const int4 r0 = rec4[0], r1 = rec4[1];
+  const int cidx = r0.x;
+  const int4 ch = make_int4(r0.y, r0.z, r0.w, 0);  // {row0, len, seq, -}
   int need = 0, rec = 0;
   if (ch.y > 0) {
     rec = ch.z * H + h;
-    need = ((const int2*)a.ws.p[R_SEQS])[ch.z].y - ch.w;
+    need = r1.x;
   }
   ScanGate gate{sv.base + kSyncRec + 32 * rec, V / 16, need, sv.abort, spin_limit, &s_failed};
-  dense_tile<K, V>(a, cidx, h, gate);
+  dense_tile<K, V>(a, cidx, h, ch, gate);
   __syncthreads();  // the dense part's stores are complete and visible to this workgroup
-  decay_tile<K>(a, cidx, h);
+  decay_tile<K>(a, cidx, h, ch);
   __syncthreads();
   if (s_failed && ch.y > 0) poison_tile<K, V>(a, cidx, h);  // computed from unwritten histories
 }
@@ -1871,7 +1879,7 @@ static int launch_backward(const kda_chunk_problem* p, const ChunkGeom& g, BwdAr
     return KDA_OK;
   };
   if ((stages & all) == all && p->num_seqs > 0 && g.max_chunks > 0 && fused_backward_enabled()) {
-    // one launch: scan members + ticketed dense / decay tiles (see chunk_bwd_fused_kernel)
+    // one launch: scan members + prep workgroups + dense / decay tiles (see chunk_bwd_fused_kernel)
     constexpr size_t smem =
         cmax_sz(kFusedSPW * BwdScanLds<K, V>::bytes + 2048, cmax_sz(DenseSmem<K, V>::bytes, DecaySmem<K>::bytes));
     static_assert(smem + 16 <= 160 * 1024, "fused backward LDS");

@@ -81,7 +81,8 @@ enum ScRegion {
   S_DGL,      // f32  [tile][K]      lam * dL/dlam (the state-decay part of dL/dG_last)
   S_DBETA,    // f32  [tile][64]     dL/dbeta from the dense VJP (U, M' terms)
   S_SYNC,     // int  fused backward: ticket, abort, per-record step counts, per-tile strip arrivals
-  S_ORDER,    // int  [max_chunks]   chunks in the fused backward's order (reverse rank, then sequence)
+  S_ORDER,    // int4 [max_chunks][2] the fused backward's order (reverse rank, then sequence): position p ->
+              //   {chunk, row0, len, seq} {steps the tile's record must publish, 0, 0, 0}
   S_COUNT
 };
 
@@ -131,7 +132,7 @@ __host__ __device__ inline size_t sc_region_bytes(const ChunkGeom& g, int r) {
     case S_DGL: return nt * K * 4;
     case S_DBETA: return nt * 64 * 4;
     case S_SYNC: return (32 + 32 * (size_t)g.num_seqs * g.heads + nt) * 4;
-    case S_ORDER: return (size_t)g.max_chunks * 4;
+    case S_ORDER: return (size_t)g.max_chunks * 32;
     default: return 0;
   }
 }
