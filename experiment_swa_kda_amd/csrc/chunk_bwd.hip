@@ -68,6 +68,7 @@ struct BwdArgs {
   long gld_qk, gld_v;  // row strides (elements per token) of dq / dk and of dv
   long dbeta_ld;       // row stride of dbeta; the dbeta_pad elements after a row's H are zeroed
   int dbeta_pad;
+  int fixed_T;  // > 0: every sequence has this length (chunk c = sequence * n + index)
 };
 
 // ---------------------------------------------------------------------------
@@ -1739,6 +1740,24 @@ __global__ __launch_bounds__(1024) void chunk_bwd_sched_kernel(BwdArgs a, int ma
   bwd_sched_body(a, max_chunks, sync_words);
 }
 
+// Position p of the fused backward's order -> chunk, its table entry {row0, len, seq, -} and
+// the steps its record must publish.  Sequences of one length: arithmetic (position
+// p = rank * sequences + sequence); otherwise the scheduling launch's record.
+struct TilePos {
+  int cidx, need;
+  int4 ch;
+};
+__device__ __forceinline__ TilePos tile_position(const BwdArgs& a, int p) {
+  if (a.fixed_T > 0) {
+    const int n = (a.fixed_T + kChunk - 1) / kChunk;
+    const int r = p / a.num_seqs, seq = p % a.num_seqs, j = n - 1 - r;
+    return {seq * n + j, r + 1, make_int4(seq * a.fixed_T + j * kChunk, min(kChunk, a.fixed_T - j * kChunk), seq, 0)};
+  }
+  const int4* rec4 = (const int4*)a.sc.p[S_ORDER] + 2 * p;
+  const int4 r0 = rec4[0], r1 = rec4[1];
+  return {r0.x, r1.x, make_int4(r0.y, r0.z, r0.w, 0)};
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a, int scan_blocks, int prep_blocks,
                                                                       long long spin_limit) {
@@ -1753,7 +1772,7 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
     // first steps find their operands first
     if (threadIdx.x >= kPrepThreads) return;
     const int i = blockIdx.x - scan_blocks;
-    const int cidx = ((const int4*)a.sc.p[S_ORDER])[2 * (i / a.H)].x, h = i % a.H;
+    const int cidx = tile_position(a, i / a.H).cidx, h = i % a.H;
     bwd_prep_body<K, V, true>(a, cidx, h);
     wait_vmcnt<0>();  // every write-through store of the tile is complete
     __syncthreads();
@@ -1766,14 +1785,13 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_fused_kernel(BwdArgs a,
   // tile t in the scan's order: workgroups are dispatched in index order, so the tiles start
   // in the order the scan finalises them (a tile waits only on scan members)
   const int t = blockIdx.x - scan_blocks - prep_blocks, H = a.H, h = t % H;
-  const int4* rec4 = (const int4*)a.sc.p[S_ORDER] + 2 * (t / H);
-  const int4 r0 = rec4[0], r1 = rec4[1];
-  const int cidx = r0.x;
-  const int4 ch = make_int4(r0.y, r0.z, r0.w, 0);  // {row0, len, seq, -}
+  const TilePos tp = tile_position(a, t / H);
+  const int cidx = tp.cidx;
+  const int4 ch = tp.ch;  // {row0, len, seq, -}
   int need = 0, rec = 0;
   if (ch.y > 0) {
     rec = ch.z * H + h;
-    need = r1.x;
+    need = tp.need;
   }
   ScanGate gate{sv.base + kSyncRec + 32 * rec, V / 16, need, sv.abort, spin_limit, &s_failed};
   dense_tile<K, V>(a, cidx, h, ch, gate);
@@ -2025,6 +2043,7 @@ static int chunk_backward_impl(int stages, const kda_chunk_problem* p, const voi
   BwdArgs a;
   a.H = p->heads;
   a.num_seqs = p->num_seqs;
+  a.fixed_T = (p->cu_seqlens == nullptr && g.max_chunks > 0) ? p->seq_len : 0;
   a.gate_mode = p->gate_mode;
   a.lb = p->lower_bound;
   a.scale = p->scale;
