@@ -71,6 +71,15 @@ struct BwdArgs {
   int fixed_T;  // > 0: every sequence has this length (chunk c = sequence * n + index)
 };
 
+// Sequence table entry {first chunk, chunk count}: arithmetic for sequences of one length.
+__device__ __forceinline__ int2 seq_entry(const BwdArgs& a, int seq) {
+  if (a.fixed_T > 0) {
+    const int nc = (a.fixed_T + kChunk - 1) / kChunk;
+    return make_int2(seq * nc, nc);
+  }
+  return ((const int2*)a.ws.p[R_SEQS])[seq];
+}
+
 // ---------------------------------------------------------------------------
 // reverse state-gradient scan (transition form)
 // ---------------------------------------------------------------------------
@@ -388,7 +397,7 @@ __device__ __forceinline__ void bwd_scan_body(const BwdArgs& a, int* progress, c
   const int seq = rec / H, h = rec % H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int lr = lane % 16, kg = lane / 16;
-  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int2 sq = seq_entry(a, seq);  // {first chunk, chunk count}
   const int n = sq.y;
   auto tile_of = [&](int r) { return (size_t)(sq.x + max(n - 1 - r, 0)) * H + h; };  // step r's chunk
   auto group = [&](int g) { return smem + g * L::bytes; };  // a strip's LDS (E ring, X staging)

@@ -71,6 +71,17 @@ struct FwdArgs {
   int conv_W;
 };
 
+// Sequence table entry {first chunk, chunk count}: arithmetic for sequences of one length
+// (no dependent load at a kernel's start), else the table chunk_prep_kernel built.
+template <class Args>
+__device__ __forceinline__ int2 seq_entry(const Args& a, int seq) {
+  if (a.fixed_T > 0) {
+    const int nc = (a.fixed_T + kChunk - 1) / kChunk;
+    return make_int2(seq * nc, nc);
+  }
+  return ((const int2*)a.ws.p[R_SEQS])[seq];
+}
+
 // ---------------------------------------------------------------------------
 // chunk / sequence tables
 // ---------------------------------------------------------------------------
@@ -854,7 +865,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_fwd_scan_kernel(FwdArgs a)
   const int seq = rec / H, h = rec % H, v0 = strip * 16;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lr = lane % 16, kg = lane / 16;
-  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int2 sq = seq_entry(a, seq);  // {first chunk, chunk count}
   const int n = sq.y;
   if (n <= 0) {
     if (wave == 0 && a.sfin) {
@@ -1081,7 +1092,7 @@ __global__ __launch_bounds__(kSegThreads) void chunk_fwd_seg_kernel(FwdArgs a, i
   const int seq = rec / H, h = rec % H;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lr = lane % 16, kg = lane / 16;
-  const int2 sq = ((const int2*)a.ws.p[R_SEQS])[seq];
+  const int2 sq = seq_entry(a, seq);  // {first chunk, chunk count}
   const int n = sq.y;
   const int nseg = (n + seg_len - 1) / seg_len;
   const int u_first = group * C::SPG;  // the workgroup's strips, V strips first
@@ -1305,7 +1316,7 @@ __global__ __launch_bounds__(kCombThreads) void chunk_fwd_combine_kernel(FwdArgs
   if (!xcd_strip_coords(a.num_seqs * H, VS, rec, strip)) return;
   const int seq = rec / H, h = rec % H;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, lr = lane % 16, kg = lane / 16;
-  const int n = ((const int2*)a.ws.p[R_SEQS])[seq].y;
+  const int n = seq_entry(a, seq).y;
   const int nseg = (n + seg_len - 1) / seg_len;
   if (nseg <= 1) return;
   const int v = 16 * strip + lr;
