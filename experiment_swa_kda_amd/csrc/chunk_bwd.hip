@@ -71,6 +71,15 @@ struct BwdArgs {
   int fixed_T;  // > 0: every sequence has this length (chunk c = sequence * n + index)
 };
 
+// Chunk table entry {row0, len, sequence, index}: arithmetic for sequences of one length.
+__device__ __forceinline__ int4 chunk_entry(const BwdArgs& a, int c) {
+  if (a.fixed_T > 0) {
+    const int nc = (a.fixed_T + kChunk - 1) / kChunk, sq = c / nc, j = c % nc;
+    return make_int4(sq * a.fixed_T + j * kChunk, min(kChunk, a.fixed_T - j * kChunk), sq, j);
+  }
+  return ((const int4*)a.ws.p[R_CHUNKS])[c];
+}
+
 // Sequence table entry {first chunk, chunk count}: arithmetic for sequences of one length.
 __device__ __forceinline__ int2 seq_entry(const BwdArgs& a, int seq) {
   if (a.fixed_T > 0) {
@@ -143,7 +152,7 @@ __device__ __forceinline__ void bwd_prep_body(const BwdArgs& a, int cidx, int h)
   bf16* sW = (bf16*)(smem + L::off_w);
   bf16* sA = (bf16*)(smem + L::off_a);
   const int H = a.H;
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  const int4 ch = chunk_entry(a, cidx);
   const int len = ch.y, row0 = ch.x;
   if (len <= 0) return;
   const size_t tile = (size_t)cidx * H + h;
@@ -1605,10 +1614,10 @@ __global__ __launch_bounds__(kVjpThreads) void chunk_bwd_vjp_kernel(BwdArgs a, i
   const int item = blockIdx.x;
   if (item < dense_count) {
     const int t = dense_begin + item;
-    dense_tile<K, V>(a, t / a.H, t % a.H, ((const int4*)a.ws.p[R_CHUNKS])[t / a.H]);
+    dense_tile<K, V>(a, t / a.H, t % a.H, chunk_entry(a, t / a.H));
   } else {
     const int t = decay_begin + item - dense_count;
-    decay_tile<K>(a, t / a.H, t % a.H, ((const int4*)a.ws.p[R_CHUNKS])[t / a.H]);
+    decay_tile<K>(a, t / a.H, t % a.H, chunk_entry(a, t / a.H));
   }
 }
 
@@ -1694,7 +1703,7 @@ struct ScanGate {
 // dbeta and its K3-parameter partials (the parameter reduction then yields NaN).
 template <int K, int V>
 __device__ void poison_tile(const BwdArgs& a, int cidx, int h) {
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[cidx];
+  const int4 ch = chunk_entry(a, cidx);
   const int row0 = ch.x, len = ch.y, H = a.H;
   const float nan = __builtin_nanf("");
   const bf16 nanb = to_bf16(nan);

@@ -71,6 +71,16 @@ struct FwdArgs {
   int conv_W;
 };
 
+// Chunk table entry {row0, len, sequence, index}: arithmetic for sequences of one length.
+template <class Args>
+__device__ __forceinline__ int4 chunk_entry(const Args& a, int c) {
+  if (a.fixed_T > 0) {
+    const int nc = (a.fixed_T + kChunk - 1) / kChunk, sq = c / nc, j = c % nc;
+    return make_int4(sq * a.fixed_T + j * kChunk, min(kChunk, a.fixed_T - j * kChunk), sq, j);
+  }
+  return ((const int4*)a.ws.p[R_CHUNKS])[c];
+}
+
 // Sequence table entry {first chunk, chunk count}: arithmetic for sequences of one length
 // (no dependent load at a kernel's start), else the table chunk_prep_kernel built.
 template <class Args>
@@ -1415,7 +1425,7 @@ template <int K, int V>
 __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   constexpr int OP = V + 8;  // bf16 row stride of a wave's 16-row staging tile
   __shared__ __attribute__((aligned(16))) bf16 sOut[4][16 * OP];
-  const int4 ch = ((const int4*)a.ws.p[R_CHUNKS])[blockIdx.x];
+  const int4 ch = chunk_entry(a, blockIdx.x);
   const int len = ch.y;
   if (len <= 0) return;
   const int H = a.H, h = blockIdx.y;
