@@ -537,11 +537,6 @@ __global__ __launch_bounds__(kIntraThreads, 2 * kIntraNH) void chunk_fwd_intra_k
       *(float4*)r = make_float4(g[s][0], g[s][1], g[s][2], g[s][3]);
       *(float4*)(r + 4) = make_float4(g[s][4], g[s][5], g[s][6], g[s][7]);
     }
-    if (i == 63) {
-      float* lam = (float*)a.ws.p[R_LAM] + tile * K + 32 * S(s) + 8 * kg;
-      *(float4*)lam = make_float4(expf(g[s][0]), expf(g[s][1]), expf(g[s][2]), expf(g[s][3]));
-      *(float4*)(lam + 4) = make_float4(expf(g[s][4]), expf(g[s][5]), expf(g[s][6]), expf(g[s][7]));
-    }
   }
   __syncthreads();
 
@@ -800,6 +795,10 @@ __global__ __launch_bounds__(kIntraThreads, 2 * kIntraNH) void chunk_fwd_intra_k
   emit_frags<64, K, kIntraThreads, true>((bf16*)a.ws.p[R_QGF] + tile * 64 * K, tid,
                                          [&](int r, int c) { return sQg[r * RS + c]; });
   emit_frags_tr<K, 64, kIntraThreads, true>((bf16*)a.ws.p[R_KDTF] + tile * K * 64, tid, sKd, RS);
+  // lam = e^{G_last}, one channel per thread from the staged last row (off the critical
+  // path: computed by the lanes holding row 63 it delayed every wave at the cumulative-decay
+  // barrier)
+  if (tid < K) ((float*)a.ws.p[R_LAM])[tile * K + tid] = expf(sGref[4 * K + tid]);
 }
 
 // ---------------------------------------------------------------------------
