@@ -672,26 +672,46 @@ __global__ __launch_bounds__(kIntraThreads, 2 * kIntraNH) void chunk_fwd_intra_k
   __syncthreads();
 
   // ---- phase 3: T = (I + diag(beta) M')^-1 (waves of part 0) ----
-  // diagonal blocks by forward substitution, one column per lane (lanes of group kg = 0)
+  // Diagonal blocks: N = diag(beta) M' on a 16 x 16 diagonal block is strictly lower, so
+  // N^16 = 0 and (I + N)^-1 = (I + P)(I + P^2)(I + P^4)(I + P^8) with P = -N: three
+  // squarings and three updates X <- X + X P^(2^k), every product four
+  // v_mfma_f32_16x16x4_f32 steps on registers.  A matrix M is held in the accumulator layout
+  // (lane (c, q) holds M[4q + r][c], r < 4); with the contraction index of step s and lane
+  // group q taken as k = 4q + s, that layout is the B operand as it stands and the A operand
+  // of M^T, so each matrix is carried together with its transpose (P with Q = P^T, X with
+  // Y = X^T).  All 64 lanes work, and the chain is 6 products deep instead of a 16-step
+  // substitution per column.
   {
-    const int o = 16 * rb, j = lr;
-    float x[16];
+    const int o = 16 * rb;
     if (hh == 0) {
+      auto mm = [&](const f32x4& at, const f32x4& b, f32x4 acc) {  // acc + A B, at = A^T's registers
 #pragma unroll
-      for (int ii = 0; ii < 16; ++ii) {
-        float sacc = (ii == j) ? 1.f : 0.f;
-        const float bi = sBeta[o + ii];
+        for (int st = 0; st < 4; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(at[st], b[st], acc, 0, 0, 0);
+        return acc;
+      };
+      f32x4 P, Q, X, Y;
 #pragma unroll
-        for (int m = 0; m < ii; ++m) sacc = fmaf(-bi * sM[(o + ii) * 65 + o + m], x[m], sacc);
-        x[ii] = (ii < j) ? 0.f : sacc;
+      for (int r = 0; r < 4; ++r) {
+        const int ii = 4 * kg + r;  // row of this register, lr the column
+        P[r] = ii > lr ? -sBeta[o + ii] * sM[(o + ii) * 65 + o + lr] : 0.f;  // -N[ii][lr]
+        Q[r] = lr > ii ? -sBeta[o + lr] * sM[(o + lr) * 65 + o + ii] : 0.f;  // -N[lr][ii]
+        X[r] = P[r] + (ii == lr ? 1.f : 0.f);
+        Y[r] = Q[r] + (ii == lr ? 1.f : 0.f);
       }
-    }
-    __syncthreads();  // sA (aliasing sT) is no longer read
-    if (hh == 0) {
-      if (kg == 0) {
 #pragma unroll
-        for (int ii = 0; ii < 16; ++ii) sT[(o + ii) * 65 + o + j] = x[ii];
+      for (int it = 0; it < 3; ++it) {
+        const f32x4 P2 = mm(Q, P, zero4());  // P^2 (A = P through Q = P^T)
+        const f32x4 Xn = mm(Y, P2, X);       // X + X P^2
+        if (it < 2) {
+          const f32x4 Q2 = mm(P, Q, zero4());  // (P^2)^T = Q Q
+          Y = mm(P2, Y, Y);                    // Y + (P^2)^T Y = (X + X P^2)^T
+          Q = Q2;
+        }
+        P = P2;
+        X = Xn;
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sT[(o + 4 * kg + r) * 65 + o + lr] = X[r];
       for (int idx = lane; idx < 16 * 16 * (3 - rb); idx += kWave) {  // zero blocks right of the diagonal
         const int cb = rb + 1 + idx / 256, rr = (idx % 256) / 16, cc = idx % 16;
         sT[(o + rr) * 65 + 16 * cb + cc] = 0.f;
