@@ -1297,6 +1297,8 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   __syncthreads();
   const bool unsafe = (sF[0] | sF[1] | sF[2] | sF[3]) != 0;
 
+  // the dense part's dbeta partial of row tid (needed after P1; requested now)
+  const float dbeta_dense = tid < 64 ? ((const float*)a.sc.p[S_DBETA])[tile * 64 + tid] : 0.f;
   // ---- P1: per pass (K/2 key columns) build the decay-scaled operands, then one item per
   // wave: row side + column side + all per-element terms ----
 #pragma unroll 1
@@ -1468,7 +1470,7 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   // per-row dot products (fixed order) and dbeta
   if (tid < 64) {
     const int t = tid;
-    float dotq = 0.f, dotk = 0.f, db = ((const float*)a.sc.p[S_DBETA])[tile * 64 + t];
+    float dotq = 0.f, dotk = 0.f, db = dbeta_dense;
 #pragma unroll
     for (int q = 0; q < K / 16; ++q) {
       dotq += sPQ[q * 64 + t];
@@ -1537,7 +1539,11 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   const int c = tid % K, seg = tid / K;
   const bool k3 = a.gate_mode == KDA_GATE_K3;
   // K3: this thread's raw gate values, requested together before the segment sums (rows
-  // past the chunk end read the last row and are not used)
+  // past the chunk end read the last row and are not used), with the column's dG_last part
+  // and gate parameters (loaded after the barrier they were a round trip of their own)
+  const float dgl = ((const float*)a.sc.p[S_DGL])[tile * K + c];
+  const float alog = k3 ? a.A_log[h] : 0.f;
+  const float bias = k3 ? a.dt_bias[h * K + c] : 0.f;
   float graw[RPS];
   if (k3) {
 #pragma unroll
@@ -1554,13 +1560,12 @@ __device__ __forceinline__ void decay_tile(const BwdArgs& a, int cidx, int hidx,
   }
   __syncthreads();
   {
-    float acc = ((const float*)a.sc.p[S_DGL])[tile * K + c];
+    float acc = dgl;
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc += sGL[q * K + c];
     for (int s = NSEG - 1; s > seg; --s) acc += sSeg[s * K + c];
     float p0 = 0.f, p1 = 0.f;
-    const float ea = k3 ? expf(a.A_log[h]) : 0.f;
-    const float bias = k3 ? a.dt_bias[h * K + c] : 0.f;
+    const float ea = k3 ? expf(alog) : 0.f;
 #pragma unroll
     for (int r = RPS - 1; r >= 0; --r) {
       const int t = seg * RPS + r;
