@@ -1461,6 +1461,22 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   for (int s = 0; s < K / 32; ++s) fq[s] = *(const bf16x8*)(QGF + frag_off(K, wave, s, lane));
 #pragma unroll
   for (int s = 0; s < 2; ++s) fa[s] = *(const bf16x8*)(AF + frag_off(64, wave, s, lane));
+  // the optional norm epilogue's gate values and weights, requested with the operands (after
+  // the products they were a round trip of their own)
+  const bool ng = a.ng_out != nullptr;
+  bf16 gvr[V / 16][4];
+  float w[V / 16];
+  if (ng) {
+#pragma unroll
+    for (int ct = 0; ct < V / 16; ++ct) {
+      w[ct] = a.ng_weight[16 * ct + lr];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = min(16 * wave + 4 * kg + r, len - 1);
+        gvr[ct][r] = a.ng_gate[(size_t)(ch.x + t) * a.ng_gate_ld + (size_t)h * V + 16 * ct + lr];
+      }
+    }
+  }
   // o of this lane's 4 rows x V/16 columns, kept for the optional norm epilogue
   float ov[V / 16][4];
 #pragma unroll
@@ -1495,20 +1511,15 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   };
   __builtin_amdgcn_wave_barrier();
   store_tile(a.out);
-  if (a.ng_out == nullptr) return;
+  if (!ng) return;
   // fused RMSNorm * weight * sigmoid(gate) over each token's V values of this head, from the
   // bf16-rounded o exactly as the standalone norm kernel reads it: a row's V values live in
   // the 16 lanes of one lane group (V/16 columns each)
-  float gv[V / 16][4], w[V / 16];
+  float gv[V / 16][4];
 #pragma unroll
-  for (int ct = 0; ct < V / 16; ++ct) {
-    w[ct] = a.ng_weight[16 * ct + lr];
+  for (int ct = 0; ct < V / 16; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = min(16 * wave + 4 * kg + r, len - 1);
-      gv[ct][r] = to_f32(a.ng_gate[(size_t)(ch.x + t) * a.ng_gate_ld + (size_t)h * V + 16 * ct + lr]);
-    }
-  }
+    for (int r = 0; r < 4; ++r) gv[ct][r] = to_f32(gvr[ct][r]);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float ss = 0.f;
