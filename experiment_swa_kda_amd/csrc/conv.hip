@@ -24,7 +24,7 @@ namespace kda {
 // Tile shapes (tokens per thread, channel groups per workgroup); the token slices per
 // workgroup are 256 / channel groups.  Overridable at build time for tuning sweeps.
 #ifndef KDA_CONV_FWD_TOK
-#define KDA_CONV_FWD_TOK 8
+#define KDA_CONV_FWD_TOK 2
 #endif
 #ifndef KDA_CONV_FWD_CGS
 #define KDA_CONV_FWD_CGS 16
@@ -77,20 +77,22 @@ __device__ __forceinline__ void load_taps(const bf16* __restrict__ w, int c0, fl
     for (int j = 0; j < W; ++j) wt[e][j] = (float)v[(e * W + j) / 8][(e * W + j) % 8];
 }
 
-// N rows of 8 channels of x at tokens t = p0 - (W-1) + i (i < N), i.e. xp[p0 + i].  All
-// loads are issued first (row index clamped into [0, T-1]); rows with t < 0 then come
-// from the initial state (or zero), rows with t >= T are zero.
+// N rows of 8 channels of x at tokens t = p0 - (W-1) + i (i < N), i.e. xp[p0 + i].
+// issue_xp_row issues one row's load (row index clamped into [0, T-1]); fix_xp_rows then
+// replaces rows with t < 0 by the initial state (or zero) and rows with t >= T by zero.
+// The fix-up is a per-lane branch that waits for every row it may overwrite, so all other
+// loads a thread needs are issued before it (one memory round trip, not two).
+template <int W>
+__device__ __forceinline__ bf16x8 issue_xp_row(const bf16* __restrict__ x, int b, int T, long ldx, int c0,
+                                               int p0, int i) {
+  int t = p0 - (W - 1) + i;
+  t = t < 0 ? 0 : (t >= T ? T - 1 : t);
+  return *reinterpret_cast<const bf16x8*>(x + (size_t)b * T * ldx + c0 + (size_t)t * ldx);
+}
+
 template <int W, int N>
-__device__ __forceinline__ void load_xp_rows(const bf16* __restrict__ x, const bf16* __restrict__ st,
-                                             int b, int T, int C, long ldx, int c0, int p0,
-                                             bf16x8 (&raw)[N]) {
-  const bf16* base = x + (size_t)b * T * ldx + c0;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    int t = p0 - (W - 1) + i;
-    t = t < 0 ? 0 : (t >= T ? T - 1 : t);
-    raw[i] = *reinterpret_cast<const bf16x8*>(base + (size_t)t * ldx);
-  }
+__device__ __forceinline__ void fix_xp_rows(const bf16* __restrict__ st, int b, int T, int C, int c0, int p0,
+                                            bf16x8 (&raw)[N]) {
   const bf16 zero = (bf16)0.f;
   if (p0 < W - 1 || p0 - (W - 1) + N > T) {
 #pragma unroll
@@ -126,7 +128,9 @@ __global__ __launch_bounds__(256) void conv_fwd_kernel(FwdGeom g, const bf16* __
   float wt[8][W];
   load_taps<W>(w, P.c0, wt);
   bf16x8 xr[NX];
-  load_xp_rows<W, NX>(x, st, P.b, g.T, g.C, g.ldx, P.c0, P.t0, xr);
+#pragma unroll
+  for (int i = 0; i < NX; ++i) xr[i] = issue_xp_row<W>(x, P.b, g.T, g.ldx, P.c0, P.t0, i);
+  fix_xp_rows<W, NX>(st, P.b, g.T, g.C, P.c0, P.t0, xr);
   bf16* yb = y + ((size_t)P.b * g.T + P.t0) * g.C + P.c0;
 #pragma unroll
   for (int u = 0; u < kTok; ++u) {
@@ -204,13 +208,18 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
     load_taps<W>(w, c0, wt);
     constexpr int NX = kTok + W - 1;
     bf16x8 xr[NX], gr[kTok];
-    load_xp_rows<W, NX>(x, st, b, g.T, g.C, g.ldx, c0, s0, xr);
+    // in the order the tokens consume them (loads complete in order): token u needs
+    // rows u .. u+W-1 of xp and dy row u
     const bf16* dyb = dy + (size_t)b * g.T * g.C + c0;
 #pragma unroll
+    for (int i = 0; i < W - 1; ++i) xr[i] = issue_xp_row<W>(x, b, g.T, g.ldx, c0, s0, i);
+#pragma unroll
     for (int u = 0; u < kTok; ++u) {
+      xr[u + W - 1] = issue_xp_row<W>(x, b, g.T, g.ldx, c0, s0, u + W - 1);
       const int sc = s0 + u < g.T ? s0 + u : g.T - 1;
       gr[u] = *reinterpret_cast<const bf16x8*>(dyb + (size_t)sc * g.C);
     }
+    fix_xp_rows<W, NX>(st, b, g.T, g.C, c0, s0, xr);
 #pragma unroll
     for (int u = 0; u < kTok; ++u) {
       const bool live = s0 + u < g.T;
@@ -224,7 +233,10 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
         float pre = 0.f;
 #pragma unroll
         for (int j = 0; j < W; ++j) pre = fmaf(xv[j], wt[e][j], pre);
-        dp[e] = live ? (float)gr[u][e] * silu_grad(pre) : 0.f;
+        // computed for every lane, then selected (a conditional expression around the
+        // exp/rcp chain compiles to a branch per element, which serialises the chains)
+        const float d = (float)gr[u][e] * silu_grad(pre);
+        dp[e] = live ? d : 0.f;
         const float dpo = owned ? dp[e] : 0.f;
 #pragma unroll
         for (int j = 0; j < W; ++j) dwacc[e][j] = fmaf(dpo, xv[j], dwacc[e][j]);
@@ -270,16 +282,38 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(BwdGeom g, const bf16* __
       store8(dxb + (size_t)u * g.ldd, o);
     }
   }
-  // reduce the kWave/kCgs token slices of each wave across lanes, then the waves via LDS
+  // the 8 token slices of a wave (lane bits 3-5) summed by halving exchanges: at each
+  // step a lane keeps half of its values and adds its partner's copy of that half, so
+  // after the lane ^ 8, ^ 16 and ^ 32 steps each lane holds W of the 8W sums (no masked
+  // per-value chains); then the waves through LDS, in a fixed order
+  static_assert(kCgs == 8, "slice bits are lane bits 3-5");
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  float h1[4 * W], h2[2 * W], h3[W];
+  const bool b3 = lane & 8, b4 = lane & 16, b5 = lane & 32;
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
+  for (int i = 0; i < 4 * W; ++i) {
+    const float lo = dwacc[i / W][i % W], hi = dwacc[(i + 4 * W) / W][(i + 4 * W) % W];
+    const float keep = b3 ? hi : lo, give = b3 ? lo : hi;
+    h1[i] = keep + dpp_mov<0x128>(give);  // row_ror:8: the value of lane ^ 8
+  }
 #pragma unroll
-    for (int j = 0; j < W; ++j) {
-      float v = dwacc[e][j];
-      v = lane_stride_sum<kCgs>(v);
-      if (lane < kCgs) s_dw[wave][(lg * 8 + e) * W + j] = v;
-    }
+  for (int i = 0; i < 2 * W; ++i) {
+    // even rows keep h1[i], odd rows h1[i + 2W]; the swap hands each row its partner's half
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, h1[i]),
+                                                    __builtin_bit_cast(unsigned, h1[i + 2 * W]), false, false);
+    h2[i] = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, h2[i]),
+                                                    __builtin_bit_cast(unsigned, h2[i + W]), false, false);
+    h3[i] = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  }
+  {
+    const int base = (b3 ? 4 * W : 0) + (b4 ? 2 * W : 0) + (b5 ? W : 0);
+#pragma unroll
+    for (int i = 0; i < W; ++i) s_dw[wave][lg * 8 * W + base + i] = h3[i];
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < kCgs * 8 * W; i += 256) {
     float acc = 0.f;
