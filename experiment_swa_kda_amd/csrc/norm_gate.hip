@@ -14,12 +14,12 @@
 
 namespace kda {
 
-// Rows per thread.  Forward: 3 gives 48 rows per workgroup at D = 128, i.e. 512 workgroups
-// (two per CU, evenly) for the 24,576 rows of B2 T4096 H3 (4 left half the CUs with one more
-// workgroup than the rest).  Backward: 6, one workgroup per CU, and half the weight-gradient
-// partials for the reduction launch (measured: 9.5 us against 10.0 with 3 and 10.3 with 4).
+// Rows per thread.  Forward: 1, 16 rows per workgroup at D = 128 (1,536 workgroups for the
+// 24,576 rows of B2 T4096 H3; measured 3.5 us against 3.7 with 2, 4.0 with 3, 4.5 with 4).
+// Backward: 6, one workgroup per CU, and half the weight-gradient partials for the
+// reduction launch (measured: 9.3 us against 10.2 with 3, 10.3 with 4 and 11.2 with 2).
 #ifndef KDA_NORM_ROWS_FWD
-#define KDA_NORM_ROWS_FWD 3
+#define KDA_NORM_ROWS_FWD 1
 #endif
 #ifndef KDA_NORM_ROWS_BWD
 #define KDA_NORM_ROWS_BWD 6
@@ -48,6 +48,11 @@ __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf1
     xr[i] = *reinterpret_cast<const bf16x8*>(x + r * D + c0);
     gr[i] = *reinterpret_cast<const bf16x8*>(gate + r * D + c0);
   }
+  // every row load issued before any use: left alone, the compiler sinks a gate row's load
+  // into the row's store branch (its only use), behind the wait for the earlier rows -- a
+  // second memory round trip.  The empty asm "uses" the gate rows here.
+#pragma unroll
+  for (int i = 0; i < kRowsFwd; ++i) asm volatile("" : "+v"(gr[i]));
 #pragma unroll
   for (int i = 0; i < kRowsFwd; ++i) {
     const long r = r0 + (long)i * RPP;
@@ -105,6 +110,7 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     gr[i] = *reinterpret_cast<const bf16x8*>(gate + goff(r, gld) + c0);
     dr[i] = *reinterpret_cast<const bf16x8*>(dy + r * D + c0);
   }
+  __builtin_amdgcn_sched_barrier(0);  // every row load issued before any use (as above)
 #pragma unroll
   for (int e = 0; e < 8; ++e) dwacc[e] = 0.f;
 #pragma unroll
