@@ -1440,6 +1440,9 @@ __global__ __launch_bounds__(kCombThreads) void chunk_fwd_combine_kernel(FwdArgs
 // ---------------------------------------------------------------------------
 // One 256-thread workgroup per (chunk, head); wave w owns the 16-token row tile w and
 // walks the V/16 column tiles, so its Qg and A operands are loaded once.
+#ifndef KDA_OUT_AHEAD
+#define KDA_OUT_AHEAD 2  // column tiles whose fragments are in flight ahead of the products
+#endif
 template <int K, int V>
 __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
   constexpr int OP = V + 8;  // bf16 row stride of a wave's 16-row staging tile
@@ -1477,21 +1480,35 @@ __global__ __launch_bounds__(256) void chunk_fwd_output_kernel(FwdArgs a) {
       }
     }
   }
-  // o of this lane's 4 rows x V/16 columns, kept for the optional norm epilogue
+  // o of this lane's 4 rows x V/16 columns, kept for the optional norm epilogue.  The state
+  // and delta fragments of KDA_OUT_AHEAD column tiles are requested before the first
+  // product (left to the scheduler, only 2-4 were in flight: a chain of round trips).
+  constexpr int kAhead = KDA_OUT_AHEAD < V / 16 ? KDA_OUT_AHEAD : V / 16;
+  bf16x8 sf[V / 16][K / 32], df[V / 16][2];
+  auto fetch = [&](int ct) {
+    const bf16* sb = SHBF + (size_t)ct * 16 * K;
+    const bf16* db = DLF + (size_t)ct * 16 * 64;
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) sf[ct][s] = *(const bf16x8*)(sb + ((size_t)s * 64 + lane) * 8);
+    df[ct][0] = *(const bf16x8*)(db + (size_t)lane * 8);
+    df[ct][1] = *(const bf16x8*)(db + (size_t)(64 + lane) * 8);
+  };
+#pragma unroll
+  for (int ct = 0; ct < kAhead; ++ct) fetch(ct);
+  __builtin_amdgcn_sched_barrier(0);
   float ov[V / 16][4];
 #pragma unroll
   for (int ct = 0; ct < V / 16; ++ct) {
+    if (ct + kAhead < V / 16) fetch(ct + kAhead);
     const int vcol = 16 * ct + lr;
-    const bf16* sb = SHBF + (size_t)ct * 16 * K;
-    const bf16* db = DLF + (size_t)ct * 16 * 64;
     f32x4 o0 = zero4(), o1 = zero4();
 #pragma unroll
     for (int s = 0; s < K / 32; s += 2) {
-      o0 = mfma16(fq[s], *(const bf16x8*)(sb + ((size_t)s * 64 + lane) * 8), o0);
-      o1 = mfma16(fq[s + 1], *(const bf16x8*)(sb + ((size_t)(s + 1) * 64 + lane) * 8), o1);
+      o0 = mfma16(fq[s], sf[ct][s], o0);
+      o1 = mfma16(fq[s + 1], sf[ct][s + 1], o1);
     }
-    o0 = mfma16(fa[0], *(const bf16x8*)(db + (size_t)lane * 8), o0);
-    o1 = mfma16(fa[1], *(const bf16x8*)(db + (size_t)(64 + lane) * 8), o1);
+    o0 = mfma16(fa[0], df[ct][0], o0);
+    o1 = mfma16(fa[1], df[ct][1], o1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bf16 ob = to_bf16(o0[r] + o1[r]);
