@@ -73,6 +73,10 @@ SIGNATURES = {
                                                          _P, _P]),
     "kda_softcap_cross_entropy_forward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P]),
     "kda_softcap_cross_entropy_backward": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P, _P]),
+    "kda_softcap_cross_entropy_fused_supported": (ctypes.c_int, [_I, _L]),
+    "kda_softcap_cross_entropy_fused": (ctypes.c_int, [_L, _I, _L, _F, _P, _P, _L, _P, _P, _P, _P, _P]),
+    "kda_softcap_cross_entropy_count": (ctypes.c_int, [_L, _P, _L, _F, _P, _P, _P]),
+    "kda_bf16_rescale_if_changed": (ctypes.c_int, [_L, _P, _P, _F, _P]),
     "kda_weight_grad_scratch_bytes": (ctypes.c_size_t, [_L, _I, _I]),
     "kda_weight_grad": (ctypes.c_int, [_L, _I, _I, _P, _L, _P, _L, _P, _P, _P]),
     "kda_resid_mix_backward_scratch_bytes": (ctypes.c_size_t, [_L]),

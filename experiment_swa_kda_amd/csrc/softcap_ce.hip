@@ -265,6 +265,185 @@ __global__ __launch_bounds__(kCeThreads) void softcap_ce_bwd_kernel(
   }
 }
 
+// Forward and backward in one pass for rows of 4096 NV columns, all of them vocabulary
+// (NV <= 8: up to 32768; other shapes take the two-kernel path): one 512-thread workgroup
+// per row at a time holds the whole row in registers (NV 16-byte vectors per thread, the
+// next row's already in flight), sums exp(z) over the row (waves, then eight partials
+// through LDS in a fixed order), and from the same registers writes the gradient for the
+// expected upstream gradient (*grad_scale = expected dL/dmean / count).  The logits are read
+// once instead of twice; the backward only has to confirm the scale.  Row loss, lse and
+// gradient use the forward's and the backward's formulas (the row sum is taken in another
+// order, so they agree with the two-kernel path to rounding, not bit for bit).  The body is
+// free of per-lane branches (their exec masks spilled the scalar registers): the one thread
+// holding the target column reads its logit and afterwards re-stores its vector with the
+// target's term.
+constexpr int kCeFusedThreads = 512;               // 8 waves per row
+constexpr int kCeFusedCols = kCeFusedThreads * 8;  // columns per 16-byte vector pass of a workgroup
+constexpr int kCeFusedMaxVec = 8;                  // rows up to 32768 columns (two rows in registers)
+constexpr int kCeFusedPerCu = 1;                   // 66 KB table, 8 waves per workgroup
+
+template <int NV>
+__global__ __launch_bounds__(kCeFusedThreads) void softcap_ce_fused_kernel(
+    long rows, int vocab, float cap, const bf16* __restrict__ logits, const int64_t* __restrict__ targets,
+    int64_t ignore_index, const float* __restrict__ grad_scale, float* __restrict__ loss_row,
+    float* __restrict__ lse_row, bf16* __restrict__ grad) {
+  __shared__ float2 tab[kTabSize];
+  __shared__ float s_part[2][kCeFusedThreads / kWave];
+  __shared__ float s_zt[2];
+  for (int i = threadIdx.x; i < kTabSize; i += kCeFusedThreads) {
+    const float th = tanhf(tab_pattern_value(i) / cap);
+    tab[i] = make_float2(expf(cap * th), 1.0f - th * th);
+  }
+  __syncthreads();
+  const float2* tabz = tab - (kTabELo << 7);
+  const float gs = *grad_scale;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const long G = gridDim.x;
+  constexpr long kRow = (long)NV * kCeFusedCols;  // = vocab = row stride
+  auto load = [&](long r, bf16x8* x) {
+    const bf16* p = logits + r * kRow + tid * 8;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) x[v] = *reinterpret_cast<const bf16x8*>(p + v * kCeFusedCols);
+  };
+  auto process = [&](long r, const bf16x8* x, int64_t t, int slot) {
+    const bool ign = t == ignore_index, in_range = t >= 0 && t < vocab;
+    const int tc = in_range ? (int)t : -1;
+    const bool owner = in_range && (tc % kCeFusedCols) / 8 == tid;  // holds the target column
+    const int vt = tc / kCeFusedCols, et = tc % 8;
+    // the row sum of exp(z) (NaN if a logit is NaN)
+    float sum = 0.f;
+    u16x2 mag = (u16x2)0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const uint4 w = __builtin_bit_cast(uint4, x[v]);
+      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+      float sb = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int i0, i1;
+        tab_index2_biased(ws[e], i0, i1);
+        mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, ws[e] & 0x7fff7fffu));
+        sb += tabz[i0].x + tabz[i1].x;
+      }
+      sum += sb;
+    }
+    if (owner) {
+      float raw = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) raw = (v == vt && e == et) ? (float)x[v][e] : raw;
+      s_zt[slot] = cap * tanhf(raw / cap);
+    }
+    const bool nan_here = mag.x > 0x7f80 || mag.y > 0x7f80;
+    const float wsum = wave_sum(nan_here ? __builtin_nanf("") : sum);
+    if (lane == 0) s_part[slot][wave] = wsum;
+    wait_lgkm0();
+    ring_barrier();  // the partials (and the target's z) are in LDS; loads stay in flight
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kCeFusedThreads / kWave; ++w) tot += s_part[slot][w];
+    const float lse = __logf(tot);
+    if (tid == 0) {
+      loss_row[r] = ign ? 0.f : (in_range ? lse - s_zt[slot] : __builtin_nanf(""));
+      lse_row[r] = lse;
+    }
+    // the gradient, as the backward kernel forms it
+    const float g = ign ? 0.f : gs;
+    const float einv = __expf(-lse);
+    const float ge = g * einv;
+    bf16* q = grad + r * kRow + tid * 8;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const uint4 w = __builtin_bit_cast(uint4, x[v]);
+      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+      bf16x8 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int i0, i1;
+        tab_index2_biased(ws[e], i0, i1);
+        const float2 v0 = tabz[i0], v1 = tabz[i1];
+        y[2 * e] = to_bf16(v0.x * ge * v0.y);
+        y[2 * e + 1] = to_bf16(v1.x * ge * v1.y);
+      }
+      *reinterpret_cast<bf16x8*>(q + v * kCeFusedCols) = y;
+    }
+    if (owner) {  // the target's vector again, every element in the backward's general form
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        if (v == vt) {
+          bf16x8 y;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float2 vv = tab[tab_index(bf16_bits(x[v][e]))];
+            y[e] = to_bf16(g * (vv.x * einv - (e == et ? 1.0f : 0.0f)) * vv.y);
+          }
+          *reinterpret_cast<bf16x8*>(q + v * kCeFusedCols) = y;
+        }
+    }
+  };
+  // rows blockIdx.x, + G, ...; two register buffers, the next row's loads issued before the
+  // current row is processed; the LDS slots alternate so one barrier per row suffices
+  bf16x8 xa[NV], xb[NV];
+  long r = blockIdx.x;
+  int64_t ta = 0, tb = 0;
+  if (r < rows) {
+    load(r, xa);
+    ta = targets[r];
+  }
+  for (; r < rows; r += 2 * G) {
+    const long r1 = r + G;
+    if (r1 < rows) {
+      load(r1, xb);
+      tb = targets[r1];
+    }
+    process(r, xa, ta, 0);
+    if (r1 >= rows) break;
+    const long r2 = r1 + G;
+    if (r2 < rows) {
+      load(r2, xa);
+      ta = targets[r2];
+    }
+    process(r1, xb, tb, 1);
+  }
+}
+
+// Non-ignored target count and the gradient scale the fused kernel assumes:
+// count = #(t != ignore_index), grad_scale = expected / count (one workgroup, fixed order).
+__global__ __launch_bounds__(1024) void softcap_ce_count_kernel(long rows, const int64_t* __restrict__ targets,
+                                                                int64_t ignore_index, float expected,
+                                                                float* __restrict__ count,
+                                                                float* __restrict__ grad_scale) {
+  __shared__ long long red[1024 / kWave];
+  long long c = 0;
+  for (long r = threadIdx.x; r < rows; r += 1024) c += targets[r] != ignore_index ? 1 : 0;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) c += __shfl_xor(c, o);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long tc = 0;
+    for (int w = 0; w < 1024 / kWave; ++w) tc += red[w];
+    *count = (float)tc;
+    *grad_scale = expected / (float)tc;
+  }
+}
+
+// data *= actual / expected, unless *actual == expected (then nothing is touched): the
+// backward of the fused cross entropy when the upstream gradient is not the one assumed.
+__global__ __launch_bounds__(256) void bf16_rescale_kernel(long n8, bf16* __restrict__ data,
+                                                           const float* __restrict__ actual, float expected) {
+  const float a = *actual;
+  if (a == expected) return;
+  const float f = a / expected;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n8; i += (long)gridDim.x * 256) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(data + i * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = to_bf16((float)v[e] * f);
+    *reinterpret_cast<bf16x8*>(data + i * 8) = v;
+  }
+}
+
 static unsigned ce_grid(int64_t rows, int per_cu) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
@@ -320,6 +499,76 @@ extern "C" int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, i
                      (long)stride, softcap, (const bf16*)logits, targets, ignore_index, lse_rows,
                      grad_scale, (bf16*)grad_logits);
   KDA_LAUNCH_CHECK("softcap_cross_entropy_backward");
+  return KDA_OK;
+}
+
+extern "C" int kda_softcap_cross_entropy_fused_supported(int32_t vocab, int64_t stride) {
+  return vocab > 0 && (int64_t)vocab == stride && stride % kda::kCeFusedCols == 0 &&
+         stride <= (int64_t)kda::kCeFusedCols * kda::kCeFusedMaxVec;
+}
+
+extern "C" int kda_softcap_cross_entropy_fused(int64_t rows, int32_t vocab, int64_t stride, float softcap,
+                                               const void* logits, const int64_t* targets,
+                                               int64_t ignore_index, const float* grad_scale,
+                                               float* loss_rows, float* lse_rows, void* grad_logits,
+                                               hipStream_t stream) {
+  using namespace kda;
+  int rc = check_ce_args(rows, vocab, stride, softcap, logits, targets);
+  if (rc != KDA_OK) return rc;
+  KDA_REQUIRE(kda_softcap_cross_entropy_fused_supported(vocab, stride),
+              "softcap_cross_entropy_fused: needs vocab == stride, a multiple of %d and at most %d",
+              kCeFusedCols, kCeFusedCols * kCeFusedMaxVec);
+  KDA_REQUIRE(grad_scale && loss_rows && lse_rows && grad_logits, "softcap_cross_entropy_fused: null pointer");
+  KDA_REQUIRE(aligned16(grad_logits), "softcap_cross_entropy_fused: grad must be 16-byte aligned");
+  if (rows == 0) return KDA_OK;
+  // one workgroup per CU (at most one per row)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const unsigned grid = (unsigned)(rows < (long)cus * kCeFusedPerCu ? rows : (long)cus * kCeFusedPerCu);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kCeFusedThreads), 0, stream, (long)rows, vocab, softcap,
+                       (const bf16*)logits, targets, ignore_index, grad_scale, loss_rows, lse_rows,
+                       (bf16*)grad_logits);
+  };
+  switch (stride / kCeFusedCols) {
+    case 1: launch(softcap_ce_fused_kernel<1>); break;
+    case 2: launch(softcap_ce_fused_kernel<2>); break;
+    case 3: launch(softcap_ce_fused_kernel<3>); break;
+    case 4: launch(softcap_ce_fused_kernel<4>); break;
+    case 5: launch(softcap_ce_fused_kernel<5>); break;
+    case 6: launch(softcap_ce_fused_kernel<6>); break;
+    case 7: launch(softcap_ce_fused_kernel<7>); break;
+    default: launch(softcap_ce_fused_kernel<8>); break;
+  }
+  KDA_LAUNCH_CHECK("softcap_cross_entropy_fused");
+  return KDA_OK;
+}
+
+extern "C" int kda_softcap_cross_entropy_count(int64_t rows, const int64_t* targets, int64_t ignore_index,
+                                               float expected_grad, float* count, float* grad_scale,
+                                               hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(rows >= 0, "softcap_cross_entropy_count: negative row count");
+  KDA_REQUIRE(count && grad_scale && (rows == 0 || targets), "softcap_cross_entropy_count: null pointer");
+  hipLaunchKernelGGL(softcap_ce_count_kernel, dim3(1), dim3(1024), 0, stream, (long)rows, targets, ignore_index,
+                     expected_grad, count, grad_scale);
+  KDA_LAUNCH_CHECK("softcap_cross_entropy_count");
+  return KDA_OK;
+}
+
+extern "C" int kda_bf16_rescale_if_changed(int64_t n, void* data, const float* actual, float expected,
+                                           hipStream_t stream) {
+  using namespace kda;
+  KDA_REQUIRE(n >= 0 && n % 8 == 0, "bf16_rescale_if_changed: n must be a non-negative multiple of 8");
+  KDA_REQUIRE(actual && (n == 0 || data), "bf16_rescale_if_changed: null pointer");
+  KDA_REQUIRE(expected != 0.f, "bf16_rescale_if_changed: expected must be nonzero");
+  KDA_REQUIRE(aligned16(data), "bf16_rescale_if_changed: data must be 16-byte aligned");
+  if (n == 0) return KDA_OK;
+  const long n8 = n / 8;
+  const long blocks = (n8 + 255) / 256;
+  hipLaunchKernelGGL(bf16_rescale_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, stream,
+                     n8, (bf16*)data, actual, expected);
+  KDA_LAUNCH_CHECK("bf16_rescale_if_changed");
   return KDA_OK;
 }
 

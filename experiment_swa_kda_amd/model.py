@@ -150,11 +150,43 @@ class _SoftcapCrossEntropy(torch.autograd.Function):
         return dlogits, None, None, None, None
 
 
-def softcap_cross_entropy(logits, targets, vocab, softcap=15.0, ignore_index=-1):
+class _SoftcapCrossEntropyFused(torch.autograd.Function):
+    """The same loss with its gradient formed in the forward pass: one read of the logits
+    writes the row losses and the logit gradient for an assumed upstream gradient
+    ``expected_grad``.  The backward returns that buffer, rescaled on the device only if the
+    actual upstream gradient differs (no host synchronisation either way)."""
+
+    @staticmethod
+    def forward(ctx, logits, targets, vocab, softcap, ignore_index, expected_grad):
+        loss_rows, _, dlogits, _ = ops.softcap_cross_entropy_fused(logits, targets, vocab, softcap,
+                                                                   ignore_index, expected_grad)
+        loss, _ = ops.softcap_cross_entropy_mean(loss_rows, targets, ignore_index)
+        ctx.save_for_backward(dlogits)
+        ctx.expected = expected_grad
+        ctx.used = False
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad):
+        if ctx.used:  # the gradient buffer is handed out (and rescaled) in place
+            raise RuntimeError("softcap_cross_entropy: the fused form's backward can run only once")
+        ctx.used = True
+        (dlogits,) = ctx.saved_tensors
+        ops.rescale_bf16_if_changed(dlogits, grad, ctx.expected)
+        return dlogits, None, None, None, None, None
+
+
+def softcap_cross_entropy(logits, targets, vocab, softcap=15.0, ignore_index=-1, expected_grad=None):
     """mean cross_entropy(softcap * tanh(logits[:, :vocab] / softcap), targets) over rows whose
     target is not ignore_index; logits [rows, padded vocab].  bf16 CUDA logits run the fused
-    HIP kernels, anything else the eager f32 form."""
+    HIP kernels, anything else the eager f32 form.  With ``expected_grad`` (the dL/dloss the
+    caller will back-propagate) and a gradient to form, rows whose columns are all vocabulary
+    take the one-pass forward + backward kernel."""
     if logits.is_cuda and logits.dtype == torch.bfloat16:
+        if (expected_grad is not None and expected_grad != 0 and torch.is_grad_enabled() and logits.requires_grad
+                and logits.ndim == 2 and ops.softcap_cross_entropy_fused_supported(vocab, logits.shape[1])):
+            return _SoftcapCrossEntropyFused.apply(logits, targets, vocab, float(softcap), ignore_index,
+                                                   float(expected_grad))
         return _SoftcapCrossEntropy.apply(logits, targets, vocab, float(softcap), ignore_index)
     z = softcap * torch.tanh(logits[:, :vocab].float() / softcap)
     return F.cross_entropy(z, targets, ignore_index=ignore_index)
@@ -383,6 +415,10 @@ class GPT(nn.Module):
         self.backout_lambda = nn.Parameter(0.2 * torch.ones(1))
         # the constant weight of x in the backout mix x - backout_lambda * mid
         self.register_buffer("_one", torch.ones(1), persistent=False)
+        # the dL/dloss the caller will back-propagate (1 for loss.backward()); the soft-capped
+        # cross entropy forms its logit gradient for it in the forward pass and rescales in
+        # the backward only if the actual one differs.  None: gradient formed in the backward.
+        self.loss_grad_hint = 1.0
 
     def cache_bf16_weights(self) -> list:
         """Casts the f32 projection weights to bf16 once: every Linear the forward calls and
@@ -489,7 +525,7 @@ class GPT(nn.Module):
         logits = self.lm_head(h)
         if targets is not None:
             return softcap_cross_entropy(logits.flatten(0, 1), targets.flatten(), self.config.vocab_size,
-                                         15.0, -1)
+                                         15.0, -1, expected_grad=self.loss_grad_hint)
         return 15 * torch.tanh(logits[..., : self.config.vocab_size].float() / 15)
 
 
@@ -578,6 +614,7 @@ class GraphedUpdate:
         self._w16 = self.model.cache_bf16_weights()  # kept alive with the captured graph
         try:
             for mb in self.batches:
+                self.model.loss_grad_hint = 1.0 / n  # the loss below is scaled by 1/n
                 loss = self.model(mb[:, :-1], mb[:, 1:]) / n
                 grads = torch.autograd.grad(loss, params, allow_unused=True)
                 if acc is None:
@@ -596,6 +633,7 @@ class GraphedUpdate:
                 total = loss.detach() if total is None else total + loss.detach()
         finally:
             self.model.drop_bf16_weights()
+            self.model.loss_grad_hint = 1.0
         for p, g in zip(params, acc):
             p.grad = g
         self.opt.step()

@@ -588,6 +588,55 @@ def softcap_cross_entropy_mean(loss_rows, targets, ignore_index=-1):
     return out[0], out[1]
 
 
+def softcap_cross_entropy_fused_supported(vocab, stride):
+    """True where the one-pass forward + backward kernel takes rows of this shape (every
+    column is vocabulary, a multiple of 4096 columns, at most 32768)."""
+    return bool(_lib.load().kda_softcap_cross_entropy_fused_supported(int(vocab), int(stride)))
+
+
+def softcap_cross_entropy_fused(logits, targets, vocab, softcap, ignore_index=-1, expected_grad=1.0):
+    """Forward and backward in one read of the logits: -> (loss_rows, lse_rows, grad_logits,
+    count).  grad_logits is the gradient for an upstream dL/dmean of ``expected_grad``
+    (rescale it with rescale_bf16_if_changed when the actual one differs); count is the
+    non-ignored row count (f32 device scalar)."""
+    dev = _require_cuda("softcap_cross_entropy_fused", logits, targets)
+    _check_dtype("softcap_cross_entropy_fused", logits, torch.bfloat16, "logits")
+    _check_dtype("softcap_cross_entropy_fused", targets, torch.int64, "targets")
+    if logits.ndim != 2 or targets.shape != logits.shape[:1]:
+        raise RuntimeError("softcap_cross_entropy_fused: logits [rows, stride] and targets [rows]")
+    logits, targets = _c(logits), _c(targets)
+    rows, stride = logits.shape
+    loss = torch.empty(rows, dtype=torch.float32, device=dev)
+    lse = torch.empty(rows, dtype=torch.float32, device=dev)
+    grad = torch.empty_like(logits)
+    sc = torch.empty(2, dtype=torch.float32, device=dev)  # count, grad scale
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.kda_softcap_cross_entropy_count(rows, ptr(targets), int(ignore_index), float(expected_grad),
+                                                 ptr(sc), sc.data_ptr() + 4, _stream(dev))
+        check(rc, "kda_softcap_cross_entropy_count")
+        rc = lib.kda_softcap_cross_entropy_fused(rows, int(vocab), stride, float(softcap), ptr(logits),
+                                                 ptr(targets), int(ignore_index), sc.data_ptr() + 4, ptr(loss),
+                                                 ptr(lse), ptr(grad), _stream(dev))
+    check(rc, "kda_softcap_cross_entropy_fused")
+    return loss, lse, grad, sc[0]
+
+
+def rescale_bf16_if_changed(data, actual, expected):
+    """data (bf16, contiguous, numel % 8 == 0) *= actual / expected in place unless the
+    device scalar ``actual`` equals ``expected`` (decided on the device, no host sync)."""
+    dev = _require_cuda("rescale_bf16_if_changed", data, actual)
+    _check_dtype("rescale_bf16_if_changed", data, torch.bfloat16, "data")
+    if not data.is_contiguous():
+        raise RuntimeError("rescale_bf16_if_changed: data must be contiguous")
+    actual = actual.to(torch.float32).reshape(1).contiguous()
+    with torch.cuda.device(dev):
+        rc = _lib.load().kda_bf16_rescale_if_changed(data.numel(), ptr(data), ptr(actual), float(expected),
+                                                     _stream(dev))
+    check(rc, "kda_bf16_rescale_if_changed")
+    return data
+
+
 def embedding_backward(idx, grad_output, vocab):
     """Gradient of an embedding lookup: idx int64 [...], grad_output bf16 [..., dim] ->
     grad_weight bf16 [vocab, dim] (token-order f32 sums, deterministic)."""

@@ -355,6 +355,41 @@ int kda_softcap_cross_entropy_backward(int64_t rows, int32_t vocab, int64_t stri
                                        hipStream_t stream);
 
 /*
+ * Forward and backward of the above in one pass (one read of the logits instead of two),
+ * for rows whose columns are all vocabulary: vocab == stride, a multiple of 4096, at most
+ * 32768 (kda_softcap_cross_entropy_fused_supported; other shapes use the two calls above).
+ * Writes loss_rows and lse_rows as the forward does and grad_logits as the backward would
+ * for the device scalar grad_scale (the expected dL/dmean / non-ignored count, as written by
+ * kda_softcap_cross_entropy_count).  Same semantics as nanochat/gpt.py:600-608 plus its
+ * autograd backward; no counterpart entry point in the reference (its cross entropy runs
+ * under torch.compile).
+ */
+int kda_softcap_cross_entropy_fused_supported(int32_t vocab, int64_t stride);
+int kda_softcap_cross_entropy_fused(int64_t rows, int32_t vocab, int64_t stride, float softcap,
+                                    const void* logits, const int64_t* targets, int64_t ignore_index,
+                                    const float* grad_scale, float* loss_rows, float* lse_rows,
+                                    void* grad_logits, hipStream_t stream);
+
+/*
+ * count[0] = number of targets != ignore_index, grad_scale[0] = expected_grad / count[0]
+ * (device scalars; one workgroup, fixed order): the scale the fused call above assumes when
+ * the mean loss will be back-propagated with gradient expected_grad.  Trainer support, no
+ * counterpart in the reference.
+ */
+int kda_softcap_cross_entropy_count(int64_t rows, const int64_t* targets, int64_t ignore_index,
+                                    float expected_grad, float* count, float* grad_scale,
+                                    hipStream_t stream);
+
+/*
+ * data[0..n) (bf16, n a multiple of 8) *= actual[0] / expected, unless actual[0] == expected,
+ * in which case nothing is read or written: the backward of the fused cross entropy when the
+ * upstream gradient (a device scalar) is not the one its forward assumed.  No host
+ * synchronisation.  Trainer support, no counterpart in the reference.
+ */
+int kda_bf16_rescale_if_changed(int64_t n, void* data, const float* actual, float expected,
+                                hipStream_t stream);
+
+/*
  * Mean of loss_rows [rows] over the rows whose target differs from ignore_index, and that
  * row count (both f32 scalars on the device; loss is NaN when every row is ignored).  The
  * reduction F.cross_entropy(reduction="mean") applies in nanochat/gpt.py:600-608, in one

@@ -115,6 +115,75 @@ def test_softcap_ce_deterministic_and_scaled_gradient():
     assert torch.equal((g1.float() * 0.25).bfloat16(), g2)
 
 
+@pytest.mark.parametrize("rows,vocab,ignore_every,expected,actual", [
+    (64, 32768, 0, 1.0, 1.0),     # the trainer's vocabulary, gradient as assumed
+    (37, 32768, 5, 0.25, 0.25),   # ignored rows, the graphed update's 1/4 scale
+    (300, 4096, 7, 1.0, 0.3),     # one vector per thread; actual gradient differs: rescaled
+    (16, 12288, 3, 0.5, -2.0),    # three vectors per thread; negative upstream gradient
+])
+def test_softcap_ce_fused_matches_oracle(rows, vocab, ignore_every, expected, actual):
+    """The one-pass forward + backward: loss, row losses and lse against the fp64 oracle,
+    and the logit gradient for the actual upstream gradient, whether or not it is the one
+    the forward assumed."""
+    x, t = _case(rows, vocab, vocab, 2.0, seed=rows + 3, ignore_every=ignore_every)
+    loss_o, rows_o, lse_o, d_o = O.softcap_cross_entropy(x.double().numpy(), t.numpy(), vocab, 15.0, -1)
+    xd, td = x.cuda().requires_grad_(), t.cuda()
+    loss = softcap_cross_entropy(xd, td, vocab, 15.0, -1, expected_grad=expected)
+    assert loss.grad_fn is not None and "Fused" in type(loss.grad_fn).__name__
+    loss.backward(torch.tensor(actual, device="cuda"))
+    assert abs(loss.item() - loss_o) <= 1e-5 * max(1.0, abs(loss_o))
+    lr, lse, g, count = ops.softcap_cross_entropy_fused(xd.detach(), td, vocab, 15.0, -1, expected)
+    np.testing.assert_allclose(lse.cpu().double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(lr.cpu().double().numpy(), rows_o, rtol=2e-5, atol=2e-5)
+    assert count.item() == float((t != -1).sum())
+    assert rel_err(g.float().cpu(), expected * d_o) < 5e-3
+    d = xd.grad.float().cpu()
+    assert rel_err(d, actual * d_o) < 5e-3
+    if ignore_every:
+        assert torch.all(d[::ignore_every] == 0)
+    # the two-kernel path gives the same values to rounding
+    lr2, lse2 = ops.softcap_cross_entropy_forward(xd.detach(), td, vocab, 15.0, -1)
+    assert torch.allclose(lse, lse2, rtol=1e-6, atol=1e-6)
+    g2 = ops.softcap_cross_entropy_backward(xd.detach(), td, lse2, torch.tensor(expected, device="cuda") / count,
+                                            vocab, 15.0)
+    assert rel_err(g.float().cpu(), g2.float().cpu().double().numpy()) < 1e-2
+
+
+def test_softcap_ce_fused_nan_row_and_fallbacks():
+    """A NaN logit poisons its row's loss, lse and gradient in the one-pass kernel too; a
+    second backward raises (the gradient buffer is handed out in place); shapes the kernel
+    does not take (vocabulary padding, rows over 32768 columns) and forward-only calls use the
+    two-kernel path."""
+    rows, vocab = 8, 8192
+    x, t = _case(rows, vocab, vocab, 4.0, seed=21)
+    x[2, 17] = float("nan")
+    xd, td = x.cuda(), t.cuda()
+    lr, lse, g, _ = ops.softcap_cross_entropy_fused(xd, td, vocab, 15.0, -1, 1.0)
+    lr, lse, g = lr.cpu(), lse.cpu(), g.float().cpu()
+    assert math.isnan(lr[2]) and math.isnan(lse[2]) and torch.isnan(g[2]).all()
+    good = torch.tensor([r for r in range(rows) if r != 2])
+    assert torch.isfinite(lr[good]).all() and torch.isfinite(g[good]).all()
+    _, rows_o, lse_o, _ = O.softcap_cross_entropy(x[good].double().numpy(), t[good].numpy(), vocab, 15.0, -1)
+    np.testing.assert_allclose(lse[good].double().numpy(), lse_o, rtol=2e-6, atol=2e-6)
+    x2, t2 = _case(4, 4096, 4096, 1.0, seed=22)
+    xg = x2.cuda().requires_grad_()
+    loss = softcap_cross_entropy(xg, t2.cuda(), 4096, 15.0, -1, expected_grad=1.0)
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError):
+        loss.backward()
+    assert not ops.softcap_cross_entropy_fused_supported(8000, 8192)
+    assert not ops.softcap_cross_entropy_fused_supported(4100, 4104)
+    assert not ops.softcap_cross_entropy_fused_supported(65536, 65536)
+    assert ops.softcap_cross_entropy_fused_supported(32768, 32768)
+    x3, t3 = _case(4, 1000, 1024, 1.0, seed=23)
+    x3d = x3.cuda().requires_grad_()
+    loss = softcap_cross_entropy(x3d, t3.cuda(), 1000, 15.0, -1, expected_grad=1.0)
+    assert "Fused" not in type(loss.grad_fn).__name__
+    with torch.no_grad():
+        loss = softcap_cross_entropy(xg, t2.cuda(), 4096, 15.0, -1, expected_grad=1.0)
+    assert loss.grad_fn is None
+
+
 def test_softcap_ce_rejects_bad_arguments():
     x = torch.zeros(4, 12, dtype=torch.bfloat16, device="cuda")
     t = torch.zeros(4, dtype=torch.int64, device="cuda")
