@@ -27,6 +27,19 @@ def np64(t):
     return None if t is None else t.detach().double().cpu().numpy()
 
 
+def mixer_oracle_weights(layer):
+    """kda_oracle.full_layer keyword arguments of a KimiDeltaAttention layer (the layer
+    multiplies with bf16 copies of its f32 weights)."""
+    w = lambda m: np64(m.weight.bfloat16())  # noqa: E731
+    c = lambda m: np64(m.weight[:, 0].bfloat16())  # noqa: E731
+    return dict(q_weight=w(layer.q_proj), k_weight=w(layer.k_proj), v_weight=w(layer.v_proj),
+                q_conv_weight=c(layer.q_conv1d), k_conv_weight=c(layer.k_conv1d), v_conv_weight=c(layer.v_conv1d),
+                forget_a_weight=w(layer.f_a_proj), forget_b_weight=w(layer.f_b_proj), beta_weight=w(layer.b_proj),
+                A_log=np64(layer.A_log), dt_bias=np64(layer.dt_bias), output_gate_weight=w(layer.g_proj),
+                norm_weight=np64(layer.o_norm.weight), output_weight=w(layer.o_proj), num_heads=layer.num_heads,
+                norm_eps=layer.o_norm.eps)
+
+
 def make_kda_inputs(B, T, H, K, V, *, seed, gate="k3", state=False, dist="reference", device="cuda"):
     """Seeded bf16 activations, f32 params (built on the CPU, then moved).
 

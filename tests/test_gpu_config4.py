@@ -11,25 +11,13 @@ import pytest
 import torch
 
 from oracle import kda_oracle as O
-from tests.kda_testutil import cosine, np64, rel_err
+from tests.kda_testutil import cosine, mixer_oracle_weights, np64, rel_err
 
 pytestmark = pytest.mark.gpu
 
 if torch.cuda.is_available():
     from experiment_swa_kda_amd import KimiDeltaAttention
     from experiment_swa_kda_amd.model import GPT, GPTConfig, GraphedUpdate, make_optimizer
-
-
-def _oracle_weights(layer):
-    # the block multiplies with bf16 copies of its f32 weights
-    w = lambda m: np64(m.weight.bfloat16())  # noqa: E731
-    c = lambda m: np64(m.weight[:, 0].bfloat16())  # noqa: E731
-    return dict(q_weight=w(layer.q_proj), k_weight=w(layer.k_proj), v_weight=w(layer.v_proj),
-                q_conv_weight=c(layer.q_conv1d), k_conv_weight=c(layer.k_conv1d), v_conv_weight=c(layer.v_conv1d),
-                forget_a_weight=w(layer.f_a_proj), forget_b_weight=w(layer.f_b_proj), beta_weight=w(layer.b_proj),
-                A_log=np64(layer.A_log), dt_bias=np64(layer.dt_bias), output_gate_weight=w(layer.g_proj),
-                norm_weight=np64(layer.o_norm.weight), output_weight=w(layer.o_proj), num_heads=layer.num_heads,
-                norm_eps=layer.o_norm.eps)
 
 
 def test_mixer_block_d384_forward_and_gradients_match_oracle():
@@ -45,7 +33,7 @@ def test_mixer_block_d384_forward_and_gradients_match_oracle():
     gy = torch.randn(1, 512, 384, generator=g).bfloat16().cuda()
     y, _ = layer(x)
     y.backward(gy)
-    wts = _oracle_weights(layer)
+    wts = mixer_oracle_weights(layer)
     ey, _ = O.full_layer(np64(x), **wts)
     assert rel_err(y, ey) < 2e-2, rel_err(y, ey)
     eg = O.full_layer_backward(np64(x), np64(gy), **wts)

@@ -6,8 +6,9 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import gpt_oracle as G
 from oracle import kda_oracle as O
-from tests.kda_testutil import cosine, np64, rel_err
+from tests.kda_testutil import cosine, mixer_oracle_weights, np64, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -85,6 +86,47 @@ def test_tiny_gpt_trains_and_matches_reference_mode_logits():
             b.attn.mode = "reference"
         ref = model(idx[:, :-1])
     assert rel_err(logits, ref) < 2e-2
+
+
+def test_gpt_logits_and_loss_match_oracle():
+    """The decoder's forward (smear, residual and x0 lambdas, KDA blocks, MLPs, backout,
+    soft-capped head and loss) against the float64 oracle of nanochat/gpt.py:548-608."""
+    cfg = GPTConfig(sequence_len=128, vocab_size=500, n_layer=3, n_head=2, n_embd=256)
+    torch.manual_seed(1)
+    model = GPT(cfg).cuda()
+    model.init_weights()
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        for b in model.transformer.h:
+            b.attn.o_proj.weight.copy_(torch.randn(b.attn.o_proj.weight.shape, generator=g) * 0.03)
+            b.mlp.c_proj.weight.copy_(torch.randn(b.mlp.c_proj.weight.shape, generator=g) * 0.03)
+            b.attn.A_log.copy_(torch.randn(2, generator=g) * 0.3)
+        model.lm_head.weight.copy_(torch.randn(model.lm_head.weight.shape, generator=g) * 0.05)
+        model.resid_lambdas.copy_(1 + 0.1 * torch.randn(3, generator=g))
+        model.x0_lambdas.copy_(0.2 * torch.randn(3, generator=g))
+        model.smear_lambda.fill_(0.6)
+        model.smear_gate.weight.copy_(torch.randn(1, 24, generator=g) * 0.3)
+        model.backout_lambda.fill_(0.35)
+    idx = torch.randint(0, 500, (2, 97), generator=g).cuda()  # T = 96: one full and one partial chunk
+    idx[1, 40] = 499
+    tg = idx[:, 1:].clone()
+    tg[0, 7] = -1
+    bf = lambda w: np64(w.bfloat16())  # noqa: E731
+    params = dict(wte=np64(model.transformer.wte.weight), lm_head=bf(model.lm_head.weight),
+                  resid_lambdas=np64(model.resid_lambdas), x0_lambdas=np64(model.x0_lambdas),
+                  smear_gate=bf(model.smear_gate.weight), smear_lambda=model.smear_lambda.item(),
+                  backout_lambda=model.backout_lambda.item(),
+                  layers=[dict(mixer_oracle_weights(b.attn), c_fc=bf(b.mlp.c_fc.weight), c_proj=bf(b.mlp.c_proj.weight))
+                          for b in model.transformer.h])
+    x = idx[:, :-1].cpu().numpy()
+    with torch.no_grad():
+        logits = model(idx[:, :-1])
+        loss = model(idx[:, :-1], tg)
+    want = G.gpt_forward(x, params, vocab=500)
+    assert logits.shape == want.shape
+    assert rel_err(logits, want) < 3e-2, rel_err(logits, want)
+    want_loss = G.gpt_forward(x, params, vocab=500, targets=tg.cpu().numpy())
+    assert abs(float(loss) - want_loss) < 2e-2 * want_loss, (float(loss), want_loss)
 
 
 def test_graphed_update_matches_eager_updates():
