@@ -16,15 +16,21 @@ namespace kda {
 
 // Rows per thread.  Forward: 1, 16 rows per workgroup at D = 128 (1,536 workgroups for the
 // 24,576 rows of B2 T4096 H3; measured 3.5 us against 3.7 with 2, 4.0 with 3, 4.5 with 4).
-// Backward: 6, one workgroup per CU, and half the weight-gradient partials for the
-// reduction launch (measured: 9.3 us against 10.2 with 3, 10.3 with 4 and 11.2 with 2).
+// Backward: 768 threads x 2 rows, 96 rows per workgroup (one workgroup per CU, 12 waves),
+// and half the weight-gradient partials for the reduction launch (measured at config 2:
+// 8.98 us against 9.06 with 512 x 3, 9.3 with 256 x 6 or 1024 x 2, 10.2 with 256 x 3).
+// Summing the partials in the launch itself (the last workgroup to finish, counted by one
+// atomic word) was slower than the separate launch: 11.7 us.
 #ifndef KDA_NORM_ROWS_FWD
 #define KDA_NORM_ROWS_FWD 1
 #endif
 #ifndef KDA_NORM_ROWS_BWD
-#define KDA_NORM_ROWS_BWD 6
+#define KDA_NORM_ROWS_BWD 2
 #endif
-constexpr int kRowsFwd = KDA_NORM_ROWS_FWD, kRowsBwd = KDA_NORM_ROWS_BWD;
+#ifndef KDA_NORM_BWD_THREADS
+#define KDA_NORM_BWD_THREADS 768
+#endif
+constexpr int kRowsFwd = KDA_NORM_ROWS_FWD, kRowsBwd = KDA_NORM_ROWS_BWD, kBwdThreads = KDA_NORM_BWD_THREADS;
 
 template <int D>
 __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf16* __restrict__ x,
@@ -72,7 +78,7 @@ __global__ __launch_bounds__(256) void norm_gate_fwd_kernel(long rows, const bf1
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
+__global__ __launch_bounds__(kBwdThreads) void norm_gate_bwd_kernel(
     long rows, int heads, const bf16* __restrict__ x, const bf16* __restrict__ gate, long gld,
     const float* __restrict__ weight, const float* __restrict__ inv_rms,
     const bf16* __restrict__ dy, bf16* __restrict__ dx, bf16* __restrict__ dgate, long dgld,
@@ -86,8 +92,8 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
     return (long)tok * ld + (long)((unsigned)r - tok * (unsigned)heads) * D;
   };
   constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;
-  __shared__ float s_dw[256 / kWave][D];
+  constexpr int RPP = kBwdThreads / LPR;
+  __shared__ float s_dw[kBwdThreads / kWave][D];
   const int lane = threadIdx.x % LPR;
   const int c0 = lane * 8;
   const long r0 = (long)blockIdx.x * RPP * kRowsBwd + threadIdx.x / LPR;
@@ -155,7 +161,7 @@ __global__ __launch_bounds__(256) void norm_gate_bwd_kernel(
   if (threadIdx.x < D) {
     float acc = 0.f;
 #pragma unroll
-    for (int s = 0; s < 256 / kWave; ++s) acc += s_dw[s][threadIdx.x];
+    for (int s = 0; s < kBwdThreads / kWave; ++s) acc += s_dw[s][threadIdx.x];
     dw_part[(size_t)blockIdx.x * D + threadIdx.x] = acc;
   }
 }
@@ -259,8 +265,8 @@ static int gen_norm_blocks(long rows) {
 
 static bool fast_dim(int dim) { return dim == 64 || dim == 128; }
 
-static int norm_blocks(long rows, int dim, int rows_per_thread) {
-  const long rpb = 256 / (dim / 8) * rows_per_thread;
+static int norm_blocks(long rows, int dim, int rows_per_thread, int threads = 256) {
+  const long rpb = threads / (dim / 8) * rows_per_thread;
   long nb = (rows + rpb - 1) / rpb;
   if (nb < 1) nb = 1;
   return (int)nb;
@@ -302,7 +308,7 @@ extern "C" int kda_rmsnorm_gate_forward(int64_t rows, int32_t dim, const void* x
 
 extern "C" size_t kda_rmsnorm_gate_backward_scratch_bytes(int64_t rows, int32_t dim) {
   if (dim < 1 || dim > kda::kGenNormMaxD) return 0;
-  const size_t nb = kda::fast_dim(dim) ? kda::norm_blocks(rows, dim, kda::kRowsBwd) : kda::gen_norm_blocks(rows);
+  const size_t nb = kda::fast_dim(dim) ? kda::norm_blocks(rows, dim, kda::kRowsBwd, kda::kBwdThreads) : kda::gen_norm_blocks(rows);
   return kda::align256(nb * dim * sizeof(float)) + 256;
 }
 
@@ -343,14 +349,14 @@ extern "C" int kda_rmsnorm_gate_backward_strided(int64_t rows, int32_t dim, int3
     KDA_LAUNCH_CHECK("rmsnorm_gate_dweight_reduce");
     return KDA_OK;
   }
-  const int nb = norm_blocks(rows, dim, kRowsBwd);
+  const int nb = norm_blocks(rows, dim, kRowsBwd, kBwdThreads);
   if (rows > 0) {
     if (dim == 128)
-      hipLaunchKernelGGL(norm_gate_bwd_kernel<128>, dim3(nb), dim3(256), 0, stream, (long)rows, (int)heads,
+      hipLaunchKernelGGL(norm_gate_bwd_kernel<128>, dim3(nb), dim3(kBwdThreads), 0, stream, (long)rows, (int)heads,
                          (const bf16*)x, (const bf16*)gate, (long)gate_row_stride, weight, inv_rms,
                          (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, (long)dgate_row_stride, part);
     else
-      hipLaunchKernelGGL(norm_gate_bwd_kernel<64>, dim3(nb), dim3(256), 0, stream, (long)rows, (int)heads,
+      hipLaunchKernelGGL(norm_gate_bwd_kernel<64>, dim3(nb), dim3(kBwdThreads), 0, stream, (long)rows, (int)heads,
                          (const bf16*)x, (const bf16*)gate, (long)gate_row_stride, weight, inv_rms,
                          (const bf16*)grad_output, (bf16*)dx, (bf16*)dgate, (long)dgate_row_stride, part);
     KDA_LAUNCH_CHECK("rmsnorm_gate_backward");
