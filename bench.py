@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the 6-layer training throughput")
+    ap.add_argument("--train-only", action="store_true",
+                    help="print only the 6-layer training throughput (3 graphed updates) and exit")
     ap.add_argument("--hbm-sweep", action="store_true",
                     help="print the HBM-peak fraction of conv / norm-gate / copy over batch sizes and exit")
     ap.add_argument("--hbm-kernels", action="store_true",
@@ -474,6 +476,9 @@ def main():
         return
     if args.hbm_kernels:
         print(json.dumps(hbm_kernels(torch)), flush=True)
+        return
+    if args.train_only:
+        print(json.dumps(train_throughput(torch, updates=3, warmup=1)), flush=True)
         return
     if args.mfma_probe:
         for shape in (0, 1):
