@@ -88,10 +88,12 @@ def test_tiny_gpt_trains_and_matches_reference_mode_logits():
     assert rel_err(logits, ref) < 2e-2
 
 
-def test_gpt_logits_and_loss_match_oracle():
+@pytest.mark.parametrize("n_embd,n_head", [(256, 2), (384, 3)])
+def test_gpt_logits_and_loss_match_oracle(n_embd, n_head):
     """The decoder's forward (smear, residual and x0 lambdas, KDA blocks, MLPs, backout,
-    soft-capped head and loss) against the float64 oracle of nanochat/gpt.py:548-608."""
-    cfg = GPTConfig(sequence_len=128, vocab_size=500, n_layer=3, n_head=2, n_embd=256)
+    soft-capped head and loss) against the float64 oracle of nanochat/gpt.py:548-608, at a
+    small width and at config 4's d384 / 3 heads of 128."""
+    cfg = GPTConfig(sequence_len=128, vocab_size=500, n_layer=3, n_head=n_head, n_embd=n_embd)
     torch.manual_seed(1)
     model = GPT(cfg).cuda()
     model.init_weights()
@@ -100,7 +102,7 @@ def test_gpt_logits_and_loss_match_oracle():
         for b in model.transformer.h:
             b.attn.o_proj.weight.copy_(torch.randn(b.attn.o_proj.weight.shape, generator=g) * 0.03)
             b.mlp.c_proj.weight.copy_(torch.randn(b.mlp.c_proj.weight.shape, generator=g) * 0.03)
-            b.attn.A_log.copy_(torch.randn(2, generator=g) * 0.3)
+            b.attn.A_log.copy_(torch.randn(n_head, generator=g) * 0.3)
         model.lm_head.weight.copy_(torch.randn(model.lm_head.weight.shape, generator=g) * 0.05)
         model.resid_lambdas.copy_(1 + 0.1 * torch.randn(3, generator=g))
         model.x0_lambdas.copy_(0.2 * torch.randn(3, generator=g))
